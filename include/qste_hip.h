@@ -1,0 +1,157 @@
+/*
+ * qste_hip.h -- C ABI of the MI355X (gfx950) binary-linear kernels.
+ *
+ * Every entry point takes raw device pointers, int64 sizes and a HIP stream
+ * (passed as `void*`, i.e. a hipStream_t; NULL is the default stream), runs
+ * asynchronously on that stream, never synchronizes the host and never
+ * allocates: scratch space, where an operation needs it, is passed in by the
+ * caller through `workspace` / `workspace_bytes`, sized by the matching
+ * `*_workspace_bytes` query.  Every entry returns 0 on success, a positive
+ * hipError_t when a launch fails, or a negative QSTE_E_* code for an argument
+ * the kernels cannot take (qste_error_string() names it).  Nothing is
+ * written on an argument error.
+ *
+ * Layouts (the reference's own, src/qste/surface.py:67-79):
+ *   packed sign  uint8 [rows, (cols + 7) / 8], bit j of byte b is column
+ *                8b + j, set means +1 (value >= 0); pad bits are zero.
+ *   coordinate / moment_q     int8  [rows, cols] row-major
+ *   moment_scale              fp16  [ceil(rows * cols / block_size)]
+ *   row_v / col_v             fp16  [rows] / [cols]
+ *   activations and gradients row-major [samples, features] in `dtype`.
+ *
+ * Each declaration names the reference interface it replaces (file:line in
+ * BleedingXiko/QSTE).  The Python binding is qste_amd/kernels/_lib.py.
+ */
+#ifndef QSTE_HIP_H
+#define QSTE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types of activations / gradients / outputs */
+#define QSTE_F32 0
+#define QSTE_F16 1
+#define QSTE_BF16 2
+
+/* argument errors (negative so they never collide with hipError_t) */
+#define QSTE_E_DTYPE (-1)
+#define QSTE_E_SHAPE (-2)
+#define QSTE_E_NULL (-3)
+#define QSTE_E_WORKSPACE (-4)
+#define QSTE_E_BLOCK (-5)
+#define QSTE_E_ALIGN (-6)
+
+/* Library version; bumps when an entry point's contract changes. */
+int qste_version(void);
+
+/* Text for a return code of any entry point. */
+const char* qste_error_string(int code);
+
+/* Sign bits of an int8 coordinate matrix (coord >= 0 -> 1).
+ * Replaces qste.kernels.pack_coordinate (src/qste/kernels/loader.py:285-289;
+ * spec fallback.py:91-92). */
+int qste_pack_coordinate(const int8_t* coordinate, uint8_t* packed, int64_t rows,
+                         int64_t cols, void* stream);
+
+/* Expand packed signs to +-1 (times row_scale[r] when row_scale != NULL) in
+ * out_dtype, pad columns dropped: out [rows, cols].
+ * Replaces qste.kernels.unpack_rows (loader.py:247-254; fallback.py:27-29). */
+int qste_unpack_rows(const uint8_t* packed, const float* row_scale, void* out,
+                     int out_dtype, int64_t rows, int64_t cols, void* stream);
+
+/* One-bit affine encoding of each row of x [rows, cols] (fp32 arithmetic on
+ * the dtype's values): offset = mean, bits = (x - offset >= 0),
+ * scale = mean |x - offset|.
+ * Replaces qste.kernels.pack_affine_rows (loader.py:278-282;
+ * fallback.py:77-88), called by encode_activation (functional.py:98-115). */
+int qste_pack_affine_rows(const void* x, int dtype, uint8_t* packed, float* offset,
+                          float* scale, int64_t rows, int64_t cols, void* stream);
+
+/* y [m, rows] = (x [m, cols] @ sign^T) * scale + bias, output in x's dtype,
+ * fp32 accumulation, scale (fp32 [rows]) and bias (fp32 [rows] or NULL)
+ * applied in fp32 after the product.  Skinny m (decode) and large m share
+ * this entry.
+ * Replaces qste.kernels.packed_linear_affine (loader.py:292-297;
+ * fallback.py:95-108; PackedLinear.forward modules.py:114-120). */
+int qste_packed_linear_affine(const void* x, int dtype, const uint8_t* packed,
+                              const float* scale, const float* bias, void* y, int64_t m,
+                              int64_t rows, int64_t cols, void* stream);
+
+/* dx [m, cols] = dy [m, rows] @ (row_scale (*) sign), output in dy's dtype.
+ * row_scale (fp32 [rows], may be NULL) is folded into the expanded operand
+ * and rounded to dy's dtype there, as the reference GPU path does
+ * (src/qste/kernels/cuda.py:1585-1586).
+ * Replaces qste.kernels.packed_transpose (loader.py:299-304;
+ * fallback.py:111-123). */
+int qste_packed_transpose(const void* dy, int dtype, const uint8_t* packed,
+                          const float* row_scale, void* dx, int64_t m, int64_t rows,
+                          int64_t cols, void* stream);
+
+/* evidence fp32 [rows, cols] = dy[samples, rows]^T @ (row_scale (*) sign_x),
+ * sign_x from packed_x uint8 [samples, (cols+7)/8]; row_scale (fp32
+ * [samples], may be NULL) is rounded to dy's dtype as in cuda.py:1625.
+ * Replaces qste.kernels.evidence_from_packed (loader.py:306-313;
+ * fallback.py:126-138). */
+int qste_evidence_from_packed(const void* dy, int dtype, const uint8_t* packed_x,
+                              const float* row_scale, float* evidence, int64_t samples,
+                              int64_t rows, int64_t cols, void* stream);
+
+/* out fp32 [rows] = sum_c matrix[r, c] * sign[r, c], matrix fp32 [rows, cols].
+ * Replaces qste.kernels.packed_row_inner (loader.py:315-320;
+ * fallback.py:141-148). */
+int qste_packed_row_inner(const float* matrix, const uint8_t* packed, float* out,
+                          int64_t rows, int64_t cols, void* stream);
+
+/* The whole backward of one binary linear layer (QSTELinearFn.backward,
+ * src/qste/functional.py:173-194) in one call:
+ *   dx       [samples, cols] = dy @ (scale (*) sign_w)             (dy dtype)
+ *   E0       = dy^T @ (x_scale (*) sign_x) + (dy^T @ x_offset) 1^T
+ *              (decoded_evidence, functional.py:118-145)
+ *   grad_scale fp32 [rows] = sum_c E0 * sign_w         (packed_row_inner)
+ *   evidence fp32 [rows, cols] = E0 * scale[r]           (functional.py:190)
+ *   grad_bias fp32 [rows] = sum_t dy  (written when grad_bias != NULL)
+ * x_offset / x_scale are the fp32 [samples] rows of the saved aux.
+ * Needs qste_linear_backward_workspace_bytes() bytes of workspace.
+ * No counterpart as a single call in the reference: it fuses five of its
+ * calls (cuda.py:1568-1688, functional.py:143, 193). */
+size_t qste_linear_backward_workspace_bytes(int64_t samples, int64_t rows, int64_t cols);
+int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x,
+                         const float* x_offset, const float* x_scale,
+                         const uint8_t* packed_w, const float* scale, void* dx,
+                         float* evidence, float* grad_scale, float* grad_bias,
+                         int64_t samples, int64_t rows, int64_t cols, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/* One fused QSTE coordinate step on one surface
+ * (qste.kernels.coordinate_update, loader.py:329-368; spec
+ * fallback.py:158-242): factored second moment, global RMS clip, block
+ * momentum through fp16 scales, hash-seeded stochastic rounding of the int8
+ * coordinate, momentum requantization, sign repack and flip count.
+ *   evidence      fp32 [rows, cols], read only (the reference consumes it as
+ *                 scratch; this implementation does not write it)
+ *   step          used when step_device == NULL, else *step_device (int64 on
+ *                 the device) is read at run time (graph replay)
+ *   flips_out     device int64, set to the number of sign flips (NULL: skip)
+ *   update_enabled device uint8 or NULL; when it holds 0, no state is
+ *                 written and flips_out is set to 0 (cuda.py:1724-1729)
+ * block_size must be a power of two.  Needs
+ * qste_coordinate_update_workspace_bytes() bytes of workspace. */
+size_t qste_coordinate_update_workspace_bytes(int64_t rows, int64_t cols, int64_t block_size);
+int qste_coordinate_update(const float* evidence, int8_t* coordinate, uint8_t* packed,
+                           int8_t* moment_q, uint16_t* moment_scale, uint16_t* row_v,
+                           uint16_t* col_v, int64_t rows, int64_t cols, double beta1,
+                           double beta2, double update_clip, double coordinate_lr,
+                           int64_t block_size, int64_t seed, int64_t step,
+                           const int64_t* step_device, int64_t* flips_out,
+                           const uint8_t* update_enabled, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QSTE_HIP_H */

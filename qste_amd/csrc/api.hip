@@ -1,0 +1,256 @@
+// extern "C" entry points declared in include/qste_hip.h: argument checks,
+// workspace carving and kernel dispatch.  Nothing here allocates or
+// synchronizes; every launch goes on the caller's stream.
+#include "common.hpp"
+
+namespace qste {
+int launch_pack_coordinate(const int8_t*, uint8_t*, int64_t, int64_t, hipStream_t);
+int launch_unpack_rows(const uint8_t*, const float*, void*, int, int64_t, int64_t, hipStream_t);
+int launch_pack_affine_rows(const void*, int, uint8_t*, float*, float*, int64_t, int64_t, hipStream_t);
+int simt_linear_forward(const void*, int, const uint8_t*, const float*, const float*, void*, int64_t,
+                        int64_t, int64_t, hipStream_t);
+int simt_linear_dgrad(const void*, int, const uint8_t*, const float*, void*, int64_t, int64_t, int64_t,
+                      hipStream_t);
+int simt_evidence(const void*, int, const uint8_t*, const float*, float*, int64_t, int64_t, int64_t,
+                  const float*, const float*, const uint8_t*, float*, hipStream_t);
+int simt_evidence_tiles(int64_t cols);
+int launch_row_inner(const float*, const uint8_t*, float*, int64_t, int64_t, hipStream_t);
+int launch_sum_partials(const float*, int64_t, int64_t, float*, hipStream_t);
+int colsum_chunks(int64_t samples);
+int launch_colsums(const void*, int, const float*, int64_t, int64_t, float*, float*, float*, float*,
+                   hipStream_t);
+size_t coordinate_update_workspace(int64_t, int64_t, int64_t);
+int launch_coordinate_update(const float*, int8_t*, uint8_t*, int8_t*, uint16_t*, uint16_t*, uint16_t*,
+                             int64_t, int64_t, double, double, double, double, int64_t, int64_t, int64_t,
+                             const int64_t*, int64_t*, const uint8_t*, void*, size_t, hipStream_t);
+// MFMA paths (gemm_mfma.hip): return 1 when the shape/dtype is not theirs.
+int mfma_linear_forward(const void*, int, const uint8_t*, const float*, const float*, void*, int64_t,
+                        int64_t, int64_t, hipStream_t);
+int mfma_linear_dgrad(const void*, int, const uint8_t*, const float*, void*, int64_t, int64_t, int64_t,
+                      hipStream_t);
+int mfma_evidence(const void*, int, const uint8_t*, const float*, float*, int64_t, int64_t, int64_t,
+                  const float*, const float*, const uint8_t*, float*, hipStream_t);
+int64_t mfma_evidence_tiles(int64_t cols);
+int gemv_linear_forward(const void*, int, const uint8_t*, const float*, const float*, void*, int64_t,
+                        int64_t, int64_t, hipStream_t);
+}  // namespace qste
+
+using namespace qste;
+
+namespace {
+
+inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+inline bool dtype_ok(int d) { return d == QSTE_F32 || d == QSTE_F16 || d == QSTE_BF16; }
+inline size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+struct BackwardLayout {
+  size_t v_part, db_part, v, gs_part, total;
+  int64_t chunks, tiles;
+};
+
+BackwardLayout backward_layout(int64_t samples, int64_t rows, int64_t cols) {
+  BackwardLayout l{};
+  l.chunks = colsum_chunks(samples);
+  int64_t tiles = simt_evidence_tiles(cols);
+  const int64_t mt = mfma_evidence_tiles(cols);
+  if (mt > tiles) tiles = mt;
+  l.tiles = tiles;
+  size_t at = 0;
+  l.v_part = at; at += align_up(sizeof(float) * static_cast<size_t>((l.chunks > 0 ? l.chunks : 1) * rows));
+  l.db_part = at; at += align_up(sizeof(float) * static_cast<size_t>((l.chunks > 0 ? l.chunks : 1) * rows));
+  l.v = at; at += align_up(sizeof(float) * static_cast<size_t>(rows));
+  l.gs_part = at; at += align_up(sizeof(float) * static_cast<size_t>(tiles * rows));
+  l.total = at;
+  return l;
+}
+
+int forward_dispatch(const void* x, int dtype, const uint8_t* packed, const float* scale,
+                     const float* bias, void* y, int64_t m, int64_t rows, int64_t cols, hipStream_t s) {
+  int rc = gemv_linear_forward(x, dtype, packed, scale, bias, y, m, rows, cols, s);
+  if (rc != 1) return rc;
+  rc = mfma_linear_forward(x, dtype, packed, scale, bias, y, m, rows, cols, s);
+  if (rc != 1) return rc;
+  return simt_linear_forward(x, dtype, packed, scale, bias, y, m, rows, cols, s);
+}
+
+int dgrad_dispatch(const void* dy, int dtype, const uint8_t* packed, const float* row_scale, void* dx,
+                   int64_t m, int64_t rows, int64_t cols, hipStream_t s) {
+  int rc = mfma_linear_dgrad(dy, dtype, packed, row_scale, dx, m, rows, cols, s);
+  if (rc != 1) return rc;
+  return simt_linear_dgrad(dy, dtype, packed, row_scale, dx, m, rows, cols, s);
+}
+
+int evidence_dispatch(const void* dy, int dtype, const uint8_t* packed_x, const float* x_scale,
+                      float* ev, int64_t samples, int64_t rows, int64_t cols, const float* m_add,
+                      const float* m_scale, const uint8_t* w_bits, float* gs_part, int64_t* tiles,
+                      hipStream_t s) {
+  int rc = mfma_evidence(dy, dtype, packed_x, x_scale, ev, samples, rows, cols, m_add, m_scale, w_bits,
+                         gs_part, s);
+  if (rc != 1) {
+    *tiles = mfma_evidence_tiles(cols);
+    return rc;
+  }
+  *tiles = simt_evidence_tiles(cols);
+  return simt_evidence(dy, dtype, packed_x, x_scale, ev, samples, rows, cols, m_add, m_scale, w_bits,
+                       gs_part, s);
+}
+
+// A zero-fill that is a kernel, so the library records no memset node when
+// a caller captures it into a graph.
+__global__ void fill_zero_kernel(float* p, int64_t n) {
+  const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
+__global__ void set_i64_kernel(int64_t* p, int64_t v) { *p = v; }
+
+int fill_zero(float* p, int64_t n, hipStream_t s) {
+  if (n <= 0) return 0;
+  fill_zero_kernel<<<ceil_div(n, 256), 256, 0, s>>>(p, n);
+  return static_cast<int>(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" {
+
+int qste_version(void) { return 1; }
+
+const char* qste_error_string(int code) {
+  switch (code) {
+    case 0: return "success";
+    case QSTE_E_DTYPE: return "qste: unsupported dtype code";
+    case QSTE_E_SHAPE: return "qste: invalid shape (negative size or inconsistent dimensions)";
+    case QSTE_E_NULL: return "qste: required pointer is NULL";
+    case QSTE_E_WORKSPACE: return "qste: workspace missing or smaller than the *_workspace_bytes query";
+    case QSTE_E_BLOCK: return "qste: momentum block size must be a positive power of two";
+    case QSTE_E_ALIGN: return "qste: pointer alignment not supported";
+    default: return hipGetErrorString(static_cast<hipError_t>(code));
+  }
+}
+
+int qste_pack_coordinate(const int8_t* coordinate, uint8_t* packed, int64_t rows, int64_t cols,
+                         void* stream) {
+  if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  if (rows * cols > 0 && (!coordinate || !packed)) return QSTE_E_NULL;
+  return launch_pack_coordinate(coordinate, packed, rows, cols, as_stream(stream));
+}
+
+int qste_unpack_rows(const uint8_t* packed, const float* row_scale, void* out, int out_dtype, int64_t rows,
+                     int64_t cols, void* stream) {
+  if (!dtype_ok(out_dtype)) return QSTE_E_DTYPE;
+  if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  if (rows * cols > 0 && (!packed || !out)) return QSTE_E_NULL;
+  return launch_unpack_rows(packed, row_scale, out, out_dtype, rows, cols, as_stream(stream));
+}
+
+int qste_pack_affine_rows(const void* x, int dtype, uint8_t* packed, float* offset, float* scale,
+                          int64_t rows, int64_t cols, void* stream) {
+  if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
+  if (rows < 0 || cols <= 0) return QSTE_E_SHAPE;
+  if (rows > 0 && (!x || !packed || !offset || !scale)) return QSTE_E_NULL;
+  return launch_pack_affine_rows(x, dtype, packed, offset, scale, rows, cols, as_stream(stream));
+}
+
+int qste_packed_linear_affine(const void* x, int dtype, const uint8_t* packed, const float* scale,
+                              const float* bias, void* y, int64_t m, int64_t rows, int64_t cols,
+                              void* stream) {
+  if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
+  if (m < 0 || rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  if (m * rows == 0) return 0;
+  if (!y || !scale || (cols > 0 && (!x || !packed))) return QSTE_E_NULL;
+  return forward_dispatch(x, dtype, packed, scale, bias, y, m, rows, cols, as_stream(stream));
+}
+
+int qste_packed_transpose(const void* dy, int dtype, const uint8_t* packed, const float* row_scale,
+                          void* dx, int64_t m, int64_t rows, int64_t cols, void* stream) {
+  if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
+  if (m < 0 || rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  if (m * cols == 0) return 0;
+  if (!dx || (rows > 0 && (!dy || !packed))) return QSTE_E_NULL;
+  return dgrad_dispatch(dy, dtype, packed, row_scale, dx, m, rows, cols, as_stream(stream));
+}
+
+int qste_evidence_from_packed(const void* dy, int dtype, const uint8_t* packed_x, const float* row_scale,
+                              float* evidence, int64_t samples, int64_t rows, int64_t cols, void* stream) {
+  if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
+  if (samples < 0 || rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  if (rows * cols == 0) return 0;
+  if (!evidence || (samples > 0 && (!dy || !packed_x))) return QSTE_E_NULL;
+  int64_t tiles = 0;
+  return evidence_dispatch(dy, dtype, packed_x, row_scale, evidence, samples, rows, cols, nullptr, nullptr,
+                           nullptr, nullptr, &tiles, as_stream(stream));
+}
+
+int qste_packed_row_inner(const float* matrix, const uint8_t* packed, float* out, int64_t rows,
+                          int64_t cols, void* stream) {
+  if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  if (rows == 0) return 0;
+  if (!out || (cols > 0 && (!matrix || !packed))) return QSTE_E_NULL;
+  return launch_row_inner(matrix, packed, out, rows, cols, as_stream(stream));
+}
+
+size_t qste_linear_backward_workspace_bytes(int64_t samples, int64_t rows, int64_t cols) {
+  if (samples < 0 || rows < 0 || cols < 0) return 0;
+  return backward_layout(samples, rows, cols).total;
+}
+
+int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x, const float* x_offset,
+                         const float* x_scale, const uint8_t* packed_w, const float* scale, void* dx,
+                         float* evidence, float* grad_scale, float* grad_bias, int64_t samples,
+                         int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
+  if (samples < 0 || rows <= 0 || cols <= 0) return QSTE_E_SHAPE;
+  if (!dx || !evidence || !grad_scale || !scale || !packed_w) return QSTE_E_NULL;
+  if (samples > 0 && (!dy || !packed_x || !x_offset || !x_scale)) return QSTE_E_NULL;
+  const BackwardLayout l = backward_layout(samples, rows, cols);
+  if (!workspace || workspace_bytes < l.total) return QSTE_E_WORKSPACE;
+  hipStream_t s = as_stream(stream);
+  char* base = static_cast<char*>(workspace);
+  float* v_part = reinterpret_cast<float*>(base + l.v_part);
+  float* db_part = reinterpret_cast<float*>(base + l.db_part);
+  float* v = reinterpret_cast<float*>(base + l.v);
+  float* gs_part = reinterpret_cast<float*>(base + l.gs_part);
+  int rc;
+  if (samples > 0) {
+    if ((rc = dgrad_dispatch(dy, dtype, packed_w, scale, dx, samples, rows, cols, s))) return rc;
+    if ((rc = launch_colsums(dy, dtype, x_offset, samples, rows, v_part, grad_bias ? db_part : nullptr, v,
+                             grad_bias, s)))
+      return rc;
+  } else {
+    if ((rc = fill_zero(v, rows, s))) return rc;
+    if (grad_bias && (rc = fill_zero(grad_bias, rows, s))) return rc;
+  }
+  int64_t tiles = 0;
+  if ((rc = evidence_dispatch(dy, dtype, packed_x, x_scale, evidence, samples, rows, cols, v, scale, packed_w,
+                              gs_part, &tiles, s)))
+    return rc;
+  return launch_sum_partials(gs_part, tiles, rows, grad_scale, s);
+}
+
+size_t qste_coordinate_update_workspace_bytes(int64_t rows, int64_t cols, int64_t block_size) {
+  return coordinate_update_workspace(rows, cols, block_size);
+}
+
+int qste_coordinate_update(const float* evidence, int8_t* coordinate, uint8_t* packed, int8_t* moment_q,
+                           uint16_t* moment_scale, uint16_t* row_v, uint16_t* col_v, int64_t rows,
+                           int64_t cols, double beta1, double beta2, double update_clip,
+                           double coordinate_lr, int64_t block_size, int64_t seed, int64_t step,
+                           const int64_t* step_device, int64_t* flips_out, const uint8_t* update_enabled,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  if (block_size <= 0 || (block_size & (block_size - 1))) return QSTE_E_BLOCK;
+  if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  hipStream_t s = as_stream(stream);
+  if (rows == 0 || cols == 0) {
+    if (!flips_out) return 0;
+    set_i64_kernel<<<1, 1, 0, s>>>(flips_out, 0);
+    return static_cast<int>(hipGetLastError());
+  }
+  if (!evidence || !coordinate || !packed || !moment_q || !moment_scale || !row_v || !col_v)
+    return QSTE_E_NULL;
+  return launch_coordinate_update(evidence, coordinate, packed, moment_q, moment_scale, row_v, col_v, rows,
+                                  cols, beta1, beta2, update_clip, coordinate_lr, block_size, seed, step,
+                                  step_device, flips_out, update_enabled, workspace, workspace_bytes, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,134 @@
+// Shared device helpers for the gfx950 binary-linear kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/qste_hip.h"
+
+namespace qste {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Element conversions. bf16 / fp16 values widen to fp32 exactly; narrowing
+// rounds to nearest even.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+template <int DT>
+struct Elem;
+
+template <>
+struct Elem<QSTE_F32> {
+  using T = float;
+  __device__ __forceinline__ static float load(const T* p, int64_t i) { return p[i]; }
+  __device__ __forceinline__ static void store(T* p, int64_t i, float v) { p[i] = v; }
+  // rounding of a folded scale into the operand dtype (identity for fp32)
+  __device__ __forceinline__ static float round(float v) { return v; }
+};
+
+template <>
+struct Elem<QSTE_F16> {
+  using T = uint16_t;
+  __device__ __forceinline__ static float load(const T* p, int64_t i) { return f16_to_f32(p[i]); }
+  __device__ __forceinline__ static void store(T* p, int64_t i, float v) { p[i] = f32_to_f16(v); }
+  __device__ __forceinline__ static float round(float v) { return f16_to_f32(f32_to_f16(v)); }
+};
+
+template <>
+struct Elem<QSTE_BF16> {
+  using T = uint16_t;
+  __device__ __forceinline__ static float load(const T* p, int64_t i) { return bf16_to_f32(p[i]); }
+  __device__ __forceinline__ static void store(T* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+  __device__ __forceinline__ static float round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+};
+
+// ---------------------------------------------------------------------------
+// Packed signs: bit j of byte b is column 8b + j; set means +1.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float sign_of(const uint8_t* row, int64_t col) {
+  return ((row[col >> 3] >> (col & 7)) & 1) ? 1.0f : -1.0f;
+}
+
+// ---------------------------------------------------------------------------
+// The rounding stream (src/qste/kernels/stream.py:41-66): Thomas Wang's
+// 32-bit avalanche with the reference's constants, in uint32 so every shift
+// is logical and every product wraps.
+// ---------------------------------------------------------------------------
+
+constexpr uint32_t kSalt = 0x2545F491u;
+constexpr uint32_t kMultiplier = 0x27D4EB2Du;
+
+__host__ __device__ __forceinline__ uint32_t scramble(uint32_t v) {
+  v = (v ^ 61u) ^ (v >> 16);
+  v = v + (v << 3);
+  v = v ^ (v >> 4);
+  v = v * kMultiplier;
+  v = v ^ (v >> 15);
+  return v;
+}
+
+__host__ __device__ __forceinline__ uint32_t seed_hash(int64_t seed) {
+  return scramble(static_cast<uint32_t>(static_cast<uint64_t>(seed)));
+}
+
+__host__ __device__ __forceinline__ uint32_t step_hash(int64_t step) {
+  return scramble(static_cast<uint32_t>(static_cast<uint64_t>(step)) ^ kSalt);
+}
+
+// ---------------------------------------------------------------------------
+// Reductions across one wavefront (64 lanes) and one workgroup.
+// ---------------------------------------------------------------------------
+
+template <class T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int offset = kWave / 2; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int offset = kWave / 2; offset > 0; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, kWave));
+  return v;
+}
+
+// Sum over the workgroup; every thread gets the total. `scratch` holds one
+// T per wave. blockDim.x must be a multiple of 64.
+template <class T>
+__device__ __forceinline__ T block_sum(T v, T* scratch) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int waves = blockDim.x / kWave;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  T total = 0;
+  for (int w = 0; w < waves; ++w) total += scratch[w];
+  return total;
+}
+
+inline int ceil_div(int64_t a, int64_t b) { return static_cast<int>((a + b - 1) / b); }
+
+}  // namespace qste

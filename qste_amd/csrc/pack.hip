@@ -1,0 +1,222 @@
+// Sign packing, expansion and the one-bit affine activation encoding.
+//
+// pack_coordinate  -- src/qste/kernels/fallback.py:91-92 (bits of coord >= 0)
+// unpack_rows      -- fallback.py:27-29
+// pack_affine_rows -- fallback.py:77-88, the encoding of functional.py:98-115
+//
+// All three are HBM-bound byte work: one thread owns one packed output byte,
+// so no two threads ever write the same byte and no atomics are needed.
+#include "common.hpp"
+
+namespace qste {
+
+// Nonnegative-lane byte of eight int8 values held in a 64-bit word: the sign
+// bit of each byte is moved to bit 0 of that byte, inverted, then the eight
+// bits are gathered into the top byte by a multiply whose partial products
+// land on distinct bit positions (so no carries can disturb the result).
+__device__ __forceinline__ uint32_t nonneg_bits8(uint64_t w) {
+  uint64_t neg = (w >> 7) & 0x0101010101010101ull;
+  uint64_t pos = neg ^ 0x0101010101010101ull;
+  return static_cast<uint32_t>((pos * 0x0102040810204080ull) >> 56);
+}
+
+__global__ void pack_coordinate_kernel(const int8_t* __restrict__ coord,
+                                       uint8_t* __restrict__ packed, int64_t rows,
+                                       int64_t cols, int64_t stride) {
+  const int64_t total = rows * stride;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = idx / stride;
+    const int64_t b = idx - r * stride;
+    const int64_t c0 = b * 8;
+    const int8_t* src = coord + r * cols + c0;
+    uint32_t byte;
+    if ((cols & 7) == 0) {
+      byte = nonneg_bits8(*reinterpret_cast<const uint64_t*>(src));
+    } else {
+      const int64_t n = cols - c0 < 8 ? cols - c0 : 8;
+      byte = 0;
+      for (int j = 0; j < n; ++j) byte |= (src[j] >= 0 ? 1u : 0u) << j;
+    }
+    packed[idx] = static_cast<uint8_t>(byte);
+  }
+}
+
+template <int DT>
+__global__ void unpack_rows_kernel(const uint8_t* __restrict__ packed,
+                                   const float* __restrict__ row_scale,
+                                   typename Elem<DT>::T* __restrict__ out, int64_t rows,
+                                   int64_t cols, int64_t stride) {
+  const int64_t total = rows * cols;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = idx / cols;
+    const int64_t c = idx - r * cols;
+    float v = sign_of(packed + r * stride, c);
+    if (row_scale) v *= row_scale[r];
+    Elem<DT>::store(out, idx, v);
+  }
+}
+
+// One workgroup per row. Pass 1 sums the row in double (the correctly
+// rounded fp32 sum in all but vanishingly rare cases, independent of the
+// thread count); offset = fp32(sum) / fp32(cols), as ATen's mean is
+// sum-then-divide. Pass 2 writes each byte from eight centered values and
+// sums |x - offset| the same way.
+template <int DT, int THREADS>
+__global__ __launch_bounds__(THREADS) void pack_affine_rows_kernel(
+    const typename Elem<DT>::T* __restrict__ x, uint8_t* __restrict__ packed,
+    float* __restrict__ offset, float* __restrict__ scale, int64_t cols, int64_t stride) {
+  __shared__ double red[THREADS / kWave];
+  const int64_t row = blockIdx.x;
+  const typename Elem<DT>::T* src = x + row * cols;
+  uint8_t* dst = packed + row * stride;
+
+  double sum = 0.0;
+  for (int64_t c = threadIdx.x; c < cols; c += THREADS) sum += static_cast<double>(Elem<DT>::load(src, c));
+  sum = block_sum(sum, red);
+  const float n = static_cast<float>(cols);
+  const float mean = static_cast<float>(sum) / n;
+
+  double dev = 0.0;
+  for (int64_t b = threadIdx.x; b < stride; b += THREADS) {
+    const int64_t c0 = b * 8;
+    const int64_t cnt = cols - c0 < 8 ? cols - c0 : 8;
+    uint32_t byte = 0;
+    for (int j = 0; j < cnt; ++j) {
+      const float centered = Elem<DT>::load(src, c0 + j) - mean;
+      dev += static_cast<double>(fabsf(centered));
+      byte |= (centered >= 0.0f ? 1u : 0u) << j;
+    }
+    dst[b] = static_cast<uint8_t>(byte);
+  }
+  dev = block_sum(dev, red);
+  if (threadIdx.x == 0) {
+    offset[row] = mean;
+    scale[row] = static_cast<float>(dev) / n;
+  }
+}
+
+// Vectorized variant for bf16 rows whose width is a multiple of 8: each
+// thread reads 16 bytes (8 values) per packed byte it owns.
+template <int THREADS>
+__global__ __launch_bounds__(THREADS) void pack_affine_rows_bf16x8_kernel(
+    const uint16_t* __restrict__ x, uint8_t* __restrict__ packed, float* __restrict__ offset,
+    float* __restrict__ scale, int64_t cols, int64_t stride) {
+  __shared__ double red[THREADS / kWave];
+  const int64_t row = blockIdx.x;
+  const uint4* src = reinterpret_cast<const uint4*>(x + row * cols);
+  uint8_t* dst = packed + row * stride;
+
+  double sum = 0.0;
+  for (int64_t b = threadIdx.x; b < stride; b += THREADS) {
+    const uint4 v = src[b];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sum += static_cast<double>(__uint_as_float(w[i] << 16));
+      sum += static_cast<double>(__uint_as_float(w[i] & 0xFFFF0000u));
+    }
+  }
+  sum = block_sum(sum, red);
+  const float n = static_cast<float>(cols);
+  const float mean = static_cast<float>(sum) / n;
+
+  double dev = 0.0;
+  for (int64_t b = threadIdx.x; b < stride; b += THREADS) {
+    const uint4 v = src[b];
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t byte = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lo = __uint_as_float(w[i] << 16) - mean;
+      const float hi = __uint_as_float(w[i] & 0xFFFF0000u) - mean;
+      dev += static_cast<double>(fabsf(lo));
+      dev += static_cast<double>(fabsf(hi));
+      byte |= (lo >= 0.0f ? 1u : 0u) << (2 * i);
+      byte |= (hi >= 0.0f ? 1u : 0u) << (2 * i + 1);
+    }
+    dst[b] = static_cast<uint8_t>(byte);
+  }
+  dev = block_sum(dev, red);
+  if (threadIdx.x == 0) {
+    offset[row] = mean;
+    scale[row] = static_cast<float>(dev) / n;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+
+static int grid_for(int64_t work, int threads) {
+  int64_t blocks = (work + threads - 1) / threads;
+  if (blocks > 65536) blocks = 65536;
+  if (blocks < 1) blocks = 1;
+  return static_cast<int>(blocks);
+}
+
+int launch_pack_coordinate(const int8_t* coord, uint8_t* packed, int64_t rows, int64_t cols,
+                           hipStream_t stream) {
+  const int64_t stride = (cols + 7) / 8;
+  if (rows * stride == 0) return 0;
+  pack_coordinate_kernel<<<grid_for(rows * stride, 256), 256, 0, stream>>>(coord, packed, rows,
+                                                                            cols, stride);
+  return static_cast<int>(hipGetLastError());
+}
+
+int launch_unpack_rows(const uint8_t* packed, const float* row_scale, void* out, int dtype,
+                       int64_t rows, int64_t cols, hipStream_t stream) {
+  const int64_t stride = (cols + 7) / 8;
+  if (rows * cols == 0) return 0;
+  const int grid = grid_for(rows * cols, 256);
+  switch (dtype) {
+    case QSTE_F32:
+      unpack_rows_kernel<QSTE_F32><<<grid, 256, 0, stream>>>(packed, row_scale,
+                                                             static_cast<float*>(out), rows, cols, stride);
+      break;
+    case QSTE_F16:
+      unpack_rows_kernel<QSTE_F16><<<grid, 256, 0, stream>>>(packed, row_scale,
+                                                             static_cast<uint16_t*>(out), rows, cols, stride);
+      break;
+    case QSTE_BF16:
+      unpack_rows_kernel<QSTE_BF16><<<grid, 256, 0, stream>>>(packed, row_scale,
+                                                              static_cast<uint16_t*>(out), rows, cols, stride);
+      break;
+    default:
+      return QSTE_E_DTYPE;
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
+int launch_pack_affine_rows(const void* x, int dtype, uint8_t* packed, float* offset, float* scale,
+                            int64_t rows, int64_t cols, hipStream_t stream) {
+  const int64_t stride = (cols + 7) / 8;
+  if (rows == 0) return 0;
+  constexpr int T = 256;
+  const bool aligned16 = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  switch (dtype) {
+    case QSTE_F32:
+      pack_affine_rows_kernel<QSTE_F32, T><<<rows, T, 0, stream>>>(
+          static_cast<const float*>(x), packed, offset, scale, cols, stride);
+      break;
+    case QSTE_F16:
+      pack_affine_rows_kernel<QSTE_F16, T><<<rows, T, 0, stream>>>(
+          static_cast<const uint16_t*>(x), packed, offset, scale, cols, stride);
+      break;
+    case QSTE_BF16:
+      if ((cols & 7) == 0 && aligned16) {
+        pack_affine_rows_bf16x8_kernel<T><<<rows, T, 0, stream>>>(
+            static_cast<const uint16_t*>(x), packed, offset, scale, cols, stride);
+      } else {
+        pack_affine_rows_kernel<QSTE_BF16, T><<<rows, T, 0, stream>>>(
+            static_cast<const uint16_t*>(x), packed, offset, scale, cols, stride);
+      }
+      break;
+    default:
+      return QSTE_E_DTYPE;
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
+}  // namespace qste

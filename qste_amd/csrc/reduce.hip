@@ -1,0 +1,107 @@
+// Row and column reductions of the backward pass.
+//
+//   row_inner   gs[r] = sum_c E[r, c] * sign[r, c]   (fallback.py:141-148)
+//   colsums     v[r]  = sum_t dy[t, r] * offset[t]   (functional.py:139-144)
+//               db[r] = sum_t dy[t, r]               (functional.py:193)
+//
+// Column sums run in two deterministic stages (chunk partials, then a fixed
+// order sum) so results do not depend on scheduling; nothing uses atomics.
+#include "common.hpp"
+
+namespace qste {
+
+constexpr int kRowThreads = 256;
+constexpr int kColChunk = 256;
+
+__global__ __launch_bounds__(kRowThreads) void row_inner_kernel(const float* __restrict__ mat,
+                                                                const uint8_t* __restrict__ packed,
+                                                                float* __restrict__ out,
+                                                                int64_t cols, int64_t stride) {
+  __shared__ float red[kRowThreads / kWave];
+  const int64_t r = blockIdx.x;
+  const float* row = mat + r * cols;
+  const uint8_t* bits = packed + r * stride;
+  float acc = 0.0f;
+  for (int64_t c = threadIdx.x; c < cols; c += kRowThreads) acc += row[c] * sign_of(bits, c);
+  acc = block_sum(acc, red);
+  if (threadIdx.x == 0) out[r] = acc;
+}
+
+// Sum of `parts` partial vectors [parts][n] into out[n].
+__global__ void sum_partials_kernel(const float* __restrict__ partial, int64_t parts, int64_t n,
+                                    float* __restrict__ out) {
+  const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (i >= n) return;
+  float s = 0.0f;
+  for (int64_t p = 0; p < parts; ++p) s += partial[p * n + i];
+  out[i] = s;
+}
+
+template <int DT>
+__global__ void colsum_partial_kernel(const typename Elem<DT>::T* __restrict__ dy,
+                                      const float* __restrict__ offset, int64_t samples,
+                                      int64_t rows, float* __restrict__ v_part,
+                                      float* __restrict__ db_part) {
+  const int64_t r = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (r >= rows) return;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kColChunk;
+  const int64_t t1 = t0 + kColChunk < samples ? t0 + kColChunk : samples;
+  float v = 0.0f, db = 0.0f;
+  for (int64_t t = t0; t < t1; ++t) {
+    const float g = Elem<DT>::load(dy, t * rows + r);
+    v = fmaf(g, offset[t], v);
+    db += g;
+  }
+  v_part[blockIdx.y * rows + r] = v;
+  if (db_part) db_part[blockIdx.y * rows + r] = db;
+}
+
+int launch_row_inner(const float* mat, const uint8_t* packed, float* out, int64_t rows,
+                     int64_t cols, hipStream_t stream) {
+  if (rows == 0) return 0;
+  row_inner_kernel<<<rows, kRowThreads, 0, stream>>>(mat, packed, out, cols, (cols + 7) / 8);
+  return static_cast<int>(hipGetLastError());
+}
+
+int launch_sum_partials(const float* partial, int64_t parts, int64_t n, float* out,
+                        hipStream_t stream) {
+  if (n == 0) return 0;
+  sum_partials_kernel<<<ceil_div(n, 256), 256, 0, stream>>>(partial, parts, n, out);
+  return static_cast<int>(hipGetLastError());
+}
+
+int colsum_chunks(int64_t samples) { return ceil_div(samples, kColChunk); }
+
+// v_part / db_part: [colsum_chunks(samples)][rows] floats each.
+int launch_colsums(const void* dy, int dtype, const float* offset, int64_t samples, int64_t rows,
+                   float* v_part, float* db_part, float* v_out, float* db_out,
+                   hipStream_t stream) {
+  if (rows == 0) return 0;
+  const int chunks = colsum_chunks(samples);
+  if (chunks > 0) {
+    dim3 grid(ceil_div(rows, 256), chunks);
+    switch (dtype) {
+      case QSTE_F32:
+        colsum_partial_kernel<QSTE_F32><<<grid, 256, 0, stream>>>(
+            static_cast<const float*>(dy), offset, samples, rows, v_part, db_part);
+        break;
+      case QSTE_F16:
+        colsum_partial_kernel<QSTE_F16><<<grid, 256, 0, stream>>>(
+            static_cast<const uint16_t*>(dy), offset, samples, rows, v_part, db_part);
+        break;
+      case QSTE_BF16:
+        colsum_partial_kernel<QSTE_BF16><<<grid, 256, 0, stream>>>(
+            static_cast<const uint16_t*>(dy), offset, samples, rows, v_part, db_part);
+        break;
+      default:
+        return QSTE_E_DTYPE;
+    }
+    int rc = static_cast<int>(hipGetLastError());
+    if (rc) return rc;
+  }
+  int rc = launch_sum_partials(v_part, chunks, rows, v_out, stream);
+  if (rc || !db_out) return rc;
+  return launch_sum_partials(db_part, chunks, rows, db_out, stream);
+}
+
+}  // namespace qste

@@ -1,0 +1,105 @@
+"""Autograd for binary linear layers on the gfx950 kernels.
+
+Forward (``QSTELinearFn``, reference ``src/qste/functional.py:153-171``):
+``y = (x @ sign^T) * scale + bias`` and, for backward, the input kept as one
+bit per element plus two floats per sample (``encode_activation``,
+functional.py:98-115): ``x ~ offset + xscale * sign(x - offset)``.
+
+Backward (functional.py:173-194) is one library call, ``linear_backward``:
+the input gradient, the decoded evidence with its rank-one offset correction,
+the scale gradient, the evidence times the row scale, and the bias gradient.
+The evidence goes to the surface -- usually straight into the coordinate step,
+inside ``loss.backward()``.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+from torch.autograd import Function
+
+from . import kernels
+from .surface import Surface
+
+
+def _autocast(value: Tensor) -> Tensor:
+    """Cast like autocast would cast a native GEMM input (functional.py:39-53)."""
+
+    device = value.device.type
+    if device not in ("cuda", "cpu") or not torch.is_autocast_enabled(device):
+        return value
+    return value.to(dtype=torch.get_autocast_dtype(device))
+
+
+def encode_activation(flat: Tensor) -> tuple[Tensor, Tensor]:
+    """``(bits, aux)`` with ``aux = stack(offset, scale)`` fp32 [2, samples]."""
+
+    packed, offset, scale = kernels.pack_affine_rows(flat)
+    return packed, torch.stack((offset, scale))
+
+
+class QSTELinearFn(Function):
+    @staticmethod
+    def forward(ctx, inputs, packed, scale, bias, surface: Surface):
+        columns = surface.columns
+        output = kernels.packed_linear_affine(inputs, packed, scale, bias, columns)
+        flat = inputs.reshape(-1, columns)
+        payload, aux = encode_activation(flat)
+        ctx.save_for_backward(payload, aux, packed, scale)
+        ctx.surface = surface
+        ctx.columns = columns
+        ctx.input_shape = inputs.shape
+        ctx.input_dtype = inputs.dtype
+        ctx.bias_dtype = None if bias is None else bias.dtype
+        return output.to(inputs.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        payload, aux, packed, scale = ctx.saved_tensors
+        grad2 = grad_output.reshape(-1, grad_output.shape[-1])
+        grad_inputs, evidence, grad_scale, grad_bias = kernels.linear_backward(
+            grad2, payload, aux[0], aux[1], packed, scale.detach(), ctx.columns,
+            need_bias=ctx.bias_dtype is not None)
+        ctx.surface.consume_evidence(evidence)
+        grad_inputs = grad_inputs.reshape(ctx.input_shape).to(ctx.input_dtype)
+        if grad_bias is not None:
+            grad_bias = grad_bias.to(ctx.bias_dtype)
+        return grad_inputs, None, grad_scale.to(scale.dtype), grad_bias, None
+
+
+def qste_linear(inputs: Tensor, surface: Surface, bias: Tensor | None = None) -> Tensor:
+    """Functional binary linear (functional.py:197-205)."""
+
+    surface.note_forward()
+    return QSTELinearFn.apply(_autocast(inputs), surface.packed_sign, surface.scale, bias, surface)
+
+
+class QSTEWeightFn(Function):
+    """Differentiable dense ``sign * scale`` for code that reads ``.weight``.
+
+    functional.py:213-245: the gradient of the dense matrix becomes the
+    surface's evidence, and its row inner product with the signs the scale
+    gradient.
+    """
+
+    @staticmethod
+    def forward(ctx, packed, scale, surface: Surface):
+        ctx.save_for_backward(packed, scale)
+        ctx.surface = surface
+        sign = kernels.unpack_rows(packed, surface.columns, dtype=torch.float32)
+        return sign.mul_(scale.detach().float().unsqueeze(1)).to(scale.dtype)
+
+    @staticmethod
+    def backward(ctx, grad_weight):
+        packed, scale = ctx.saved_tensors
+        surface = ctx.surface
+        grad_weight = grad_weight.float().contiguous()
+        grad_scale = kernels.packed_row_inner(grad_weight, packed, surface.columns)
+        evidence = grad_weight.mul_(scale.detach().float().unsqueeze(1))
+        surface.consume_evidence(evidence)
+        return None, grad_scale.to(scale.dtype), None
+
+
+def qste_weight(surface: Surface) -> Tensor:
+    surface.note_forward()
+    return QSTEWeightFn.apply(surface.packed_sign, surface.scale, surface)

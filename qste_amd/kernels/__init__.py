@@ -1,0 +1,381 @@
+"""The operator layer: QSTE's ``qste.kernels`` API on gfx950 HIP kernels.
+
+Same names, arguments, return values and error behaviour as the reference's
+dispatch layer (``src/qste/kernels/loader.py:247-368``), for tensors on a
+ROCm device.  Every call goes to ``libqste_hip.so`` through its C ABI
+(``include/qste_hip.h``) on torch's current stream.  There is no CPU or
+pure-torch path: a tensor that is not on the GPU, or a missing library, is an
+error (``RuntimeError``), never a silent fallback.
+
+Outputs are allocated through torch's caching allocator, as are the
+workspaces the C entry points ask for; the library itself never allocates.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from ._lib import KernelError
+
+_DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+__all__ = [
+    "KernelError",
+    "coordinate_update",
+    "cuda_available",
+    "evidence_from_packed",
+    "linear_backward",
+    "native_available",
+    "pack_affine_rows",
+    "pack_coordinate",
+    "packed_linear_affine",
+    "packed_row_inner",
+    "packed_transpose",
+    "status",
+    "unpack_rows",
+]
+
+
+# ---------------------------------------------------------------------------
+# plumbing
+# ---------------------------------------------------------------------------
+
+
+def _require_gpu(*tensors: Tensor) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"qste_amd kernels run on the GPU only; got a tensor on {t.device} "
+                "(move the model to the ROCm device first)"
+            )
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise RuntimeError(f"tensors on different devices: {device} and {t.device}")
+    if device is None:
+        raise RuntimeError("no tensor argument to place the kernel on")
+    return device
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _dtype_code(t: Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; expected float32, float16 or bfloat16") from None
+
+
+def _ptr(t: Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _packed_width(columns: int) -> int:
+    return (int(columns) + 7) // 8
+
+
+def _check_packed(packed: Tensor, columns: int, rows: int | None = None) -> Tensor:
+    if packed.dtype != torch.uint8 or packed.dim() != 2:
+        raise ValueError("packed signs must be a rank-2 uint8 tensor")
+    if packed.shape[1] != _packed_width(columns):
+        raise ValueError(
+            f"packed sign width {packed.shape[1]} does not match {columns} columns "
+            f"(expected {_packed_width(columns)})"
+        )
+    if rows is not None and packed.shape[0] != rows:
+        raise ValueError(f"packed signs have {packed.shape[0]} rows, expected {rows}")
+    return packed.contiguous()
+
+
+def _f32(t: Tensor | None) -> Tensor | None:
+    if t is None:
+        return None
+    return t.detach().to(torch.float32).contiguous()
+
+
+def _workspace(nbytes: int, device: torch.device) -> Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def native_available() -> bool:
+    """Whether the HIP library loads (it does not need a GPU to load)."""
+
+    try:
+        _lib.load()
+        return True
+    except KernelError:
+        return False
+
+
+def cuda_available() -> bool:
+    return torch.cuda.is_available() and native_available()
+
+
+def status() -> dict:
+    """Whether the HIP library is built and loadable, and why not if not."""
+
+    ok = native_available()
+    return {
+        "native": ok,
+        "library": str(_lib.LIB_PATH),
+        "version": _lib.load().qste_version() if ok else None,
+        "failure": _lib.failure(),
+        "gpu": torch.cuda.is_available(),
+    }
+
+
+# ---------------------------------------------------------------------------
+# operators (reference: src/qste/kernels/loader.py:247-368)
+# ---------------------------------------------------------------------------
+
+
+def pack_coordinate(coordinate: Tensor) -> Tensor:
+    """Sign bits of an int8 coordinate matrix, LSB first (fallback.py:91-92)."""
+
+    device = _require_gpu(coordinate)
+    if coordinate.dtype != torch.int8 or coordinate.dim() != 2:
+        raise ValueError("pack_coordinate expects a rank-2 int8 tensor")
+    coordinate = coordinate.contiguous()
+    rows, cols = coordinate.shape
+    packed = torch.empty(rows, _packed_width(cols), dtype=torch.uint8, device=device)
+    code = _lib.load().qste_pack_coordinate(
+        _ptr(coordinate), _ptr(packed), rows, cols, _stream(device))
+    _lib.check(code, "pack_coordinate")
+    return packed
+
+
+def unpack_rows(packed: Tensor, columns: int, *, dtype: torch.dtype | None = None,
+                row_scale: Tensor | None = None) -> Tensor:
+    """+-1 matrix of the packed signs (fallback.py:27-29)."""
+
+    dtype = dtype or torch.float32
+    device = _require_gpu(packed, row_scale)
+    packed = _check_packed(packed, columns)
+    out = torch.empty(packed.shape[0], int(columns), dtype=dtype, device=device)
+    code = _lib.load().qste_unpack_rows(
+        _ptr(packed), _ptr(_f32(row_scale)), _ptr(out), _dtype_code(out), packed.shape[0],
+        int(columns), _stream(device))
+    _lib.check(code, "unpack_rows")
+    return out
+
+
+def pack_affine_rows(values: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """(bits, offset, scale) of each row: x ~ offset + scale * sign(x - offset).
+
+    fallback.py:77-88. Arithmetic in fp32 on the dtype's values.
+    """
+
+    device = _require_gpu(values)
+    if values.dim() != 2:
+        raise ValueError("pack_affine_rows expects a rank-2 tensor")
+    values = values.contiguous()
+    rows, cols = values.shape
+    if cols == 0:
+        raise ValueError("pack_affine_rows needs at least one column")
+    packed = torch.empty(rows, _packed_width(cols), dtype=torch.uint8, device=device)
+    offset = torch.empty(rows, dtype=torch.float32, device=device)
+    scale = torch.empty(rows, dtype=torch.float32, device=device)
+    code = _lib.load().qste_pack_affine_rows(
+        _ptr(values), _dtype_code(values), _ptr(packed), _ptr(offset), _ptr(scale), rows, cols,
+        _stream(device))
+    _lib.check(code, "pack_affine_rows")
+    return packed, offset, scale
+
+
+def packed_linear_affine(inputs: Tensor, packed: Tensor, scale: Tensor, bias: Tensor | None,
+                         columns: int) -> Tensor:
+    """``(x @ sign^T) * scale + bias`` in the input dtype (fallback.py:95-108)."""
+
+    device = _require_gpu(inputs, packed, scale, bias)
+    if inputs.shape[-1] != columns:
+        raise ValueError(f"activation width {inputs.shape[-1]} does not match {columns} columns")
+    packed = _check_packed(packed, columns)
+    rows = packed.shape[0]
+    if scale.numel() != rows:
+        raise ValueError("scale must have one entry per output row")
+    if bias is not None and bias.numel() != rows:
+        raise ValueError("bias must have one entry per output row")
+    flat = inputs.reshape(-1, columns).contiguous()
+    out = torch.empty(flat.shape[0], rows, dtype=inputs.dtype, device=device)
+    code = _lib.load().qste_packed_linear_affine(
+        _ptr(flat), _dtype_code(flat), _ptr(packed), _ptr(_f32(scale)), _ptr(_f32(bias)),
+        _ptr(out), flat.shape[0], rows, int(columns), _stream(device))
+    _lib.check(code, "packed_linear_affine")
+    return out.view(*inputs.shape[:-1], rows)
+
+
+def packed_transpose(inputs: Tensor, packed: Tensor, columns: int,
+                     row_scale: Tensor | None = None) -> Tensor:
+    """``inputs @ (row_scale * sign)`` in the input dtype (fallback.py:111-123)."""
+
+    device = _require_gpu(inputs, packed, row_scale)
+    packed = _check_packed(packed, columns)
+    rows = packed.shape[0]
+    if inputs.shape[-1] != rows:
+        raise ValueError(f"transpose width {inputs.shape[-1]} does not match {rows} rows")
+    if row_scale is not None and row_scale.numel() != rows:
+        raise ValueError("transpose row scale must have one entry per packed row")
+    flat = inputs.reshape(-1, rows).contiguous()
+    out = torch.empty(flat.shape[0], int(columns), dtype=inputs.dtype, device=device)
+    code = _lib.load().qste_packed_transpose(
+        _ptr(flat), _dtype_code(flat), _ptr(packed), _ptr(_f32(row_scale)), _ptr(out),
+        flat.shape[0], rows, int(columns), _stream(device))
+    _lib.check(code, "packed_transpose")
+    return out.view(*inputs.shape[:-1], int(columns))
+
+
+def evidence_from_packed(grad: Tensor, packed: Tensor, columns: int,
+                         row_scale: Tensor | None = None) -> Tensor:
+    """``grad^T @ (row_scale * sign(x))`` as fp32 [rows, columns] (fallback.py:126-138)."""
+
+    device = _require_gpu(grad, packed, row_scale)
+    if grad.dim() != 2:
+        raise ValueError("evidence grad must be a rank-2 tensor")
+    packed = _check_packed(packed, columns)
+    samples, rows = grad.shape
+    if packed.shape[0] != samples:
+        raise ValueError("evidence grad and packed activations disagree on sample count")
+    if row_scale is not None and row_scale.numel() != samples:
+        raise ValueError("evidence row scale must have one entry per sample")
+    grad = grad.contiguous()
+    out = torch.empty(rows, int(columns), dtype=torch.float32, device=device)
+    code = _lib.load().qste_evidence_from_packed(
+        _ptr(grad), _dtype_code(grad), _ptr(packed), _ptr(_f32(row_scale)), _ptr(out), samples,
+        rows, int(columns), _stream(device))
+    _lib.check(code, "evidence_from_packed")
+    return out
+
+
+def packed_row_inner(matrix: Tensor, packed: Tensor, columns: int) -> Tensor:
+    """``sum_c matrix[r, c] * sign[r, c]`` (fallback.py:141-148)."""
+
+    device = _require_gpu(matrix, packed)
+    if matrix.dim() != 2 or matrix.shape[1] != columns:
+        raise ValueError("row inner shape mismatch")
+    packed = _check_packed(packed, columns, matrix.shape[0])
+    m = matrix.detach().to(torch.float32).contiguous()
+    out = torch.empty(m.shape[0], dtype=torch.float32, device=device)
+    code = _lib.load().qste_packed_row_inner(
+        _ptr(m), _ptr(packed), _ptr(out), m.shape[0], int(columns), _stream(device))
+    _lib.check(code, "packed_row_inner")
+    return out.to(matrix.dtype)
+
+
+def linear_backward(grad: Tensor, packed_x: Tensor, x_offset: Tensor, x_scale: Tensor,
+                    packed_w: Tensor, scale: Tensor, columns: int, *, need_bias: bool):
+    """All of ``QSTELinearFn.backward``'s products in one call (functional.py:173-194).
+
+    Returns ``(grad_input [samples, columns] in grad's dtype, evidence fp32
+    [rows, columns] already multiplied by the row scale, grad_scale fp32
+    [rows], grad_bias fp32 [rows] or None)``.
+    """
+
+    device = _require_gpu(grad, packed_x, x_offset, x_scale, packed_w, scale)
+    grad = grad.contiguous()
+    samples, rows = grad.shape
+    packed_w = _check_packed(packed_w, columns, rows)
+    packed_x = _check_packed(packed_x, columns, samples)
+    lib = _lib.load()
+    dx = torch.empty(samples, int(columns), dtype=grad.dtype, device=device)
+    evidence = torch.empty(rows, int(columns), dtype=torch.float32, device=device)
+    grad_scale = torch.empty(rows, dtype=torch.float32, device=device)
+    grad_bias = torch.empty(rows, dtype=torch.float32, device=device) if need_bias else None
+    nbytes = lib.qste_linear_backward_workspace_bytes(samples, rows, int(columns))
+    work = _workspace(nbytes, device)
+    code = lib.qste_linear_backward(
+        _ptr(grad), _dtype_code(grad), _ptr(packed_x), _ptr(_f32(x_offset)), _ptr(_f32(x_scale)),
+        _ptr(packed_w), _ptr(_f32(scale)), _ptr(dx), _ptr(evidence), _ptr(grad_scale),
+        _ptr(grad_bias), samples, rows, int(columns), _ptr(work), work.numel(), _stream(device))
+    _lib.check(code, "linear_backward")
+    return dx, evidence, grad_scale, grad_bias
+
+
+def coordinate_update(
+    gradient: Tensor,
+    coordinate: Tensor,
+    packed: Tensor,
+    moment_q: Tensor,
+    moment_scale: Tensor,
+    row_v: Tensor,
+    col_v: Tensor,
+    *,
+    beta1: float,
+    beta2: float,
+    update_clip: float,
+    coordinate_lr: float,
+    block_size: int,
+    seed: int,
+    step,
+    flips: Tensor | None = None,
+    update_enabled: Tensor | None = None,
+):
+    """One fused coordinate step (fallback.py:158-242; GPU signature cuda.py:1705-1729).
+
+    Returns the flip count as an int, or -- when ``flips`` (a device int64
+    tensor) is given -- writes it there without a host synchronization and
+    returns that tensor. ``step`` may be a device int64 scalar (read at run
+    time, for graph replay). ``update_enabled`` (device uint8) gates every
+    state write. ``gradient`` is read, not modified.
+    """
+
+    device = _require_gpu(gradient, coordinate, packed, moment_q, moment_scale, row_v, col_v)
+    if block_size <= 0 or block_size & (block_size - 1):
+        raise ValueError("momentum block size must be a positive power of two")
+    gradient = gradient.detach().to(torch.float32).contiguous()
+    rows, cols = gradient.shape
+    for name, t, dt in (("coordinate", coordinate, torch.int8), ("packed", packed, torch.uint8),
+                        ("moment_q", moment_q, torch.int8), ("moment_scale", moment_scale, torch.float16),
+                        ("row_v", row_v, torch.float16), ("col_v", col_v, torch.float16)):
+        if t.dtype != dt:
+            raise ValueError(f"{name} must be {dt}, got {t.dtype}")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous (it is updated in place)")
+    if coordinate.shape != gradient.shape or moment_q.shape != gradient.shape:
+        raise ValueError("coordinate state shape mismatch")
+    if packed.shape != (rows, _packed_width(cols)):
+        raise ValueError("packed sign shape mismatch")
+    blocks = (rows * cols + block_size - 1) // block_size
+    if moment_scale.numel() != blocks:
+        raise ValueError("momentum scale shape mismatch")
+    if row_v.numel() != rows or col_v.numel() != cols:
+        raise ValueError("factored statistics shape mismatch")
+
+    step_device = None
+    step_value = 0
+    if torch.is_tensor(step):
+        if step.device != device or step.dtype != torch.int64:
+            raise ValueError("a tensor step must be an int64 scalar on the surface's device")
+        step_device = step
+    else:
+        step_value = int(step)
+    enabled = None
+    if update_enabled is not None:
+        enabled = update_enabled.to(device=device, dtype=torch.uint8).contiguous()
+    out = flips
+    if out is None or out.dtype != torch.int64 or out.device != device:
+        out_dev = torch.empty((), dtype=torch.int64, device=device)
+    else:
+        out_dev = out
+
+    lib = _lib.load()
+    nbytes = lib.qste_coordinate_update_workspace_bytes(rows, cols, int(block_size))
+    work = _workspace(nbytes, device)
+    wrap = lambda v: ((int(v) + (1 << 63)) % (1 << 64)) - (1 << 63)  # noqa: E731
+    code = lib.qste_coordinate_update(
+        _ptr(gradient), _ptr(coordinate), _ptr(packed), _ptr(moment_q), _ptr(moment_scale),
+        _ptr(row_v), _ptr(col_v), rows, cols, float(beta1), float(beta2), float(update_clip),
+        float(coordinate_lr), int(block_size), wrap(seed), wrap(step_value), _ptr(step_device),
+        _ptr(out_dev), _ptr(enabled), _ptr(work), work.numel(), _stream(device))
+    _lib.check(code, "coordinate_update")
+    if flips is None:
+        return int(out_dev.item())
+    if out_dev is not flips:
+        flips.copy_(out_dev)
+    return flips

@@ -1,0 +1,83 @@
+"""Drop-in modules: ``QSTELinear`` (training) and ``PackedLinear`` (inference).
+
+Constructor attributes, ``weight``/``bias`` surface and call signature follow
+the reference (``src/qste/modules.py:21-123``) so code that introspects an
+``nn.Linear`` keeps working.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from . import kernels
+from .config import QSTEConfig, coerce_config
+from .functional import qste_linear, qste_weight
+from .surface import Surface
+
+
+class QSTELinear(nn.Module):
+    """``y = (x @ sign^T) * scale + bias`` with a binary forward matrix."""
+
+    def __init__(self, surface: Surface, bias: Tensor | None = None):
+        super().__init__()
+        self.surface = surface
+        self.in_features = surface.columns
+        self.out_features = surface.rows
+        if bias is None:
+            self.register_parameter("bias", None)
+        else:
+            self.bias = nn.Parameter(bias.detach().float().clone())
+
+    @classmethod
+    def from_linear(cls, module: nn.Linear, cfg: QSTEConfig | None = None,
+                    surface: Surface | None = None) -> "QSTELinear":
+        return cls(surface or Surface(module.weight, coerce_config(cfg)), module.bias)
+
+    @property
+    def scale(self) -> Tensor:
+        return self.surface.scale
+
+    @property
+    def packed_sign(self) -> Tensor:
+        return self.surface.packed_sign
+
+    @property
+    def weight(self) -> Tensor:
+        """Differentiable dense equivalent (materializes out x in floats)."""
+
+        return qste_weight(self.surface)
+
+    def forward(self, inputs: Tensor) -> Tensor:
+        return qste_linear(inputs, self.surface, self.bias)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"bias={self.bias is not None}")
+
+
+class PackedLinear(nn.Module):
+    """Inference-only linear over packed signs, a row scale and a bias.
+
+    The reference casts the input to fp32 and the output back
+    (modules.py:114-120). Widening bf16/fp16 to fp32 is exact and the kernel
+    accumulates in fp32 either way, so the input is passed in its own dtype;
+    the output is in the input dtype as in the reference.
+    """
+
+    def __init__(self, packed: Tensor, scale: Tensor, columns: int, bias: Tensor | None):
+        super().__init__()
+        self.register_buffer("packed_sign", packed)
+        self.register_buffer("scale", scale)
+        self.in_features = columns
+        self.out_features = packed.shape[0]
+        self.register_buffer("bias", bias)
+
+    @torch.no_grad()
+    def forward(self, inputs: Tensor) -> Tensor:
+        return kernels.packed_linear_affine(
+            inputs, self.packed_sign, self.scale, self.bias, self.in_features).to(inputs.dtype)
+
+    def extra_repr(self) -> str:
+        return f"in_features={self.in_features}, out_features={self.out_features}"

@@ -1,0 +1,314 @@
+"""HIP kernels against the CPU oracle, on the GPU, through the C ABI.
+
+Bars (stated per test):
+* integer and byte outputs -- packed signs, activation bits, coordinates,
+  momentum, fp16 statistics, flip counts -- bit-exact against the oracle run
+  on the same inputs;
+* float outputs within a relative L2 error against the float64 oracle whose
+  operands are rounded exactly as the kernel's contract says (a scale folded
+  into a bf16 operand is rounded to bf16 first; a bf16 output is the oracle
+  rounded to bf16).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+@pytest.fixture(autouse=True)
+def _gpu():
+    _need_gpu()
+    from qste_amd import kernels
+
+    assert kernels.native_available(), kernels.status()
+    yield
+
+
+def K():
+    from qste_amd import kernels
+
+    return kernels
+
+
+def rel_l2(got, want) -> float:
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    denom = np.linalg.norm(want)
+    return float(np.linalg.norm(got - want) / (denom if denom > 0 else 1.0))
+
+
+def t(a, dtype=None):
+    x = torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    return x if dtype is None else x.to(dtype)
+
+
+def f32(x: torch.Tensor) -> np.ndarray:
+    return x.float().cpu().numpy()
+
+
+DT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def as_dtype_values(a: np.ndarray, dt: str) -> np.ndarray:
+    """fp32 values exactly representable in dtype ``dt`` (round once)."""
+
+    return torch.from_numpy(a).to(DT[dt]).float().numpy()
+
+
+def round_out(a: np.ndarray, dt: str) -> np.ndarray:
+    return torch.from_numpy(np.asarray(a, dtype=np.float32)).to(DT[dt]).float().numpy()
+
+
+def round_scale(s: np.ndarray, dt: str) -> np.ndarray:
+    return s if dt == "f32" else as_dtype_values(s.astype(np.float32), dt)
+
+
+# ---------------------------------------------------------------------------
+# packing
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (5, 7), (3, 8), (17, 13), (64, 64), (33, 130),
+                                       (128, 4096), (7, 1000)])
+def test_pack_coordinate_bit_exact(rows, cols):
+    rng = np.random.default_rng(rows * 7919 + cols)
+    coord = rng.integers(-127, 128, size=(rows, cols)).astype(np.int8)
+    coord.flat[:: max(1, coord.size // 5)] = 0
+    got = K().pack_coordinate(t(coord)).cpu().numpy()
+    assert np.array_equal(got, oracle.pack_coordinate(coord))
+
+
+@pytest.mark.parametrize("cols", [1, 7, 8, 9, 63, 64, 65])
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_unpack_rows_exact(cols, dt):
+    rng = np.random.default_rng(cols)
+    coord = rng.integers(-127, 128, size=(5, cols)).astype(np.int8)
+    packed = oracle.pack_coordinate(coord)
+    got = f32(K().unpack_rows(t(packed), cols, dtype=DT[dt]))
+    assert np.array_equal(got, oracle.unpack_rows(packed, cols))
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("rows,cols", [(9, 7), (17, 64), (16, 1024), (8, 4096), (5, 1001), (3, 14336)])
+def test_pack_affine_rows_bit_exact(dt, rows, cols):
+    rng = np.random.default_rng(rows * 31 + cols)
+    x = as_dtype_values((rng.standard_normal((rows, cols)) * 2 + 0.3).astype(np.float32), dt)
+    bits, off, xs = K().pack_affine_rows(t(x, DT[dt]))
+    ob, oo, ox = oracle.pack_affine_rows(x)
+    assert np.array_equal(bits.cpu().numpy(), ob)
+    assert np.array_equal(off.cpu().numpy(), oo)
+    assert np.array_equal(xs.cpu().numpy(), ox)
+
+
+def test_pack_affine_rows_against_reference_vectors(golden):
+    g = golden("pack_affine")
+    for name in sorted({k.split("__")[0] for k in g}):
+        x = g[f"{name}__x"]
+        bits, off, xs = K().pack_affine_rows(t(x))
+        assert np.array_equal(bits.cpu().numpy(), g[f"{name}__bits"]), name
+        np.testing.assert_allclose(off.cpu().numpy(), g[f"{name}__offset"], rtol=1e-6, atol=1e-7)
+        np.testing.assert_allclose(xs.cpu().numpy(), g[f"{name}__scale"], rtol=1e-6, atol=1e-7)
+
+
+# ---------------------------------------------------------------------------
+# products
+# ---------------------------------------------------------------------------
+
+SHAPES = [(17, 13, 5), (64, 64, 32), (128, 96, 40), (33, 8, 7), (1, 1, 1), (300, 256, 129),
+          (512, 1024, 256), (1024, 512, 16), (256, 4096, 4), (64, 2048, 1)]
+
+
+def _problem(rows, cols, m, dt, seed):
+    rng = np.random.default_rng(seed)
+    coord = rng.integers(-127, 128, size=(rows, cols)).astype(np.int8)
+    packed = oracle.pack_coordinate(coord)
+    x = as_dtype_values(rng.standard_normal((m, cols)).astype(np.float32), dt)
+    scale = (np.abs(rng.standard_normal(rows)) * 0.02 + 0.01).astype(np.float32)
+    bias = rng.standard_normal(rows).astype(np.float32) * 0.1
+    dy = as_dtype_values(rng.standard_normal((m, rows)).astype(np.float32), dt)
+    return packed, x, scale, bias, dy
+
+
+@pytest.mark.parametrize("rows,cols,m", SHAPES)
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_linear_forward(rows, cols, m, dt):
+    packed, x, scale, bias, _ = _problem(rows, cols, m, dt, rows + cols + m)
+    got = f32(K().packed_linear_affine(t(x, DT[dt]), t(packed), t(scale), t(bias), cols))
+    want = oracle.linear_fwd(x, packed, scale, bias, cols)
+    if dt == "f32":
+        assert rel_l2(got, want) <= 1e-5
+    else:
+        want_r = round_out(want, dt)
+        assert rel_l2(got, want_r) <= 1e-3
+        # all but a sliver of elements equal the rounded oracle
+        assert np.mean(got != want_r) < 0.01
+    nob = f32(K().packed_linear_affine(t(x, DT[dt]), t(packed), t(scale), None, cols))
+    want0 = oracle.linear_fwd(x, packed, scale, None, cols)
+    assert rel_l2(nob, want0 if dt == "f32" else round_out(want0, dt)) <= (1e-5 if dt == "f32" else 1e-3)
+
+
+@pytest.mark.parametrize("rows,cols,m", SHAPES)
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_linear_dgrad(rows, cols, m, dt):
+    packed, _, scale, _, dy = _problem(rows, cols, m, dt, 3 * rows + cols + m)
+    got = f32(K().packed_transpose(t(dy, DT[dt]), t(packed), cols, row_scale=t(scale)))
+    want = oracle.linear_dgrad(dy, packed, cols, round_scale(scale, dt))
+    if dt == "f32":
+        assert rel_l2(got, want) <= 1e-5
+    else:
+        assert rel_l2(got, round_out(want, dt)) <= 1e-3
+    plain = f32(K().packed_transpose(t(dy, DT[dt]), t(packed), cols))
+    want1 = oracle.linear_dgrad(dy, packed, cols)
+    assert rel_l2(plain, want1 if dt == "f32" else round_out(want1, dt)) <= (1e-5 if dt == "f32" else 1e-3)
+
+
+@pytest.mark.parametrize("rows,cols,m", SHAPES)
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_evidence(rows, cols, m, dt):
+    packed_w, x, scale, _, dy = _problem(rows, cols, m, dt, 5 * rows + cols + m)
+    xbits, off, xs = oracle.pack_affine_rows(x)
+    got = K().evidence_from_packed(t(dy, DT[dt]), t(xbits), cols, row_scale=t(xs)).cpu().numpy()
+    want = oracle.evidence(dy, xbits, cols, round_scale(xs, dt))
+    assert rel_l2(got, want) <= 1e-5
+
+
+@pytest.mark.parametrize("rows,cols", [(17, 13), (64, 64), (300, 1000), (1024, 4096)])
+def test_row_inner(rows, cols):
+    rng = np.random.default_rng(rows)
+    coord = rng.integers(-127, 128, size=(rows, cols)).astype(np.int8)
+    packed = oracle.pack_coordinate(coord)
+    mat = rng.standard_normal((rows, cols)).astype(np.float32)
+    got = K().packed_row_inner(t(mat), t(packed), cols).cpu().numpy()
+    assert rel_l2(got, oracle.row_inner(mat, packed, cols)) <= 1e-5
+
+
+@pytest.mark.parametrize("rows,cols,m", [(17, 13, 5), (64, 64, 32), (300, 256, 129), (512, 1024, 256),
+                                         (1024, 512, 64), (96, 4096, 1)])
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_fused_linear_backward(rows, cols, m, dt, with_bias):
+    packed_w, x, scale, _, dy = _problem(rows, cols, m, dt, 7 * rows + cols + m)
+    xbits, off, xs = oracle.pack_affine_rows(x)
+    dx, ev, gs, db = K().linear_backward(
+        t(dy, DT[dt]), t(xbits), t(off), t(xs), t(packed_w), t(scale), cols, need_bias=with_bias)
+    want_dx = oracle.linear_dgrad(dy, packed_w, cols, round_scale(scale, dt))
+    e0 = oracle.evidence(dy, xbits, cols, round_scale(xs, dt)) + oracle.offset_correction(dy, off)[:, None]
+    want_gs = oracle.row_inner(e0.astype(np.float32), packed_w, cols)
+    if dt == "f32":
+        assert rel_l2(f32(dx), want_dx) <= 1e-5
+    else:
+        assert rel_l2(f32(dx), round_out(want_dx, dt)) <= 1e-3
+    assert rel_l2(ev.cpu().numpy(), e0 * scale[:, None]) <= 1e-5
+    assert rel_l2(gs.cpu().numpy(), want_gs) <= 1e-4
+    if with_bias:
+        assert rel_l2(db.cpu().numpy(), dy.astype(np.float64).sum(0)) <= 1e-5
+    else:
+        assert db is None
+
+
+# ---------------------------------------------------------------------------
+# coordinate step
+# ---------------------------------------------------------------------------
+
+KEYS = ("coordinate", "packed", "moment_q", "moment_scale", "row_v", "col_v")
+
+
+def _to_gpu_state(state):
+    return {k: t(v.copy()) for k, v in state.items()}
+
+
+def _gpu_step(ev, gstate, **kw):
+    return K().coordinate_update(
+        t(ev), gstate["coordinate"], gstate["packed"], gstate["moment_q"], gstate["moment_scale"],
+        gstate["row_v"], gstate["col_v"], **kw)
+
+
+def _assert_state_equal(gstate, state, tag):
+    for k in KEYS:
+        got = gstate[k].cpu().numpy()
+        want = state[k]
+        assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), (tag, k, int((got != want).sum()))
+
+
+def test_coordinate_update_reference_vectors(golden):
+    """GPU vs the reference's own outputs: exact outside the rounding band."""
+
+    g = golden("coordinate_update")
+    for name in sorted({k.split("__")[0] for k in g}):
+        p = g[f"{name}__params"]
+        kw = dict(beta1=p[0], beta2=p[1], update_clip=p[2], coordinate_lr=p[3],
+                  block_size=int(p[4]), seed=int(p[5]), step=int(p[6]))
+        state = {k: np.ascontiguousarray(g[f"{name}__in_{k}"]) for k in KEYS}
+        gstate = _to_gpu_state(state)
+        flips = _gpu_step(g[f"{name}__evidence"], gstate, **kw)
+        # the oracle on the same inputs: GPU must equal it bit for bit
+        ostate = {k: v.copy() for k, v in state.items()}
+        oflips, tm, mm = oracle.coordinate_update(g[f"{name}__evidence"], ostate, margins=True, **kw)
+        _assert_state_equal(gstate, ostate, name)
+        assert flips == oflips, name
+        # and the reference's outputs, up to the declared band
+        bad = gstate["coordinate"].cpu().numpy() != g[f"{name}__out_coordinate"]
+        assert not np.any(bad & (tm >= 2.0 ** -16)), name
+
+
+@pytest.mark.parametrize("rows,cols,block", [(16, 32, 64), (37, 45, 64), (256, 1024, 256), (1024, 384, 256),
+                                             (200, 200, 128), (3, 5000, 256), (512, 4096, 256)])
+def test_coordinate_update_matches_oracle(rows, cols, block):
+    rng = np.random.default_rng(rows * cols)
+    coord = rng.integers(-127, 128, size=(rows, cols)).astype(np.int8)
+    state = oracle.fresh_state(coord, block)
+    gstate = _to_gpu_state(state)
+    for step in range(3):
+        ev = (rng.standard_normal((rows, cols)) * (0.01 * (step + 1))).astype(np.float32)
+        kw = dict(beta1=0.9, beta2=0.99, update_clip=2.0, coordinate_lr=1.0, block_size=block,
+                  seed=1 + 1_000_003 * 2, step=step)
+        flips = _gpu_step(ev, gstate, **kw)
+        oflips = oracle.coordinate_update(ev, state, **kw)
+        _assert_state_equal(gstate, state, (rows, cols, step))
+        assert flips == oflips
+
+
+def test_coordinate_update_device_step_flips_and_gate():
+    rows, cols, block = 64, 96, 64
+    rng = np.random.default_rng(5)
+    coord = rng.integers(-127, 128, size=(rows, cols)).astype(np.int8)
+    ev = rng.standard_normal((rows, cols)).astype(np.float32)
+    kw = dict(beta1=0.9, beta2=0.99, update_clip=2.0, coordinate_lr=4.0, block_size=block, seed=9)
+    # gate off: nothing changes, flips reported as zero
+    state = oracle.fresh_state(coord, block)
+    gstate = _to_gpu_state(state)
+    flips = torch.full((), -1, dtype=torch.int64, device=DEV)
+    gate = torch.zeros((), dtype=torch.uint8, device=DEV)
+    out = _gpu_step(ev, gstate, step=3, flips=flips, update_enabled=gate, **kw)
+    assert out is flips and int(flips.item()) == 0
+    _assert_state_equal(gstate, state, "gated")
+    # device step tensor == host step
+    step_t = torch.tensor(3, dtype=torch.int64, device=DEV)
+    gate.fill_(1)
+    _gpu_step(ev, gstate, step=step_t, flips=flips, update_enabled=gate, **kw)
+    oflips = oracle.coordinate_update(ev, state, step=3, **kw)
+    _assert_state_equal(gstate, state, "device step")
+    assert int(flips.item()) == oflips
+
+
+def test_coordinate_update_rejects_bad_block():
+    z = torch.zeros(4, 8, dtype=torch.int8, device=DEV)
+    with pytest.raises(ValueError):
+        K().coordinate_update(torch.zeros(4, 8, device=DEV), z, torch.zeros(4, 1, dtype=torch.uint8, device=DEV),
+                              z.clone(), torch.zeros(1, dtype=torch.float16, device=DEV),
+                              torch.zeros(4, dtype=torch.float16, device=DEV),
+                              torch.zeros(8, dtype=torch.float16, device=DEV), beta1=0.9, beta2=0.99,
+                              update_clip=2.0, coordinate_lr=1.0, block_size=48, seed=1, step=0)
