@@ -1,0 +1,284 @@
+"""Benchmark of the binary-linear hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+
+Headline workload: a Llama-3-8B-shaped SwiGLU MLP,
+d=4096, ffn=14336, gate/up/down all QSTE, bf16, 16384 tokens of N(0,1)
+activations, seeded int8 coordinates U{-127..127}, row scales |N(0,1)|*0.01,
+upstream gradient N(0,1).  One step = forward of the three layers (with the
+1-bit activation encoding), backward (input gradient, evidence, scale
+gradient) and the coordinate step of all three surfaces, which runs inside
+backward as in the reference.  ``value`` = 6 * T * sum(R*C) / step time.
+
+Alongside, measured live with HIP events on the stream the kernels run on:
+each GEMM kind at the gate-layer shape (the dominant kernel is reported as
+``roofline``), the coordinate step of one 14336 x 4096 surface (HBM), and
+the skinny-M decode GEMV of config 5 (K=8192, N=28672, M in {1, 4, 16}) over
+rotated weight copies larger than the 256 MB Infinity Cache.  The CPU
+baseline is the reference's CPU algorithm (oracle/cpu_baseline.py) timed on
+this host on a token sample of the same layers.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+MFMA_BF16_PEAK = 2.5e15  # dense, FLOP/s
+HBM_PEAK = 8.0e12        # B/s
+METRIC = "binary-linear fwd+bwd TFLOP/s + % MFMA peak at d=4096; decode GEMV HBM GB/s"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--tokens", type=int, default=16384)
+    ap.add_argument("--d", type=int, default=4096)
+    ap.add_argument("--ffn", type=int, default=14336)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip per-kernel, step and GEMV timing")
+    ap.add_argument("--cpu-tokens", type=int, default=256)
+    return ap.parse_args()
+
+
+def make_layer(rows, cols, seed, device, scale_std=0.01):
+    import torch
+
+    import qste_amd as qste
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    coord = torch.randint(-127, 128, (rows, cols), generator=g, device=device, dtype=torch.int32).to(torch.int8)
+    scale = torch.randn(rows, generator=g, device=device).abs_().mul_(scale_std).clamp_min_(1e-6)
+    surface = qste.Surface.from_state(coord, scale.log())
+    return qste.QSTELinear(surface, None)
+
+
+class SwiGLU:
+    def __init__(self, d, ffn, device):
+        import torch.nn as nn
+
+        self.gate = make_layer(ffn, d, 11, device)
+        self.up = make_layer(ffn, d, 21, device)
+        self.down = make_layer(d, ffn, 31, device)
+        self.modules = nn.ModuleList([self.gate, self.up, self.down])
+
+    def __call__(self, x):
+        import torch.nn.functional as F
+
+        return self.down(F.silu(self.gate(x)) * self.up(x))
+
+
+def timed_events(fn, iters, stream=None):
+    """Average milliseconds of ``fn`` over ``iters`` calls, by HIP events."""
+
+    import torch
+
+    stream = stream or torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    stop.record(stream)
+    stop.synchronize()
+    return start.elapsed_time(stop) / iters
+
+
+def gemm_kernels(T, d, ffn, device):
+    """Per-launch time of each product kind at the gate-layer shape."""
+
+    import torch
+
+    import oracle
+    from qste_amd import kernels
+
+    g = torch.Generator(device=device).manual_seed(7)
+    x = torch.randn(T, d, generator=g, device=device).to(torch.bfloat16)
+    dy = torch.randn(T, ffn, generator=g, device=device).to(torch.bfloat16)
+    layer = make_layer(ffn, d, 11, device)
+    packed = layer.surface.packed_sign.data
+    scale = layer.scale.detach().float()
+    xbits, off, xs = kernels.pack_affine_rows(x)
+    flop = 2.0 * T * ffn * d
+    out = {}
+    runs = {
+        "forward": lambda: kernels.packed_linear_affine(x, packed, scale, None, d),
+        "dgrad": lambda: kernels.packed_transpose(dy, packed, d, row_scale=scale),
+        "evidence": lambda: kernels.evidence_from_packed(dy, xbits, d, row_scale=xs),
+    }
+    for name, fn in runs.items():
+        ms = timed_events(fn, 5)
+        out[name] = {"ms": round(ms, 4), "tflops": round(flop / ms / 1e9, 2),
+                     "frac_of_mfma_peak": round(flop / (ms * 1e-3) / MFMA_BF16_PEAK, 4)}
+    del oracle
+    return out, flop
+
+
+def step_bandwidth(rows, cols, device):
+    import torch
+
+    from qste_amd import kernels
+
+    g = torch.Generator(device=device).manual_seed(5)
+    ev = torch.randn(rows, cols, generator=g, device=device).mul_(0.01)
+    coord = torch.randint(-127, 128, (rows, cols), generator=g, device=device, dtype=torch.int32).to(torch.int8)
+    packed = kernels.pack_coordinate(coord)
+    blocks = (rows * cols + 255) // 256
+    mq = torch.zeros_like(coord)
+    ms_ = torch.full((blocks,), 1 / 127, dtype=torch.float16, device=device)
+    rv = torch.zeros(rows, dtype=torch.float16, device=device)
+    cv = torch.zeros(cols, dtype=torch.float16, device=device)
+    flips = torch.empty((), dtype=torch.int64, device=device)
+    fn = lambda: kernels.coordinate_update(  # noqa: E731
+        ev, coord, packed, mq, ms_, rv, cv, beta1=0.9, beta2=0.99, update_clip=2.0,
+        coordinate_lr=1.0, block_size=256, seed=1, step=0, flips=flips)
+    ms = timed_events(fn, 5)
+    nbytes = rows * cols * (4 + 2 + 2) + rows * ((cols + 7) // 8) + 4 * blocks + 4 * (rows + cols)
+    return {"rows": rows, "cols": cols, "ms": round(ms, 4), "algorithmic_bytes": nbytes,
+            "gbps": round(nbytes / ms / 1e6, 1), "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / HBM_PEAK, 4)}
+
+
+def decode_gemv(device, K=8192, N=28672, copies=10):
+    import torch
+
+    from qste_amd import kernels
+
+    g = torch.Generator(device=device).manual_seed(1)
+    pb = K // 8
+    weights = [torch.randint(0, 256, (N, pb), generator=g, device=device, dtype=torch.int32).to(torch.uint8)
+               for _ in range(copies)]
+    scales = [torch.randn(N, generator=g, device=device).abs_().mul_(0.02) for _ in range(copies)]
+    res = {}
+    for M in (1, 4, 16):
+        x = torch.randn(M, K, generator=g, device=device).to(torch.bfloat16)
+        state = {"i": 0}
+
+        def fn():
+            i = state["i"] % copies
+            state["i"] += 1
+            kernels.packed_linear_affine(x, weights[i], scales[i], None, K)
+
+        ms = timed_events(fn, 5 * copies)
+        nbytes = N * pb + 4 * N + 2 * M * K + 2 * M * N
+        res[f"M{M}"] = {"us": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
+                        "gbps": round(nbytes / ms / 1e6, 1),
+                        "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / HBM_PEAK, 4)}
+    return res
+
+
+def cpu_baseline(d, ffn, tokens):
+    import numpy as np
+
+    import oracle
+    from oracle import cpu_baseline as cb
+
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((tokens, d), dtype=np.float32)
+    dy = rng.standard_normal((tokens, d), dtype=np.float32)
+    layers = []
+    for rows, cols in ((ffn, d), (ffn, d), (d, ffn)):
+        coord = rng.integers(-127, 128, size=(rows, cols), dtype=np.int8)
+        packed = oracle.pack_coordinate(coord)
+        scale = (np.abs(rng.standard_normal(rows)) * 0.01).astype(np.float32)
+        layers.append((packed, scale, oracle.fresh_state(coord, 256)))
+    t0 = time.perf_counter()
+    iters = 0
+    while True:
+        cb.swiglu_mlp_step(x, layers, dy, step=iters)
+        iters += 1
+        if time.perf_counter() - t0 > 10.0 or iters >= 3:
+            break
+    secs = (time.perf_counter() - t0) / iters
+    flop = 6.0 * tokens * (2 * ffn * d + d * ffn)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(flop / secs / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"SwiGLU d={d} ffn={ffn} fwd+bwd+coordinate step on {tokens} tokens "
+                      f"(of {16384}), fp32, numpy BLAS + C oracle, {iters} iteration(s), "
+                      f"{secs:.2f} s each"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import qste_amd as qste
+
+    if not torch.cuda.is_available():
+        print("bench.py needs the GPU", file=sys.stderr)
+        sys.exit(2)
+    device = torch.device("cuda:0")
+    T, d, ffn = args.tokens, args.d, args.ffn
+
+    mlp = SwiGLU(d, ffn, device)
+    coords = qste.QSTEOptimizer(list(qste.surfaces(mlp.modules)))
+    g = torch.Generator(device=device).manual_seed(0)
+    x = torch.randn(T, d, generator=g, device=device).to(torch.bfloat16).requires_grad_(False)
+    g4 = torch.Generator(device=device).manual_seed(4)
+    dy = torch.randn(T, d, generator=g4, device=device).to(torch.bfloat16)
+
+    def step():
+        y = mlp(x)
+        y.backward(dy)
+        return coords.step()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    secs = (time.perf_counter() - t0) / max(1, args.steps)
+    flop = 6.0 * T * (2 * ffn * d + d * ffn)
+    value = flop / secs / 1e12
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(secs * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations and gradients, U{-127..127} int8 coordinates)",
+        "config": {"workload": "cfg4 Llama-3-8B SwiGLU MLP fwd+bwd+coordinate step",
+                   "tokens": T, "d": d, "ffn": ffn, "layers": 3, "flop_per_step": flop},
+        "frac_of_mfma_peak": round(flop / secs / MFMA_BF16_PEAK, 4),
+    }
+    if not args.no_extras:
+        kernels_t, kflop = gemm_kernels(T, d, ffn, device)
+        dominant = max(kernels_t, key=lambda k: kernels_t[k]["ms"])
+        dk = kernels_t[dominant]
+        line["roofline"] = {"bound": "mfma", "kernel": dominant, "achieved": dk["tflops"],
+                            "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
+                            "frac": round(dk["tflops"] * 1e12 / MFMA_BF16_PEAK, 4), "traffic": None}
+        line["kernels"] = kernels_t
+        line["coordinate_step"] = step_bandwidth(ffn, d, device)
+        line["decode_gemv"] = decode_gemv(device)
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(d, ffn, args.cpu_tokens)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -87,6 +87,33 @@ class Surface(nn.Module):
         self._pending_calls = 0
         self._immediate = None  # set by QSTEOptimizer
 
+    @classmethod
+    def from_state(cls, coordinate: Tensor, log_scale: Tensor,
+                   cfg: QSTEConfig | None = None) -> "Surface":
+        """A surface holding the given int8 coordinate and fp32 log row scale.
+
+        For restoring saved state or building seeded synthetic layers; the
+        packed signs are derived from the coordinate on the GPU.
+        """
+
+        if coordinate.dtype != torch.int8 or coordinate.ndim != 2:
+            raise ValueError("coordinate must be a rank-2 int8 tensor")
+        if log_scale.shape != (coordinate.shape[0],):
+            raise ValueError("log_scale must have one entry per row")
+        self = cls.__new__(cls)
+        nn.Module.__init__(self)
+        self.cfg = coerce_config(cfg)
+        self.rows, self.columns = (int(s) for s in coordinate.shape)
+        self.coordinate = nn.Parameter(coordinate.contiguous(), requires_grad=False)
+        self.packed_sign = nn.Parameter(_on_gpu(kernels.pack_coordinate, self.coordinate.data),
+                                        requires_grad=False)
+        self.log_scale = nn.Parameter(log_scale.detach().float().clone())
+        self._evidence = None
+        self._call_evidence = None
+        self._pending_calls = 0
+        self._immediate = None
+        return self
+
     # -- forward-side state ------------------------------------------------
 
     @property
