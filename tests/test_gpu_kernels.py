@@ -312,3 +312,61 @@ def test_coordinate_update_rejects_bad_block():
                               torch.zeros(4, dtype=torch.float16, device=DEV),
                               torch.zeros(8, dtype=torch.float16, device=DEV), beta1=0.9, beta2=0.99,
                               update_clip=2.0, coordinate_lr=1.0, block_size=48, seed=1, step=0)
+
+
+# ---------------------------------------------------------------------------
+# MFMA path: ragged tiles and the full config-4 shapes (row-sampled oracle)
+# ---------------------------------------------------------------------------
+
+MFMA_SHAPES = [(576, 320, 300), (1024, 2048, 1000), (128, 64, 17), (256, 512, 2), (4096, 1024, 257)]
+
+
+@pytest.mark.parametrize("rows,cols,m", MFMA_SHAPES)
+def test_mfma_products_ragged(rows, cols, m):
+    packed, x, scale, bias, dy = _problem(rows, cols, m, "bf16", rows * 3 + m)
+    bf = torch.bfloat16
+    y = f32(K().packed_linear_affine(t(x, bf), t(packed), t(scale), t(bias), cols))
+    assert rel_l2(y, round_out(oracle.linear_fwd(x, packed, scale, bias, cols), "bf16")) <= 1e-3
+    dx = f32(K().packed_transpose(t(dy, bf), t(packed), cols, row_scale=t(scale)))
+    assert rel_l2(dx, round_out(oracle.linear_dgrad(dy, packed, cols, round_scale(scale, "bf16")), "bf16")) <= 1e-3
+    xbits, off, xs = oracle.pack_affine_rows(x)
+    ev = K().evidence_from_packed(t(dy, bf), t(xbits), cols, row_scale=t(xs)).cpu().numpy()
+    assert rel_l2(ev, oracle.evidence(dy, xbits, cols, round_scale(xs, "bf16"))) <= 1e-5
+    dxf, evf, gs, db = K().linear_backward(t(dy, bf), t(xbits), t(off), t(xs), t(packed), t(scale), cols,
+                                           need_bias=True)
+    e0 = oracle.evidence(dy, xbits, cols, round_scale(xs, "bf16")) + oracle.offset_correction(dy, off)[:, None]
+    assert rel_l2(evf.cpu().numpy(), e0 * scale[:, None]) <= 1e-5
+    assert rel_l2(gs.cpu().numpy(), oracle.row_inner(e0.astype(np.float32), packed, cols)) <= 1e-4
+    assert rel_l2(f32(dxf), dx) == 0.0
+
+
+@pytest.mark.parametrize("rows,cols", [(14336, 4096), (4096, 14336)])
+def test_full_size_products_sampled_rows(rows, cols):
+    """Config-4 layer shapes, 16384 tokens; oracle on a sample of rows."""
+
+    T = 16384
+    g = torch.Generator(device=DEV).manual_seed(rows)
+    bf = torch.bfloat16
+    x = torch.randn(T, cols, generator=g, device=DEV).to(bf)
+    dy = torch.randn(T, rows, generator=g, device=DEV).to(bf)
+    coord = torch.randint(-127, 128, (rows, cols), generator=g, device=DEV, dtype=torch.int32).to(torch.int8)
+    packed = K().pack_coordinate(coord)
+    scale = torch.rand(rows, generator=g, device=DEV) * 0.02 + 0.005
+    y = K().packed_linear_affine(x, packed, scale, None, cols)
+    dx = K().packed_transpose(dy, packed, cols, row_scale=scale)
+    xbits, off, xs = K().pack_affine_rows(x)
+    ev = K().evidence_from_packed(dy, xbits, cols, row_scale=xs)
+    torch.cuda.synchronize()
+    pk, sc = packed.cpu().numpy(), scale.cpu().numpy()
+    rng = np.random.default_rng(1)
+    trows = rng.choice(T, 6, replace=False)
+    xs_np = x[trows].float().cpu().numpy()
+    want_y = round_out(oracle.linear_fwd(xs_np, pk, sc, None, cols), "bf16")
+    assert rel_l2(f32(y[trows]), want_y) <= 1e-3
+    dys = dy[trows].float().cpu().numpy()
+    want_dx = round_out(oracle.linear_dgrad(dys, pk, cols, round_scale(sc, "bf16")), "bf16")
+    assert rel_l2(f32(dx[trows]), want_dx) <= 1e-3
+    erows = rng.choice(rows, 3, replace=False)
+    dy_cols = dy[:, erows].float().cpu().numpy()
+    want_e = oracle.evidence(dy_cols, xbits.cpu().numpy(), cols, round_scale(xs.cpu().numpy(), "bf16"))
+    assert rel_l2(ev[erows].cpu().numpy(), want_e) <= 1e-5
