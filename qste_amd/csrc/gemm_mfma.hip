@@ -15,10 +15,11 @@
 //
 // Tile: 256 x 128 per workgroup of 4 waves (2 x 2), each wave 128 x 64 as
 // 4 x 2 blocks of 32 x 32, K step 64 (4 MFMA k-steps of 16).  The dense
-// operand (A) goes through LDS; the next K step's global loads are issued
-// before the current step's MFMAs so their latency hides under compute.
-// Where bits run along N they are staged through LDS as a small transposed
-// byte tile (already inverted, so a set bit means "negative").
+// operand (A) goes through double-buffered LDS with one barrier per K step;
+// the next step's global loads (buffer loads, whose out-of-range reads
+// return zero and so pad ragged edges for free) are issued before the
+// current step's MFMAs.  Where bits run along N they are staged through LDS
+// as a small transposed byte tile, inverted so a set bit means "negative".
 //
 // MFMA 32x32x16 bf16 operand layout used here: lane l holds A[l%32][8(l/32)
 // + i] and B[8(l/32) + i][l%32], i = 0..7; the accumulator's register r
@@ -31,32 +32,74 @@ namespace mfma {
 typedef short bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 256, BN = 128, BK = 64, THREADS = 256;
-constexpr int LDA = BK + 8;        // bf16 per LDS row of A (144 B: conflict-free b128 reads)
-constexpr int LDB = BK + 8;        // bytes per LDS row of staged bits ([n/8][k])
+constexpr int LDA = BK + 8;                 // bf16 per LDS row of A (144 B)
+constexpr int LDB = BK + 8;                 // bytes per LDS row of staged bits ([n/8][k])
+constexpr int A_TILE = BM * LDA;            // bf16 elements per A buffer
+constexpr int B_TILE = (BN / 8) * LDB;      // bytes per staged-bits buffer
+constexpr uint32_t kRsrcWord3 = 0x00020000u;
 
-union Frag {
-  bf16x8 v;
-  uint32_t d[4];
-  uint4 q;
+enum { A_ROWS_M = 0, A_ROWS_K = 1 };        // A[m][k] stored with k (or m) contiguous
+enum { B_BITS_ALONG_K = 0, B_BITS_ALONG_N = 1 };
+enum { EPI_FORWARD = 0, EPI_PLAIN = 1, EPI_EVIDENCE = 2 };
+
+struct Params {
+  const uint16_t* a;     // bf16 dense operand (x or dy)
+  const uint8_t* bits;   // packed signs of the +-1 operand
+  const float* kscale;   // per-k scale folded into the bit operand (dgrad/evidence)
+  void* out;
+  int64_t M, N, K;
+  int64_t lda;           // elements between rows of the dense source
+  int64_t pb;            // bytes per packed row
+  int64_t a_rows;        // rows of the dense source (bounds of its buffer)
+  int64_t bit_rows;      // rows of the packed source
+  // epilogue
+  const float* n_scale;  // forward
+  const float* n_bias;   // forward
+  const float* m_add;    // evidence
+  const float* m_scale;  // evidence
+  const uint8_t* w_bits; // evidence: sign_w for the scale gradient
+  float* gs_partial;     // evidence: [2 * tiles_n][M]
 };
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
+  const uint32_t n = bytes > 0xFFFFFFFFll ? 0xFFFFFFFFu : static_cast<uint32_t>(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(n), kRsrcWord3);
+}
+
+__device__ __forceinline__ uint4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
+}
+__device__ __forceinline__ uint64_t ld64(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(off), 0, 0));
+}
+__device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0);
+}
+
 __device__ __forceinline__ uint32_t pk_shl(uint32_t x, u16x2 sh) {
-  u16x2 v = __builtin_bit_cast(u16x2, x);
-  v = v << sh;
-  return __builtin_bit_cast(uint32_t, v);
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, x) << sh);
+}
+
+// 0x3F803F80 (a pair of bf16 +1.0) held in a VGPR so the sign insertion below
+// is one v_and_or_b32 per pair.
+__device__ __forceinline__ uint32_t bf16_one_pair() {
+  uint32_t v;
+  asm volatile("v_mov_b32 %0, 0x3F803F80" : "=v"(v));
+  return v;
 }
 
 // 8 signs along k from one byte; `neg` has bit i set where k-offset i is -1.
-__device__ __forceinline__ bf16x8 signs_along_k(uint32_t neg) {
-  const uint32_t tt = neg | (neg << 16);
-  Frag f;
-  f.d[0] = (pk_shl(tt, u16x2{15, 14}) & 0x80008000u) | 0x3F803F80u;
-  f.d[1] = (pk_shl(tt, u16x2{13, 12}) & 0x80008000u) | 0x3F803F80u;
-  f.d[2] = (pk_shl(tt, u16x2{11, 10}) & 0x80008000u) | 0x3F803F80u;
-  f.d[3] = (pk_shl(tt, u16x2{9, 8}) & 0x80008000u) | 0x3F803F80u;
-  return f.v;
+__device__ __forceinline__ bf16x8 signs_along_k(uint32_t neg, uint32_t one) {
+  const uint32_t tt = neg * 0x10001u;
+  u32x4 r;
+  r.x = (pk_shl(tt, u16x2{15, 14}) & 0x80008000u) | one;
+  r.y = (pk_shl(tt, u16x2{13, 12}) & 0x80008000u) | one;
+  r.z = (pk_shl(tt, u16x2{11, 10}) & 0x80008000u) | one;
+  r.w = (pk_shl(tt, u16x2{9, 8}) & 0x80008000u) | one;
+  return __builtin_bit_cast(bf16x8, r);
 }
 
 // 8 scaled signs across k: byte i of `neg8` is the (inverted) bit row for
@@ -65,19 +108,27 @@ __device__ __forceinline__ bf16x8 signs_along_k(uint32_t neg) {
 __device__ __forceinline__ bf16x8 signs_across_k(uint64_t neg8, int bit, uint4 scale) {
   const uint64_t x = neg8 >> bit;
   const uint32_t lo = static_cast<uint32_t>(x), hi = static_cast<uint32_t>(x >> 32);
-  Frag f;
-  f.d[0] = pk_shl(__builtin_amdgcn_perm(hi, lo, 0x0C010C00u), u16x2{15, 15}) | scale.x;
-  f.d[1] = pk_shl(__builtin_amdgcn_perm(hi, lo, 0x0C030C02u), u16x2{15, 15}) | scale.y;
-  f.d[2] = pk_shl(__builtin_amdgcn_perm(hi, lo, 0x0C050C04u), u16x2{15, 15}) | scale.z;
-  f.d[3] = pk_shl(__builtin_amdgcn_perm(hi, lo, 0x0C070C06u), u16x2{15, 15}) | scale.w;
-  return f.v;
+  u32x4 r;
+  r.x = pk_shl(__builtin_amdgcn_perm(hi, lo, 0x0C010C00u), u16x2{15, 15}) | scale.x;
+  r.y = pk_shl(__builtin_amdgcn_perm(hi, lo, 0x0C030C02u), u16x2{15, 15}) | scale.y;
+  r.z = pk_shl(__builtin_amdgcn_perm(hi, lo, 0x0C050C04u), u16x2{15, 15}) | scale.z;
+  r.w = pk_shl(__builtin_amdgcn_perm(hi, lo, 0x0C070C06u), u16x2{15, 15}) | scale.w;
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+// Workgroup barrier for LDS hand-off only.  __syncthreads() carries a
+// workgroup memory fence, which makes the compiler wait for every
+// outstanding global load (vmcnt(0)) at each barrier and so cancels the
+// prefetch; here only this wave's LDS operations are drained (lgkmcnt(0))
+// before the barrier, and in-flight global loads stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt: no wait, expcnt: no wait, lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
 }
 
 __device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
-
-__device__ __forceinline__ uint16_t bf16_rne(float f) { return f32_to_bf16(f); }
 
 // Workgroup -> output tile.  Consecutive workgroup ids land on different
 // XCDs (round-robin), so ids are first regrouped so each XCD gets a
@@ -96,28 +147,18 @@ __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& 
   tn = in_group / gm;
 }
 
-struct Params {
-  const uint16_t* a;     // bf16 dense operand (x or dy)
-  const uint8_t* bits;   // packed signs of the +-1 operand
-  const float* kscale;   // per-k scale folded into the bit operand (dgrad/evidence)
-  void* out;
-  int64_t M, N, K;
-  int64_t lda;           // elements between rows of the dense source
-  int64_t pb;            // bytes per packed row
-  // epilogue
-  const float* n_scale;  // forward
-  const float* n_bias;   // forward
-  const float* m_add;    // evidence
-  const float* m_scale;  // evidence
-  const uint8_t* w_bits; // evidence: sign_w for the scale gradient
-  float* gs_partial;     // evidence: [2 * tiles_n][M]
-};
+// Index of this 16-byte chunk of a transposed (A_ROWS_K) A row in LDS: XOR
+// swizzled by (row / 8) so the transposed stores do not collide on banks.
+__device__ __forceinline__ int a_chunk(int akind, int chunk, int row) {
+  return akind == A_ROWS_K ? (chunk ^ ((row >> 3) & 7)) : chunk;
+}
 
-// ---------------------------------------------------------------------------
-// forward: y[m, n] = sum_k x[m, k] sign_w[n, k]; bits of row n run along k
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(THREADS, 2) void forward_kernel(Params p) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[BM * LDA];
+template <int AKIND, int BKIND, int EPI>
+__global__ __launch_bounds__(THREADS, 2) void gemm_kernel(Params p) {
+  __shared__ __attribute__((aligned(16))) uint16_t As[2 * A_TILE];
+  __shared__ __attribute__((aligned(16))) uint8_t Bs[BKIND == B_BITS_ALONG_N ? 2 * B_TILE : 16];
+  __shared__ __attribute__((aligned(16))) uint16_t Ss[BKIND == B_BITS_ALONG_N ? 2 * BK : 8];
+
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int wm = wave >> 1, wn = wave & 1;
@@ -127,6 +168,8 @@ __global__ __launch_bounds__(THREADS, 2) void forward_kernel(Params p) {
   int tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  const uint32_t one = bf16_one_pair();
+  const int nk = static_cast<int>((p.K + BK - 1) / BK);
 
   f32x16 acc[4][2];
 #pragma unroll
@@ -134,310 +177,207 @@ __global__ __launch_bounds__(THREADS, 2) void forward_kernel(Params p) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-  uint4 areg[8];
+  // ---- A source --------------------------------------------------------
+  // A_ROWS_M: thread loads rows (arow + 32 i), 16-byte chunk achunk.
+  // A_ROWS_K: thread loads an 8 x 8 block: k rows 8kb..8kb+7, m cols 8rb..
   const int arow = tid >> 3, achunk = tid & 7;
-  auto load_a = [&](int64_t k0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t r = m0 + arow + 32 * i;
-      areg[i] = r < p.M ? *reinterpret_cast<const uint4*>(p.a + r * p.lda + k0 + achunk * 8)
-                        : make_uint4(0, 0, 0, 0);
-    }
-  };
-  uint64_t breg[2];
-  auto load_b = [&](int64_t k0) {
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int64_t n = n0 + 64 * wn + 32 * nb + l32;
-      breg[nb] = n < p.N ? *reinterpret_cast<const uint64_t*>(p.bits + n * p.pb + k0 / 8) : 0ull;
-    }
-  };
-
-  load_a(0);
-  load_b(0);
-  for (int64_t k0 = 0; k0 < p.K; k0 += BK) {
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      *reinterpret_cast<uint4*>(&As[(arow + 32 * i) * LDA + achunk * 8]) = areg[i];
-    __syncthreads();
-    const uint64_t neg0 = ~breg[0], neg1 = ~breg[1];
-    if (k0 + BK < p.K) {
-      load_a(k0 + BK);
-      load_b(k0 + BK);
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int sh = 8 * (2 * s + kg);
-      bf16x8 b0 = signs_along_k(static_cast<uint32_t>(neg0 >> sh) & 0xFFu);
-      bf16x8 b1 = signs_along_k(static_cast<uint32_t>(neg1 >> sh) & 0xFFu);
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const int row = 128 * wm + 32 * mb + l32;
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&As[row * LDA + 16 * s + 8 * kg]);
-        acc[mb][0] = mma(a, b0, acc[mb][0]);
-        acc[mb][1] = mma(a, b1, acc[mb][1]);
-      }
-    }
-  }
-
-  uint16_t* y = static_cast<uint16_t*>(p.out);
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int64_t col = n0 + 64 * wn + 32 * nb + l32;
-    if (col >= p.N) continue;
-    const float sc = p.n_scale ? p.n_scale[col] : 1.0f;
-    const float bi = p.n_bias ? p.n_bias[col] : 0.0f;
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
-        if (row < p.M) {
-          float v = acc[mb][nb][r] * sc;
-          v = v + bi;
-          y[row * p.N + col] = bf16_rne(v);
-        }
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Bits along N, staged per K step into LDS as [n/8][k] inverted bytes, and
-// the per-k scale as bf16.  Thread t stages one dword (32 columns) of row
-// k = t / 4 of the tile.
-// ---------------------------------------------------------------------------
-struct BitStage {
-  uint32_t word;
-  float scale;
-};
-
-__device__ __forceinline__ BitStage load_bits_kn(const Params& p, int64_t k0, int64_t n0, int tid) {
-  BitStage s;
-  const int64_t k = k0 + (tid >> 2);
-  const int64_t byte = n0 / 8 + (tid & 3) * 4;
-  s.word = (k < p.K && byte < p.pb) ? *reinterpret_cast<const uint32_t*>(p.bits + k * p.pb + byte) : 0u;
-  s.scale = 0.0f;
-  if (tid < BK) {
-    const int64_t kk = k0 + tid;
-    s.scale = kk < p.K ? (p.kscale ? p.kscale[kk] : 1.0f) : 0.0f;
-  }
-  return s;
-}
-
-__device__ __forceinline__ void store_bits_kn(uint8_t* Bs, uint16_t* Ss, const BitStage& s, int tid) {
-  const int k = tid >> 2;
-  const int col = (tid & 3) * 4;
-  const uint32_t neg = ~s.word;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) Bs[(col + i) * LDB + k] = static_cast<uint8_t>(neg >> (8 * i));
-  if (tid < BK) Ss[tid] = bf16_rne(s.scale);
-}
-
-__device__ __forceinline__ bf16x8 b_frag_kn(const uint8_t* Bs, const uint16_t* Ss, int ncol, int s,
-                                            int kg) {
-  const int kk = 16 * s + 8 * kg;
-  const uint64_t neg8 = *reinterpret_cast<const uint64_t*>(&Bs[(ncol >> 3) * LDB + kk]);
-  const uint4 sc = *reinterpret_cast<const uint4*>(&Ss[kk]);
-  return signs_across_k(neg8, ncol & 7, sc);
-}
-
-// ---------------------------------------------------------------------------
-// dgrad: dx[m, n] = sum_k dy[m, k] bf16(s[k]) sign_w[k, n]
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(THREADS, 2) void dgrad_kernel(Params p) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[BM * LDA];
-  __shared__ __attribute__((aligned(16))) uint8_t Bs[(BN / 8) * LDB];
-  __shared__ __attribute__((aligned(16))) uint16_t Ss[BK];
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int l32 = lane & 31, kg = lane >> 5;
-  const int tiles_m = static_cast<int>((p.M + BM - 1) / BM);
-  const int tiles_n = static_cast<int>((p.N + BN - 1) / BN);
-  int tm, tn;
-  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
-
-  f32x16 acc[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-
-  uint4 areg[8];
-  const int arow = tid >> 3, achunk = tid & 7;
-  auto load_a = [&](int64_t k0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t r = m0 + arow + 32 * i;
-      areg[i] = r < p.M ? *reinterpret_cast<const uint4*>(p.a + r * p.lda + k0 + achunk * 8)
-                        : make_uint4(0, 0, 0, 0);
-    }
-  };
-  BitStage bst = load_bits_kn(p, 0, n0, tid);
-  load_a(0);
-  for (int64_t k0 = 0; k0 < p.K; k0 += BK) {
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      *reinterpret_cast<uint4*>(&As[(arow + 32 * i) * LDA + achunk * 8]) = areg[i];
-    store_bits_kn(Bs, Ss, bst, tid);
-    __syncthreads();
-    if (k0 + BK < p.K) {
-      load_a(k0 + BK);
-      bst = load_bits_kn(p, k0 + BK, n0, tid);
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const bf16x8 b0 = b_frag_kn(Bs, Ss, 64 * wn + l32, s, kg);
-      const bf16x8 b1 = b_frag_kn(Bs, Ss, 64 * wn + 32 + l32, s, kg);
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const int row = 128 * wm + 32 * mb + l32;
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&As[row * LDA + 16 * s + 8 * kg]);
-        acc[mb][0] = mma(a, b0, acc[mb][0]);
-        acc[mb][1] = mma(a, b1, acc[mb][1]);
-      }
-    }
-  }
-
-  uint16_t* dx = static_cast<uint16_t*>(p.out);
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int64_t col = n0 + 64 * wn + 32 * nb + l32;
-    if (col >= p.N) continue;
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
-        if (row < p.M) dx[row * p.N + col] = bf16_rne(acc[mb][nb][r]);
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// evidence: E[m, n] = sum_k dy[k, m] bf16(xs[k]) sign_x[k, n]  (m = output row
-// r of the layer, k = sample t).  dy is read as [k][m] rows, an 8 x 8 block
-// per thread, transposed in registers with v_perm and written to LDS as
-// [m][k] with the 16-byte chunk index XOR-swizzled by (m / 8) so the
-// transposed stores do not collide on LDS banks.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ int swz(int chunk, int row) { return chunk ^ ((row >> 3) & 7); }
-
-__global__ __launch_bounds__(THREADS, 2) void evidence_kernel(Params p) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[BM * LDA];
-  __shared__ __attribute__((aligned(16))) uint8_t Bs[(BN / 8) * LDB];
-  __shared__ __attribute__((aligned(16))) uint16_t Ss[BK];
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int l32 = lane & 31, kg = lane >> 5;
-  const int tiles_m = static_cast<int>((p.M + BM - 1) / BM);
-  const int tiles_n = static_cast<int>((p.N + BN - 1) / BN);
-  int tm, tn;
-  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
-
-  f32x16 acc[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-
-  // this thread's 8 x 8 block: m in [m0 + 8*rb, +8), k in [k0 + 8*kb, +8)
   const int rb = tid & 31, kb = tid >> 5;
+  __amdgpu_buffer_rsrc_t ra;
+  uint32_t aoff;
+  if (AKIND == A_ROWS_M) {
+    // buffer starts at the tile's first row: rows past M read as zero
+    const int64_t rows_left = p.a_rows - m0;
+    ra = rsrc(p.a + m0 * p.lda, rows_left * p.lda * 2);
+    aoff = static_cast<uint32_t>((arow * p.lda + achunk * 8) * 2);
+  } else {
+    // buffer starts at column m0: k rows past K read as zero
+    ra = rsrc(p.a + m0, (p.a_rows * p.lda - m0) * 2);
+    aoff = static_cast<uint32_t>(((8 * kb) * p.lda + 8 * rb) * 2);
+  }
+  const uint32_t a_step = AKIND == A_ROWS_M ? BK * 2 : static_cast<uint32_t>(BK * p.lda * 2);
+  const uint32_t a_stride = AKIND == A_ROWS_M ? static_cast<uint32_t>(32 * p.lda * 2)
+                                              : static_cast<uint32_t>(p.lda * 2);
   uint4 areg[8];
-  auto load_a = [&](int64_t k0) {
-    const int64_t m = m0 + 8 * rb;
+  auto load_a = [&](int it) {
+    const uint32_t base = aoff + static_cast<uint32_t>(it) * a_step;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t k = k0 + 8 * kb + i;
-      areg[i] = (k < p.K && m < p.M) ? *reinterpret_cast<const uint4*>(p.a + k * p.lda + m)
-                                     : make_uint4(0, 0, 0, 0);
-    }
+    for (int i = 0; i < 8; ++i) areg[i] = ld128(ra, base + i * a_stride);
   };
-  BitStage bst = load_bits_kn(p, 0, n0, tid);
-  load_a(0);
-  for (int64_t k0 = 0; k0 < p.K; k0 += BK) {
-    __syncthreads();
-    {
-      // transpose: out[j] holds k = 8kb..8kb+7 for m = 8rb + j
+  auto store_a = [&](uint16_t* buf) {
+    if (AKIND == A_ROWS_M) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(&buf[(arow + 32 * i) * LDA + achunk * 8]) = areg[i];
+    } else {
       const uint32_t* in = reinterpret_cast<const uint32_t*>(areg);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
         uint4 o;
-        o.x = __builtin_amdgcn_perm(in[1 * 4 + (j >> 1)], in[0 * 4 + (j >> 1)], sel);
-        o.y = __builtin_amdgcn_perm(in[3 * 4 + (j >> 1)], in[2 * 4 + (j >> 1)], sel);
-        o.z = __builtin_amdgcn_perm(in[5 * 4 + (j >> 1)], in[4 * 4 + (j >> 1)], sel);
-        o.w = __builtin_amdgcn_perm(in[7 * 4 + (j >> 1)], in[6 * 4 + (j >> 1)], sel);
+        o.x = __builtin_amdgcn_perm(in[4 + (j >> 1)], in[0 + (j >> 1)], sel);
+        o.y = __builtin_amdgcn_perm(in[12 + (j >> 1)], in[8 + (j >> 1)], sel);
+        o.z = __builtin_amdgcn_perm(in[20 + (j >> 1)], in[16 + (j >> 1)], sel);
+        o.w = __builtin_amdgcn_perm(in[28 + (j >> 1)], in[24 + (j >> 1)], sel);
         const int row = 8 * rb + j;
-        *reinterpret_cast<uint4*>(&As[row * LDA + swz(kb, row) * 8]) = o;
+        *reinterpret_cast<uint4*>(&buf[row * LDA + a_chunk(A_ROWS_K, kb, row) * 8]) = o;
       }
     }
-    store_bits_kn(Bs, Ss, bst, tid);
-    __syncthreads();
-    if (k0 + BK < p.K) {
-      load_a(k0 + BK);
-      bst = load_bits_kn(p, k0 + BK, n0, tid);
+  };
+
+  // ---- B source ----------------------------------------------------------
+  __amdgpu_buffer_rsrc_t rb_bits = rsrc(p.bits, p.bit_rows * p.pb);
+  __amdgpu_buffer_rsrc_t rb_scale = rsrc(p.kscale, p.kscale ? p.K * 4 : 0);
+  uint64_t breg[2] = {0, 0};   // B_BITS_ALONG_K: this lane's 64 k-bits of its two columns
+  uint32_t bword = 0;          // B_BITS_ALONG_N: one staged dword of bits
+  float bscale = 0.0f;
+  uint32_t boff[2];
+  if (BKIND == B_BITS_ALONG_K) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int64_t n = n0 + 64 * wn + 32 * nb + l32;
+      boff[nb] = static_cast<uint32_t>(n * p.pb);  // rows past N read as zero
     }
+  } else {
+    boff[0] = static_cast<uint32_t>((tid >> 2) * p.pb + n0 / 8 + (tid & 3) * 4);
+    boff[1] = 0;
+  }
+  auto load_b = [&](int it) {
+    const int64_t k0 = static_cast<int64_t>(it) * BK;
+    if (BKIND == B_BITS_ALONG_K) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) breg[nb] = ld64(rb_bits, boff[nb] + static_cast<uint32_t>(k0 / 8));
+    } else {
+      bword = ld32(rb_bits, boff[0] + static_cast<uint32_t>(k0 * p.pb));
+      if (tid < BK) bscale = p.kscale ? __uint_as_float(ld32(rb_scale, static_cast<uint32_t>((k0 + tid) * 4)))
+                                      : (k0 + tid < p.K ? 1.0f : 0.0f);
+    }
+  };
+  auto store_b = [&](int buf) {
+    if (BKIND == B_BITS_ALONG_N) {
+      uint8_t* bs = Bs + buf * B_TILE;
+      const int k = tid >> 2, col = (tid & 3) * 4;
+      const uint32_t neg = ~bword;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bs[(col + i) * LDB + k] = static_cast<uint8_t>(neg >> (8 * i));
+      if (tid < BK) Ss[buf * BK + tid] = f32_to_bf16(bscale);
+    }
+  };
+
+  // ---- main loop ---------------------------------------------------------
+  load_a(0);
+  load_b(0);
+  store_a(As);
+  store_b(0);
+  uint64_t bcur[2] = {~breg[0], ~breg[1]};
+  lds_barrier();
+
+  for (int it = 0; it < nk; ++it) {
+    const int cur = it & 1;
+    const bool more = it + 1 < nk;
+    if (more) {
+      load_a(it + 1);
+      load_b(it + 1);
+    }
+    const uint16_t* a_buf = As + cur * A_TILE;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const bf16x8 b0 = b_frag_kn(Bs, Ss, 64 * wn + l32, s, kg);
-      const bf16x8 b1 = b_frag_kn(Bs, Ss, 64 * wn + 32 + l32, s, kg);
+      bf16x8 b0, b1;
+      if (BKIND == B_BITS_ALONG_K) {
+        const int sh = 8 * (2 * s + kg);
+        b0 = signs_along_k(static_cast<uint32_t>(bcur[0] >> sh) & 0xFFu, one);
+        b1 = signs_along_k(static_cast<uint32_t>(bcur[1] >> sh) & 0xFFu, one);
+      } else {
+        const uint8_t* bs = Bs + cur * B_TILE;
+        const int kk = 16 * s + 8 * kg;
+        const uint4 sc = *reinterpret_cast<const uint4*>(&Ss[cur * BK + kk]);
+        const int c0 = 64 * wn + l32, c1 = c0 + 32;
+        b0 = signs_across_k(*reinterpret_cast<const uint64_t*>(&bs[(c0 >> 3) * LDB + kk]), c0 & 7, sc);
+        b1 = signs_across_k(*reinterpret_cast<const uint64_t*>(&bs[(c1 >> 3) * LDB + kk]), c1 & 7, sc);
+      }
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         const int row = 128 * wm + 32 * mb + l32;
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&As[row * LDA + swz(2 * s + kg, row) * 8]);
+        const bf16x8 a =
+            *reinterpret_cast<const bf16x8*>(&a_buf[row * LDA + a_chunk(AKIND, 2 * s + kg, row) * 8]);
         acc[mb][0] = mma(a, b0, acc[mb][0]);
         acc[mb][1] = mma(a, b1, acc[mb][1]);
       }
     }
-  }
-
-  // epilogue: E0 = acc + v[m]; row partials of E0 * sign_w; E = E0 * s[m]
-  float* ev = static_cast<float*>(p.out);
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    float part[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) part[r] = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t row = m0 + 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
-      if (row >= p.M) continue;
-      const float add = p.m_add ? p.m_add[row] : 0.0f;
-      const float mul = p.m_scale ? p.m_scale[row] : 1.0f;
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const int64_t col = n0 + 64 * wn + 32 * nb + l32;
-        if (col >= p.N) continue;
-        const float e0 = acc[mb][nb][r] + add;
-        if (p.w_bits) {
-          const uint32_t byte = p.w_bits[row * p.pb + (col >> 3)];
-          part[r] += ((byte >> (col & 7)) & 1u) ? e0 : -e0;
-        }
-        ev[row * p.N + col] = e0 * mul;
+    if (more) {
+      store_a(As + (cur ^ 1) * A_TILE);
+      store_b(cur ^ 1);
+      if (BKIND == B_BITS_ALONG_K) {
+        bcur[0] = ~breg[0];
+        bcur[1] = ~breg[1];
       }
     }
-    if (p.gs_partial) {
+    lds_barrier();
+  }
+
+  // ---- epilogue ------------------------------------------------------------
+  if (EPI == EPI_FORWARD || EPI == EPI_PLAIN) {
+    uint16_t* y = static_cast<uint16_t*>(p.out);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float v = part[r];
+    for (int nb = 0; nb < 2; ++nb) {
+      const int64_t col = n0 + 64 * wn + 32 * nb + l32;
+      if (col >= p.N) continue;
+      const float sc = (EPI == EPI_FORWARD && p.n_scale) ? p.n_scale[col] : 1.0f;
+      const float bi = (EPI == EPI_FORWARD && p.n_bias) ? p.n_bias[col] : 0.0f;
 #pragma unroll
-        for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-        part[r] = v;
-      }
-      if (l32 == 0) {
-        const int64_t slot = 2 * static_cast<int64_t>(tn) + wn;
+      for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int64_t row = m0 + 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
-          if (row < p.M) p.gs_partial[slot * p.M + row] = part[r];
+          if (row < p.M) {
+            float v = acc[mb][nb][r];
+            if (EPI == EPI_FORWARD) {
+              v = v * sc;
+              v = v + bi;
+            }
+            y[row * p.N + col] = f32_to_bf16(v);
+          }
+        }
+      }
+    }
+  } else {
+    // E0 = acc + v[m]; row partials of E0 * sign_w; E = E0 * s[m]
+    float* ev = static_cast<float*>(p.out);
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      float part[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        part[r] = 0.0f;
+        const int64_t row = m0 + 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
+        if (row >= p.M) continue;
+        const float add = p.m_add ? p.m_add[row] : 0.0f;
+        const float mul = p.m_scale ? p.m_scale[row] : 1.0f;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          const int64_t col = n0 + 64 * wn + 32 * nb + l32;
+          if (col >= p.N) continue;
+          const float e0 = acc[mb][nb][r] + add;
+          if (p.w_bits) {
+            const uint32_t byte = p.w_bits[row * p.pb + (col >> 3)];
+            part[r] += ((byte >> (col & 7)) & 1u) ? e0 : -e0;
+          }
+          ev[row * p.N + col] = e0 * mul;
+        }
+      }
+      if (p.gs_partial) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float v = part[r];
+#pragma unroll
+          for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+          part[r] = v;
+        }
+        if (l32 == 0) {
+          const int64_t slot = 2 * static_cast<int64_t>(tn) + wn;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int64_t row = m0 + 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
+            if (row < p.M) p.gs_partial[slot * p.M + row] = part[r];
+          }
         }
       }
     }
@@ -456,25 +396,32 @@ static int grid_tiles(int64_t M, int64_t N) {
   return static_cast<int>(((M + mfma::BM - 1) / mfma::BM) * ((N + mfma::BN - 1) / mfma::BN));
 }
 
+// Buffer offsets are 32-bit: every operand must stay under 4 GiB.
+static bool fits32(int64_t bytes) { return bytes < (int64_t{1} << 32); }
+
 int mfma_linear_forward(const void* x, int dtype, const uint8_t* packed, const float* scale,
                         const float* bias, void* y, int64_t m, int64_t rows, int64_t cols,
                         hipStream_t stream) {
-  if (dtype != QSTE_BF16 || cols % 64 != 0 || cols == 0 || !aligned16(x) || !aligned16(packed)) return 1;
+  if (dtype != QSTE_BF16 || cols % 64 != 0 || cols == 0 || m == 0 || !aligned16(x) || !aligned16(packed) ||
+      !fits32(m * cols * 2) || !fits32(rows * cols / 8))
+    return 1;
   mfma::Params p{};
   p.a = static_cast<const uint16_t*>(x);
   p.bits = packed;
   p.out = y;
   p.M = m; p.N = rows; p.K = cols;
   p.lda = cols; p.pb = cols / 8;
+  p.a_rows = m; p.bit_rows = rows;
   p.n_scale = scale; p.n_bias = bias;
-  mfma::forward_kernel<<<grid_tiles(m, rows), mfma::THREADS, 0, stream>>>(p);
+  mfma::gemm_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD>
+      <<<grid_tiles(m, rows), mfma::THREADS, 0, stream>>>(p);
   return static_cast<int>(hipGetLastError());
 }
 
 int mfma_linear_dgrad(const void* dy, int dtype, const uint8_t* packed, const float* row_scale, void* dx,
                       int64_t m, int64_t rows, int64_t cols, hipStream_t stream) {
-  if (dtype != QSTE_BF16 || cols % 64 != 0 || rows % 64 != 0 || rows == 0 || cols == 0 || !aligned16(dy) ||
-      !aligned16(packed))
+  if (dtype != QSTE_BF16 || cols % 64 != 0 || rows % 64 != 0 || rows == 0 || cols == 0 || m == 0 ||
+      !aligned16(dy) || !aligned16(packed) || !fits32(m * rows * 2) || !fits32(rows * cols / 8))
     return 1;
   mfma::Params p{};
   p.a = static_cast<const uint16_t*>(dy);
@@ -483,7 +430,9 @@ int mfma_linear_dgrad(const void* dy, int dtype, const uint8_t* packed, const fl
   p.out = dx;
   p.M = m; p.N = cols; p.K = rows;
   p.lda = rows; p.pb = cols / 8;
-  mfma::dgrad_kernel<<<grid_tiles(m, cols), mfma::THREADS, 0, stream>>>(p);
+  p.a_rows = m; p.bit_rows = rows;
+  mfma::gemm_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_N, mfma::EPI_PLAIN>
+      <<<grid_tiles(m, cols), mfma::THREADS, 0, stream>>>(p);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -493,7 +442,7 @@ int mfma_evidence(const void* dy, int dtype, const uint8_t* packed_x, const floa
                   int64_t samples, int64_t rows, int64_t cols, const float* m_add, const float* m_scale,
                   const uint8_t* w_bits, float* gs_partial, hipStream_t stream) {
   if (dtype != QSTE_BF16 || cols % 64 != 0 || rows % 64 != 0 || rows == 0 || cols == 0 || samples == 0 ||
-      !aligned16(dy) || !aligned16(packed_x))
+      !aligned16(dy) || !aligned16(packed_x) || !fits32(samples * rows * 2) || !fits32(samples * cols / 8))
     return 1;
   mfma::Params p{};
   p.a = static_cast<const uint16_t*>(dy);
@@ -502,8 +451,10 @@ int mfma_evidence(const void* dy, int dtype, const uint8_t* packed_x, const floa
   p.out = ev;
   p.M = rows; p.N = cols; p.K = samples;
   p.lda = rows; p.pb = cols / 8;
+  p.a_rows = samples; p.bit_rows = samples;
   p.m_add = m_add; p.m_scale = m_scale; p.w_bits = w_bits; p.gs_partial = gs_partial;
-  mfma::evidence_kernel<<<grid_tiles(rows, cols), mfma::THREADS, 0, stream>>>(p);
+  mfma::gemm_kernel<mfma::A_ROWS_K, mfma::B_BITS_ALONG_N, mfma::EPI_EVIDENCE>
+      <<<grid_tiles(rows, cols), mfma::THREADS, 0, stream>>>(p);
   return static_cast<int>(hipGetLastError());
 }
 
