@@ -5,24 +5,29 @@
 // the new momentum -- so it runs as a short chain of passes over the fp32
 // evidence, none of which writes the evidence:
 //
-//   stats     row and column sums of g^2 + 1e-12         -> row_part, col_part
-//   cols      column EMA, fp16 col_v, column factor       (one thread/column)
-//   rows      row EMA, fp16 row_v, mean row statistic, row factor (1 group)
-//   usq       sum of U^2, U = g * rf * cf                 -> usq_part
-//   scalars   RMS clip divisor
-//   moment    m = q*S*b1 + (1-b1)*U/div per block: new fp16 scale, sum m^2
-//   scalars   coordinate step size lr / rms(m)
-//   final     stochastic rounding, momentum requantization, sign repack,
-//             flip count (one thread per packed byte)
-//   finish    new block scales into place, flip total
+//   stats    one workgroup per strip of rows: row sums of g^2 + 1e-12 (so
+//            the row EMA, fp16 row_v and the clamped row statistic are
+//            finished here), column partial sums per strip
+//   cols     column EMA, fp16 col_v, column factor; block 0 also finishes
+//            the mean row statistic
+//   usq      sum of U^2, U = g * rf * cf, per workgroup
+//   moment   (prologue: RMS clip divisor) m = q*S*b1 + (1-b1)*U/div for one
+//            momentum block per wave: new fp16 block scale, sum of m^2
+//   final    (prologue: step size lr / rms(m)) stochastic rounding, momentum
+//            requantization, sign repack and flip count, 8 columns (one
+//            packed byte) per thread
+//   finish   new block scales into place, flip total
 //
 // Float semantics follow the specification operation by operation: every
 // element-wise product and sum rounds in fp32 (this file is compiled with
 // -ffp-contract=off), torch's `add_(x, alpha=a)` is a fused multiply-add
 // (fmaf), divisions and square roots are correctly rounded.  Reductions
-// accumulate in double in a fixed order and round once, so the result does
-// not depend on launch geometry and equals the correctly rounded sum but in
+// accumulate in double in a fixed order and round once, so results do not
+// depend on launch geometry and equal the correctly rounded sums but in
 // vanishingly rare cases.
+//
+// Fast paths (vector loads) need cols % 8 == 0 and block_size >= 8; other
+// shapes take scalar code with the same arithmetic.
 #include "common.hpp"
 
 namespace qste {
@@ -30,10 +35,11 @@ namespace qste {
 namespace step {
 
 constexpr int kThreads = 256;
-constexpr int kChunkCols = 1024;  // columns per stats workgroup (4 per thread)
 constexpr int kStrip = 64;        // rows per stats workgroup
+constexpr int kColChunk = 1024;   // columns per stats workgroup (4 per thread)
 constexpr int kUsqGroups = 1024;
 constexpr int kMomentGroups = 1024;
+constexpr int kFinalGroups = 2048;
 
 struct Params {
   float b1, a1, b2, a2, clip, lr;
@@ -43,259 +49,475 @@ struct Params {
   int64_t step;
   const int64_t* step_device;
   const uint8_t* enabled;
+  bool vec;       // cols % 8 == 0 and block_size >= 8
+  bool small;     // rows * cols < 2^32: 32-bit index arithmetic
+  uint32_t bpr;   // momentum blocks per row when cols % block_size == 0, else 0
 };
 
+// Row and column of flat index i.
+__device__ __forceinline__ void row_col(int64_t i, const Params& p, int64_t& r, int64_t& c) {
+  if (p.small) {
+    const uint32_t ii = static_cast<uint32_t>(i), cc = static_cast<uint32_t>(p.cols);
+    const uint32_t rr = ii / cc;
+    r = rr;
+    c = ii - rr * cc;
+  } else {
+    r = i / p.cols;
+    c = i - r * p.cols;
+  }
+}
+
 struct Work {
-  double* row_part;   // [nchunks][rows]
-  double* col_part;   // [nstrips][cols]
-  float* new_row;     // [rows]
-  float* row_factor;  // [rows]
-  float* new_col;     // [cols]
-  float* col_factor;  // [cols]
-  double* usq_part;   // [kUsqGroups]
-  double* msq_part;   // [kMomentGroups * waves]
-  float* scalars;     // [0] divisor, [1] step size
-  uint16_t* s_new;    // [blocks]
-  int64_t* flips_part;// [final groups]
-  int64_t nchunks, nstrips, final_groups;
+  double* col_part;    // [nstrips][cols]
+  double* clamp_part;  // [nstrips * nchunks] partial sums of max(new_row, 1e-10)
+  double* row_part;    // [nchunks][rows]
+  float* new_row;      // [rows]
+  float* row_factor;   // [rows] (written by the usq pass)
+  float* new_col;      // [cols]
+  float* col_factor;   // [cols]
+  double* usq_part;    // [kUsqGroups]
+  double* msq_part;    // [kMomentGroups]
+  float* scalars;      // [0] sqrt(mean row stat), [1] divisor, [2] step size
+  uint16_t* s_new;     // [blocks]
+  int64_t* flips_part; // [kFinalGroups]
+  int64_t nstrips, nchunks;
 };
 
 __device__ __forceinline__ bool enabled(const Params& p) {
   return p.enabled == nullptr || *p.enabled != 0;
 }
 
-// -- stats -------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void stats_kernel(const float* __restrict__ g, Params p,
+__device__ __forceinline__ float square_eps(float v) {
+  float sq = v * v;
+  return sq + 1e-12f;
+}
+
+__device__ __forceinline__ float normalized(float g, float rf, float cf) {
+  float u = g * rf;
+  return u * cf;
+}
+
+__device__ __forceinline__ float row_factor_of(float sqrt_mean, float new_row) {
+  return sqrt_mean / sqrtf(fmaxf(new_row, 1e-10f));
+}
+
+// x / d, correctly rounded, for a divisor shared by many quotients: with
+// r = RN(1/d) and q0 = RN(x r) within one ulp of x/d, the residual
+// x - q0 d is exact under FMA and RN(q0 + r (x - q0 d)) is the correctly
+// rounded quotient (Markstein's correction step).  Three operations instead
+// of a full IEEE division per element.
+__device__ __forceinline__ float div_by(float x, float d, float r) {
+  const float q0 = x * r;
+  const float e = fmaf(-q0, d, x);
+  return fmaf(e, r, q0);
+}
+
+__device__ __forceinline__ float moment_of(float u2, float prev, float s_old, const Params& p) {
+  float decoded = prev * s_old;
+  decoded = decoded * p.b1;
+  return fmaf(u2, p.a1, decoded);
+}
+
+// -- stats: strip of rows x chunk of columns --------------------------------
+// Thread t owns columns c0 + 4t .. c0 + 4t + 3 of the chunk.  When the whole
+// row fits one chunk (cols <= 1024) the row sums complete here; otherwise
+// per-chunk row partials go to row_part and are combined in `cols`.
+__global__ __launch_bounds__(kThreads) void stats_kernel(const float* __restrict__ g,
+                                                         uint16_t* __restrict__ row_v, Params p,
                                                          Work w) {
   __shared__ double red[kStrip][kThreads / kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int64_t chunk = blockIdx.x;
   const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kStrip;
-  const int64_t c0 = chunk * kChunkCols + threadIdx.x * 4;
-  const float eps = 1e-12f;
-  double col_acc[4] = {0.0, 0.0, 0.0, 0.0};
+  const int64_t c0 = chunk * kColChunk + threadIdx.x * 4;
   const int rows_here = static_cast<int>(p.rows - r0 < kStrip ? p.rows - r0 : kStrip);
-  for (int rr = 0; rr < rows_here; ++rr) {
-    const float* line = g + (r0 + rr) * p.cols;
-    double rp = 0.0;
+  double col_acc[4] = {0.0, 0.0, 0.0, 0.0};
+  const bool full4 = p.vec && c0 + 4 <= p.cols;
+  for (int rr0 = 0; rr0 < rows_here; rr0 += 4) {
+    // four rows' loads in flight before any reduction
+    float4 v[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t c = c0 + j;
-      if (c < p.cols) {
-        const float v = line[c];
-        float sq = v * v;
-        sq = sq + eps;
-        col_acc[j] += static_cast<double>(sq);
-        rp += static_cast<double>(sq);
-      }
+    for (int u = 0; u < 4; ++u) {
+      v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (full4 && rr0 + u < rows_here) v[u] = *reinterpret_cast<const float4*>(g + (r0 + rr0 + u) * p.cols + c0);
     }
-    rp = wave_sum(rp);
-    if (lane == 0) red[rr][wave] = rp;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int rr = rr0 + u;
+      if (rr >= rows_here) break;
+      double rp = 0.0;
+      if (full4) {
+        const float s0 = square_eps(v[u].x), s1 = square_eps(v[u].y);
+        const float s2 = square_eps(v[u].z), s3 = square_eps(v[u].w);
+        col_acc[0] += s0; col_acc[1] += s1; col_acc[2] += s2; col_acc[3] += s3;
+        rp = (static_cast<double>(s0) + static_cast<double>(s1)) +
+             (static_cast<double>(s2) + static_cast<double>(s3));
+      } else {
+        const float* line = g + (r0 + rr) * p.cols;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (c0 + j < p.cols) {
+            const float sq = square_eps(line[c0 + j]);
+            col_acc[j] += static_cast<double>(sq);
+            rp += static_cast<double>(sq);
+          }
+        }
+      }
+      rp = wave_sum(rp);
+      if (lane == 0) red[rr][wave] = rp;
+    }
   }
   __syncthreads();
   if (threadIdx.x < rows_here) {
     double s = 0.0;
     for (int k = 0; k < kThreads / kWave; ++k) s += red[threadIdx.x][k];
-    w.row_part[chunk * p.rows + r0 + threadIdx.x] = s;
+    const int64_t r = r0 + threadIdx.x;
+    if (w.nchunks == 1) {
+      const float mean = static_cast<float>(s) / static_cast<float>(p.cols);
+      const float nr = fmaf(mean, p.a2, f16_to_f32(row_v[r]) * p.b2);
+      w.new_row[r] = nr;
+      if (enabled(p)) row_v[r] = f32_to_f16(nr);
+    } else {
+      w.row_part[chunk * p.rows + r] = s;
+    }
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t c = c0 + j;
-    if (c < p.cols) w.col_part[static_cast<int64_t>(blockIdx.y) * p.cols + c] = col_acc[j];
-  }
+  for (int j = 0; j < 4; ++j)
+    if (c0 + j < p.cols) w.col_part[static_cast<int64_t>(blockIdx.y) * p.cols + c0 + j] = col_acc[j];
 }
 
-// -- column and row statistics ----------------------------------------------
-__global__ void cols_kernel(uint16_t* __restrict__ col_v, Params p, Work w) {
-  const int64_t c = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-  if (c >= p.cols) return;
-  double s = 0.0;
-  for (int64_t k = 0; k < w.nstrips; ++k) s += w.col_part[k * p.cols + c];
-  const float mean = static_cast<float>(s) / static_cast<float>(p.rows);
-  const float decayed = f16_to_f32(col_v[c]) * p.b2;
-  const float nc = fmaf(mean, p.a2, decayed);
-  w.new_col[c] = nc;
-  w.col_factor[c] = 1.0f / sqrtf(fmaxf(nc, 1e-10f));
-  if (enabled(p)) col_v[c] = f32_to_f16(nc);
-}
-
-__global__ __launch_bounds__(1024) void rows_kernel(uint16_t* __restrict__ row_v, Params p, Work w) {
-  __shared__ double red[1024 / kWave];
-  double acc = 0.0;
-  const bool on = enabled(p);
-  for (int64_t r = threadIdx.x; r < p.rows; r += blockDim.x) {
-    double s = 0.0;
-    for (int64_t k = 0; k < w.nchunks; ++k) s += w.row_part[k * p.rows + r];
-    const float mean = static_cast<float>(s) / static_cast<float>(p.cols);
-    const float decayed = f16_to_f32(row_v[r]) * p.b2;
-    const float nr = fmaf(mean, p.a2, decayed);
-    w.new_row[r] = nr;
-    acc += static_cast<double>(fmaxf(nr, 1e-10f));
-    if (on) row_v[r] = f32_to_f16(nr);
-  }
-  acc = block_sum(acc, red);
-  const float sqrt_mean = sqrtf(static_cast<float>(acc) / static_cast<float>(p.rows));
-  for (int64_t r = threadIdx.x; r < p.rows; r += blockDim.x)
-    w.row_factor[r] = sqrt_mean / sqrtf(fmaxf(w.new_row[r], 1e-10f));
-}
-
-// -- update RMS ---------------------------------------------------------------
-__device__ __forceinline__ float normalized(float g, float rf, float cf) {
-  float u = g * rf;
-  u = u * cf;
-  return u;
-}
-
-__global__ __launch_bounds__(kThreads) void usq_kernel(const float* __restrict__ g, Params p,
-                                                       Work w) {
+// Rows whose sums were split over chunks; also the clamped row statistic.
+__global__ __launch_bounds__(kThreads) void rows_kernel(uint16_t* __restrict__ row_v, Params p, Work w) {
   __shared__ double red[kThreads / kWave];
   double acc = 0.0;
+  const bool on = enabled(p);
+  for (int64_t r = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; r < p.rows;
+       r += static_cast<int64_t>(gridDim.x) * kThreads) {
+    float nr;
+    if (w.nchunks > 1) {
+      double s = 0.0;
+      for (int64_t k = 0; k < w.nchunks; ++k) s += w.row_part[k * p.rows + r];
+      const float mean = static_cast<float>(s) / static_cast<float>(p.cols);
+      nr = fmaf(mean, p.a2, f16_to_f32(row_v[r]) * p.b2);
+      w.new_row[r] = nr;
+      if (on) row_v[r] = f32_to_f16(nr);
+    } else {
+      nr = w.new_row[r];
+    }
+    acc += static_cast<double>(fmaxf(nr, 1e-10f));
+  }
+  acc = block_sum(acc, red);
+  if (threadIdx.x == 0) w.clamp_part[blockIdx.x] = acc;
+}
+
+// -- column statistics; block 0 also finishes the mean row statistic --------
+// A workgroup owns 64 columns; its 4 waves sum interleaved subsets of the
+// strips and the 4 partials are combined in a fixed order.
+__global__ __launch_bounds__(kThreads) void cols_kernel(uint16_t* __restrict__ col_v, Params p, Work w,
+                                                        int64_t clamp_parts) {
+  __shared__ double part[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t c = blockIdx.x * 64ll + lane;
+  double s = 0.0;
+  if (c < p.cols)
+    for (int64_t k = wave; k < w.nstrips; k += 4) s += w.col_part[k * p.cols + c];
+  part[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && c < p.cols) {
+    const double t = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+    const float mean = static_cast<float>(t) / static_cast<float>(p.rows);
+    const float nc = fmaf(mean, p.a2, f16_to_f32(col_v[c]) * p.b2);
+    w.new_col[c] = nc;
+    w.col_factor[c] = 1.0f / sqrtf(fmaxf(nc, 1e-10f));
+    if (enabled(p)) col_v[c] = f32_to_f16(nc);
+  }
+  if (blockIdx.x == 0) {
+    __shared__ double red[kThreads / kWave];
+    double acc = 0.0;
+    for (int64_t i = threadIdx.x; i < clamp_parts; i += kThreads) acc += w.clamp_part[i];
+    acc = block_sum(acc, red);
+    if (threadIdx.x == 0) w.scalars[0] = sqrtf(static_cast<float>(acc) / static_cast<float>(p.rows));
+  }
+}
+
+// -- sum of U^2, one row at a time per workgroup -----------------------------
+__global__ __launch_bounds__(kThreads) void usq_kernel(const float* __restrict__ g, Params p, Work w) {
+  __shared__ double red[kThreads / kWave];
+  const float sqrt_mean = w.scalars[0];
+  double acc = 0.0;
   for (int64_t r = blockIdx.x; r < p.rows; r += gridDim.x) {
-    const float rf = w.row_factor[r];
+    const float rf = row_factor_of(sqrt_mean, w.new_row[r]);
+    if (threadIdx.x == 0) w.row_factor[r] = rf;
     const float* line = g + r * p.cols;
-    for (int64_t c = threadIdx.x; c < p.cols; c += kThreads) {
-      const float u = normalized(line[c], rf, w.col_factor[c]);
-      const float s = u * u;
-      acc += static_cast<double>(s);
+    if (p.vec) {
+      const float4* l4 = reinterpret_cast<const float4*>(line);
+      const float4* cf4 = reinterpret_cast<const float4*>(w.col_factor);
+      for (int64_t q = threadIdx.x; q < p.cols / 4; q += kThreads) {
+        const float4 v = l4[q], cf = cf4[q];
+        const float u0 = normalized(v.x, rf, cf.x), u1 = normalized(v.y, rf, cf.y);
+        const float u2 = normalized(v.z, rf, cf.z), u3 = normalized(v.w, rf, cf.w);
+        const float s0 = u0 * u0, s1 = u1 * u1, s2 = u2 * u2, s3 = u3 * u3;
+        acc += (static_cast<double>(s0) + static_cast<double>(s1)) +
+               (static_cast<double>(s2) + static_cast<double>(s3));
+      }
+    } else {
+      for (int64_t c = threadIdx.x; c < p.cols; c += kThreads) {
+        const float u = normalized(line[c], rf, w.col_factor[c]);
+        const float s = u * u;
+        acc += static_cast<double>(s);
+      }
     }
   }
   acc = block_sum(acc, red);
   if (threadIdx.x == 0) w.usq_part[blockIdx.x] = acc;
 }
 
-__global__ __launch_bounds__(kThreads) void divisor_kernel(Params p, Work w, int64_t parts) {
-  __shared__ double red[kThreads / kWave];
+__device__ __forceinline__ float divisor_of(const double* usq_part, int64_t parts, int64_t count,
+                                            float clip, double* red) {
   double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < parts; i += kThreads) acc += w.usq_part[i];
+  for (int64_t i = threadIdx.x; i < parts; i += kThreads) acc += usq_part[i];
   acc = block_sum(acc, red);
-  if (threadIdx.x == 0) {
-    float rms = sqrtf(static_cast<float>(acc) / static_cast<float>(p.count));
-    rms = fmaxf(rms, 1e-8f);
-    const float ratio = rms / p.clip;
-    w.scalars[0] = ratio > 1.0f ? ratio : 1.0f;
-  }
+  float rms = sqrtf(static_cast<float>(acc) / static_cast<float>(count));
+  rms = fmaxf(rms, 1e-8f);
+  const float ratio = rms / clip;
+  return ratio > 1.0f ? ratio : 1.0f;
 }
 
-// -- momentum -------------------------------------------------------------------
-__device__ __forceinline__ float moment_of(float g, float rf, float cf, float divisor, float prev,
-                                           float s_old, const Params& p) {
-  const float u = normalized(g, rf, cf) / divisor;
-  float decoded = prev * s_old;
-  decoded = decoded * p.b1;
-  return fmaf(u, p.a1, decoded);
-}
-
-// One wave per momentum block at a time; lanes stride the block's elements.
+// -- momentum: one wave per block at a time, 4 elements per lane ------------
 __global__ __launch_bounds__(kThreads) void moment_kernel(const float* __restrict__ g,
                                                           const int8_t* __restrict__ moment_q,
                                                           const uint16_t* __restrict__ moment_scale,
                                                           Params p, Work w) {
+  __shared__ double red[kThreads / kWave];
+  __shared__ double wsum[kThreads / kWave];
+  const float divisor = divisor_of(w.usq_part, kUsqGroups, p.count, p.clip, red);
+  if (blockIdx.x == 0 && threadIdx.x == 0) w.scalars[1] = divisor;
+  const float rdiv = 1.0f / divisor;
   const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
   const int64_t waves = static_cast<int64_t>(gridDim.x) * (kThreads / kWave);
-  const int64_t wave_id = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + threadIdx.x / kWave;
-  const float divisor = w.scalars[0];
+  const int64_t wave_id = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + wave;
   double msq = 0.0;
-  for (int64_t b = wave_id; b < p.blocks; b += waves) {
-    const float s_old = f16_to_f32(moment_scale[b]);
-    float amax = 0.0f;
-    for (int64_t j = lane; j < p.block_size; j += kWave) {
-      const int64_t i = b * p.block_size + j;
-      float m = 0.0f;
-      if (i < p.count) {
-        const int64_t r = i / p.cols;
-        const int64_t c = i - r * p.cols;
-        m = moment_of(g[i], w.row_factor[r], w.col_factor[c], divisor,
-                      static_cast<float>(moment_q[i]), s_old, p);
+  constexpr int G = 4;  // blocks per wave iteration: four independent loads per lane
+  for (int64_t g0 = wave_id * G; g0 < p.blocks; g0 += waves * G) {
+    float amax[G] = {0.f, 0.f, 0.f, 0.f};
+    for (int64_t j = 4 * lane; j < p.block_size; j += 4 * kWave) {
+      float4 v[G], cf[G];
+      uint32_t q4[G];
+      float rf[G];
+      bool fast[G];
+#pragma unroll
+      for (int k = 0; k < G; ++k) {
+        const int64_t b = g0 + k;
+        const int64_t i = b * p.block_size + j;
+        fast[k] = p.vec && b < p.blocks && i + 4 <= p.count;
+        if (fast[k]) {
+          int64_t r, c;
+          if (p.bpr) {
+            const uint32_t bb = static_cast<uint32_t>(b);
+            const uint32_t br = bb / p.bpr;
+            r = br;
+            c = static_cast<int64_t>(bb - br * p.bpr) * p.block_size + j;
+          } else {
+            row_col(i, p, r, c);
+          }
+          v[k] = *reinterpret_cast<const float4*>(g + i);
+          cf[k] = *reinterpret_cast<const float4*>(w.col_factor + c);
+          q4[k] = *reinterpret_cast<const uint32_t*>(moment_q + i);
+          rf[k] = w.row_factor[r];
+        }
       }
-      amax = fmaxf(amax, fabsf(m));
-      const float s = m * m;
-      msq += static_cast<double>(s);
+#pragma unroll
+      for (int k = 0; k < G; ++k) {
+        const int64_t b = g0 + k;
+        if (b >= p.blocks) break;
+        const float s_old = f16_to_f32(moment_scale[b]);
+        const int64_t i = b * p.block_size + j;
+        float m[4] = {0.f, 0.f, 0.f, 0.f};
+        if (fast[k]) {
+          const float gv[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+          const float cv[4] = {cf[k].x, cf[k].y, cf[k].z, cf[k].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float u2 = div_by(normalized(gv[e], rf[k], cv[e]), divisor, rdiv);
+            const float prev = static_cast<float>(static_cast<int8_t>(q4[k] >> (8 * e)));
+            m[e] = moment_of(u2, prev, s_old, p);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int64_t ie = i + e;
+            if (j + e < p.block_size && ie < p.count) {
+              int64_t r, c;
+              row_col(ie, p, r, c);
+              const float u2 = div_by(normalized(g[ie], w.row_factor[r], w.col_factor[c]), divisor, rdiv);
+              m[e] = moment_of(u2, static_cast<float>(moment_q[ie]), s_old, p);
+            }
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          amax[k] = fmaxf(amax[k], fabsf(m[e]));
+          const float sq = m[e] * m[e];
+          msq += static_cast<double>(sq);
+        }
+      }
     }
-    amax = wave_max(amax);
-    if (lane == 0) w.s_new[b] = f32_to_f16(fmaxf(amax, 1e-6f) / 127.0f);
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+      const int64_t b = g0 + k;
+      const float a = wave_max(amax[k]);
+      if (lane == 0 && b < p.blocks) w.s_new[b] = f32_to_f16(fmaxf(a, 1e-6f) / 127.0f);
+    }
   }
   msq = wave_sum(msq);
-  if (lane == 0) w.msq_part[wave_id] = msq;
-}
-
-__global__ __launch_bounds__(kThreads) void step_size_kernel(Params p, Work w, int64_t parts) {
-  __shared__ double red[kThreads / kWave];
-  double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < parts; i += kThreads) acc += w.msq_part[i];
-  acc = block_sum(acc, red);
+  __syncthreads();
+  if (lane == 0) wsum[wave] = msq;
+  __syncthreads();
   if (threadIdx.x == 0) {
-    const float padded = static_cast<float>(p.blocks * p.block_size);
-    float mrms = sqrtf(static_cast<float>(acc) / padded);
-    mrms = fmaxf(mrms, 1e-8f);
-    w.scalars[1] = p.lr / mrms;
+    double t = 0.0;
+    for (int k = 0; k < kThreads / kWave; ++k) t += wsum[k];
+    w.msq_part[blockIdx.x] = t;
   }
 }
 
-// -- final element pass -------------------------------------------------------
+// -- final element pass: one packed byte (8 columns) per thread ---------------
+__device__ __forceinline__ uint32_t final_byte(const float* __restrict__ g, int8_t* __restrict__ coord,
+                                               int8_t* __restrict__ moment_q,
+                                               const uint16_t* __restrict__ moment_scale, const Params& p,
+                                               const Work& w, int64_t r, int64_t b, float rf, float divisor,
+                                               float rdiv, float step_size, uint32_t combined, bool on) {
+  const int64_t c0 = b * 8;
+  const int64_t i0 = r * p.cols + c0;
+  const int n = static_cast<int>(p.cols - c0 < 8 ? p.cols - c0 : 8);
+  float gv[8], cv[8], prev[8], cur[8];
+  float s_old = 0.f, s_new = 0.f, rdec = 1.0f;
+  if (p.vec) {
+    const float4 ga = *reinterpret_cast<const float4*>(g + i0);
+    const float4 gb = *reinterpret_cast<const float4*>(g + i0 + 4);
+    const float4 ca = *reinterpret_cast<const float4*>(w.col_factor + c0);
+    const float4 cb = *reinterpret_cast<const float4*>(w.col_factor + c0 + 4);
+    const uint64_t q8 = *reinterpret_cast<const uint64_t*>(moment_q + i0);
+    const uint64_t c8 = *reinterpret_cast<const uint64_t*>(coord + i0);
+    gv[0] = ga.x; gv[1] = ga.y; gv[2] = ga.z; gv[3] = ga.w; gv[4] = gb.x; gv[5] = gb.y; gv[6] = gb.z; gv[7] = gb.w;
+    cv[0] = ca.x; cv[1] = ca.y; cv[2] = ca.z; cv[3] = ca.w; cv[4] = cb.x; cv[5] = cb.y; cv[6] = cb.z; cv[7] = cb.w;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      prev[j] = static_cast<float>(static_cast<int8_t>(q8 >> (8 * j)));
+      cur[j] = static_cast<float>(static_cast<int8_t>(c8 >> (8 * j)));
+    }
+    const int64_t blk = i0 >> p.block_shift;  // block_size >= 8: one block for the byte
+    s_old = f16_to_f32(moment_scale[blk]);
+    s_new = f16_to_f32(w.s_new[blk]);
+    rdec = 1.0f / fmaxf(s_new, 1e-12f);
+  } else {
+    for (int j = 0; j < 8; ++j) {
+      if (j < n) {
+        gv[j] = g[i0 + j];
+        cv[j] = w.col_factor[c0 + j];
+        prev[j] = static_cast<float>(moment_q[i0 + j]);
+        cur[j] = static_cast<float>(coord[i0 + j]);
+      } else {
+        gv[j] = cv[j] = prev[j] = cur[j] = 0.f;
+      }
+    }
+  }
+  uint32_t byte = 0;
+  uint64_t cnew8 = 0, qnew8 = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if (j >= n) continue;
+    const int64_t i = i0 + j;
+    float so = s_old, sn = s_new;
+    if (!p.vec) {
+      const int64_t blk = i >> p.block_shift;
+      so = f16_to_f32(moment_scale[blk]);
+      sn = f16_to_f32(w.s_new[blk]);
+    }
+    const float u2 = div_by(normalized(gv[j], rf, cv[j]), divisor, rdiv);
+    const float m = moment_of(u2, prev[j], so, p);
+    const float delta = m * step_size;
+    const float target = cur[j] - delta;
+    const float lower = floorf(target);
+    const float u = static_cast<float>(scramble(static_cast<uint32_t>(static_cast<uint64_t>(i)) ^ combined)) *
+                    (1.0f / 4294967296.0f);
+    const float frac = target - lower;
+    float rounded = lower + (u < frac ? 1.0f : 0.0f);
+    rounded = fminf(127.0f, fmaxf(-127.0f, rounded));
+    const float decode = fmaxf(sn, 1e-12f);
+    float q = rintf(div_by(m, decode, p.vec ? rdec : 1.0f / decode));
+    q = fminf(127.0f, fmaxf(-127.0f, q));
+    const int8_t cn = static_cast<int8_t>(rounded), qn = static_cast<int8_t>(q);
+    cnew8 |= static_cast<uint64_t>(static_cast<uint8_t>(cn)) << (8 * j);
+    qnew8 |= static_cast<uint64_t>(static_cast<uint8_t>(qn)) << (8 * j);
+    byte |= (rounded >= 0.0f ? 1u : 0u) << j;
+    if (on && !p.vec) {
+      coord[i] = cn;
+      moment_q[i] = qn;
+    }
+  }
+  if (on && p.vec) {
+    *reinterpret_cast<uint64_t*>(coord + i0) = cnew8;
+    *reinterpret_cast<uint64_t*>(moment_q + i0) = qnew8;
+  }
+  return byte;
+}
+
 __global__ __launch_bounds__(kThreads) void final_kernel(const float* __restrict__ g,
                                                          int8_t* __restrict__ coord,
                                                          uint8_t* __restrict__ packed,
                                                          int8_t* __restrict__ moment_q,
                                                          const uint16_t* __restrict__ moment_scale,
                                                          Params p, Work w) {
-  __shared__ int64_t red[kThreads / kWave];
-  const int64_t stride = (p.cols + 7) / 8;
-  const int64_t total = p.rows * stride;
-  const int64_t idx = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x;
-  const float divisor = w.scalars[0];
-  const float step_size = w.scalars[1];
+  __shared__ double red[kThreads / kWave];
+  __shared__ int64_t ired[kThreads / kWave];
+  // step size from the momentum RMS
+  double acc = 0.0;
+  for (int64_t i = threadIdx.x; i < kMomentGroups; i += kThreads) acc += w.msq_part[i];
+  acc = block_sum(acc, red);
+  const float padded = static_cast<float>(p.blocks * p.block_size);
+  float mrms = sqrtf(static_cast<float>(acc) / padded);
+  mrms = fmaxf(mrms, 1e-8f);
+  const float step_size = p.lr / mrms;
+  if (blockIdx.x == 0 && threadIdx.x == 0) w.scalars[2] = step_size;
+  const float divisor = w.scalars[1];
+  const float rdiv = 1.0f / divisor;
   const int64_t step = p.step_device ? *p.step_device : p.step;
   const uint32_t combined = p.seed_part ^ step_hash(step);
   const bool on = enabled(p);
+
+  const int64_t stride = (p.cols + 7) / 8;
+  const int64_t total = p.rows * stride;
   int64_t flips = 0;
-  if (idx < total) {
-    const int64_t r = idx / stride;
-    const int64_t b = idx - r * stride;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * kThreads) {
+    int64_t r, b;
+    if (p.small) {
+      const uint32_t ii = static_cast<uint32_t>(idx), ss = static_cast<uint32_t>(stride);
+      const uint32_t rr = ii / ss;
+      r = rr;
+      b = ii - rr * ss;
+    } else {
+      r = idx / stride;
+      b = idx - r * stride;
+    }
+    const float rf = w.row_factor[r];
+    const uint32_t old_byte = packed[idx];
+    const uint32_t byte = final_byte(g, coord, moment_q, moment_scale, p, w, r, b, rf, divisor, rdiv, step_size,
+                                     combined, on);
     const int64_t c0 = b * 8;
     const int n = static_cast<int>(p.cols - c0 < 8 ? p.cols - c0 : 8);
-    const float rf = w.row_factor[r];
-    uint32_t byte = 0;
-    int8_t cnew[8], qnew[8];
-    for (int j = 0; j < n; ++j) {
-      const int64_t c = c0 + j;
-      const int64_t i = r * p.cols + c;
-      const int64_t blk = i >> p.block_shift;
-      const float m = moment_of(g[i], rf, w.col_factor[c], divisor,
-                                static_cast<float>(moment_q[i]), f16_to_f32(moment_scale[blk]), p);
-      const float delta = m * step_size;
-      const float target = static_cast<float>(coord[i]) - delta;
-      const float lower = floorf(target);
-      const float u = static_cast<float>(scramble(static_cast<uint32_t>(static_cast<uint64_t>(i)) ^ combined)) *
-                      (1.0f / 4294967296.0f);
-      const float frac = target - lower;
-      float rounded = lower + (u < frac ? 1.0f : 0.0f);
-      rounded = fminf(127.0f, fmaxf(-127.0f, rounded));
-      cnew[j] = static_cast<int8_t>(rounded);
-      const float decode = fmaxf(f16_to_f32(w.s_new[blk]), 1e-12f);
-      float q = rintf(m / decode);
-      q = fminf(127.0f, fmaxf(-127.0f, q));
-      qnew[j] = static_cast<int8_t>(q);
-      byte |= (rounded >= 0.0f ? 1u : 0u) << j;
-    }
     const uint32_t mask = n >= 8 ? 0xFFu : ((1u << n) - 1u);
-    flips = __popc((static_cast<uint32_t>(packed[idx]) ^ byte) & mask);
-    if (on) {
-      for (int j = 0; j < n; ++j) {
-        const int64_t i = r * p.cols + c0 + j;
-        coord[i] = cnew[j];
-        moment_q[i] = qnew[j];
-      }
-      packed[idx] = static_cast<uint8_t>(byte);
-    }
+    flips += __popc((old_byte ^ byte) & mask);
+    if (on) packed[idx] = static_cast<uint8_t>(byte);
   }
-  flips = block_sum(flips, red);
+  flips = block_sum(flips, ired);
   if (threadIdx.x == 0) w.flips_part[blockIdx.x] = on ? flips : 0;
 }
 
 __global__ __launch_bounds__(kThreads) void finish_kernel(uint16_t* __restrict__ moment_scale,
-                                                          int64_t* __restrict__ flips_out, Params p,
-                                                          Work w) {
+                                                          int64_t* __restrict__ flips_out, Params p, Work w) {
   __shared__ int64_t red[kThreads / kWave];
   if (enabled(p)) {
     for (int64_t b = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; b < p.blocks;
@@ -304,43 +526,45 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(uint16_t* __restrict__
   }
   if (blockIdx.x == 0 && flips_out) {
     int64_t acc = 0;
-    for (int64_t i = threadIdx.x; i < w.final_groups; i += kThreads) acc += w.flips_part[i];
+    for (int64_t i = threadIdx.x; i < kFinalGroups; i += kThreads) acc += w.flips_part[i];
     acc = block_sum(acc, red);
     if (threadIdx.x == 0) *flips_out = acc;
   }
 }
 
 // -- plan ------------------------------------------------------------------------
+constexpr int kSegments = 12;
+constexpr int kRowsGroups = 64;
+
 struct Layout {
-  size_t off[11];
+  size_t off[kSegments];
   size_t total;
 };
 
 static size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 static Layout layout(int64_t rows, int64_t cols, int64_t block_size, Work* w) {
-  const int64_t nchunks = (cols + kChunkCols - 1) / kChunkCols;
+  const int64_t nchunks = (cols + kColChunk - 1) / kColChunk;
   const int64_t nstrips = (rows + kStrip - 1) / kStrip;
   const int64_t count = rows * cols;
   const int64_t blocks = (count + block_size - 1) / block_size;
-  const int64_t stride = (cols + 7) / 8;
-  const int64_t final_groups = (rows * stride + kThreads - 1) / kThreads;
-  const size_t sizes[11] = {
-      sizeof(double) * static_cast<size_t>(nchunks * rows),
+  const size_t sizes[kSegments] = {
       sizeof(double) * static_cast<size_t>(nstrips * cols),
+      sizeof(double) * kRowsGroups,
+      sizeof(double) * static_cast<size_t>(nchunks > 1 ? nchunks * rows : 1),
       sizeof(float) * static_cast<size_t>(rows),
       sizeof(float) * static_cast<size_t>(rows),
       sizeof(float) * static_cast<size_t>(cols),
       sizeof(float) * static_cast<size_t>(cols),
       sizeof(double) * kUsqGroups,
-      sizeof(double) * kMomentGroups * (kThreads / kWave),
+      sizeof(double) * kMomentGroups,
       sizeof(float) * 4,
       sizeof(uint16_t) * static_cast<size_t>(blocks),
-      sizeof(int64_t) * static_cast<size_t>(final_groups > 0 ? final_groups : 1),
+      sizeof(int64_t) * kFinalGroups,
   };
   Layout l{};
   size_t at = 0;
-  for (int i = 0; i < 11; ++i) {
+  for (int i = 0; i < kSegments; ++i) {
     l.off[i] = at;
     at += align_up(sizes[i]);
   }
@@ -348,7 +572,6 @@ static Layout layout(int64_t rows, int64_t cols, int64_t block_size, Work* w) {
   if (w) {
     w->nchunks = nchunks;
     w->nstrips = nstrips;
-    w->final_groups = final_groups;
   }
   return l;
 }
@@ -373,17 +596,18 @@ int launch_coordinate_update(const float* g, int8_t* coord, uint8_t* packed, int
   const Layout l = layout(rows, cols, block_size, &w);
   if (workspace_bytes < l.total || workspace == nullptr) return QSTE_E_WORKSPACE;
   char* base = static_cast<char*>(workspace);
-  w.row_part = reinterpret_cast<double*>(base + l.off[0]);
-  w.col_part = reinterpret_cast<double*>(base + l.off[1]);
-  w.new_row = reinterpret_cast<float*>(base + l.off[2]);
-  w.row_factor = reinterpret_cast<float*>(base + l.off[3]);
-  w.new_col = reinterpret_cast<float*>(base + l.off[4]);
-  w.col_factor = reinterpret_cast<float*>(base + l.off[5]);
-  w.usq_part = reinterpret_cast<double*>(base + l.off[6]);
-  w.msq_part = reinterpret_cast<double*>(base + l.off[7]);
-  w.scalars = reinterpret_cast<float*>(base + l.off[8]);
-  w.s_new = reinterpret_cast<uint16_t*>(base + l.off[9]);
-  w.flips_part = reinterpret_cast<int64_t*>(base + l.off[10]);
+  w.col_part = reinterpret_cast<double*>(base + l.off[0]);
+  w.clamp_part = reinterpret_cast<double*>(base + l.off[1]);
+  w.row_part = reinterpret_cast<double*>(base + l.off[2]);
+  w.new_row = reinterpret_cast<float*>(base + l.off[3]);
+  w.row_factor = reinterpret_cast<float*>(base + l.off[4]);
+  w.new_col = reinterpret_cast<float*>(base + l.off[5]);
+  w.col_factor = reinterpret_cast<float*>(base + l.off[6]);
+  w.usq_part = reinterpret_cast<double*>(base + l.off[7]);
+  w.msq_part = reinterpret_cast<double*>(base + l.off[8]);
+  w.scalars = reinterpret_cast<float*>(base + l.off[9]);
+  w.s_new = reinterpret_cast<uint16_t*>(base + l.off[10]);
+  w.flips_part = reinterpret_cast<int64_t*>(base + l.off[11]);
 
   Params p{};
   p.b1 = static_cast<float>(beta1);
@@ -404,25 +628,24 @@ int launch_coordinate_update(const float* g, int8_t* coord, uint8_t* packed, int
   p.step = step_;
   p.step_device = step_device;
   p.enabled = update_enabled;
+  p.vec = (cols % 8 == 0) && block_size >= 8 && (reinterpret_cast<uintptr_t>(g) & 15) == 0 &&
+          (reinterpret_cast<uintptr_t>(coord) & 7) == 0 && (reinterpret_cast<uintptr_t>(moment_q) & 7) == 0;
+  p.small = p.count < (int64_t{1} << 32) && p.blocks * p.block_size < (int64_t{1} << 32);
+  p.bpr = (p.small && cols % block_size == 0) ? static_cast<uint32_t>(cols / block_size) : 0u;
 
   int rc;
   stats_kernel<<<dim3(static_cast<unsigned>(w.nchunks), static_cast<unsigned>(w.nstrips)), kThreads, 0,
-                 stream>>>(g, p, w);
+                 stream>>>(g, row_v, p, w);
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
-  cols_kernel<<<ceil_div(cols, 256), 256, 0, stream>>>(col_v, p, w);
+  rows_kernel<<<kRowsGroups, kThreads, 0, stream>>>(row_v, p, w);
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
-  rows_kernel<<<1, 1024, 0, stream>>>(row_v, p, w);
+  cols_kernel<<<ceil_div(cols, 64), kThreads, 0, stream>>>(col_v, p, w, kRowsGroups);
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
   usq_kernel<<<kUsqGroups, kThreads, 0, stream>>>(g, p, w);
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
-  divisor_kernel<<<1, kThreads, 0, stream>>>(p, w, kUsqGroups);
-  if ((rc = static_cast<int>(hipGetLastError()))) return rc;
   moment_kernel<<<kMomentGroups, kThreads, 0, stream>>>(g, moment_q, moment_scale, p, w);
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
-  step_size_kernel<<<1, kThreads, 0, stream>>>(p, w, kMomentGroups * (kThreads / kWave));
-  if ((rc = static_cast<int>(hipGetLastError()))) return rc;
-  final_kernel<<<static_cast<unsigned>(w.final_groups), kThreads, 0, stream>>>(
-      g, coord, packed, moment_q, moment_scale, p, w);
+  final_kernel<<<kFinalGroups, kThreads, 0, stream>>>(g, coord, packed, moment_q, moment_scale, p, w);
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
   finish_kernel<<<ceil_div(p.blocks, kThreads) < 1024 ? ceil_div(p.blocks, kThreads) : 1024, kThreads, 0,
                   stream>>>(moment_scale, flips_out, p, w);
