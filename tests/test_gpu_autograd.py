@@ -1,0 +1,182 @@
+"""The user API end to end on the GPU: QSTELinear forward/backward, the
+coordinate step inside backward, PackedLinear decode, and size-independent
+properties of the step at the config-4 surface shape.
+
+Float outputs: relative L2 against the float64 oracle (bf16 outputs against
+the oracle rounded to bf16, a folded scale rounded to bf16 first) -- 1e-3 for
+bf16, 1e-5 for fp32. Integer state: bit-exact against the oracle's step run on
+the evidence the GPU produced.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    yield
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    n = np.linalg.norm(b)
+    return float(np.linalg.norm(a - b) / (n if n > 0 else 1.0))
+
+
+def bf(a):
+    return torch.from_numpy(np.asarray(a, np.float32)).to(torch.bfloat16).float().numpy()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,cols,m", [(384, 256, 200), (1024, 512, 64), (96, 130, 33)])
+def test_qste_linear_forward_backward(dtype, rows, cols, m):
+    import qste_amd as qste
+
+    torch.manual_seed(rows + cols)
+    lin = nn.Linear(cols, rows)
+    layer = qste.QSTELinear.from_linear(lin).to(DEV)
+    x = torch.randn(m, cols, device=DEV).to(dtype).requires_grad_(True)
+    dy = torch.randn(m, rows, device=DEV).to(dtype)
+    y = layer(x)
+    y.backward(dy)
+    packed = layer.surface.packed_sign.cpu().numpy()
+    s = layer.scale.detach().float().cpu().numpy()
+    xb = x.detach().float().cpu().numpy()
+    dyb = dy.float().cpu().numpy()
+    want_y = oracle.linear_fwd(xb, packed, s, layer.bias.detach().cpu().numpy(), cols)
+    tol = 1e-5 if dtype == torch.float32 else 1e-3
+    rnd = (lambda a: a) if dtype == torch.float32 else bf
+    assert rel_l2(y.detach().float().cpu().numpy(), rnd(want_y)) <= tol
+    s_op = s if dtype == torch.float32 else bf(s)
+    want_dx = oracle.linear_dgrad(dyb, packed, cols, s_op)
+    assert rel_l2(x.grad.float().cpu().numpy(), rnd(want_dx)) <= tol
+    bits, off, xs = oracle.pack_affine_rows(xb)
+    xs_op = xs if dtype == torch.float32 else bf(xs)
+    e0 = oracle.evidence(dyb, bits, cols, xs_op) + oracle.offset_correction(dyb, off)[:, None]
+    gs = oracle.row_inner(e0.astype(np.float32), packed, cols)
+    assert rel_l2(layer.surface.log_scale.grad.cpu().numpy(), gs * s) <= 1e-4
+    assert rel_l2(layer.bias.grad.cpu().numpy(), dyb.astype(np.float64).sum(0)) <= 1e-5
+
+
+def test_immediate_step_equals_oracle_on_the_gpu_evidence(monkeypatch):
+    """The step that runs inside backward, checked exactly."""
+
+    import qste_amd as qste
+    from qste_amd import kernels
+
+    torch.manual_seed(0)
+    model = nn.Sequential(nn.Linear(256, 512), nn.ReLU(), nn.Linear(512, 128)).to(DEV)
+    qste.convert(model, include=["0", "2"], config={"seed": 3})
+    coords = qste.QSTEOptimizer(model)
+    real = kernels.coordinate_update
+    seen = []
+
+    def spy(gradient, coordinate, packed, moment_q, moment_scale, row_v, col_v, **kw):
+        seen.append((gradient.detach().float().cpu().numpy().copy(),
+                     {"coordinate": coordinate.cpu().numpy().copy(), "packed": packed.cpu().numpy().copy(),
+                      "moment_q": moment_q.cpu().numpy().copy(), "moment_scale": moment_scale.cpu().numpy().copy(),
+                      "row_v": row_v.cpu().numpy().copy(), "col_v": col_v.cpu().numpy().copy()},
+                     dict(kw), (coordinate, packed, moment_q, moment_scale, row_v, col_v)))
+        return real(gradient, coordinate, packed, moment_q, moment_scale, row_v, col_v, **kw)
+
+    monkeypatch.setattr(kernels, "coordinate_update", spy)
+    for it in range(2):
+        x = torch.randn(128, 256, device=DEV, dtype=torch.bfloat16)
+        model(x).float().square().mean().backward()
+        coords.step()
+    assert len(seen) == 4
+    for ev, state, kw, after in seen:
+        kw = {k: v for k, v in kw.items() if k not in ("flips", "update_enabled")}
+        oracle.coordinate_update(ev, state, **kw)
+    # the last step of each surface: GPU state now equals the oracle's
+    for ev, state, kw, after in seen[2:]:
+        names = ("coordinate", "packed", "moment_q", "moment_scale", "row_v", "col_v")
+        for name, t in zip(names, after):
+            assert np.array_equal(t.cpu().numpy().view(np.uint8), state[name].view(np.uint8)), name
+
+
+def test_training_step_is_reproducible():
+    import qste_amd as qste
+
+    results = []
+    for _ in range(2):
+        torch.manual_seed(11)
+        model = nn.Sequential(nn.Linear(128, 256), nn.GELU(), nn.Linear(256, 128)).to(DEV)
+        qste.convert(model, include=["0", "2"])
+        opt = torch.optim.AdamW(qste.continuous_parameters(model), lr=1e-3)
+        coords = qste.QSTEOptimizer(model)
+        g = torch.Generator(device=DEV).manual_seed(5)
+        for _ in range(3):
+            x = torch.randn(64, 128, device=DEV, generator=g)
+            loss = model(x).square().mean()
+            loss.backward()
+            opt.step(); coords.step()
+            opt.zero_grad(); coords.zero_grad()
+        results.append([s.coordinate.detach().cpu().clone() for s in qste.surfaces(model)])
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_packed_linear_decode(M):
+    import qste_amd as qste
+
+    K, N = 2048, 3072
+    g = torch.Generator(device=DEV).manual_seed(M)
+    packed = torch.randint(0, 256, (N, K // 8), generator=g, device=DEV, dtype=torch.int32).to(torch.uint8)
+    scale = torch.rand(N, generator=g, device=DEV) * 0.02 + 0.001
+    bias = torch.randn(N, generator=g, device=DEV) * 0.1
+    layer = qste.PackedLinear(packed, scale, K, bias)
+    x = torch.randn(M, K, generator=g, device=DEV).to(torch.bfloat16)
+    y = layer(x)
+    assert y.dtype == torch.bfloat16
+    want = oracle.linear_fwd(x.float().cpu().numpy(), packed.cpu().numpy(), scale.cpu().numpy(),
+                             bias.cpu().numpy(), K)
+    assert rel_l2(y.float().cpu().numpy(), bf(want)) <= 1e-3
+
+
+def test_full_size_step_properties():
+    """Config-4 gate surface (14336 x 4096): integer invariants and reproducibility."""
+
+    from qste_amd import kernels
+
+    R, C = 14336, 4096
+    g = torch.Generator(device=DEV).manual_seed(2)
+    ev = torch.randn(R, C, generator=g, device=DEV) * 0.01
+    coord0 = torch.randint(-127, 128, (R, C), generator=g, device=DEV, dtype=torch.int32).to(torch.int8)
+    outs = []
+    for _ in range(2):
+        coord = coord0.clone()
+        packed = kernels.pack_coordinate(coord)
+        before = packed.clone()
+        blocks = (R * C + 255) // 256
+        mq = torch.zeros_like(coord)
+        ms = torch.full((blocks,), 1 / 127, dtype=torch.float16, device=DEV)
+        rv = torch.zeros(R, dtype=torch.float16, device=DEV)
+        cv = torch.zeros(C, dtype=torch.float16, device=DEV)
+        flips = kernels.coordinate_update(ev, coord, packed, mq, ms, rv, cv, beta1=0.9, beta2=0.99,
+                                          update_clip=2.0, coordinate_lr=1.0, block_size=256, seed=1, step=0)
+        assert torch.equal(packed, kernels.pack_coordinate(coord))
+        assert int(coord.abs().max()) <= 127 and int(mq.int().abs().max()) <= 127
+        diff = torch.bitwise_xor(before, packed)
+        pop = sum(int(((diff >> k) & 1).sum()) for k in range(8))
+        assert flips == pop
+        moved = (coord.int() - coord0.int()).abs()
+        assert int(moved.max()) <= 3
+        outs.append((coord.cpu(), mq.cpu(), ms.cpu(), rv.cpu(), cv.cpu(), flips))
+    for a, b in zip(outs[0][:5], outs[1][:5]):
+        assert torch.equal(a.view(torch.uint8) if a.dtype == torch.float16 else a,
+                           b.view(torch.uint8) if b.dtype == torch.float16 else b)
+    assert outs[0][5] == outs[1][5]

@@ -1,0 +1,338 @@
+"""Host-side logic and the C ABI, without a GPU.
+
+* The HIP library loads and exports every entry point `include/qste_hip.h`
+  declares; argument errors come back as codes without touching a device.
+* The user API (`convert`, `Surface`, `QSTELinearFn`, `QSTEOptimizer`,
+  `PackedLinear`, `export_packed`) is driven on CPU through a fake operator
+  layer built from the oracle -- test-only: the product's operator layer has no
+  CPU path -- to check the orchestration the reference defines: layer
+  selection and tying (`convert.py:159-243`), surface initialization
+  (`surface.py:41-62`), the backward composition (`functional.py:173-194`),
+  immediate evidence application with seed `cfg.seed + 1_000_003 * position`
+  and the pre-increment step number (`optim.py:156-201`), scale clamping and
+  state_dict round trips (`optim.py:212-232`).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+import oracle
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+# ---------------------------------------------------------------------------
+# the C ABI
+# ---------------------------------------------------------------------------
+
+
+def _declared():
+    text = (ROOT / "include" / "qste_hip.h").read_text()
+    return sorted(set(re.findall(r"\b(qste_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from qste_amd.kernels import _lib
+
+    lib = _lib.load()
+    names = _declared()
+    assert len(names) >= 12
+    for name in names:
+        assert hasattr(lib, name), name
+    # and the binding's signature table covers them all
+    assert set(names) == set(_lib.SIGNATURES)
+
+
+def test_error_codes_and_workspace_queries_need_no_gpu():
+    from qste_amd.kernels import _lib
+
+    lib = _lib.load()
+    assert lib.qste_version() >= 1
+    for code, word in ((-1, b"dtype"), (-2, b"shape"), (-3, b"NULL"), (-4, b"workspace"), (-5, b"power of two")):
+        assert word in lib.qste_error_string(code)
+    assert lib.qste_coordinate_update_workspace_bytes(4096, 14336, 256) > 0
+    assert lib.qste_coordinate_update_workspace_bytes(0, 8, 256) == 0
+    assert lib.qste_linear_backward_workspace_bytes(16384, 14336, 4096) > 0
+    # argument errors are reported before any device work
+    assert lib.qste_packed_linear_affine(None, 7, None, None, None, None, 1, 1, 8, None) == -1
+    assert lib.qste_packed_transpose(None, 2, None, None, None, -1, 4, 8, None) == -2
+    assert lib.qste_pack_affine_rows(None, 0, None, None, None, 4, 0, None) == -2
+    assert lib.qste_coordinate_update(None, None, None, None, None, None, None, 4, 8, 0.9, 0.99, 2.0, 1.0,
+                                      48, 1, 0, None, None, None, None, 0, None) == -5
+    assert lib.qste_coordinate_update(None, None, None, None, None, None, None, 4, 8, 0.9, 0.99, 2.0, 1.0,
+                                      64, 1, 0, None, None, None, None, 0, None) == -3
+
+
+def test_operator_layer_refuses_cpu_tensors():
+    from qste_amd import kernels
+
+    with pytest.raises(RuntimeError, match="GPU"):
+        kernels.pack_coordinate(torch.zeros(2, 8, dtype=torch.int8))
+    with pytest.raises(RuntimeError, match="GPU"):
+        kernels.packed_linear_affine(torch.zeros(2, 8), torch.zeros(3, 1, dtype=torch.uint8),
+                                     torch.ones(3), None, 8)
+
+
+# ---------------------------------------------------------------------------
+# fake operator layer on the oracle (test-only)
+# ---------------------------------------------------------------------------
+
+
+class OracleKernels:
+    """qste_amd.kernels' operators, computed by the oracle on CPU tensors."""
+
+    def __init__(self):
+        self.calls = []
+
+    def pack_coordinate(self, coord):
+        return torch.from_numpy(oracle.pack_coordinate(coord.numpy()))
+
+    def unpack_rows(self, packed, columns, *, dtype=None, row_scale=None):
+        out = torch.from_numpy(oracle.unpack_rows(packed.numpy(), columns))
+        if row_scale is not None:
+            out = out * row_scale.float()[:, None]
+        return out.to(dtype or torch.float32)
+
+    def pack_affine_rows(self, values):
+        b, o, s = oracle.pack_affine_rows(values.float().numpy())
+        return torch.from_numpy(b), torch.from_numpy(o), torch.from_numpy(s)
+
+    def packed_linear_affine(self, inputs, packed, scale, bias, columns):
+        y = oracle.linear_fwd(inputs.float().numpy(), packed.numpy(), scale.detach().float().numpy(),
+                              None if bias is None else bias.detach().float().numpy(), columns)
+        return torch.from_numpy(y).float().to(inputs.dtype).view(*inputs.shape[:-1], packed.shape[0])
+
+    def packed_row_inner(self, matrix, packed, columns):
+        return torch.from_numpy(oracle.row_inner(matrix.float().numpy(), packed.numpy(), columns)).float()
+
+    def linear_backward(self, grad, packed_x, x_offset, x_scale, packed_w, scale, columns, *, need_bias):
+        g = grad.float().numpy()
+        s = scale.detach().float().numpy()
+        dx = oracle.linear_dgrad(g, packed_w.numpy(), columns, s)
+        e0 = oracle.decoded_evidence(g, packed_x.numpy(), x_offset.numpy(), x_scale.numpy(), columns)
+        gs = oracle.row_inner(e0.astype(np.float32), packed_w.numpy(), columns)
+        ev = (e0 * s[:, None]).astype(np.float32)
+        db = torch.from_numpy(g.astype(np.float64).sum(0)).float() if need_bias else None
+        return (torch.from_numpy(dx).float().to(grad.dtype), torch.from_numpy(ev),
+                torch.from_numpy(gs).float(), db)
+
+    def coordinate_update(self, gradient, coordinate, packed, moment_q, moment_scale, row_v, col_v, *,
+                          beta1, beta2, update_clip, coordinate_lr, block_size, seed, step, flips=None,
+                          update_enabled=None):
+        self.calls.append({"seed": seed, "step": int(step), "evidence": gradient.clone()})
+        state = {"coordinate": coordinate.numpy(), "packed": packed.numpy(), "moment_q": moment_q.numpy(),
+                 "moment_scale": moment_scale.numpy(), "row_v": row_v.numpy(), "col_v": col_v.numpy()}
+        n = oracle.coordinate_update(gradient.float().numpy(), state, beta1=beta1, beta2=beta2,
+                                     update_clip=update_clip, coordinate_lr=coordinate_lr,
+                                     block_size=block_size, seed=seed, step=int(step))
+        if flips is not None:
+            flips.fill_(n)
+            return flips
+        return n
+
+
+@pytest.fixture
+def fake(monkeypatch):
+    import qste_amd
+    from qste_amd import kernels, surface
+
+    ok = OracleKernels()
+    for name in ("pack_coordinate", "unpack_rows", "pack_affine_rows", "packed_linear_affine",
+                 "packed_row_inner", "linear_backward", "coordinate_update"):
+        monkeypatch.setattr(kernels, name, getattr(ok, name))
+    monkeypatch.setattr(surface, "_on_gpu", lambda fn, t, *a, **k: fn(t, *a, **k))
+    return ok
+
+
+# ---------------------------------------------------------------------------
+# convert / Surface
+# ---------------------------------------------------------------------------
+
+
+class Block(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.fc1 = nn.Linear(16, 32)
+        self.act = nn.ReLU()
+        self.fc2 = nn.Linear(32, 16, bias=False)
+        self.emb = nn.Embedding(10, 16)
+
+
+def test_convert_selects_by_glob_and_records_config(fake):
+    import qste_amd as qste
+
+    torch.manual_seed(0)
+    model = Block()
+    qste.convert(model, include=["fc*"], exclude=["fc2"], config={"seed": 7})
+    assert isinstance(model.fc1, qste.QSTELinear) and isinstance(model.fc2, nn.Linear)
+    assert model._qste_config.seed == 7
+    assert model.fc1.in_features == 16 and model.fc1.out_features == 32
+    assert model.fc1.bias.dtype == torch.float32
+    with pytest.raises(ValueError):
+        qste.convert(Block(), include=["nothing*"])
+    with pytest.raises(NotImplementedError):
+        qste.convert(Block(), include=["emb"])
+    with pytest.raises(ValueError):
+        qste.convert(Block(), include=["fc1"], activations="sometimes")
+
+
+def test_tied_weights_share_one_surface(fake):
+    import qste_amd as qste
+
+    a, b = nn.Linear(8, 8), nn.Linear(8, 8)
+    b.weight = a.weight
+    model = nn.Sequential(a, b)
+    qste.convert(model)
+    assert model[0].surface is model[1].surface
+    assert len(qste.surfaces(model)) == 1
+
+
+def test_surface_initialization_formula(fake):
+    """surface.py:41-62, recomputed in float64 numpy."""
+
+    import qste_amd as qste
+
+    torch.manual_seed(1)
+    w = torch.randn(24, 40) * 0.05
+    w[3, 5] = 0.0
+    s = qste.Surface(w)
+    wd = w.double().numpy()
+    scale = np.maximum(np.abs(wd).mean(1), 1e-5)
+    latent = np.clip(wd / scale[:, None], -1.5, 1.5) * 0.25
+    q = np.clip(np.round(latent / 1.5 * 127), -127, 127)
+    q = np.where(q == 0, np.where(wd >= 0, 1, -1), q)
+    assert np.array_equal(s.coordinate.numpy(), q.astype(np.int8))
+    assert np.array_equal(s.packed_sign.numpy(), oracle.pack_coordinate(q.astype(np.int8)))
+    np.testing.assert_allclose(s.log_scale.detach().numpy(), np.log(scale), rtol=1e-6)
+    assert s.coordinate.requires_grad is False and s.log_scale.requires_grad is True
+    torch.testing.assert_close(s.scale, s.log_scale.exp().clamp(1e-6, 4.0))
+
+
+# ---------------------------------------------------------------------------
+# autograd composition and the optimizer
+# ---------------------------------------------------------------------------
+
+
+def _mlp(seed=0):
+    torch.manual_seed(seed)
+    return nn.Sequential(nn.Linear(24, 40), nn.ReLU(), nn.Linear(40, 16))
+
+
+def test_forward_backward_composition(fake):
+    import qste_amd as qste
+
+    model = _mlp()
+    qste.convert(model, include=["0", "2"])
+    layer = model[0]
+    x = torch.randn(7, 24)
+    y = layer(x)
+    packed = layer.surface.packed_sign.numpy()
+    want = oracle.linear_fwd(x.numpy(), packed, layer.scale.detach().numpy(), layer.bias.detach().numpy(), 24)
+    np.testing.assert_allclose(y.detach().numpy(), want, rtol=1e-6, atol=1e-6)
+    xg = x.clone().requires_grad_(True)
+    dy = torch.randn(7, 40)
+    layer(xg).backward(dy)
+    s = layer.scale.detach().numpy()
+    np.testing.assert_allclose(xg.grad.numpy(), oracle.linear_dgrad(dy.numpy(), packed, 24, s),
+                               rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(layer.bias.grad.numpy(), dy.numpy().sum(0), rtol=1e-5, atol=1e-6)
+    # log_scale gradient = row inner product of E0 with the signs, times
+    # d scale / d log_scale = scale (clamp inactive)
+    bits, off, xs = oracle.pack_affine_rows(x.numpy())
+    e0 = oracle.decoded_evidence(dy.numpy(), bits, off, xs, 24)
+    gs = oracle.row_inner(e0.astype(np.float32), packed, 24)
+    np.testing.assert_allclose(layer.surface.log_scale.grad.numpy(), gs * s, rtol=1e-4, atol=1e-6)
+
+
+def test_optimizer_applies_inside_backward_with_reference_seeds(fake):
+    import qste_amd as qste
+
+    model = _mlp(3)
+    qste.convert(model, include=["0", "2"], config={"seed": 5})
+    coords = qste.QSTEOptimizer(model)
+    assert coords.step_number == 0
+    surfaces = qste.surfaces(model)
+    before = [s.coordinate.clone() for s in surfaces]
+    x = torch.randn(9, 24)
+    model(x).square().mean().backward()
+    # both surfaces stepped during backward, before step() is called
+    assert len(fake.calls) == 2
+    seeds = sorted(c["seed"] for c in fake.calls)
+    assert seeds == [5, 5 + 1_000_003]
+    assert all(c["step"] == 0 for c in fake.calls)
+    flips = coords.step()
+    assert coords.step_number == 1
+    moved = sum(int((s.coordinate != b).sum()) for s, b in zip(surfaces, before))
+    assert moved > 0
+    assert flips == sum(int(np.unpackbits((oracle.pack_coordinate(b.numpy()) ^ s.packed_sign.numpy()),
+                                          axis=1, bitorder="little")[:, :s.columns].sum())
+                        for s, b in zip(surfaces, before))
+    model(x).square().mean().backward()
+    assert [c["step"] for c in fake.calls[2:]] == [1, 1]
+
+
+def test_optimizer_flush_clamp_and_state_dict(fake):
+    import qste_amd as qste
+
+    model = _mlp(4)
+    qste.convert(model, include=["0"])
+    coords = qste.QSTEOptimizer(model)
+    s = qste.surfaces(model)[0]
+    with torch.no_grad():
+        s.log_scale[0] = 10.0
+        s.log_scale[1] = -50.0
+    # a forward with no backward leaves a pending count; step() still clamps
+    model(torch.randn(3, 24))
+    coords.step()
+    assert math.isclose(float(s.log_scale.detach()[0]), math.log(4.0), rel_tol=1e-6)
+    assert math.isclose(float(s.log_scale.detach()[1]), math.log(1e-6), rel_tol=1e-6)
+    # deferred evidence is applied by step() with the step number of that call
+    coords.defer(True)
+    model(torch.randn(5, 24)).sum().backward()
+    assert fake.calls == []
+    coords.step()
+    assert [c["step"] for c in fake.calls] == [1]
+    state = coords.state_dict()
+    other = qste.QSTEOptimizer(model)
+    other.load_state_dict(state)
+    assert other.step_number == coords.step_number
+    for k, v in coords.state[id(s)].items():
+        assert torch.equal(other.state[id(s)][k], v)
+    assert coords.state_bytes() > 0
+
+
+def test_export_packed_gives_the_same_forward(fake):
+    import qste_amd as qste
+
+    model = _mlp(6)
+    qste.convert(model, include=["0", "2"])
+    x = torch.randn(4, 24)
+    with torch.no_grad():
+        want = model(x)
+    exported = qste.export_packed(model)
+    assert isinstance(exported[0], qste.PackedLinear)
+    with torch.no_grad():
+        torch.testing.assert_close(exported(x), want)
+    report = qste.memory_report(model)
+    assert report["training_ratio"] > 1 and report["inference_ratio"] > report["training_ratio"]
+
+
+def test_multirank_group_requires_an_explicit_reducer(monkeypatch, fake):
+    import qste_amd as qste
+
+    model = _mlp(7)
+    qste.convert(model, include=["0"])
+    monkeypatch.setattr(torch.distributed, "is_initialized", lambda: True)
+    monkeypatch.setattr(torch.distributed, "get_world_size", lambda: 2)
+    with pytest.raises(RuntimeError, match="gradient_reducer"):
+        qste.QSTEOptimizer(model)
+    assert qste.QSTEOptimizer(model, gradient_reducer=False).gradient_reducer is None
