@@ -458,9 +458,4 @@ int mfma_evidence(const void* dy, int dtype, const uint8_t* packed_x, const floa
   return static_cast<int>(hipGetLastError());
 }
 
-int gemv_linear_forward(const void*, int, const uint8_t*, const float*, const float*, void*, int64_t,
-                        int64_t, int64_t, hipStream_t) {
-  return 1;
-}
-
 }  // namespace qste

@@ -173,8 +173,9 @@ def test_full_size_step_properties():
         diff = torch.bitwise_xor(before, packed)
         pop = sum(int(((diff >> k) & 1).sum()) for k in range(8))
         assert flips == pop
-        moved = (coord.int() - coord0.int()).abs()
-        assert int(moved.max()) <= 3
+        # a coordinate moves by about |m| / rms(m): mean |z| of a normal is 0.8
+        moved = (coord.int() - coord0.int()).abs().float()
+        assert 0.3 < float(moved.mean()) < 1.5
         outs.append((coord.cpu(), mq.cpu(), ms.cpu(), rv.cpu(), cv.cpu(), flips))
     for a, b in zip(outs[0][:5], outs[1][:5]):
         assert torch.equal(a.view(torch.uint8) if a.dtype == torch.float16 else a,
