@@ -132,12 +132,13 @@ __device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
 
 // Workgroup -> output tile.  Consecutive workgroup ids land on different
 // XCDs (round-robin), so ids are first regrouped so each XCD gets a
-// contiguous range, then walked in column-major groups of 8 M-tiles so
-// workgroups that run together share operand tiles in their XCD's L2.
+// contiguous range, then walked in column-major groups of 2 M-tiles, so the
+// workgroups that run together on one XCD share two dense-operand row blocks
+// (the large operand) and many small bit tiles in that XCD's L2.
 __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int total = tiles_m * tiles_n;
   if (total % 8 == 0) pid = (pid % 8) * (total / 8) + pid / 8;
-  constexpr int G = 8;
+  constexpr int G = 2;
   const int per_group = G * tiles_n;
   const int group = pid / per_group;
   const int first_m = group * G;
@@ -384,6 +385,235 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_kernel(Params p) {
   }
 }
 
+
+// ===========================================================================
+// Wide tiles for the forward product: 256 x 256 outputs per workgroup of 4
+// waves (2 x 2, each 128 x 128 = 4 x 4 blocks of 32 x 32 held in AGPRs), one
+// workgroup per CU.  Operands reach LDS by direct buffer->LDS loads (no
+// register staging) into four stages, issued three K steps ahead; the
+// workgroup synchronises once per K step, three quarters into it, after
+// which the next stage's first fragments are read while the step's last
+// MFMAs run.  Output rows leave through LDS as 16-byte stores.
+// ===========================================================================
+namespace wide {
+constexpr int BM = 256, BN = 256, BK = 64, THREADS = 256;
+constexpr int A_STAGE = BM * BK * 2;  // bytes: 256 rows x 128 B, 16-byte chunks XOR-swizzled
+constexpr int B_STAGE = BN * BK / 8;  // bytes: 256 rows x 8 B of sign bits
+constexpr int EPL = 272;              // bytes per staged output row (256 + pad)
+constexpr int LOADS_PER_STEP = 10;    // buffer->LDS loads per wave per K step
+typedef __attribute__((address_space(3))) void lds_t;
+
+// Chunk c of A row r is stored at chunk c ^ swz(r): the 16 rows that one
+// ds_read_b128 quarter-wave touches then cover all 64 banks once.
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
+// Wait until at most N vector-memory operations of this wave are in flight
+// (the buffer->LDS loads retire in order), then barrier the workgroup.
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  compiler_fence();
+  // s_waitcnt fields: vmcnt [3:0] and [15:14], expcnt [6:4] (7: none), lgkmcnt [11:8] (0)
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (((N >> 4) & 3) << 14) | 0x70);
+  __builtin_amdgcn_s_barrier();
+  compiler_fence();
+}
+
+__global__ __launch_bounds__(THREADS, 1) void forward_kernel(Params p) {
+  // one array per stage: the compiler then tracks each stage's direct loads
+  // separately and waits only where this code says
+  __shared__ __attribute__((aligned(16))) uint8_t A0[A_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t A1[A_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t A2[A_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t A3[A_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t B0[B_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t B1[B_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t B2[B_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t B3[B_STAGE];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, kg = lane >> 5;
+  const int tiles_m = static_cast<int>((p.M + BM - 1) / BM);
+  const int tiles_n = static_cast<int>((p.N + BN - 1) / BN);
+  int tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
+  const uint32_t one = bf16_one_pair();
+  const int nk = static_cast<int>(p.K / BK);
+
+  // A (x rows, K contiguous): the buffer starts at row m0, so rows past M
+  // read zero.  Wave w fills rows 64w .. 64w+63 with 8 loads of 8 rows;
+  // lane -> row 8j + lane/8 and LDS chunk lane%8, which holds global chunk
+  // (lane%8) ^ swz(row); swz depends on j only through its parity.
+  const __amdgpu_buffer_rsrc_t ra = rsrc(p.a + m0 * p.lda, (p.a_rows - m0) * p.lda * 2);
+  const int q8 = lane >> 3, pos = lane & 7;
+  uint32_t a_voff[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par)
+    a_voff[par] = static_cast<uint32_t>((64 * wave + q8) * p.lda * 2 + 16 * (pos ^ (4 * par + (q8 >> 1))));
+  const uint32_t a_row8 = static_cast<uint32_t>(8 * p.lda * 2);
+  // B (sign bits along K): 256 rows x 8 bytes per stage; wave w fills rows
+  // 64w .. 64w+63 with 2 loads of 4 bytes per lane.
+  const __amdgpu_buffer_rsrc_t rb = rsrc(p.bits + n0 * p.pb, (p.bit_rows - n0) * p.pb);
+  const uint32_t b_voff = static_cast<uint32_t>((64 * wave + (lane >> 1)) * p.pb + 4 * (lane & 1));
+  const uint32_t b_row32 = static_cast<uint32_t>(32 * p.pb);
+
+  // Steps past the end are issued too, at an offset past every buffer's
+  // end: they read zero without touching memory and keep the number of
+  // loads in flight the same on every step.
+  auto issue = [&](int it, uint8_t* As, uint8_t* Bs) {
+    const bool live = it < nk;
+    const uint32_t k_off = live ? static_cast<uint32_t>(it) * (BK * 2) : 0x80000000u;
+    const uint32_t kb = live ? static_cast<uint32_t>(it) * (BK / 8) : 0x80000000u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_t*)(As + (64 * wave + 8 * j) * 128), 16, a_voff[j & 1],
+                                               static_cast<int>(j * a_row8 + k_off), 0, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_t*)(Bs + (64 * wave + 32 * j) * 8), 4, b_voff,
+                                               static_cast<int>(j * b_row32 + kb), 0, 0);
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  // fragments: a[buf][mb] rows of x, b[buf][nb] expanded signs; substep s
+  // (k = 16s .. 16s+15 of the step) uses buffer s & 1
+  bf16x8 a[2][4], b[2][4];
+  uint64_t bits[4];
+  auto load_a = [&](const uint8_t* As, int s, bf16x8* dst) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int row = 128 * wm + 32 * mb + l32;
+      dst[mb] = *reinterpret_cast<const bf16x8*>(As + row * 128 + 16 * ((2 * s + kg) ^ swz(row)));
+    }
+  };
+  auto load_bits = [&](const uint8_t* Bs) {
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+      bits[nb] = ~*reinterpret_cast<const uint64_t*>(Bs + 8 * (128 * wn + 32 * nb + l32));
+  };
+  auto expand_b = [&](int s, bf16x8* dst) {
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+      dst[nb] = signs_along_k(static_cast<uint32_t>(bits[nb] >> (8 * (2 * s + kg))) & 0xFFu, one);
+  };
+  auto mfmas = [&](int s) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = mma(a[s & 1][mb], b[s & 1][nb], acc[mb][nb]);
+  };
+
+  // K step `it` on stage As (its bits already in `bits`, substep 0's
+  // fragments in buffer 0).  After substep 2 every wave has finished step
+  // it-1, so step it+3 may overwrite that step's stage (N3a, N3b); waiting
+  // for all but the newest step's loads makes step it+1's stage (N1a, N1b)
+  // complete, and its first fragments are read during substep 3.
+  auto step = [&](int it, const uint8_t* As, const uint8_t* N1a, const uint8_t* N1b, uint8_t* N3a,
+                  uint8_t* N3b) {
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+      load_a(As, s + 1, a[(s + 1) & 1]);
+      mfmas(s);
+      expand_b(s + 1, b[(s + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    stage_barrier<LOADS_PER_STEP>();
+    issue(it + 3, N3a, N3b);
+    load_a(N1a, 0, a[0]);
+    load_bits(N1b);
+    mfmas(3);
+    expand_b(0, b[0]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  issue(0, A0, B0);
+  issue(1, A1, B1);
+  issue(2, A2, B2);
+  stage_barrier<2 * LOADS_PER_STEP>();
+  load_a(A0, 0, a[0]);
+  load_bits(B0);
+  expand_b(0, b[0]);
+  int it = 0;
+  for (; it + 4 <= nk; it += 4) {
+    step(it, A0, A1, B1, A3, B3);
+    step(it + 1, A1, A2, B2, A0, B0);
+    step(it + 2, A2, A3, B3, A1, B1);
+    step(it + 3, A3, A0, B0, A2, B2);
+  }
+  if (it < nk) step(it, A0, A1, B1, A3, B3);
+  if (it + 1 < nk) step(it + 1, A1, A2, B2, A0, B0);
+  if (it + 2 < nk) step(it + 2, A2, A3, B3, A1, B1);
+
+  // Epilogue: scale and bias, round to bf16, stage through LDS one quarter
+  // (32 of the wave's 128 rows) at a time so each row segment of 128
+  // outputs leaves as 16 lanes x 16 contiguous bytes.  Waves 0, 1 stage in
+  // A0 and waves 2, 3 in A1, after every in-flight load has landed.
+  stage_barrier<0>();
+  uint16_t* y = static_cast<uint16_t*>(p.out);
+  uint8_t* stg = (wave < 2 ? A0 : A1) + (wave & 1) * (32 * EPL);
+  float sc[4], bi[4];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    const int64_t col = n0 + 128 * wn + 32 * nb + l32;
+    sc[nb] = (col < p.N && p.n_scale) ? p.n_scale[col] : 1.0f;
+    bi[nb] = (col < p.N && p.n_bias) ? p.n_bias[col] : 0.0f;
+  }
+  // Lanes l, l^1 trade one value per row pair so each holds two adjacent
+  // columns of one row: even lanes row r, odd lanes row r+1.
+  const bool odd = l32 & 1;
+  const bool vec_ok = (p.N & 7) == 0;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        float v0 = acc[mb][nb][r] * sc[nb];
+        v0 = v0 + bi[nb];
+        float v1 = acc[mb][nb][r + 1] * sc[nb];
+        v1 = v1 + bi[nb];
+        const float send = odd ? v0 : v1;
+        const float recv = __int_as_float(
+            __builtin_amdgcn_update_dpp(0, __float_as_int(send), 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
+        const float lo = odd ? recv : v0;
+        const float hi = odd ? v1 : recv;
+        const uint32_t word =
+            static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+        const int row = 8 * (r >> 2) + 4 * kg + (r & 3) + (odd ? 1 : 0);
+        *reinterpret_cast<uint32_t*>(stg + row * EPL + 2 * (32 * nb + (l32 & ~1))) = word;
+      }
+    }
+    // 32 rows x 256 bytes: lane -> row 4i + lane/16, 16-byte chunk lane%16
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = 4 * i + (lane >> 4), chunk = lane & 15;
+      const uint4 v = *reinterpret_cast<const uint4*>(stg + row * EPL + 16 * chunk);
+      const int64_t grow = m0 + 128 * wm + 32 * mb + row;
+      const int64_t gcol = n0 + 128 * wn + 8 * chunk;
+      if (grow < p.M) {
+        if (vec_ok && gcol + 8 <= p.N) {
+          *reinterpret_cast<uint4*>(y + grow * p.N + gcol) = v;
+        } else {
+          const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+#pragma unroll
+          for (int t = 0; t < 8; ++t)
+            if (gcol + t < p.N) y[grow * p.N + gcol + t] = e[t];
+        }
+      }
+    }
+  }
+}
+}  // namespace wide
 }  // namespace mfma
 
 // ---------------------------------------------------------------------------
@@ -413,8 +643,9 @@ int mfma_linear_forward(const void* x, int dtype, const uint8_t* packed, const f
   p.lda = cols; p.pb = cols / 8;
   p.a_rows = m; p.bit_rows = rows;
   p.n_scale = scale; p.n_bias = bias;
-  mfma::gemm_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD>
-      <<<grid_tiles(m, rows), mfma::THREADS, 0, stream>>>(p);
+  const int grid = static_cast<int>(((m + mfma::wide::BM - 1) / mfma::wide::BM) *
+                                    ((rows + mfma::wide::BN - 1) / mfma::wide::BN));
+  mfma::wide::forward_kernel<<<grid, mfma::wide::THREADS, 0, stream>>>(p);
   return static_cast<int>(hipGetLastError());
 }
 
