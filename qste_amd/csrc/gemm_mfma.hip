@@ -9,17 +9,14 @@
 //   forward   y  = x  [M=T, K=C] . sign_w^T          -> * scale[n] + bias[n]
 //             bits run along K (row n of W): a lane's 8 k-values are one byte
 //   dgrad     dx = dy [M=T, K=R] . (s (*) sign_w)    bits run along N
-//   evidence  E  = dy^T [M=R, K=T] . (xs (*) sign_x) bits run along N,
-//             dy^T is transposed in registers on its way into LDS; fused
-//             epilogue + v[m], row partials of E0 . sign_w, * scale[m]
+//   evidence  E  = dy^T [M=R, K=T] . (xs (*) sign_x) bits run along N, dy
+//             is read as stored ([K][M]) and transposed by the LDS read;
+//             fused epilogue + v[m], row partials of E0 . sign_w, * scale[m]
 //
-// Tile: 256 x 128 per workgroup of 4 waves (2 x 2), each wave 128 x 64 as
-// 4 x 2 blocks of 32 x 32, K step 64 (4 MFMA k-steps of 16).  The dense
-// operand (A) goes through double-buffered LDS with one barrier per K step;
-// the next step's global loads (buffer loads, whose out-of-range reads
-// return zero and so pad ragged edges for free) are issued before the
-// current step's MFMAs.  Where bits run along N they are staged through LDS
-// as a small transposed byte tile, inverted so a set bit means "negative".
+// One kernel template serves all three (wide_kernel below): 256 x 256
+// outputs per workgroup of 4 waves, one workgroup per CU, the dense operand
+// brought into LDS by direct buffer->LDS loads over four stages, and buffer
+// loads' zero fill for every ragged edge.
 //
 // MFMA 32x32x16 bf16 operand layout used here: lane l holds A[l%32][8(l/32)
 // + i] and B[8(l/32) + i][l%32], i = 0..7; the accumulator's register r
@@ -34,11 +31,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 256, BN = 128, BK = 64, THREADS = 256;
-constexpr int LDA = BK + 8;                 // bf16 per LDS row of A (144 B)
-constexpr int LDB = BK + 8;                 // bytes per LDS row of staged bits ([n/8][k])
-constexpr int A_TILE = BM * LDA;            // bf16 elements per A buffer
-constexpr int B_TILE = (BN / 8) * LDB;      // bytes per staged-bits buffer
 constexpr uint32_t kRsrcWord3 = 0x00020000u;
 
 enum { A_ROWS_M = 0, A_ROWS_K = 1 };        // A[m][k] stored with k (or m) contiguous
@@ -69,12 +61,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(n), kRsrcWord3);
 }
 
-__device__ __forceinline__ uint4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0));
-}
-__device__ __forceinline__ uint64_t ld64(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(off), 0, 0));
-}
 __device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0);
 }
@@ -116,16 +102,6 @@ __device__ __forceinline__ bf16x8 signs_across_k(uint64_t neg8, int bit, uint4 s
   return __builtin_bit_cast(bf16x8, r);
 }
 
-// Workgroup barrier for LDS hand-off only.  __syncthreads() carries a
-// workgroup memory fence, which makes the compiler wait for every
-// outstanding global load (vmcnt(0)) at each barrier and so cancels the
-// prefetch; here only this wave's LDS operations are drained (lgkmcnt(0))
-// before the barrier, and in-flight global loads stay in flight.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt: no wait, expcnt: no wait, lgkmcnt(0)
-  __builtin_amdgcn_s_barrier();
-}
-
 __device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
@@ -148,259 +124,20 @@ __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& 
   tn = in_group / gm;
 }
 
-// Index of this 16-byte chunk of a transposed (A_ROWS_K) A row in LDS: XOR
-// swizzled by (row / 8) so the transposed stores do not collide on banks.
-__device__ __forceinline__ int a_chunk(int akind, int chunk, int row) {
-  return akind == A_ROWS_K ? (chunk ^ ((row >> 3) & 7)) : chunk;
-}
-
-template <int AKIND, int BKIND, int EPI>
-__global__ __launch_bounds__(THREADS, 2) void gemm_kernel(Params p) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2 * A_TILE];
-  __shared__ __attribute__((aligned(16))) uint8_t Bs[BKIND == B_BITS_ALONG_N ? 2 * B_TILE : 16];
-  __shared__ __attribute__((aligned(16))) uint16_t Ss[BKIND == B_BITS_ALONG_N ? 2 * BK : 8];
-
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int l32 = lane & 31, kg = lane >> 5;
-  const int tiles_m = static_cast<int>((p.M + BM - 1) / BM);
-  const int tiles_n = static_cast<int>((p.N + BN - 1) / BN);
-  int tm, tn;
-  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
-  const uint32_t one = bf16_one_pair();
-  const int nk = static_cast<int>((p.K + BK - 1) / BK);
-
-  f32x16 acc[4][2];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-
-  // ---- A source --------------------------------------------------------
-  // A_ROWS_M: thread loads rows (arow + 32 i), 16-byte chunk achunk.
-  // A_ROWS_K: thread loads an 8 x 8 block: k rows 8kb..8kb+7, m cols 8rb..
-  const int arow = tid >> 3, achunk = tid & 7;
-  const int rb = tid & 31, kb = tid >> 5;
-  __amdgpu_buffer_rsrc_t ra;
-  uint32_t aoff;
-  if (AKIND == A_ROWS_M) {
-    // buffer starts at the tile's first row: rows past M read as zero
-    const int64_t rows_left = p.a_rows - m0;
-    ra = rsrc(p.a + m0 * p.lda, rows_left * p.lda * 2);
-    aoff = static_cast<uint32_t>((arow * p.lda + achunk * 8) * 2);
-  } else {
-    // buffer starts at column m0: k rows past K read as zero
-    ra = rsrc(p.a + m0, (p.a_rows * p.lda - m0) * 2);
-    aoff = static_cast<uint32_t>(((8 * kb) * p.lda + 8 * rb) * 2);
-  }
-  const uint32_t a_step = AKIND == A_ROWS_M ? BK * 2 : static_cast<uint32_t>(BK * p.lda * 2);
-  const uint32_t a_stride = AKIND == A_ROWS_M ? static_cast<uint32_t>(32 * p.lda * 2)
-                                              : static_cast<uint32_t>(p.lda * 2);
-  uint4 areg[8];
-  auto load_a = [&](int it) {
-    const uint32_t base = aoff + static_cast<uint32_t>(it) * a_step;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) areg[i] = ld128(ra, base + i * a_stride);
-  };
-  auto store_a = [&](uint16_t* buf) {
-    if (AKIND == A_ROWS_M) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4*>(&buf[(arow + 32 * i) * LDA + achunk * 8]) = areg[i];
-    } else {
-      const uint32_t* in = reinterpret_cast<const uint32_t*>(areg);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-        uint4 o;
-        o.x = __builtin_amdgcn_perm(in[4 + (j >> 1)], in[0 + (j >> 1)], sel);
-        o.y = __builtin_amdgcn_perm(in[12 + (j >> 1)], in[8 + (j >> 1)], sel);
-        o.z = __builtin_amdgcn_perm(in[20 + (j >> 1)], in[16 + (j >> 1)], sel);
-        o.w = __builtin_amdgcn_perm(in[28 + (j >> 1)], in[24 + (j >> 1)], sel);
-        const int row = 8 * rb + j;
-        *reinterpret_cast<uint4*>(&buf[row * LDA + a_chunk(A_ROWS_K, kb, row) * 8]) = o;
-      }
-    }
-  };
-
-  // ---- B source ----------------------------------------------------------
-  __amdgpu_buffer_rsrc_t rb_bits = rsrc(p.bits, p.bit_rows * p.pb);
-  __amdgpu_buffer_rsrc_t rb_scale = rsrc(p.kscale, p.kscale ? p.K * 4 : 0);
-  uint64_t breg[2] = {0, 0};   // B_BITS_ALONG_K: this lane's 64 k-bits of its two columns
-  uint32_t bword = 0;          // B_BITS_ALONG_N: one staged dword of bits
-  float bscale = 0.0f;
-  uint32_t boff[2];
-  if (BKIND == B_BITS_ALONG_K) {
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int64_t n = n0 + 64 * wn + 32 * nb + l32;
-      boff[nb] = static_cast<uint32_t>(n * p.pb);  // rows past N read as zero
-    }
-  } else {
-    boff[0] = static_cast<uint32_t>((tid >> 2) * p.pb + n0 / 8 + (tid & 3) * 4);
-    boff[1] = 0;
-  }
-  auto load_b = [&](int it) {
-    const int64_t k0 = static_cast<int64_t>(it) * BK;
-    if (BKIND == B_BITS_ALONG_K) {
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) breg[nb] = ld64(rb_bits, boff[nb] + static_cast<uint32_t>(k0 / 8));
-    } else {
-      bword = ld32(rb_bits, boff[0] + static_cast<uint32_t>(k0 * p.pb));
-      if (tid < BK) bscale = p.kscale ? __uint_as_float(ld32(rb_scale, static_cast<uint32_t>((k0 + tid) * 4)))
-                                      : (k0 + tid < p.K ? 1.0f : 0.0f);
-    }
-  };
-  auto store_b = [&](int buf) {
-    if (BKIND == B_BITS_ALONG_N) {
-      uint8_t* bs = Bs + buf * B_TILE;
-      const int k = tid >> 2, col = (tid & 3) * 4;
-      const uint32_t neg = ~bword;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) bs[(col + i) * LDB + k] = static_cast<uint8_t>(neg >> (8 * i));
-      if (tid < BK) Ss[buf * BK + tid] = f32_to_bf16(bscale);
-    }
-  };
-
-  // ---- main loop ---------------------------------------------------------
-  load_a(0);
-  load_b(0);
-  store_a(As);
-  store_b(0);
-  uint64_t bcur[2] = {~breg[0], ~breg[1]};
-  lds_barrier();
-
-  for (int it = 0; it < nk; ++it) {
-    const int cur = it & 1;
-    const bool more = it + 1 < nk;
-    if (more) {
-      load_a(it + 1);
-      load_b(it + 1);
-    }
-    const uint16_t* a_buf = As + cur * A_TILE;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      bf16x8 b0, b1;
-      if (BKIND == B_BITS_ALONG_K) {
-        const int sh = 8 * (2 * s + kg);
-        b0 = signs_along_k(static_cast<uint32_t>(bcur[0] >> sh) & 0xFFu, one);
-        b1 = signs_along_k(static_cast<uint32_t>(bcur[1] >> sh) & 0xFFu, one);
-      } else {
-        const uint8_t* bs = Bs + cur * B_TILE;
-        const int kk = 16 * s + 8 * kg;
-        const uint4 sc = *reinterpret_cast<const uint4*>(&Ss[cur * BK + kk]);
-        const int c0 = 64 * wn + l32, c1 = c0 + 32;
-        b0 = signs_across_k(*reinterpret_cast<const uint64_t*>(&bs[(c0 >> 3) * LDB + kk]), c0 & 7, sc);
-        b1 = signs_across_k(*reinterpret_cast<const uint64_t*>(&bs[(c1 >> 3) * LDB + kk]), c1 & 7, sc);
-      }
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const int row = 128 * wm + 32 * mb + l32;
-        const bf16x8 a =
-            *reinterpret_cast<const bf16x8*>(&a_buf[row * LDA + a_chunk(AKIND, 2 * s + kg, row) * 8]);
-        acc[mb][0] = mma(a, b0, acc[mb][0]);
-        acc[mb][1] = mma(a, b1, acc[mb][1]);
-      }
-    }
-    if (more) {
-      store_a(As + (cur ^ 1) * A_TILE);
-      store_b(cur ^ 1);
-      if (BKIND == B_BITS_ALONG_K) {
-        bcur[0] = ~breg[0];
-        bcur[1] = ~breg[1];
-      }
-    }
-    lds_barrier();
-  }
-
-  // ---- epilogue ------------------------------------------------------------
-  if (EPI == EPI_FORWARD || EPI == EPI_PLAIN) {
-    uint16_t* y = static_cast<uint16_t*>(p.out);
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int64_t col = n0 + 64 * wn + 32 * nb + l32;
-      if (col >= p.N) continue;
-      const float sc = (EPI == EPI_FORWARD && p.n_scale) ? p.n_scale[col] : 1.0f;
-      const float bi = (EPI == EPI_FORWARD && p.n_bias) ? p.n_bias[col] : 0.0f;
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int64_t row = m0 + 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
-          if (row < p.M) {
-            float v = acc[mb][nb][r];
-            if (EPI == EPI_FORWARD) {
-              v = v * sc;
-              v = v + bi;
-            }
-            y[row * p.N + col] = f32_to_bf16(v);
-          }
-        }
-      }
-    }
-  } else {
-    // E0 = acc + v[m]; row partials of E0 * sign_w; E = E0 * s[m]
-    float* ev = static_cast<float*>(p.out);
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      float part[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        part[r] = 0.0f;
-        const int64_t row = m0 + 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
-        if (row >= p.M) continue;
-        const float add = p.m_add ? p.m_add[row] : 0.0f;
-        const float mul = p.m_scale ? p.m_scale[row] : 1.0f;
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          const int64_t col = n0 + 64 * wn + 32 * nb + l32;
-          if (col >= p.N) continue;
-          const float e0 = acc[mb][nb][r] + add;
-          if (p.w_bits) {
-            const uint32_t byte = p.w_bits[row * p.pb + (col >> 3)];
-            part[r] += ((byte >> (col & 7)) & 1u) ? e0 : -e0;
-          }
-          ev[row * p.N + col] = e0 * mul;
-        }
-      }
-      if (p.gs_partial) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float v = part[r];
-#pragma unroll
-          for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-          part[r] = v;
-        }
-        if (l32 == 0) {
-          const int64_t slot = 2 * static_cast<int64_t>(tn) + wn;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int64_t row = m0 + 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
-            if (row < p.M) p.gs_partial[slot * p.M + row] = part[r];
-          }
-        }
-      }
-    }
-  }
-}
-
-
 // ===========================================================================
-// Wide tiles for the forward product: 256 x 256 outputs per workgroup of 4
-// waves (2 x 2, each 128 x 128 = 4 x 4 blocks of 32 x 32 held in AGPRs), one
-// workgroup per CU.  Operands reach LDS by direct buffer->LDS loads (no
-// register staging) into four stages, issued three K steps ahead; the
-// workgroup synchronises once per K step, three quarters into it, after
-// which the next stage's first fragments are read while the step's last
-// MFMAs run.  Output rows leave through LDS as 16-byte stores.
+// 256 x 256 outputs per workgroup of 4 waves (2 x 2, each 128 x 128 = 4 x 4
+// blocks of 32 x 32 held in AGPRs), one workgroup per CU.  The dense operand
+// reaches LDS by direct buffer->LDS loads (no register staging) into four
+// stages, issued three K steps ahead; the workgroup synchronises once per K
+// step, three quarters into it, after which the next stage's first
+// fragments are read while the step's last MFMAs run.  bf16 outputs leave
+// through LDS as 16-byte row segments.
 // ===========================================================================
 namespace wide {
 constexpr int BM = 256, BN = 256, BK = 64, THREADS = 256;
 constexpr int A_STAGE = BM * BK * 2;  // bytes: 256 rows x 128 B, 16-byte chunks XOR-swizzled
 constexpr int B_STAGE = BN * BK / 8;  // bytes: 256 rows x 8 B of sign bits
 constexpr int EPL = 272;              // bytes per staged output row (256 + pad)
-constexpr int LOADS_PER_STEP = 10;    // buffer->LDS loads per wave per K step
 typedef __attribute__((address_space(3))) void lds_t;
 
 // Chunk c of A row r is stored at chunk c ^ swz(r): the 16 rows that one
@@ -421,17 +158,45 @@ __device__ __forceinline__ void stage_barrier() {
   compiler_fence();
 }
 
-__global__ __launch_bounds__(THREADS, 1) void forward_kernel(Params p) {
+// Bits along N (dgrad, evidence) are staged transposed, [n/8][k] with a
+// pitch of LDB_N bytes, inverted so a set bit means "negative", and the per-k
+// scale as bf16 beside them: the transposition needs registers, so those
+// loads go through VGPRs one step before their stage is written.
+constexpr int LDB_N = BK + 8;
+constexpr int BN_STAGE = (BN / 8) * LDB_N;  // bytes
+template <int BKIND>
+struct Loads {
+  // buffer loads per wave per K step: 8 A loads, plus the bit loads
+  static constexpr int value = BKIND == B_BITS_ALONG_K ? 10 : 11;
+};
+
+// A given as rows of K (evidence: A = dy^T, dy stored [K][M]) is staged
+// [k][m] with two k-rows interleaved per 16-byte chunk (one direct load
+// covers a row pair) and row pairs APK bytes apart; fragments are read with
+// ds_read_b64_tr_b16, which hands lane 4a+b of each 16-lane group element b
+// of the 8-byte reads of lanes a, a+4, a+8, a+12.
+constexpr int APK = 1152;                    // bytes per staged k-row pair (1024 + pad)
+constexpr int A_STAGE_K = (BK / 2) * APK;    // bytes
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+template <int AKIND, int BKIND, int EPI>
+__global__ __launch_bounds__(THREADS, 1) void wide_kernel(Params p) {
+  constexpr int NL = Loads<BKIND>::value;
+  constexpr int BSZ = BKIND == B_BITS_ALONG_K ? B_STAGE : BN_STAGE;
+  constexpr int ASZ = AKIND == A_ROWS_M ? A_STAGE : A_STAGE_K;
   // one array per stage: the compiler then tracks each stage's direct loads
   // separately and waits only where this code says
-  __shared__ __attribute__((aligned(16))) uint8_t A0[A_STAGE];
-  __shared__ __attribute__((aligned(16))) uint8_t A1[A_STAGE];
-  __shared__ __attribute__((aligned(16))) uint8_t A2[A_STAGE];
-  __shared__ __attribute__((aligned(16))) uint8_t A3[A_STAGE];
-  __shared__ __attribute__((aligned(16))) uint8_t B0[B_STAGE];
-  __shared__ __attribute__((aligned(16))) uint8_t B1[B_STAGE];
-  __shared__ __attribute__((aligned(16))) uint8_t B2[B_STAGE];
-  __shared__ __attribute__((aligned(16))) uint8_t B3[B_STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t A0[ASZ];
+  __shared__ __attribute__((aligned(16))) uint8_t A1[ASZ];
+  __shared__ __attribute__((aligned(16))) uint8_t A2[ASZ];
+  __shared__ __attribute__((aligned(16))) uint8_t A3[ASZ];
+  __shared__ __attribute__((aligned(16))) uint8_t B0[BSZ];
+  __shared__ __attribute__((aligned(16))) uint8_t B1[BSZ];
+  __shared__ __attribute__((aligned(16))) uint8_t B2[BSZ];
+  __shared__ __attribute__((aligned(16))) uint8_t B3[BSZ];
+  // per-k scales (bits along N) as bf16, stage i at Sc[i * BK]
+  __shared__ __attribute__((aligned(16))) uint16_t Sc[BKIND == B_BITS_ALONG_N ? 4 * BK : 8];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -443,40 +208,91 @@ __global__ __launch_bounds__(THREADS, 1) void forward_kernel(Params p) {
   tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
   const uint32_t one = bf16_one_pair();
-  const int nk = static_cast<int>(p.K / BK);
+  const int nk = static_cast<int>((p.K + BK - 1) / BK);  // K % BK != 0 only for A as rows of K
 
-  // A (x rows, K contiguous): the buffer starts at row m0, so rows past M
-  // read zero.  Wave w fills rows 64w .. 64w+63 with 8 loads of 8 rows;
+  // A (rows of M, K contiguous): the buffer starts at row m0, so rows past
+  // M read zero.  Wave w fills rows 64w .. 64w+63 with 8 loads of 8 rows;
   // lane -> row 8j + lane/8 and LDS chunk lane%8, which holds global chunk
   // (lane%8) ^ swz(row); swz depends on j only through its parity.
-  const __amdgpu_buffer_rsrc_t ra = rsrc(p.a + m0 * p.lda, (p.a_rows - m0) * p.lda * 2);
-  const int q8 = lane >> 3, pos = lane & 7;
-  uint32_t a_voff[2];
+  // A as rows of K: the buffer starts at column m0, so k-rows past K read
+  // zero.  Wave w fills row pairs 8w .. 8w+7, one direct load each; lane i
+  // loads chunk i/2 of k-row 2P + i%2.
+  __amdgpu_buffer_rsrc_t ra;
+  uint32_t a_voff[2], a_row8;
+  if (AKIND == A_ROWS_M) {
+    ra = rsrc(p.a + m0 * p.lda, (p.a_rows - m0) * p.lda * 2);
+    const int q8 = lane >> 3, pos = lane & 7;
 #pragma unroll
-  for (int par = 0; par < 2; ++par)
-    a_voff[par] = static_cast<uint32_t>((64 * wave + q8) * p.lda * 2 + 16 * (pos ^ (4 * par + (q8 >> 1))));
-  const uint32_t a_row8 = static_cast<uint32_t>(8 * p.lda * 2);
-  // B (sign bits along K): 256 rows x 8 bytes per stage; wave w fills rows
-  // 64w .. 64w+63 with 2 loads of 4 bytes per lane.
-  const __amdgpu_buffer_rsrc_t rb = rsrc(p.bits + n0 * p.pb, (p.bit_rows - n0) * p.pb);
-  const uint32_t b_voff = static_cast<uint32_t>((64 * wave + (lane >> 1)) * p.pb + 4 * (lane & 1));
-  const uint32_t b_row32 = static_cast<uint32_t>(32 * p.pb);
+    for (int par = 0; par < 2; ++par)
+      a_voff[par] = static_cast<uint32_t>((64 * wave + q8) * p.lda * 2 + 16 * (pos ^ (4 * par + (q8 >> 1))));
+    a_row8 = static_cast<uint32_t>(8 * p.lda * 2);
+  } else {
+    ra = rsrc(p.a + m0, (p.a_rows * p.lda - m0) * 2);
+    a_voff[0] = a_voff[1] = static_cast<uint32_t>(((16 * wave + (lane & 1)) * p.lda + 8 * (lane >> 1)) * 2);
+    a_row8 = static_cast<uint32_t>(2 * p.lda * 2);  // one row pair
+  }
+  const uint32_t a_kstep = AKIND == A_ROWS_M ? BK * 2 : static_cast<uint32_t>(BK * p.lda * 2);
+
+  // B along K: 256 rows x 8 bytes per stage, wave w fills rows 64w ..
+  // 64w+63 with 2 direct loads of 4 bytes per lane.
+  // B along N: 64 k-rows x 32 bytes per stage; thread t loads the dwords
+  // t and t + 256 (k-row d/8, bytes 4(d%8) ..) and one scale, k = t % 64.
+  __amdgpu_buffer_rsrc_t rb;
+  uint32_t b_voff, b_step;
+  __amdgpu_buffer_rsrc_t rs = rsrc(p.kscale, p.kscale ? p.K * 4 : 0);
+  if (BKIND == B_BITS_ALONG_K) {
+    rb = rsrc(p.bits + n0 * p.pb, (p.bit_rows - n0) * p.pb);
+    b_voff = static_cast<uint32_t>((64 * wave + (lane >> 1)) * p.pb + 4 * (lane & 1));
+    b_step = static_cast<uint32_t>(32 * p.pb);
+  } else {
+    rb = rsrc(p.bits + n0 / 8, p.bit_rows * p.pb - n0 / 8);
+    b_voff = static_cast<uint32_t>((tid >> 3) * p.pb + 4 * (tid & 7));
+    b_step = static_cast<uint32_t>(32 * p.pb);  // dword t + 256 is 32 k-rows further
+  }
+  uint32_t bw[2] = {0u, 0u};
+  float bsc = 0.0f;
 
   // Steps past the end are issued too, at an offset past every buffer's
   // end: they read zero without touching memory and keep the number of
   // loads in flight the same on every step.
   auto issue = [&](int it, uint8_t* As, uint8_t* Bs) {
     const bool live = it < nk;
-    const uint32_t k_off = live ? static_cast<uint32_t>(it) * (BK * 2) : 0x80000000u;
-    const uint32_t kb = live ? static_cast<uint32_t>(it) * (BK / 8) : 0x80000000u;
+    if (BKIND == B_BITS_ALONG_N) {
+      const uint32_t koff = live ? static_cast<uint32_t>(it) * BK * static_cast<uint32_t>(p.pb) : 0x80000000u;
+      bw[0] = ld32(rb, b_voff + koff);
+      bw[1] = ld32(rb, b_voff + b_step + koff);
+      const uint32_t soff = live ? static_cast<uint32_t>((it * BK + (tid & 63)) * 4) : 0x80000000u;
+      const uint32_t sv = ld32(rs, soff);
+      bsc = p.kscale ? __uint_as_float(sv) : ((live && it * BK + (tid & 63) < p.K) ? 1.0f : 0.0f);
+    }
+    const uint32_t k_off = live ? static_cast<uint32_t>(it) * a_kstep : 0x80000000u;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_t*)(As + (64 * wave + 8 * j) * 128), 16, a_voff[j & 1],
+    for (int j = 0; j < 8; ++j) {
+      uint8_t* dst = AKIND == A_ROWS_M ? As + (64 * wave + 8 * j) * 128 : As + (8 * wave + j) * APK;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_t*)dst, 16, a_voff[j & 1],
                                                static_cast<int>(j * a_row8 + k_off), 0, 0);
+    }
+    if (BKIND == B_BITS_ALONG_K) {
+      const uint32_t kb = live ? static_cast<uint32_t>(it) * (BK / 8) : 0x80000000u;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_t*)(Bs + (64 * wave + 32 * j) * 8), 4, b_voff,
-                                               static_cast<int>(j * b_row32 + kb), 0, 0);
+      for (int j = 0; j < 2; ++j)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_t*)(Bs + (64 * wave + 32 * j) * 8), 4, b_voff,
+                                                 static_cast<int>(j * b_step + kb), 0, 0);
+    }
+  };
+  // bits along N: write the staged registers of a step into its stage
+  auto store_b = [&](uint8_t* Bs, uint16_t* Ss) {
+    if (BKIND == B_BITS_ALONG_N) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int d = tid + 256 * h;
+        const int k = d >> 3, g = d & 7;
+        const uint32_t neg = ~bw[h];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Bs[(4 * g + i) * LDB_N + k] = static_cast<uint8_t>(neg >> (8 * i));
+      }
+      if (tid < BK) Ss[tid] = f32_to_bf16(bsc);
+    }
   };
 
   f32x16 acc[4][4];
@@ -485,26 +301,53 @@ __global__ __launch_bounds__(THREADS, 1) void forward_kernel(Params p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  // fragments: a[buf][mb] rows of x, b[buf][nb] expanded signs; substep s
+  // fragments: a[buf][mb] dense rows, b[buf][nb] expanded signs; substep s
   // (k = 16s .. 16s+15 of the step) uses buffer s & 1
   bf16x8 a[2][4], b[2][4];
   uint64_t bits[4];
+  // A as rows of K: this lane, as a source of the transposed read, names
+  // k-row 16s + 8kg + 4h + t and m = 128wm + 32mb + 16(g%2) + 4a .. +3
+  // (lane = 16g + 4a... with t = (lane%16)/4, a = lane%4, g = lane/16);
+  // as a destination it receives A[m = l32][k = 16s + 8kg + 4h + 0..3].
+  const int tr_t = (lane & 15) >> 2, tr_a = lane & 3, tr_g = lane >> 4;
+  const int tr_base = APK * (4 * (tr_g >> 1) + (tr_t >> 1)) + 32 * (16 * wm + 2 * (tr_g & 1) + (tr_a >> 1)) +
+                      16 * (tr_t & 1) + 8 * (tr_a & 1);
   auto load_a = [&](const uint8_t* As, int s, bf16x8* dst) {
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
-      const int row = 128 * wm + 32 * mb + l32;
-      dst[mb] = *reinterpret_cast<const bf16x8*>(As + row * 128 + 16 * ((2 * s + kg) ^ swz(row)));
+      if (AKIND == A_ROWS_M) {
+        const int row = 128 * wm + 32 * mb + l32;
+        dst[mb] = *reinterpret_cast<const bf16x8*>(As + row * 128 + 16 * ((2 * s + kg) ^ swz(row)));
+      } else {
+        const uint8_t* src = As + tr_base + APK * 8 * s + 128 * mb;
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(src));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(src + 2 * APK));
+        dst[mb] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
     }
   };
+  // bits along K: this lane's 64 k-bits of each of its 4 columns
   auto load_bits = [&](const uint8_t* Bs) {
+    if (BKIND == B_BITS_ALONG_K) {
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-      bits[nb] = ~*reinterpret_cast<const uint64_t*>(Bs + 8 * (128 * wn + 32 * nb + l32));
+      for (int nb = 0; nb < 4; ++nb)
+        bits[nb] = ~*reinterpret_cast<const uint64_t*>(Bs + 8 * (128 * wn + 32 * nb + l32));
+    }
   };
-  auto expand_b = [&](int s, bf16x8* dst) {
+  auto expand_b = [&](const uint8_t* Bs, const uint16_t* Ss, int s, bf16x8* dst) {
+    if (BKIND == B_BITS_ALONG_K) {
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-      dst[nb] = signs_along_k(static_cast<uint32_t>(bits[nb] >> (8 * (2 * s + kg))) & 0xFFu, one);
+      for (int nb = 0; nb < 4; ++nb)
+        dst[nb] = signs_along_k(static_cast<uint32_t>(bits[nb] >> (8 * (2 * s + kg))) & 0xFFu, one);
+    } else {
+      const int kk = 16 * s + 8 * kg;
+      const uint4 sc = *reinterpret_cast<const uint4*>(Ss + kk);
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const int c = 128 * wn + 32 * nb + l32;
+        dst[nb] = signs_across_k(*reinterpret_cast<const uint64_t*>(Bs + (c >> 3) * LDB_N + kk), c & 7, sc);
+      }
+    }
   };
   auto mfmas = [&](int s) {
 #pragma unroll
@@ -513,60 +356,149 @@ __global__ __launch_bounds__(THREADS, 1) void forward_kernel(Params p) {
       for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = mma(a[s & 1][mb], b[s & 1][nb], acc[mb][nb]);
   };
 
-  // K step `it` on stage As (its bits already in `bits`, substep 0's
-  // fragments in buffer 0).  After substep 2 every wave has finished step
-  // it-1, so step it+3 may overwrite that step's stage (N3a, N3b); waiting
-  // for all but the newest step's loads makes step it+1's stage (N1a, N1b)
-  // complete, and its first fragments are read during substep 3.
-  auto step = [&](int it, const uint8_t* As, const uint8_t* N1a, const uint8_t* N1b, uint8_t* N3a,
+  // K step `it` on stage (As, Bs, Ss); substep 0's fragments are in buffer 0.
+  // After substep 2 every wave has finished step it-1, so step it+3 may
+  // overwrite that step's stage (N3*).  Waiting for all but the newest
+  // step's direct loads (its 8 A loads when bits run along N, whose 3
+  // register loads are issued first) completes step it+1's stage (N1*) and,
+  // for bits along N, the registers of step it+2, which are then written to
+  // its stage (N2*).
+  // Step it+1's first fragments are read while substep 3 runs.
+  auto step = [&](int it, const uint8_t* As, const uint8_t* Bs, const uint16_t* Ss, const uint8_t* N1a,
+                  const uint8_t* N1b, const uint16_t* N1s, uint8_t* N2b, uint16_t* N2s, uint8_t* N3a,
                   uint8_t* N3b) {
 #pragma unroll
     for (int s = 0; s < 3; ++s) {
       load_a(As, s + 1, a[(s + 1) & 1]);
       mfmas(s);
-      expand_b(s + 1, b[(s + 1) & 1]);
+      expand_b(Bs, Ss, s + 1, b[(s + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    stage_barrier<LOADS_PER_STEP>();
+    stage_barrier<BKIND == B_BITS_ALONG_K ? NL : 8>();
+    store_b(N2b, N2s);
     issue(it + 3, N3a, N3b);
     load_a(N1a, 0, a[0]);
     load_bits(N1b);
     mfmas(3);
-    expand_b(0, b[0]);
+    expand_b(N1b, N1s, 0, b[0]);
     __builtin_amdgcn_sched_barrier(0);
   };
 
+  uint16_t* S0 = Sc;
+  uint16_t* S1 = Sc + (BKIND == B_BITS_ALONG_N ? BK : 0);
+  uint16_t* S2 = Sc + (BKIND == B_BITS_ALONG_N ? 2 * BK : 0);
+  uint16_t* S3 = Sc + (BKIND == B_BITS_ALONG_N ? 3 * BK : 0);
+  // prologue: stages 0 and 1 complete (bits along N written from registers),
+  // step 2 issued
   issue(0, A0, B0);
+  if (BKIND == B_BITS_ALONG_N) {
+    stage_barrier<8>();  // registers of step 0 (the 8 A loads may stay in flight)
+    store_b(B0, S0);
+  }
   issue(1, A1, B1);
+  if (BKIND == B_BITS_ALONG_N) {
+    stage_barrier<8>();
+    store_b(B1, S1);
+  }
   issue(2, A2, B2);
-  stage_barrier<2 * LOADS_PER_STEP>();
+  stage_barrier<NL == 10 ? 2 * NL : NL>();  // along K: steps 0, 1 complete; along N: step 0, 1
   load_a(A0, 0, a[0]);
   load_bits(B0);
-  expand_b(0, b[0]);
+  expand_b(B0, S0, 0, b[0]);
   int it = 0;
   for (; it + 4 <= nk; it += 4) {
-    step(it, A0, A1, B1, A3, B3);
-    step(it + 1, A1, A2, B2, A0, B0);
-    step(it + 2, A2, A3, B3, A1, B1);
-    step(it + 3, A3, A0, B0, A2, B2);
+    step(it, A0, B0, S0, A1, B1, S1, B2, S2, A3, B3);
+    step(it + 1, A1, B1, S1, A2, B2, S2, B3, S3, A0, B0);
+    step(it + 2, A2, B2, S2, A3, B3, S3, B0, S0, A1, B1);
+    step(it + 3, A3, B3, S3, A0, B0, S0, B1, S1, A2, B2);
   }
-  if (it < nk) step(it, A0, A1, B1, A3, B3);
-  if (it + 1 < nk) step(it + 1, A1, A2, B2, A0, B0);
-  if (it + 2 < nk) step(it + 2, A2, A3, B3, A1, B1);
+  if (it < nk) step(it, A0, B0, S0, A1, B1, S1, B2, S2, A3, B3);
+  if (it + 1 < nk) step(it + 1, A1, B1, S1, A2, B2, S2, B3, S3, A0, B0);
+  if (it + 2 < nk) step(it + 2, A2, B2, S2, A3, B3, S3, B0, S0, A1, B1);
 
-  // Epilogue: scale and bias, round to bf16, stage through LDS one quarter
-  // (32 of the wave's 128 rows) at a time so each row segment of 128
-  // outputs leaves as 16 lanes x 16 contiguous bytes.  Waves 0, 1 stage in
-  // A0 and waves 2, 3 in A1, after every in-flight load has landed.
+  // every in-flight load has landed (the stages are free for the epilogue)
   stage_barrier<0>();
+
+  if (EPI == EPI_EVIDENCE) {
+    // E0 = acc + v[m]; E = E0 * s[m] (fp32, 32 lanes x 4 bytes per row per
+    // store); row partials of E0 * sign_w over this wave's 128 columns.
+    // The tile's sign_w bits (256 rows x 32 bytes), v and s go to LDS first.
+    uint8_t* wst = A0;                                  // [256][32] bytes
+    float* vst = reinterpret_cast<float*>(A0 + 8192);   // [256]
+    float* sst = vst + BM;                              // [256]
+    {
+      const int64_t row = m0 + tid;
+      const __amdgpu_buffer_rsrc_t rw = rsrc(p.w_bits, p.w_bits ? p.M * p.pb : 0);
+      const uint32_t off = static_cast<uint32_t>(row * p.pb + n0 / 8);
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const uint32_t w = (p.w_bits && row < p.M) ? ld32(rw, off + 4 * d) : 0u;
+        *reinterpret_cast<uint32_t*>(wst + tid * 32 + 4 * d) = w;
+      }
+      vst[tid] = (p.m_add && row < p.M) ? p.m_add[row] : 0.0f;
+      sst[tid] = (p.m_scale && row < p.M) ? p.m_scale[row] : 1.0f;
+    }
+    stage_barrier<0>();
+    float* ev = static_cast<float*>(p.out);
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      float part[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int lrow = 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
+        const int64_t row = m0 + lrow;
+        const float add = vst[lrow], mul = sst[lrow];
+        const uint4 w = *reinterpret_cast<const uint4*>(wst + lrow * 32 + 16 * wn);
+        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+        float acc_part = 0.0f;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+          const int64_t col = n0 + 128 * wn + 32 * nb + l32;
+          const float e0 = acc[mb][nb][r] + add;
+          // columns past N hold zero bits and contribute -e0: skip them
+          if (col < p.N) acc_part += ((wd[nb] >> l32) & 1u) ? e0 : -e0;
+          if (row < p.M && col < p.N) ev[row * p.N + col] = e0 * mul;
+        }
+        part[r] = acc_part;
+      }
+      if (p.gs_partial) {
+        // sum part[r] over the 32 lanes of each half-wave: four halving
+        // steps leave lane l one row's partial over 16 lanes, the last step
+        // adds lane l ^ 1; row index bits come from lane bits 4, 3, 2, 1
+#pragma unroll
+        for (int o = 16, c = 16; o >= 2; o >>= 1, c >>= 1) {
+          const bool hi = (l32 & o) != 0;
+#pragma unroll
+          for (int i = 0; i < c / 2; ++i) {
+            const float keep = hi ? part[i + c / 2] : part[i];
+            const float send = hi ? part[i] : part[i + c / 2];
+            part[i] = keep + __shfl_xor(send, o, 64);
+          }
+        }
+        const float tot = part[0] + __shfl_xor(part[0], 1, 64);
+        const int r = 8 * ((l32 >> 4) & 1) + 4 * ((l32 >> 3) & 1) + 2 * ((l32 >> 2) & 1) + ((l32 >> 1) & 1);
+        const int64_t row = m0 + 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
+        if ((l32 & 1) == 0 && row < p.M) {
+          const int64_t slot = 2 * static_cast<int64_t>(tn) + wn;
+          p.gs_partial[slot * p.M + row] = tot;
+        }
+      }
+    }
+    return;
+  }
+
+  // Epilogue: (scale and bias,) round to bf16, stage through LDS one
+  // quarter (32 of the wave's 128 rows) at a time so each row segment of 128
+  // outputs leaves as 16 lanes x 16 contiguous bytes.  Waves 0, 1 stage in
+  // A0 and waves 2, 3 in A1.
   uint16_t* y = static_cast<uint16_t*>(p.out);
   uint8_t* stg = (wave < 2 ? A0 : A1) + (wave & 1) * (32 * EPL);
   float sc[4], bi[4];
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) {
     const int64_t col = n0 + 128 * wn + 32 * nb + l32;
-    sc[nb] = (col < p.N && p.n_scale) ? p.n_scale[col] : 1.0f;
-    bi[nb] = (col < p.N && p.n_bias) ? p.n_bias[col] : 0.0f;
+    sc[nb] = (EPI == EPI_FORWARD && col < p.N && p.n_scale) ? p.n_scale[col] : 1.0f;
+    bi[nb] = (EPI == EPI_FORWARD && col < p.N && p.n_bias) ? p.n_bias[col] : 0.0f;
   }
   // Lanes l, l^1 trade one value per row pair so each holds two adjacent
   // columns of one row: even lanes row r, odd lanes row r+1.
@@ -578,10 +510,13 @@ __global__ __launch_bounds__(THREADS, 1) void forward_kernel(Params p) {
     for (int nb = 0; nb < 4; ++nb) {
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
-        float v0 = acc[mb][nb][r] * sc[nb];
-        v0 = v0 + bi[nb];
-        float v1 = acc[mb][nb][r + 1] * sc[nb];
-        v1 = v1 + bi[nb];
+        float v0 = acc[mb][nb][r], v1 = acc[mb][nb][r + 1];
+        if (EPI == EPI_FORWARD) {
+          v0 = v0 * sc[nb];
+          v0 = v0 + bi[nb];
+          v1 = v1 * sc[nb];
+          v1 = v1 + bi[nb];
+        }
         const float send = odd ? v0 : v1;
         const float recv = __int_as_float(
             __builtin_amdgcn_update_dpp(0, __float_as_int(send), 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
@@ -622,9 +557,6 @@ __global__ __launch_bounds__(THREADS, 1) void forward_kernel(Params p) {
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-static int grid_tiles(int64_t M, int64_t N) {
-  return static_cast<int>(((M + mfma::BM - 1) / mfma::BM) * ((N + mfma::BN - 1) / mfma::BN));
-}
 
 // Buffer offsets are 32-bit: every operand must stay under 4 GiB.
 static bool fits32(int64_t bytes) { return bytes < (int64_t{1} << 32); }
@@ -645,7 +577,7 @@ int mfma_linear_forward(const void* x, int dtype, const uint8_t* packed, const f
   p.n_scale = scale; p.n_bias = bias;
   const int grid = static_cast<int>(((m + mfma::wide::BM - 1) / mfma::wide::BM) *
                                     ((rows + mfma::wide::BN - 1) / mfma::wide::BN));
-  mfma::wide::forward_kernel<<<grid, mfma::wide::THREADS, 0, stream>>>(p);
+  mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD><<<grid, mfma::wide::THREADS, 0, stream>>>(p);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -662,12 +594,13 @@ int mfma_linear_dgrad(const void* dy, int dtype, const uint8_t* packed, const fl
   p.M = m; p.N = cols; p.K = rows;
   p.lda = rows; p.pb = cols / 8;
   p.a_rows = m; p.bit_rows = rows;
-  mfma::gemm_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_N, mfma::EPI_PLAIN>
-      <<<grid_tiles(m, cols), mfma::THREADS, 0, stream>>>(p);
+  const int grid = static_cast<int>(((m + mfma::wide::BM - 1) / mfma::wide::BM) *
+                                    ((cols + mfma::wide::BN - 1) / mfma::wide::BN));
+  mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_N, mfma::EPI_PLAIN><<<grid, mfma::wide::THREADS, 0, stream>>>(p);
   return static_cast<int>(hipGetLastError());
 }
 
-int64_t mfma_evidence_tiles(int64_t cols) { return 2 * ((cols + mfma::BN - 1) / mfma::BN); }
+int64_t mfma_evidence_tiles(int64_t cols) { return 2 * ((cols + mfma::wide::BN - 1) / mfma::wide::BN); }
 
 int mfma_evidence(const void* dy, int dtype, const uint8_t* packed_x, const float* x_scale, float* ev,
                   int64_t samples, int64_t rows, int64_t cols, const float* m_add, const float* m_scale,
@@ -684,8 +617,10 @@ int mfma_evidence(const void* dy, int dtype, const uint8_t* packed_x, const floa
   p.lda = rows; p.pb = cols / 8;
   p.a_rows = samples; p.bit_rows = samples;
   p.m_add = m_add; p.m_scale = m_scale; p.w_bits = w_bits; p.gs_partial = gs_partial;
-  mfma::gemm_kernel<mfma::A_ROWS_K, mfma::B_BITS_ALONG_N, mfma::EPI_EVIDENCE>
-      <<<grid_tiles(rows, cols), mfma::THREADS, 0, stream>>>(p);
+  const int grid = static_cast<int>(((rows + mfma::wide::BM - 1) / mfma::wide::BM) *
+                                    ((cols + mfma::wide::BN - 1) / mfma::wide::BN));
+  mfma::wide::wide_kernel<mfma::A_ROWS_K, mfma::B_BITS_ALONG_N, mfma::EPI_EVIDENCE>
+      <<<grid, mfma::wide::THREADS, 0, stream>>>(p);
   return static_cast<int>(hipGetLastError());
 }
 

@@ -56,6 +56,65 @@ __global__ void colsum_partial_kernel(const typename Elem<DT>::T* __restrict__ d
   if (db_part) db_part[blockIdx.y * rows + r] = db;
 }
 
+// bf16 / f16 with rows % 8 == 0: each lane reduces 8 adjacent columns (one
+// 16-byte load per sample), a wave 512 columns, over kColChunk samples,
+// with UNROLL loads in flight; same per-column order as the scalar kernel.
+template <int DT>
+__global__ __launch_bounds__(64) void colsum_partial_x8_kernel(const uint16_t* __restrict__ dy,
+                                                              const float* __restrict__ offset,
+                                                              int64_t samples, int64_t rows,
+                                                              float* __restrict__ v_part,
+                                                              float* __restrict__ db_part) {
+  constexpr int UNROLL = 8;
+  const int64_t r = (blockIdx.x * static_cast<int64_t>(64) + threadIdx.x) * 8;
+  if (r >= rows) return;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kColChunk;
+  const int64_t t1 = t0 + kColChunk < samples ? t0 + kColChunk : samples;
+  float v[8], db[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = db[i] = 0.0f;
+  const uint16_t* col = dy + r;
+  int64_t t = t0;
+  for (; t + UNROLL <= t1; t += UNROLL) {
+    uint4 q[UNROLL];
+    float o[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      q[u] = *reinterpret_cast<const uint4*>(col + (t + u) * rows);
+      o[u] = offset[t + u];
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const uint16_t* e = reinterpret_cast<const uint16_t*>(&q[u]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float g = Elem<DT>::load(e, i);
+        v[i] = fmaf(g, o[u], v[i]);
+        db[i] += g;
+      }
+    }
+  }
+  for (; t < t1; ++t) {
+    const uint4 q = *reinterpret_cast<const uint4*>(col + t * rows);
+    const float o = offset[t];
+    const uint16_t* e = reinterpret_cast<const uint16_t*>(&q);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float g = Elem<DT>::load(e, i);
+      v[i] = fmaf(g, o, v[i]);
+      db[i] += g;
+    }
+  }
+  float* vp = v_part + blockIdx.y * rows + r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) vp[i] = v[i];
+  if (db_part) {
+    float* dp = db_part + blockIdx.y * rows + r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dp[i] = db[i];
+  }
+}
+
 int launch_row_inner(const float* mat, const uint8_t* packed, float* out, int64_t rows,
                      int64_t cols, hipStream_t stream) {
   if (rows == 0) return 0;
@@ -78,7 +137,19 @@ int launch_colsums(const void* dy, int dtype, const float* offset, int64_t sampl
                    hipStream_t stream) {
   if (rows == 0) return 0;
   const int chunks = colsum_chunks(samples);
-  if (chunks > 0) {
+  const bool x8 = (dtype == QSTE_BF16 || dtype == QSTE_F16) && rows % 8 == 0 &&
+                  (reinterpret_cast<uintptr_t>(dy) & 15) == 0;
+  if (chunks > 0 && x8) {
+    dim3 grid(ceil_div(rows, 512), chunks);
+    if (dtype == QSTE_BF16)
+      colsum_partial_x8_kernel<QSTE_BF16><<<grid, 64, 0, stream>>>(static_cast<const uint16_t*>(dy), offset,
+                                                                    samples, rows, v_part, db_part);
+    else
+      colsum_partial_x8_kernel<QSTE_F16><<<grid, 64, 0, stream>>>(static_cast<const uint16_t*>(dy), offset,
+                                                                   samples, rows, v_part, db_part);
+    int rc = static_cast<int>(hipGetLastError());
+    if (rc) return rc;
+  } else if (chunks > 0) {
     dim3 grid(ceil_div(rows, 256), chunks);
     switch (dtype) {
       case QSTE_F32:
