@@ -31,6 +31,8 @@ int mfma_linear_dgrad(const void*, int, const uint8_t*, const float*, void*, int
 int mfma_evidence(const void*, int, const uint8_t*, const float*, float*, int64_t, int64_t, int64_t,
                   const float*, const float*, const uint8_t*, float*, hipStream_t);
 int64_t mfma_evidence_tiles(int64_t cols);
+int mfma_backward_pair(const void*, int, const uint8_t*, const float*, float*, const uint8_t*, const float*,
+                       void*, int64_t, int64_t, int64_t, const float*, float*, hipStream_t);
 int gemv_linear_forward(const void*, int, const uint8_t*, const float*, const float*, void*, int64_t,
                         int64_t, int64_t, hipStream_t);
 }  // namespace qste
@@ -213,10 +215,15 @@ int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x, con
   float* gs_part = reinterpret_cast<float*>(base + l.gs_part);
   int rc;
   if (samples > 0) {
-    if ((rc = dgrad_dispatch(dy, dtype, packed_w, scale, dx, samples, rows, cols, s))) return rc;
     if ((rc = launch_colsums(dy, dtype, x_offset, samples, rows, v_part, grad_bias ? db_part : nullptr, v,
                              grad_bias, s)))
       return rc;
+    // evidence and dgrad together when both take the MFMA path
+    rc = mfma_backward_pair(dy, dtype, packed_x, x_scale, evidence, packed_w, scale, dx, samples, rows, cols, v,
+                            gs_part, s);
+    if (rc == 0) return launch_sum_partials(gs_part, mfma_evidence_tiles(cols), rows, grad_scale, s);
+    if (rc != 1) return rc;
+    if ((rc = dgrad_dispatch(dy, dtype, packed_w, scale, dx, samples, rows, cols, s))) return rc;
   } else {
     if ((rc = fill_zero(v, rows, s))) return rc;
     if (grad_bias && (rc = fill_zero(grad_bias, rows, s))) return rc;

@@ -180,24 +180,14 @@ constexpr int A_STAGE_K = (BK / 2) * APK;    // bytes
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
+// One output tile; the LDS stages are the caller's (one __shared__ array per
+// stage, so that the compiler tracks each stage's direct loads separately
+// and waits only where this code says).
 template <int AKIND, int BKIND, int EPI>
-__global__ __launch_bounds__(THREADS, 1) void wide_kernel(Params p) {
+__device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0, uint8_t* A1, uint8_t* A2,
+                                          uint8_t* A3, uint8_t* B0, uint8_t* B1, uint8_t* B2, uint8_t* B3,
+                                          uint16_t* Sc) {
   constexpr int NL = Loads<BKIND>::value;
-  constexpr int BSZ = BKIND == B_BITS_ALONG_K ? B_STAGE : BN_STAGE;
-  constexpr int ASZ = AKIND == A_ROWS_M ? A_STAGE : A_STAGE_K;
-  // one array per stage: the compiler then tracks each stage's direct loads
-  // separately and waits only where this code says
-  __shared__ __attribute__((aligned(16))) uint8_t A0[ASZ];
-  __shared__ __attribute__((aligned(16))) uint8_t A1[ASZ];
-  __shared__ __attribute__((aligned(16))) uint8_t A2[ASZ];
-  __shared__ __attribute__((aligned(16))) uint8_t A3[ASZ];
-  __shared__ __attribute__((aligned(16))) uint8_t B0[BSZ];
-  __shared__ __attribute__((aligned(16))) uint8_t B1[BSZ];
-  __shared__ __attribute__((aligned(16))) uint8_t B2[BSZ];
-  __shared__ __attribute__((aligned(16))) uint8_t B3[BSZ];
-  // per-k scales (bits along N) as bf16, stage i at Sc[i * BK]
-  __shared__ __attribute__((aligned(16))) uint16_t Sc[BKIND == B_BITS_ALONG_N ? 4 * BK : 8];
-
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int wm = wave >> 1, wn = wave & 1;
@@ -205,7 +195,7 @@ __global__ __launch_bounds__(THREADS, 1) void wide_kernel(Params p) {
   const int tiles_m = static_cast<int>((p.M + BM - 1) / BM);
   const int tiles_n = static_cast<int>((p.N + BN - 1) / BN);
   int tm, tn;
-  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  tile_of(pid, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
   const uint32_t one = bf16_one_pair();
   const int nk = static_cast<int>((p.K + BK - 1) / BK);  // K % BK != 0 only for A as rows of K
@@ -548,6 +538,45 @@ __global__ __launch_bounds__(THREADS, 1) void wide_kernel(Params p) {
     }
   }
 }
+
+// sizes of the per-stage arrays for a kernel instance
+template <int AKIND, int BKIND>
+struct StageSizes {
+  static constexpr int a = AKIND == A_ROWS_M ? A_STAGE : A_STAGE_K;
+  static constexpr int b = BKIND == B_BITS_ALONG_K ? B_STAGE : BN_STAGE;
+  static constexpr int s = BKIND == B_BITS_ALONG_N ? 4 * BK : 8;
+};
+
+#define QSTE_WIDE_STAGES(ASZ, BSZ, SSZ)                           \
+  __shared__ __attribute__((aligned(16))) uint8_t A0[ASZ];       \
+  __shared__ __attribute__((aligned(16))) uint8_t A1[ASZ];       \
+  __shared__ __attribute__((aligned(16))) uint8_t A2[ASZ];       \
+  __shared__ __attribute__((aligned(16))) uint8_t A3[ASZ];       \
+  __shared__ __attribute__((aligned(16))) uint8_t B0[BSZ];       \
+  __shared__ __attribute__((aligned(16))) uint8_t B1[BSZ];       \
+  __shared__ __attribute__((aligned(16))) uint8_t B2[BSZ];       \
+  __shared__ __attribute__((aligned(16))) uint8_t B3[BSZ];       \
+  __shared__ __attribute__((aligned(16))) uint16_t Sc[SSZ];
+
+template <int AKIND, int BKIND, int EPI>
+__global__ __launch_bounds__(THREADS, 1) void wide_kernel(Params p) {
+  using SZ = StageSizes<AKIND, BKIND>;
+  QSTE_WIDE_STAGES(SZ::a, SZ::b, SZ::s)
+  wide_tile<AKIND, BKIND, EPI>(p, blockIdx.x, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
+}
+
+// The two large products of a layer's backward in one launch: evidence
+// tiles first (the longer ones), then dgrad tiles, so the grid's last wave
+// of one product is filled by the other instead of leaving CUs idle.
+__global__ __launch_bounds__(THREADS, 1) void backward_pair_kernel(Params pe, Params pd, int tiles_e) {
+  QSTE_WIDE_STAGES(A_STAGE_K, BN_STAGE, 4 * BK)
+  if (static_cast<int>(blockIdx.x) < tiles_e)
+    wide_tile<A_ROWS_K, B_BITS_ALONG_N, EPI_EVIDENCE>(pe, blockIdx.x, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
+  else
+    wide_tile<A_ROWS_M, B_BITS_ALONG_N, EPI_PLAIN>(pd, blockIdx.x - tiles_e, A0, A1, A2, A3, B0, B1, B2, B3,
+                                                   Sc);
+}
+#undef QSTE_WIDE_STAGES
 }  // namespace wide
 }  // namespace mfma
 
@@ -557,35 +586,29 @@ __global__ __launch_bounds__(THREADS, 1) void wide_kernel(Params p) {
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-
 // Buffer offsets are 32-bit: every operand must stay under 4 GiB.
 static bool fits32(int64_t bytes) { return bytes < (int64_t{1} << 32); }
 
-int mfma_linear_forward(const void* x, int dtype, const uint8_t* packed, const float* scale,
-                        const float* bias, void* y, int64_t m, int64_t rows, int64_t cols,
-                        hipStream_t stream) {
-  if (dtype != QSTE_BF16 || cols % 64 != 0 || cols == 0 || m == 0 || !aligned16(x) || !aligned16(packed) ||
-      !fits32(m * cols * 2) || !fits32(rows * cols / 8))
-    return 1;
-  mfma::Params p{};
-  p.a = static_cast<const uint16_t*>(x);
-  p.bits = packed;
-  p.out = y;
-  p.M = m; p.N = rows; p.K = cols;
-  p.lda = cols; p.pb = cols / 8;
-  p.a_rows = m; p.bit_rows = rows;
-  p.n_scale = scale; p.n_bias = bias;
-  const int grid = static_cast<int>(((m + mfma::wide::BM - 1) / mfma::wide::BM) *
-                                    ((rows + mfma::wide::BN - 1) / mfma::wide::BN));
-  mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD><<<grid, mfma::wide::THREADS, 0, stream>>>(p);
-  return static_cast<int>(hipGetLastError());
+static int wide_grid(int64_t M, int64_t N) {
+  return static_cast<int>(((M + mfma::wide::BM - 1) / mfma::wide::BM) * ((N + mfma::wide::BN - 1) / mfma::wide::BN));
 }
 
-int mfma_linear_dgrad(const void* dy, int dtype, const uint8_t* packed, const float* row_scale, void* dx,
-                      int64_t m, int64_t rows, int64_t cols, hipStream_t stream) {
-  if (dtype != QSTE_BF16 || cols % 64 != 0 || rows % 64 != 0 || rows == 0 || cols == 0 || m == 0 ||
-      !aligned16(dy) || !aligned16(packed) || !fits32(m * rows * 2) || !fits32(rows * cols / 8))
-    return 1;
+static bool forward_ok(const void* x, int dtype, const uint8_t* packed, int64_t m, int64_t rows, int64_t cols) {
+  return dtype == QSTE_BF16 && cols % 64 == 0 && cols > 0 && m > 0 && rows > 0 && aligned16(x) &&
+         aligned16(packed) && fits32(m * cols * 2) && fits32(rows * cols / 8);
+}
+static bool dgrad_ok(const void* dy, int dtype, const uint8_t* packed, int64_t m, int64_t rows, int64_t cols) {
+  return dtype == QSTE_BF16 && cols % 64 == 0 && rows % 64 == 0 && rows > 0 && cols > 0 && m > 0 &&
+         aligned16(dy) && aligned16(packed) && fits32(m * rows * 2) && fits32(rows * cols / 8);
+}
+static bool evidence_ok(const void* dy, int dtype, const uint8_t* packed_x, int64_t samples, int64_t rows,
+                        int64_t cols) {
+  return dtype == QSTE_BF16 && cols % 64 == 0 && rows % 64 == 0 && rows > 0 && cols > 0 && samples > 0 &&
+         aligned16(dy) && aligned16(packed_x) && fits32(samples * rows * 2) && fits32(samples * cols / 8);
+}
+
+static mfma::Params dgrad_params(const void* dy, const uint8_t* packed, const float* row_scale, void* dx,
+                                 int64_t m, int64_t rows, int64_t cols) {
   mfma::Params p{};
   p.a = static_cast<const uint16_t*>(dy);
   p.bits = packed;
@@ -594,20 +617,12 @@ int mfma_linear_dgrad(const void* dy, int dtype, const uint8_t* packed, const fl
   p.M = m; p.N = cols; p.K = rows;
   p.lda = rows; p.pb = cols / 8;
   p.a_rows = m; p.bit_rows = rows;
-  const int grid = static_cast<int>(((m + mfma::wide::BM - 1) / mfma::wide::BM) *
-                                    ((cols + mfma::wide::BN - 1) / mfma::wide::BN));
-  mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_N, mfma::EPI_PLAIN><<<grid, mfma::wide::THREADS, 0, stream>>>(p);
-  return static_cast<int>(hipGetLastError());
+  return p;
 }
 
-int64_t mfma_evidence_tiles(int64_t cols) { return 2 * ((cols + mfma::wide::BN - 1) / mfma::wide::BN); }
-
-int mfma_evidence(const void* dy, int dtype, const uint8_t* packed_x, const float* x_scale, float* ev,
-                  int64_t samples, int64_t rows, int64_t cols, const float* m_add, const float* m_scale,
-                  const uint8_t* w_bits, float* gs_partial, hipStream_t stream) {
-  if (dtype != QSTE_BF16 || cols % 64 != 0 || rows % 64 != 0 || rows == 0 || cols == 0 || samples == 0 ||
-      !aligned16(dy) || !aligned16(packed_x) || !fits32(samples * rows * 2) || !fits32(samples * cols / 8))
-    return 1;
+static mfma::Params evidence_params(const void* dy, const uint8_t* packed_x, const float* x_scale, float* ev,
+                                    int64_t samples, int64_t rows, int64_t cols, const float* m_add,
+                                    const float* m_scale, const uint8_t* w_bits, float* gs_partial) {
   mfma::Params p{};
   p.a = static_cast<const uint16_t*>(dy);
   p.bits = packed_x;
@@ -617,10 +632,60 @@ int mfma_evidence(const void* dy, int dtype, const uint8_t* packed_x, const floa
   p.lda = rows; p.pb = cols / 8;
   p.a_rows = samples; p.bit_rows = samples;
   p.m_add = m_add; p.m_scale = m_scale; p.w_bits = w_bits; p.gs_partial = gs_partial;
-  const int grid = static_cast<int>(((rows + mfma::wide::BM - 1) / mfma::wide::BM) *
-                                    ((cols + mfma::wide::BN - 1) / mfma::wide::BN));
+  return p;
+}
+
+int mfma_linear_forward(const void* x, int dtype, const uint8_t* packed, const float* scale,
+                        const float* bias, void* y, int64_t m, int64_t rows, int64_t cols,
+                        hipStream_t stream) {
+  if (!forward_ok(x, dtype, packed, m, rows, cols)) return 1;
+  mfma::Params p{};
+  p.a = static_cast<const uint16_t*>(x);
+  p.bits = packed;
+  p.out = y;
+  p.M = m; p.N = rows; p.K = cols;
+  p.lda = cols; p.pb = cols / 8;
+  p.a_rows = m; p.bit_rows = rows;
+  p.n_scale = scale; p.n_bias = bias;
+  mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD>
+      <<<wide_grid(m, rows), mfma::wide::THREADS, 0, stream>>>(p);
+  return static_cast<int>(hipGetLastError());
+}
+
+int mfma_linear_dgrad(const void* dy, int dtype, const uint8_t* packed, const float* row_scale, void* dx,
+                      int64_t m, int64_t rows, int64_t cols, hipStream_t stream) {
+  if (!dgrad_ok(dy, dtype, packed, m, rows, cols)) return 1;
+  const mfma::Params p = dgrad_params(dy, packed, row_scale, dx, m, rows, cols);
+  mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_N, mfma::EPI_PLAIN>
+      <<<wide_grid(m, cols), mfma::wide::THREADS, 0, stream>>>(p);
+  return static_cast<int>(hipGetLastError());
+}
+
+int64_t mfma_evidence_tiles(int64_t cols) { return 2 * ((cols + mfma::wide::BN - 1) / mfma::wide::BN); }
+
+int mfma_evidence(const void* dy, int dtype, const uint8_t* packed_x, const float* x_scale, float* ev,
+                  int64_t samples, int64_t rows, int64_t cols, const float* m_add, const float* m_scale,
+                  const uint8_t* w_bits, float* gs_partial, hipStream_t stream) {
+  if (!evidence_ok(dy, dtype, packed_x, samples, rows, cols)) return 1;
+  const mfma::Params p =
+      evidence_params(dy, packed_x, x_scale, ev, samples, rows, cols, m_add, m_scale, w_bits, gs_partial);
   mfma::wide::wide_kernel<mfma::A_ROWS_K, mfma::B_BITS_ALONG_N, mfma::EPI_EVIDENCE>
-      <<<grid, mfma::wide::THREADS, 0, stream>>>(p);
+      <<<wide_grid(rows, cols), mfma::wide::THREADS, 0, stream>>>(p);
+  return static_cast<int>(hipGetLastError());
+}
+
+// Evidence (with its fused epilogue) and dgrad of one layer in one launch;
+// returns 1 when either is not for this path.
+int mfma_backward_pair(const void* dy, int dtype, const uint8_t* packed_x, const float* x_scale, float* ev,
+                       const uint8_t* packed_w, const float* scale, void* dx, int64_t samples, int64_t rows,
+                       int64_t cols, const float* m_add, float* gs_partial, hipStream_t stream) {
+  if (!evidence_ok(dy, dtype, packed_x, samples, rows, cols) || !dgrad_ok(dy, dtype, packed_w, samples, rows, cols))
+    return 1;
+  const mfma::Params pe =
+      evidence_params(dy, packed_x, x_scale, ev, samples, rows, cols, m_add, scale, packed_w, gs_partial);
+  const mfma::Params pd = dgrad_params(dy, packed_w, scale, dx, samples, rows, cols);
+  const int te = wide_grid(rows, cols), td = wide_grid(samples, cols);
+  mfma::wide::backward_pair_kernel<<<te + td, mfma::wide::THREADS, 0, stream>>>(pe, pd, te);
   return static_cast<int>(hipGetLastError());
 }
 
