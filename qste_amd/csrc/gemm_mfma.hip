@@ -245,9 +245,11 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   // Steps past the end are issued too, at an offset past every buffer's
   // end: they read zero without touching memory and keep the number of
   // loads in flight the same on every step.
-  auto issue = [&](int it, uint8_t* As, uint8_t* Bs) {
+  // part < 0: the whole step; part 0..3: a quarter of it (the register
+  // loads of bits along N first, the direct bit loads of bits along K last)
+  auto issue = [&](int it, uint8_t* As, uint8_t* Bs, int part = -1) {
     const bool live = it < nk;
-    if (BKIND == B_BITS_ALONG_N) {
+    if (BKIND == B_BITS_ALONG_N && part <= 0) {
       const uint32_t koff = live ? static_cast<uint32_t>(it) * BK * static_cast<uint32_t>(p.pb) : 0x80000000u;
       bw[0] = ld32(rb, b_voff + koff);
       bw[1] = ld32(rb, b_voff + b_step + koff);
@@ -258,11 +260,12 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
     const uint32_t k_off = live ? static_cast<uint32_t>(it) * a_kstep : 0x80000000u;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
+      if (part >= 0 && (j >> 1) != part) continue;
       uint8_t* dst = AKIND == A_ROWS_M ? As + (64 * wave + 8 * j) * 128 : As + (8 * wave + j) * APK;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_t*)dst, 16, a_voff[j & 1],
                                                static_cast<int>(j * a_row8 + k_off), 0, 0);
     }
-    if (BKIND == B_BITS_ALONG_K) {
+    if (BKIND == B_BITS_ALONG_K && (part < 0 || part == 3)) {
       const uint32_t kb = live ? static_cast<uint32_t>(it) * (BK / 8) : 0x80000000u;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -339,6 +342,31 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
       }
     }
   };
+  auto load_a1 = [&](const uint8_t* As, int s, int mb, bf16x8* dst) {
+    if (AKIND == A_ROWS_M) {
+      const int row = 128 * wm + 32 * mb + l32;
+      dst[mb] = *reinterpret_cast<const bf16x8*>(As + row * 128 + 16 * ((2 * s + kg) ^ swz(row)));
+    } else {
+      const uint8_t* src = As + tr_base + APK * 8 * s + 128 * mb;
+      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(src));
+      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(src + 2 * APK));
+      dst[mb] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+  };
+  auto expand_b1 = [&](const uint8_t* Bs, const uint16_t* Ss, int s, int nb, bf16x8* dst) {
+    if (BKIND == B_BITS_ALONG_K) {
+      dst[nb] = signs_along_k(static_cast<uint32_t>(bits[nb] >> (8 * (2 * s + kg))) & 0xFFu, one);
+    } else {
+      const int kk = 16 * s + 8 * kg;
+      const uint4 sc = *reinterpret_cast<const uint4*>(Ss + kk);
+      const int c = 128 * wn + 32 * nb + l32;
+      dst[nb] = signs_across_k(*reinterpret_cast<const uint64_t*>(Bs + (c >> 3) * LDB_N + kk), c & 7, sc);
+    }
+  };
+  auto mfma_row = [&](int s, int mb) {
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = mma(a[s & 1][mb], b[s & 1][nb], acc[mb][nb]);
+  };
   auto mfmas = [&](int s) {
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
@@ -359,17 +387,33 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
                   uint8_t* N3b) {
 #pragma unroll
     for (int s = 0; s < 3; ++s) {
-      load_a(As, s + 1, a[(s + 1) & 1]);
-      mfmas(s);
-      expand_b(Bs, Ss, s + 1, b[(s + 1) & 1]);
-      __builtin_amdgcn_sched_barrier(0);
+      // one block row of MFMAs at a time, each beside one fragment read and
+      // one sign expansion for the next substep
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        load_a1(As, s + 1, mb, a[(s + 1) & 1]);
+        mfma_row(s, mb);
+        expand_b1(Bs, Ss, s + 1, mb, b[(s + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     stage_barrier<BKIND == B_BITS_ALONG_K ? NL : 8>();
     store_b(N2b, N2s);
-    issue(it + 3, N3a, N3b);
+    // substep 3, one block row at a time, with a quarter of step it+3's
+    // loads issued beside each, then step it+1's first fragments
+    issue(it + 3, N3a, N3b, 0);
+    mfma_row(3, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(it + 3, N3a, N3b, 1);
     load_a(N1a, 0, a[0]);
+    mfma_row(3, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(it + 3, N3a, N3b, 2);
     load_bits(N1b);
-    mfmas(3);
+    mfma_row(3, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(it + 3, N3a, N3b, 3);
+    mfma_row(3, 3);
     expand_b(N1b, N1s, 0, b[0]);
     __builtin_amdgcn_sched_barrier(0);
   };
