@@ -240,7 +240,8 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
     b_step = static_cast<uint32_t>(32 * p.pb);  // dword t + 256 is 32 k-rows further
   }
   uint32_t bw[2] = {0u, 0u};
-  float bsc = 0.0f;
+  uint32_t bsv = 0u;   // loaded scale bits (with a per-k scale)
+  float balt = 0.0f;   // 1 or 0 (without one: k < K)
 
   // Steps past the end are issued too, at an offset past every buffer's
   // end: they read zero without touching memory and keep the number of
@@ -254,8 +255,8 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
       bw[0] = ld32(rb, b_voff + koff);
       bw[1] = ld32(rb, b_voff + b_step + koff);
       const uint32_t soff = live ? static_cast<uint32_t>((it * BK + (tid & 63)) * 4) : 0x80000000u;
-      const uint32_t sv = ld32(rs, soff);
-      bsc = p.kscale ? __uint_as_float(sv) : ((live && it * BK + (tid & 63) < p.K) ? 1.0f : 0.0f);
+      bsv = ld32(rs, soff);
+      balt = static_cast<float>(static_cast<int>(live) & static_cast<int>(it * BK + (tid & 63) < p.K));
     }
     const uint32_t k_off = live ? static_cast<uint32_t>(it) * a_kstep : 0x80000000u;
 #pragma unroll
@@ -284,7 +285,7 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
 #pragma unroll
         for (int i = 0; i < 4; ++i) Bs[(4 * g + i) * LDB_N + k] = static_cast<uint8_t>(neg >> (8 * i));
       }
-      if (tid < BK) Ss[tid] = f32_to_bf16(bsc);
+      if (tid < BK) Ss[tid] = f32_to_bf16(p.kscale ? __uint_as_float(bsv) : balt);
     }
   };
 
