@@ -125,8 +125,8 @@ __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& 
 }
 
 // ===========================================================================
-// 256 x 256 outputs per workgroup of 4 waves (2 x 2, each 128 x 128 = 4 x 4
-// blocks of 32 x 32 held in AGPRs), one workgroup per CU.  The dense operand
+// 256 x 256 outputs per workgroup of 4 waves (each all 256 rows and 64
+// columns = 8 x 2 blocks of 32 x 32 held in AGPRs), one workgroup per CU.  The dense operand
 // reaches LDS by direct buffer->LDS loads (no register staging) into four
 // stages, issued three K steps ahead; the workgroup synchronises once per K
 // step, three quarters into it, after which the next stage's first
@@ -137,7 +137,16 @@ namespace wide {
 constexpr int BM = 256, BN = 256, BK = 64, THREADS = 256;
 constexpr int A_STAGE = BM * BK * 2;  // bytes: 256 rows x 128 B, 16-byte chunks XOR-swizzled
 constexpr int B_STAGE = BN * BK / 8;  // bytes: 256 rows x 8 B of sign bits
-constexpr int EPL = 272;              // bytes per staged output row (256 + pad)
+// Each wave covers all 256 rows and a quarter of the columns: every sign
+// fragment it expands feeds 8 MFMAs (the expansion VALU work, not the LDS
+// reads of the dense operand, is what limits a wave).
+constexpr int WAVES_N = 4;            // waves across N, the rest across M
+constexpr int WAVES_M = 4 / WAVES_N;
+constexpr int WMR = BM / WAVES_M;     // rows per wave
+constexpr int WNC = BN / WAVES_N;     // columns per wave
+constexpr int MBN = WMR / 32, NBN = WNC / 32;  // 32 x 32 blocks per wave
+constexpr int EPL = 2 * WNC + 16;     // bytes per staged output row (+ pad)
+constexpr int EPR = WNC == 128 ? 32 : 16;  // staged output rows per piece
 typedef __attribute__((address_space(3))) void lds_t;
 
 // Chunk c of A row r is stored at chunk c ^ swz(r): the 16 rows that one
@@ -190,7 +199,7 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   constexpr int NL = Loads<BKIND>::value;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int l32 = lane & 31, kg = lane >> 5;
   const int tiles_m = static_cast<int>((p.M + BM - 1) / BM);
   const int tiles_n = static_cast<int>((p.N + BN - 1) / BN);
@@ -289,28 +298,28 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
     }
   };
 
-  f32x16 acc[4][4];
+  f32x16 acc[MBN][NBN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MBN; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < NBN; ++j) acc[i][j] = f32x16{};
 
   // fragments: a[buf][mb] dense rows, b[buf][nb] expanded signs; substep s
   // (k = 16s .. 16s+15 of the step) uses buffer s & 1
-  bf16x8 a[2][4], b[2][4];
-  uint64_t bits[4];
+  bf16x8 a[2][MBN], b[2][NBN];
+  uint64_t bits[NBN];
   // A as rows of K: this lane, as a source of the transposed read, names
   // k-row 16s + 8kg + 4h + t and m = 128wm + 32mb + 16(g%2) + 4a .. +3
   // (lane = 16g + 4a... with t = (lane%16)/4, a = lane%4, g = lane/16);
   // as a destination it receives A[m = l32][k = 16s + 8kg + 4h + 0..3].
   const int tr_t = (lane & 15) >> 2, tr_a = lane & 3, tr_g = lane >> 4;
-  const int tr_base = APK * (4 * (tr_g >> 1) + (tr_t >> 1)) + 32 * (16 * wm + 2 * (tr_g & 1) + (tr_a >> 1)) +
+  const int tr_base = APK * (4 * (tr_g >> 1) + (tr_t >> 1)) + 32 * (WMR / 8 * wm + 2 * (tr_g & 1) + (tr_a >> 1)) +
                       16 * (tr_t & 1) + 8 * (tr_a & 1);
   auto load_a = [&](const uint8_t* As, int s, bf16x8* dst) {
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int mb = 0; mb < MBN; ++mb) {
       if (AKIND == A_ROWS_M) {
-        const int row = 128 * wm + 32 * mb + l32;
+        const int row = WMR * wm + 32 * mb + l32;
         dst[mb] = *reinterpret_cast<const bf16x8*>(As + row * 128 + 16 * ((2 * s + kg) ^ swz(row)));
       } else {
         const uint8_t* src = As + tr_base + APK * 8 * s + 128 * mb;
@@ -324,28 +333,28 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   auto load_bits = [&](const uint8_t* Bs) {
     if (BKIND == B_BITS_ALONG_K) {
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
-        bits[nb] = ~*reinterpret_cast<const uint64_t*>(Bs + 8 * (128 * wn + 32 * nb + l32));
+      for (int nb = 0; nb < NBN; ++nb)
+        bits[nb] = ~*reinterpret_cast<const uint64_t*>(Bs + 8 * (WNC * wn + 32 * nb + l32));
     }
   };
   auto expand_b = [&](const uint8_t* Bs, const uint16_t* Ss, int s, bf16x8* dst) {
     if (BKIND == B_BITS_ALONG_K) {
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
+      for (int nb = 0; nb < NBN; ++nb)
         dst[nb] = signs_along_k(static_cast<uint32_t>(bits[nb] >> (8 * (2 * s + kg))) & 0xFFu, one);
     } else {
       const int kk = 16 * s + 8 * kg;
       const uint4 sc = *reinterpret_cast<const uint4*>(Ss + kk);
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        const int c = 128 * wn + 32 * nb + l32;
+      for (int nb = 0; nb < NBN; ++nb) {
+        const int c = WNC * wn + 32 * nb + l32;
         dst[nb] = signs_across_k(*reinterpret_cast<const uint64_t*>(Bs + (c >> 3) * LDB_N + kk), c & 7, sc);
       }
     }
   };
   auto load_a1 = [&](const uint8_t* As, int s, int mb, bf16x8* dst) {
     if (AKIND == A_ROWS_M) {
-      const int row = 128 * wm + 32 * mb + l32;
+      const int row = WMR * wm + 32 * mb + l32;
       dst[mb] = *reinterpret_cast<const bf16x8*>(As + row * 128 + 16 * ((2 * s + kg) ^ swz(row)));
     } else {
       const uint8_t* src = As + tr_base + APK * 8 * s + 128 * mb;
@@ -360,19 +369,21 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
     } else {
       const int kk = 16 * s + 8 * kg;
       const uint4 sc = *reinterpret_cast<const uint4*>(Ss + kk);
-      const int c = 128 * wn + 32 * nb + l32;
+      const int c = WNC * wn + 32 * nb + l32;
       dst[nb] = signs_across_k(*reinterpret_cast<const uint64_t*>(Bs + (c >> 3) * LDB_N + kk), c & 7, sc);
     }
   };
-  auto mfma_row = [&](int s, int mb) {
+  // MFMA chunk q (0..3) of a substep: blocks 4q .. 4q+3 in (mb, nb) order
+  auto mfma_row = [&](int s, int q) {
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = mma(a[s & 1][mb], b[s & 1][nb], acc[mb][nb]);
+    for (int i = 4 * q; i < 4 * q + 4; ++i)
+      acc[i / NBN][i % NBN] = mma(a[s & 1][i / NBN], b[s & 1][i % NBN], acc[i / NBN][i % NBN]);
   };
   auto mfmas = [&](int s) {
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < MBN; ++mb)
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = mma(a[s & 1][mb], b[s & 1][nb], acc[mb][nb]);
+      for (int nb = 0; nb < NBN; ++nb) acc[mb][nb] = mma(a[s & 1][mb], b[s & 1][nb], acc[mb][nb]);
   };
 
   // K step `it` on stage (As, Bs, Ss); substep 0's fragments are in buffer 0.
@@ -391,10 +402,16 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
       // one block row of MFMAs at a time, each beside one fragment read and
       // one sign expansion for the next substep
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        load_a1(As, s + 1, mb, a[(s + 1) & 1]);
-        mfma_row(s, mb);
-        expand_b1(Bs, Ss, s + 1, mb, b[(s + 1) & 1]);
+      for (int q = 0; q < 4; ++q) {
+        if (MBN >= 4) {
+#pragma unroll
+          for (int mb = q * MBN / 4; mb < (q + 1) * MBN / 4; ++mb) load_a1(As, s + 1, mb, a[(s + 1) & 1]);
+        } else if (q < MBN) {
+          load_a1(As, s + 1, q, a[(s + 1) & 1]);
+        }
+        mfma_row(s, q);
+#pragma unroll
+        for (int nb = q * NBN / 4; nb < (q + 1) * NBN / 4; ++nb) expand_b1(Bs, Ss, s + 1, nb, b[(s + 1) & 1]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -456,7 +473,7 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
 
   if (EPI == EPI_EVIDENCE) {
     // E0 = acc + v[m]; E = E0 * s[m] (fp32, 32 lanes x 4 bytes per row per
-    // store); row partials of E0 * sign_w over this wave's 128 columns.
+    // store); row partials of E0 * sign_w over this wave's columns.
     // The tile's sign_w bits (256 rows x 32 bytes), v and s go to LDS first.
     uint8_t* wst = A0;                                  // [256][32] bytes
     float* vst = reinterpret_cast<float*>(A0 + 8192);   // [256]
@@ -476,19 +493,20 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
     stage_barrier<0>();
     float* ev = static_cast<float*>(p.out);
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int mb = 0; mb < MBN; ++mb) {
       float part[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int lrow = 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
+        const int lrow = WMR * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
         const int64_t row = m0 + lrow;
         const float add = vst[lrow], mul = sst[lrow];
-        const uint4 w = *reinterpret_cast<const uint4*>(wst + lrow * 32 + 16 * wn);
-        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+        uint32_t wd[NBN];
+#pragma unroll
+        for (int h = 0; h < NBN; ++h) wd[h] = *reinterpret_cast<const uint32_t*>(wst + lrow * 32 + (WNC / 8) * wn + 4 * h);
         float acc_part = 0.0f;
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-          const int64_t col = n0 + 128 * wn + 32 * nb + l32;
+        for (int nb = 0; nb < NBN; ++nb) {
+          const int64_t col = n0 + WNC * wn + 32 * nb + l32;
           const float e0 = acc[mb][nb][r] + add;
           // columns past N hold zero bits and contribute -e0: skip them
           if (col < p.N) acc_part += ((wd[nb] >> l32) & 1u) ? e0 : -e0;
@@ -512,9 +530,9 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
         }
         const float tot = part[0] + __shfl_xor(part[0], 1, 64);
         const int r = 8 * ((l32 >> 4) & 1) + 4 * ((l32 >> 3) & 1) + 2 * ((l32 >> 2) & 1) + ((l32 >> 1) & 1);
-        const int64_t row = m0 + 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
+        const int64_t row = m0 + WMR * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
         if ((l32 & 1) == 0 && row < p.M) {
-          const int64_t slot = 2 * static_cast<int64_t>(tn) + wn;
+          const int64_t slot = WAVES_N * static_cast<int64_t>(tn) + wn;
           p.gs_partial[slot * p.M + row] = tot;
         }
       }
@@ -522,16 +540,16 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
     return;
   }
 
-  // Epilogue: (scale and bias,) round to bf16, stage through LDS one
-  // quarter (32 of the wave's 128 rows) at a time so each row segment of 128
-  // outputs leaves as 16 lanes x 16 contiguous bytes.  Waves 0, 1 stage in
-  // A0 and waves 2, 3 in A1.
+  // Epilogue: (scale and bias,) round to bf16 and stage through LDS EPR rows
+  // at a time so each row segment of the wave's WNC outputs leaves as
+  // 16-byte stores of consecutive lanes.  Waves 0, 1 stage in A0 and waves
+  // 2, 3 in A1.
   uint16_t* y = static_cast<uint16_t*>(p.out);
-  uint8_t* stg = (wave < 2 ? A0 : A1) + (wave & 1) * (32 * EPL);
-  float sc[4], bi[4];
+  uint8_t* stg = (wave < 2 ? A0 : A1) + (wave & 1) * (EPR * EPL);
+  float sc[NBN], bi[NBN];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
-    const int64_t col = n0 + 128 * wn + 32 * nb + l32;
+  for (int nb = 0; nb < NBN; ++nb) {
+    const int64_t col = n0 + WNC * wn + 32 * nb + l32;
     sc[nb] = (EPI == EPI_FORWARD && col < p.N && p.n_scale) ? p.n_scale[col] : 1.0f;
     bi[nb] = (EPI == EPI_FORWARD && col < p.N && p.n_bias) ? p.n_bias[col] : 0.0f;
   }
@@ -539,45 +557,50 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   // columns of one row: even lanes row r, odd lanes row r+1.
   const bool odd = l32 & 1;
   const bool vec_ok = (p.N & 7) == 0;
+  constexpr int CPR = 2 * WNC / 16;  // 16-byte chunks per staged row
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
+  for (int mb = 0; mb < MBN; ++mb) {
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
+    for (int h = 0; h < 32 / EPR; ++h) {
+      // rows EPR*h .. of the block row: accumulator registers (EPR/2)*h ..
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        float v0 = acc[mb][nb][r], v1 = acc[mb][nb][r + 1];
-        if (EPI == EPI_FORWARD) {
-          v0 = v0 * sc[nb];
-          v0 = v0 + bi[nb];
-          v1 = v1 * sc[nb];
-          v1 = v1 + bi[nb];
+      for (int nb = 0; nb < NBN; ++nb) {
+#pragma unroll
+        for (int r = (EPR / 2) * h; r < (EPR / 2) * (h + 1); r += 2) {
+          float v0 = acc[mb][nb][r], v1 = acc[mb][nb][r + 1];
+          if (EPI == EPI_FORWARD) {
+            v0 = v0 * sc[nb];
+            v0 = v0 + bi[nb];
+            v1 = v1 * sc[nb];
+            v1 = v1 + bi[nb];
+          }
+          const float send = odd ? v0 : v1;
+          const float recv = __int_as_float(
+              __builtin_amdgcn_update_dpp(0, __float_as_int(send), 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
+          const float lo = odd ? recv : v0;
+          const float hi = odd ? v1 : recv;
+          const uint32_t word =
+              static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+          const int row = 8 * (r >> 2) + 4 * kg + (r & 3) + (odd ? 1 : 0) - EPR * h;
+          *reinterpret_cast<uint32_t*>(stg + row * EPL + 2 * (32 * nb + (l32 & ~1))) = word;
         }
-        const float send = odd ? v0 : v1;
-        const float recv = __int_as_float(
-            __builtin_amdgcn_update_dpp(0, __float_as_int(send), 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
-        const float lo = odd ? recv : v0;
-        const float hi = odd ? v1 : recv;
-        const uint32_t word =
-            static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
-        const int row = 8 * (r >> 2) + 4 * kg + (r & 3) + (odd ? 1 : 0);
-        *reinterpret_cast<uint32_t*>(stg + row * EPL + 2 * (32 * nb + (l32 & ~1))) = word;
       }
-    }
-    // 32 rows x 256 bytes: lane -> row 4i + lane/16, 16-byte chunk lane%16
+      // EPR rows x 2*WNC bytes: lane -> row (64 / CPR) i + lane / CPR, chunk lane % CPR
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = 4 * i + (lane >> 4), chunk = lane & 15;
-      const uint4 v = *reinterpret_cast<const uint4*>(stg + row * EPL + 16 * chunk);
-      const int64_t grow = m0 + 128 * wm + 32 * mb + row;
-      const int64_t gcol = n0 + 128 * wn + 8 * chunk;
-      if (grow < p.M) {
-        if (vec_ok && gcol + 8 <= p.N) {
-          *reinterpret_cast<uint4*>(y + grow * p.N + gcol) = v;
-        } else {
-          const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+      for (int i = 0; i < EPR * CPR / 64; ++i) {
+        const int row = (64 / CPR) * i + lane / CPR, chunk = lane % CPR;
+        const uint4 v = *reinterpret_cast<const uint4*>(stg + row * EPL + 16 * chunk);
+        const int64_t grow = m0 + WMR * wm + 32 * mb + EPR * h + row;
+        const int64_t gcol = n0 + WNC * wn + 8 * chunk;
+        if (grow < p.M) {
+          if (vec_ok && gcol + 8 <= p.N) {
+            *reinterpret_cast<uint4*>(y + grow * p.N + gcol) = v;
+          } else {
+            const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
 #pragma unroll
-          for (int t = 0; t < 8; ++t)
-            if (gcol + t < p.N) y[grow * p.N + gcol + t] = e[t];
+            for (int t = 0; t < 8; ++t)
+              if (gcol + t < p.N) y[grow * p.N + gcol + t] = e[t];
+          }
         }
       }
     }
@@ -706,7 +729,7 @@ int mfma_linear_dgrad(const void* dy, int dtype, const uint8_t* packed, const fl
   return static_cast<int>(hipGetLastError());
 }
 
-int64_t mfma_evidence_tiles(int64_t cols) { return 2 * ((cols + mfma::wide::BN - 1) / mfma::wide::BN); }
+int64_t mfma_evidence_tiles(int64_t cols) { return mfma::wide::WAVES_N * ((cols + mfma::wide::BN - 1) / mfma::wide::BN); }
 
 int mfma_evidence(const void* dy, int dtype, const uint8_t* packed_x, const float* x_scale, float* ev,
                   int64_t samples, int64_t rows, int64_t cols, const float* m_add, const float* m_scale,
