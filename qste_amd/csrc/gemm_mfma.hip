@@ -34,13 +34,16 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t kRsrcWord3 = 0x00020000u;
 
 enum { A_ROWS_M = 0, A_ROWS_K = 1 };        // A[m][k] stored with k (or m) contiguous
-enum { B_BITS_ALONG_K = 0, B_BITS_ALONG_N = 1 };
+// B_BITS_ALONG_K_SCALED: bits along K (a transposed copy of the signs) and
+// a per-k bf16 scale, both brought in by direct loads.
+enum { B_BITS_ALONG_K = 0, B_BITS_ALONG_N = 1, B_BITS_ALONG_K_SCALED = 2 };
 enum { EPI_FORWARD = 0, EPI_PLAIN = 1, EPI_EVIDENCE = 2 };
 
 struct Params {
   const uint16_t* a;     // bf16 dense operand (x or dy)
   const uint8_t* bits;   // packed signs of the +-1 operand
   const float* kscale;   // per-k scale folded into the bit operand (dgrad/evidence)
+  const uint16_t* kscale16;  // the same as bf16 (bits along K with a scale)
   void* out;
   int64_t M, N, K;
   int64_t lda;           // elements between rows of the dense source
@@ -53,7 +56,8 @@ struct Params {
   const float* m_add;    // evidence
   const float* m_scale;  // evidence
   const uint8_t* w_bits; // evidence: sign_w for the scale gradient
-  float* gs_partial;     // evidence: [2 * tiles_n][M]
+  int64_t w_pb;          // evidence: bytes per row of w_bits
+  float* gs_partial;     // evidence: [WAVES_N * tiles_n][M]
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
@@ -85,6 +89,18 @@ __device__ __forceinline__ bf16x8 signs_along_k(uint32_t neg, uint32_t one) {
   r.y = (pk_shl(tt, u16x2{13, 12}) & 0x80008000u) | one;
   r.z = (pk_shl(tt, u16x2{11, 10}) & 0x80008000u) | one;
   r.w = (pk_shl(tt, u16x2{9, 8}) & 0x80008000u) | one;
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+// 8 scaled signs along k: as signs_along_k, with the 8 nonnegative bf16
+// scales (as pairs) in place of +1.
+__device__ __forceinline__ bf16x8 scaled_signs_along_k(uint32_t neg, uint4 scale) {
+  const uint32_t tt = neg * 0x10001u;
+  u32x4 r;
+  r.x = (pk_shl(tt, u16x2{15, 14}) & 0x80008000u) | scale.x;
+  r.y = (pk_shl(tt, u16x2{13, 12}) & 0x80008000u) | scale.y;
+  r.z = (pk_shl(tt, u16x2{11, 10}) & 0x80008000u) | scale.z;
+  r.w = (pk_shl(tt, u16x2{9, 8}) & 0x80008000u) | scale.w;
   return __builtin_bit_cast(bf16x8, r);
 }
 
@@ -175,7 +191,8 @@ constexpr int LDB_N = BK + 8;
 constexpr int BN_STAGE = (BN / 8) * LDB_N;  // bytes
 template <int BKIND>
 struct Loads {
-  // buffer loads per wave per K step: 8 A loads, plus the bit loads
+  // buffer loads per wave per K step: 8 A loads, plus 2 direct bit loads
+  // (and 1 scale load), or 3 register loads of bits along N
   static constexpr int value = BKIND == B_BITS_ALONG_K ? 10 : 11;
 };
 
@@ -239,7 +256,9 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   __amdgpu_buffer_rsrc_t rb;
   uint32_t b_voff, b_step;
   __amdgpu_buffer_rsrc_t rs = rsrc(p.kscale, p.kscale ? p.K * 4 : 0);
-  if (BKIND == B_BITS_ALONG_K) {
+  // bf16 scales are padded with zeros to a whole number of K steps
+  const __amdgpu_buffer_rsrc_t rs16 = rsrc(p.kscale16, BKIND == B_BITS_ALONG_K_SCALED ? int64_t{nk} * BK * 2 : 0);
+  if (BKIND != B_BITS_ALONG_N) {
     rb = rsrc(p.bits + n0 * p.pb, (p.bit_rows - n0) * p.pb);
     b_voff = static_cast<uint32_t>((64 * wave + (lane >> 1)) * p.pb + 4 * (lane & 1));
     b_step = static_cast<uint32_t>(32 * p.pb);
@@ -257,7 +276,7 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   // loads in flight the same on every step.
   // part < 0: the whole step; part 0..3: a quarter of it (the register
   // loads of bits along N first, the direct bit loads of bits along K last)
-  auto issue = [&](int it, uint8_t* As, uint8_t* Bs, int part = -1) {
+  auto issue = [&](int it, uint8_t* As, uint8_t* Bs, uint16_t* Ss, int part = -1) {
     const bool live = it < nk;
     if (BKIND == B_BITS_ALONG_N && part <= 0) {
       const uint32_t koff = live ? static_cast<uint32_t>(it) * BK * static_cast<uint32_t>(p.pb) : 0x80000000u;
@@ -275,12 +294,21 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_t*)dst, 16, a_voff[j & 1],
                                                static_cast<int>(j * a_row8 + k_off), 0, 0);
     }
-    if (BKIND == B_BITS_ALONG_K && (part < 0 || part == 3)) {
+    if (BKIND != B_BITS_ALONG_N && (part < 0 || part == 3)) {
       const uint32_t kb = live ? static_cast<uint32_t>(it) * (BK / 8) : 0x80000000u;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_t*)(Bs + (64 * wave + 32 * j) * 8), 4, b_voff,
                                                  static_cast<int>(j * b_step + kb), 0, 0);
+      if (BKIND == B_BITS_ALONG_K_SCALED) {
+        // wave w brings the bf16 scales of k = 16w .. 16w+15, a pair per
+        // lane (lanes 0..7: direct loads narrower than a dword still take a
+        // dword slot per lane)
+        const uint32_t ks = live ? static_cast<uint32_t>(it * BK + 16 * wave) * 2 : 0x80000000u;
+        if (lane < 8)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs16, (lds_t*)(Ss + 16 * wave), 4,
+                                                   static_cast<uint32_t>(4 * lane), static_cast<int>(ks), 0, 0);
+      }
     }
   };
   // bits along N: write the staged registers of a step into its stage
@@ -331,7 +359,7 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   };
   // bits along K: this lane's 64 k-bits of each of its 4 columns
   auto load_bits = [&](const uint8_t* Bs) {
-    if (BKIND == B_BITS_ALONG_K) {
+    if (BKIND != B_BITS_ALONG_N) {
 #pragma unroll
       for (int nb = 0; nb < NBN; ++nb)
         bits[nb] = ~*reinterpret_cast<const uint64_t*>(Bs + 8 * (WNC * wn + 32 * nb + l32));
@@ -342,6 +370,11 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
 #pragma unroll
       for (int nb = 0; nb < NBN; ++nb)
         dst[nb] = signs_along_k(static_cast<uint32_t>(bits[nb] >> (8 * (2 * s + kg))) & 0xFFu, one);
+    } else if (BKIND == B_BITS_ALONG_K_SCALED) {
+      const uint4 sc = *reinterpret_cast<const uint4*>(Ss + 16 * s + 8 * kg);
+#pragma unroll
+      for (int nb = 0; nb < NBN; ++nb)
+        dst[nb] = scaled_signs_along_k(static_cast<uint32_t>(bits[nb] >> (8 * (2 * s + kg))) & 0xFFu, sc);
     } else {
       const int kk = 16 * s + 8 * kg;
       const uint4 sc = *reinterpret_cast<const uint4*>(Ss + kk);
@@ -366,6 +399,9 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   auto expand_b1 = [&](const uint8_t* Bs, const uint16_t* Ss, int s, int nb, bf16x8* dst) {
     if (BKIND == B_BITS_ALONG_K) {
       dst[nb] = signs_along_k(static_cast<uint32_t>(bits[nb] >> (8 * (2 * s + kg))) & 0xFFu, one);
+    } else if (BKIND == B_BITS_ALONG_K_SCALED) {
+      const uint4 sc = *reinterpret_cast<const uint4*>(Ss + 16 * s + 8 * kg);
+      dst[nb] = scaled_signs_along_k(static_cast<uint32_t>(bits[nb] >> (8 * (2 * s + kg))) & 0xFFu, sc);
     } else {
       const int kk = 16 * s + 8 * kg;
       const uint4 sc = *reinterpret_cast<const uint4*>(Ss + kk);
@@ -396,7 +432,7 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   // Step it+1's first fragments are read while substep 3 runs.
   auto step = [&](int it, const uint8_t* As, const uint8_t* Bs, const uint16_t* Ss, const uint8_t* N1a,
                   const uint8_t* N1b, const uint16_t* N1s, uint8_t* N2b, uint16_t* N2s, uint8_t* N3a,
-                  uint8_t* N3b) {
+                  uint8_t* N3b, uint16_t* N3s) {
 #pragma unroll
     for (int s = 0; s < 3; ++s) {
       // one block row of MFMAs at a time, each beside one fragment read and
@@ -415,58 +451,58 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    stage_barrier<BKIND == B_BITS_ALONG_K ? NL : 8>();
+    stage_barrier<BKIND != B_BITS_ALONG_N ? NL : 8>();
     store_b(N2b, N2s);
     // substep 3, one block row at a time, with a quarter of step it+3's
     // loads issued beside each, then step it+1's first fragments
-    issue(it + 3, N3a, N3b, 0);
+    issue(it + 3, N3a, N3b, N3s, 0);
     mfma_row(3, 0);
     __builtin_amdgcn_sched_barrier(0);
-    issue(it + 3, N3a, N3b, 1);
+    issue(it + 3, N3a, N3b, N3s, 1);
     load_a(N1a, 0, a[0]);
     mfma_row(3, 1);
     __builtin_amdgcn_sched_barrier(0);
-    issue(it + 3, N3a, N3b, 2);
+    issue(it + 3, N3a, N3b, N3s, 2);
     load_bits(N1b);
     mfma_row(3, 2);
     __builtin_amdgcn_sched_barrier(0);
-    issue(it + 3, N3a, N3b, 3);
+    issue(it + 3, N3a, N3b, N3s, 3);
     mfma_row(3, 3);
     expand_b(N1b, N1s, 0, b[0]);
     __builtin_amdgcn_sched_barrier(0);
   };
 
   uint16_t* S0 = Sc;
-  uint16_t* S1 = Sc + (BKIND == B_BITS_ALONG_N ? BK : 0);
-  uint16_t* S2 = Sc + (BKIND == B_BITS_ALONG_N ? 2 * BK : 0);
-  uint16_t* S3 = Sc + (BKIND == B_BITS_ALONG_N ? 3 * BK : 0);
+  uint16_t* S1 = Sc + (BKIND != B_BITS_ALONG_K ? BK : 0);
+  uint16_t* S2 = Sc + (BKIND != B_BITS_ALONG_K ? 2 * BK : 0);
+  uint16_t* S3 = Sc + (BKIND != B_BITS_ALONG_K ? 3 * BK : 0);
   // prologue: stages 0 and 1 complete (bits along N written from registers),
   // step 2 issued
-  issue(0, A0, B0);
+  issue(0, A0, B0, S0);
   if (BKIND == B_BITS_ALONG_N) {
     stage_barrier<8>();  // registers of step 0 (the 8 A loads may stay in flight)
     store_b(B0, S0);
   }
-  issue(1, A1, B1);
+  issue(1, A1, B1, S1);
   if (BKIND == B_BITS_ALONG_N) {
     stage_barrier<8>();
     store_b(B1, S1);
   }
-  issue(2, A2, B2);
-  stage_barrier<NL == 10 ? 2 * NL : NL>();  // along K: steps 0, 1 complete; along N: step 0, 1
+  issue(2, A2, B2, S2);
+  stage_barrier<BKIND != B_BITS_ALONG_N ? 2 * NL : NL>();  // along K: steps 0, 1 complete; along N: step 0, 1
   load_a(A0, 0, a[0]);
   load_bits(B0);
   expand_b(B0, S0, 0, b[0]);
   int it = 0;
   for (; it + 4 <= nk; it += 4) {
-    step(it, A0, B0, S0, A1, B1, S1, B2, S2, A3, B3);
-    step(it + 1, A1, B1, S1, A2, B2, S2, B3, S3, A0, B0);
-    step(it + 2, A2, B2, S2, A3, B3, S3, B0, S0, A1, B1);
-    step(it + 3, A3, B3, S3, A0, B0, S0, B1, S1, A2, B2);
+    step(it, A0, B0, S0, A1, B1, S1, B2, S2, A3, B3, S3);
+    step(it + 1, A1, B1, S1, A2, B2, S2, B3, S3, A0, B0, S0);
+    step(it + 2, A2, B2, S2, A3, B3, S3, B0, S0, A1, B1, S1);
+    step(it + 3, A3, B3, S3, A0, B0, S0, B1, S1, A2, B2, S2);
   }
-  if (it < nk) step(it, A0, B0, S0, A1, B1, S1, B2, S2, A3, B3);
-  if (it + 1 < nk) step(it + 1, A1, B1, S1, A2, B2, S2, B3, S3, A0, B0);
-  if (it + 2 < nk) step(it + 2, A2, B2, S2, A3, B3, S3, B0, S0, A1, B1);
+  if (it < nk) step(it, A0, B0, S0, A1, B1, S1, B2, S2, A3, B3, S3);
+  if (it + 1 < nk) step(it + 1, A1, B1, S1, A2, B2, S2, B3, S3, A0, B0, S0);
+  if (it + 2 < nk) step(it + 2, A2, B2, S2, A3, B3, S3, B0, S0, A1, B1, S1);
 
   // every in-flight load has landed (the stages are free for the epilogue)
   stage_barrier<0>();
@@ -480,8 +516,8 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
     float* sst = vst + BM;                              // [256]
     {
       const int64_t row = m0 + tid;
-      const __amdgpu_buffer_rsrc_t rw = rsrc(p.w_bits, p.w_bits ? p.M * p.pb : 0);
-      const uint32_t off = static_cast<uint32_t>(row * p.pb + n0 / 8);
+      const __amdgpu_buffer_rsrc_t rw = rsrc(p.w_bits, p.w_bits ? p.M * p.w_pb : 0);
+      const uint32_t off = static_cast<uint32_t>(row * p.w_pb + n0 / 8);
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
         const uint32_t w = (p.w_bits && row < p.M) ? ld32(rw, off + 4 * d) : 0u;
@@ -611,8 +647,8 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
 template <int AKIND, int BKIND>
 struct StageSizes {
   static constexpr int a = AKIND == A_ROWS_M ? A_STAGE : A_STAGE_K;
-  static constexpr int b = BKIND == B_BITS_ALONG_K ? B_STAGE : BN_STAGE;
-  static constexpr int s = BKIND == B_BITS_ALONG_N ? 4 * BK : 8;
+  static constexpr int b = BKIND == B_BITS_ALONG_N ? BN_STAGE : B_STAGE;
+  static constexpr int s = BKIND == B_BITS_ALONG_K ? 8 : 4 * BK;
 };
 
 #define QSTE_WIDE_STAGES(ASZ, BSZ, SSZ)                           \
@@ -635,14 +671,16 @@ __global__ __launch_bounds__(THREADS, 1) void wide_kernel(Params p) {
 
 // The two large products of a layer's backward in one launch: evidence
 // tiles first (the longer ones), then dgrad tiles, so the grid's last wave
-// of one product is filled by the other instead of leaving CUs idle.
+// of one product is filled by the other instead of leaving CUs idle.  Both
+// take their signs as transposed copies (bits along K) with bf16 per-k
+// scales, prepared by the caller.
 __global__ __launch_bounds__(THREADS, 1) void backward_pair_kernel(Params pe, Params pd, int tiles_e) {
-  QSTE_WIDE_STAGES(A_STAGE_K, BN_STAGE, 4 * BK)
+  QSTE_WIDE_STAGES(A_STAGE_K, B_STAGE, 4 * BK)
   if (static_cast<int>(blockIdx.x) < tiles_e)
-    wide_tile<A_ROWS_K, B_BITS_ALONG_N, EPI_EVIDENCE>(pe, blockIdx.x, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
+    wide_tile<A_ROWS_K, B_BITS_ALONG_K_SCALED, EPI_EVIDENCE>(pe, blockIdx.x, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
   else
-    wide_tile<A_ROWS_M, B_BITS_ALONG_N, EPI_PLAIN>(pd, blockIdx.x - tiles_e, A0, A1, A2, A3, B0, B1, B2, B3,
-                                                   Sc);
+    wide_tile<A_ROWS_M, B_BITS_ALONG_K_SCALED, EPI_PLAIN>(pd, blockIdx.x - tiles_e, A0, A1, A2, A3, B0, B1, B2,
+                                                          B3, Sc);
 }
 #undef QSTE_WIDE_STAGES
 }  // namespace wide
@@ -699,7 +737,7 @@ static mfma::Params evidence_params(const void* dy, const uint8_t* packed_x, con
   p.M = rows; p.N = cols; p.K = samples;
   p.lda = rows; p.pb = cols / 8;
   p.a_rows = samples; p.bit_rows = samples;
-  p.m_add = m_add; p.m_scale = m_scale; p.w_bits = w_bits; p.gs_partial = gs_partial;
+  p.m_add = m_add; p.m_scale = m_scale; p.w_bits = w_bits; p.w_pb = cols / 8; p.gs_partial = gs_partial;
   return p;
 }
 
@@ -742,16 +780,43 @@ int mfma_evidence(const void* dy, int dtype, const uint8_t* packed_x, const floa
   return static_cast<int>(hipGetLastError());
 }
 
-// Evidence (with its fused epilogue) and dgrad of one layer in one launch;
-// returns 1 when either is not for this path.
-int mfma_backward_pair(const void* dy, int dtype, const uint8_t* packed_x, const float* x_scale, float* ev,
-                       const uint8_t* packed_w, const float* scale, void* dx, int64_t samples, int64_t rows,
-                       int64_t cols, const float* m_add, float* gs_partial, hipStream_t stream) {
-  if (!evidence_ok(dy, dtype, packed_x, samples, rows, cols) || !dgrad_ok(dy, dtype, packed_w, samples, rows, cols))
+// Whether mfma_backward_pair takes a call (workspace copies are 256-byte
+// aligned, so only the caller's operands are checked here).
+bool mfma_pair_ok(const void* dy, int dtype, int64_t samples, int64_t rows, int64_t cols) {
+  return dtype == QSTE_BF16 && cols % 64 == 0 && rows % 64 == 0 && rows > 0 && cols > 0 && samples > 0 &&
+         aligned16(dy) && fits32(samples * rows * 2) && fits32(samples * cols / 8) && fits32(rows * cols / 8);
+}
+
+// Evidence (with its fused epilogue) and dgrad of one layer in one launch,
+// from transposed sign copies: x_t [cols][x_t_pitch] (bit k of row c = sign
+// of x[k][c]) and w_t [cols][w_t_pitch] (bit r of row c = sign of W[r][c]),
+// both zero past their K, and bf16 copies of x_scale and scale, zero-padded
+// to a multiple of 64 entries.  Returns 1 when either product is not for
+// this path.
+int mfma_backward_pair(const void* dy, int dtype, const uint8_t* x_t, int64_t x_t_pitch, const uint16_t* x_scale16,
+                       float* ev, const uint8_t* w_t, int64_t w_t_pitch, const uint16_t* scale16,
+                       const uint8_t* packed_w, void* dx, int64_t samples, int64_t rows, int64_t cols,
+                       const float* m_add, const float* scale, float* gs_partial, hipStream_t stream) {
+  if (!evidence_ok(dy, dtype, x_t, samples, rows, cols) || !dgrad_ok(dy, dtype, w_t, samples, rows, cols) ||
+      !fits32(cols * x_t_pitch) || !fits32(cols * w_t_pitch))
     return 1;
-  const mfma::Params pe =
-      evidence_params(dy, packed_x, x_scale, ev, samples, rows, cols, m_add, scale, packed_w, gs_partial);
-  const mfma::Params pd = dgrad_params(dy, packed_w, scale, dx, samples, rows, cols);
+  mfma::Params pe{};
+  pe.a = static_cast<const uint16_t*>(dy);
+  pe.bits = x_t;
+  pe.kscale16 = x_scale16;
+  pe.out = ev;
+  pe.M = rows; pe.N = cols; pe.K = samples;
+  pe.lda = rows; pe.pb = x_t_pitch;
+  pe.a_rows = samples; pe.bit_rows = cols;
+  pe.m_add = m_add; pe.m_scale = scale; pe.w_bits = packed_w; pe.w_pb = cols / 8; pe.gs_partial = gs_partial;
+  mfma::Params pd{};
+  pd.a = static_cast<const uint16_t*>(dy);
+  pd.bits = w_t;
+  pd.kscale16 = scale16;
+  pd.out = dx;
+  pd.M = samples; pd.N = cols; pd.K = rows;
+  pd.lda = rows; pd.pb = w_t_pitch;
+  pd.a_rows = samples; pd.bit_rows = cols;
   const int te = wide_grid(rows, cols), td = wide_grid(samples, cols);
   mfma::wide::backward_pair_kernel<<<te + td, mfma::wide::THREADS, 0, stream>>>(pe, pd, te);
   return static_cast<int>(hipGetLastError());

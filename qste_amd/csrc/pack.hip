@@ -156,6 +156,69 @@ static int grid_for(int64_t work, int threads) {
   return static_cast<int>(blocks);
 }
 
+// Bit transpose of a packed sign matrix: in [rows][in_pitch] bytes (bit j of
+// byte b is column 8b + j) -> out [cols][out_pitch] bytes (bit i of byte b is
+// row 8b + i); bits for rows >= rows are zero.  One thread per 8 x 8 block:
+// eight row bytes become one 64-bit word (byte = row, bit = column) whose
+// transpose (three delta swaps) gives one byte per column.
+__device__ __forceinline__ uint64_t transpose_8x8(uint64_t x) {
+  uint64_t t;
+  t = (x ^ (x >> 7)) & 0x00AA00AA00AA00AAull;
+  x = x ^ t ^ (t << 7);
+  t = (x ^ (x >> 14)) & 0x0000CCCC0000CCCCull;
+  x = x ^ t ^ (t << 14);
+  t = (x ^ (x >> 28)) & 0x00000000F0F0F0F0ull;
+  x = x ^ t ^ (t << 28);
+  return x;
+}
+
+__global__ void transpose_bits_kernel(const uint8_t* __restrict__ in, uint8_t* __restrict__ out, int64_t rows,
+                                      int64_t cols, int64_t in_pitch, int64_t out_pitch) {
+  const int64_t col_blocks = (cols + 7) / 8;
+  const int64_t total = out_pitch * col_blocks;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    // consecutive threads take consecutive row blocks of one column block,
+    // so the byte stores of a column are contiguous
+    const int64_t cb = idx / out_pitch, rb = idx - cb * out_pitch;
+    uint64_t x = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t r = 8 * rb + i;
+      if (r < rows) x |= static_cast<uint64_t>(in[r * in_pitch + cb]) << (8 * i);
+    }
+    x = transpose_8x8(x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t c = 8 * cb + j;
+      if (c < cols) out[c * out_pitch + rb] = static_cast<uint8_t>(x >> (8 * j));
+    }
+  }
+}
+
+// out[i] = bf16(in[i]) for i < n, 0 for n <= i < padded
+__global__ void f32_to_bf16_kernel(const float* __restrict__ in, uint16_t* __restrict__ out, int64_t n,
+                                   int64_t padded) {
+  const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (i < padded) out[i] = i < n ? f32_to_bf16(in[i]) : 0;
+}
+
+int launch_transpose_bits(const uint8_t* in, uint8_t* out, int64_t rows, int64_t cols, int64_t in_pitch,
+                          int64_t out_pitch, hipStream_t stream) {
+  const int64_t total = out_pitch * ((cols + 7) / 8);
+  if (total == 0) return 0;
+  const int64_t blocks = (total + 255) / 256;
+  transpose_bits_kernel<<<static_cast<int>(blocks < 65536 ? blocks : 65536), 256, 0, stream>>>(
+      in, out, rows, cols, in_pitch, out_pitch);
+  return static_cast<int>(hipGetLastError());
+}
+
+int launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, int64_t padded, hipStream_t stream) {
+  if (padded == 0) return 0;
+  f32_to_bf16_kernel<<<ceil_div(padded, 256), 256, 0, stream>>>(in, out, n, padded);
+  return static_cast<int>(hipGetLastError());
+}
+
 int launch_pack_coordinate(const int8_t* coord, uint8_t* packed, int64_t rows, int64_t cols,
                            hipStream_t stream) {
   const int64_t stride = (cols + 7) / 8;
