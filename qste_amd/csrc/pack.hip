@@ -172,31 +172,67 @@ __device__ __forceinline__ uint64_t transpose_8x8(uint64_t x) {
   return x;
 }
 
-__global__ void transpose_bits_kernel(const uint8_t* __restrict__ in, uint8_t* __restrict__ out, int64_t rows,
-                                      int64_t cols, int64_t in_pitch, int64_t out_pitch) {
-  const int64_t col_blocks = (cols + 7) / 8;
-  const int64_t total = out_pitch * col_blocks;
-  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
-       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    // consecutive threads take consecutive row blocks of one column block,
-    // so the byte stores of a column are contiguous
-    const int64_t cb = idx / out_pitch, rb = idx - cb * out_pitch;
-    uint64_t x = 0;
+// A workgroup transposes a 64-row x 512-column tile through LDS: the 64
+// input rows are read as 64-byte segments, each thread transposes two 8 x 8
+// blocks (one column byte, 16 rows), and each output column's 8 bytes (the
+// tile's 64 rows) leave as one 8-byte store.  out_pitch must be a multiple
+// of 8.
+constexpr int kTrRows = 64, kTrColBytes = 64;  // tile: 64 rows x 512 columns
+__global__ __launch_bounds__(256) void transpose_bits_kernel(const uint8_t* __restrict__ in,
+                                                             uint8_t* __restrict__ out, int64_t rows,
+                                                             int64_t cols, int64_t in_pitch,
+                                                             int64_t out_pitch) {
+  __shared__ uint8_t tile[kTrRows][kTrColBytes + 4];
+  __shared__ uint64_t otile[8 * kTrColBytes];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kTrRows;
+  const int64_t cb0 = static_cast<int64_t>(blockIdx.x) * kTrColBytes;
+  const int tid = threadIdx.x;
+  {
+    // 64 rows x 64 bytes, 16 bytes per thread
+    const int row = tid >> 2, part = tid & 3;
+    const int64_t r = r0 + row;
+    const bool dwords = (in_pitch & 3) == 0 && (reinterpret_cast<uintptr_t>(in) & 3) == 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t r = 8 * rb + i;
-      if (r < rows) x |= static_cast<uint64_t>(in[r * in_pitch + cb]) << (8 * i);
-    }
-    x = transpose_8x8(x);
+    for (int d = 0; d < 4; ++d) {
+      const int64_t cb = cb0 + 16 * part + 4 * d;
+      uint32_t w = 0;
+      if (r < rows) {
+        if (dwords && cb + 4 <= in_pitch) {
+          w = *reinterpret_cast<const uint32_t*>(in + r * in_pitch + cb);
+        } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t c = 8 * cb + j;
-      if (c < cols) out[c * out_pitch + rb] = static_cast<uint8_t>(x >> (8 * j));
+          for (int i = 0; i < 4; ++i)
+            if (cb + i < in_pitch) w |= static_cast<uint32_t>(in[r * in_pitch + cb + i]) << (8 * i);
+        }
+      }
+      *reinterpret_cast<uint32_t*>(&tile[row][16 * part + 4 * d]) = w;
     }
+  }
+  __syncthreads();
+  {
+    // column byte cbl, row blocks 2 rbp and 2 rbp + 1
+    const int cbl = tid & 63, rbp = tid >> 6;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int rb = 2 * rbp + h;
+      uint64_t x = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x |= static_cast<uint64_t>(tile[8 * rb + i][cbl]) << (8 * i);
+      x = transpose_8x8(x);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        reinterpret_cast<uint8_t*>(&otile[8 * cbl + j])[rb] = static_cast<uint8_t>(x >> (8 * j));
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int cl = 2 * tid + k;
+    const int64_t c = 8 * cb0 + cl;
+    if (c < cols) *reinterpret_cast<uint64_t*>(out + c * out_pitch + r0 / 8) = otile[cl];
   }
 }
 
-// out[i] = bf16(in[i]) for i < n, 0 for n <= i < padded
 __global__ void f32_to_bf16_kernel(const float* __restrict__ in, uint16_t* __restrict__ out, int64_t n,
                                    int64_t padded) {
   const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
@@ -205,11 +241,12 @@ __global__ void f32_to_bf16_kernel(const float* __restrict__ in, uint16_t* __res
 
 int launch_transpose_bits(const uint8_t* in, uint8_t* out, int64_t rows, int64_t cols, int64_t in_pitch,
                           int64_t out_pitch, hipStream_t stream) {
-  const int64_t total = out_pitch * ((cols + 7) / 8);
-  if (total == 0) return 0;
-  const int64_t blocks = (total + 255) / 256;
-  transpose_bits_kernel<<<static_cast<int>(blocks < 65536 ? blocks : 65536), 256, 0, stream>>>(
-      in, out, rows, cols, in_pitch, out_pitch);
+  if (rows == 0 || cols == 0 || out_pitch == 0) return 0;
+  if (out_pitch % 8 != 0 || (reinterpret_cast<uintptr_t>(out) & 7)) return QSTE_E_ALIGN;
+  // row tiles cover every output byte (out_pitch * 8 rows, the padding
+  // included, which reads as zero)
+  dim3 grid(ceil_div(in_pitch, kTrColBytes), ceil_div(out_pitch * 8, kTrRows));
+  transpose_bits_kernel<<<grid, 256, 0, stream>>>(in, out, rows, cols, in_pitch, out_pitch);
   return static_cast<int>(hipGetLastError());
 }
 

@@ -27,13 +27,22 @@ __global__ __launch_bounds__(kRowThreads) void row_inner_kernel(const float* __r
   if (threadIdx.x == 0) out[r] = acc;
 }
 
-// Sum of `parts` partial vectors [parts][n] into out[n].
+// Sum of `parts` partial vectors [parts][n] into out[n], in order of p (the
+// loads are issued eight at a time; the additions stay sequential).
 __global__ void sum_partials_kernel(const float* __restrict__ partial, int64_t parts, int64_t n,
                                     float* __restrict__ out) {
   const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
   if (i >= n) return;
   float s = 0.0f;
-  for (int64_t p = 0; p < parts; ++p) s += partial[p * n + i];
+  int64_t p = 0;
+  for (; p + 8 <= parts; p += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = partial[(p + u) * n + i];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+  }
+  for (; p < parts; ++p) s += partial[p * n + i];
   out[i] = s;
 }
 
