@@ -10,9 +10,15 @@
 //            finished here), column partial sums per strip
 //   cols     column EMA, fp16 col_v, column factor; block 0 also finishes
 //            the mean row statistic
-//   usq      sum of U^2, U = g * rf * cf, per workgroup
-//   moment   (prologue: RMS clip divisor) m = q*S*b1 + (1-b1)*U/div for one
-//            momentum block per wave: new fp16 block scale, sum of m^2
+//   usq      sum of U^2, U = g * rf * cf, per workgroup; on the vector path
+//            also the momentum m = q*S*b1 + (1-b1)*U as if the clip divisor
+//            were 1: new fp16 block scales and sum of m^2
+//   moment   (prologue: RMS clip divisor) returns at once when the divisor
+//            is exactly 1 (then U / div == U and the usq pass's momentum is
+//            the exact result, which is the usual case: the clip engages
+//            only when rms(U) > update_clip); otherwise
+//            m = q*S*b1 + (1-b1)*U/div for one momentum block per wave:
+//            new fp16 block scale, sum of m^2
 //   final    (prologue: step size lr / rms(m)) stochastic rounding, momentum
 //            requantization, sign repack and flip count, 8 columns (one
 //            packed byte) per thread
@@ -52,6 +58,7 @@ struct Params {
   bool vec;       // cols % 8 == 0 and block_size >= 8
   bool small;     // rows * cols < 2^32: 32-bit index arithmetic
   uint32_t bpr;   // momentum blocks per row when cols % block_size == 0, else 0
+  bool spec;      // the usq pass also computes the momentum as if the clip divisor were 1
 };
 
 // Row and column of flat index i.
@@ -242,10 +249,18 @@ __global__ __launch_bounds__(kThreads) void cols_kernel(uint16_t* __restrict__ c
 }
 
 // -- sum of U^2, one row at a time per workgroup -----------------------------
-__global__ __launch_bounds__(kThreads) void usq_kernel(const float* __restrict__ g, Params p, Work w) {
+// On the vector path with spec set, lane l of wave w holds columns
+// 4 (64 w' + l) .. + 3 of a 1024-column slice: its 4 elements share one
+// momentum block (block_size in 4..256, a power of two, dividing cols), and
+// the block_size / 4 lanes of a block reduce its |m| maximum.
+__global__ __launch_bounds__(kThreads) void usq_kernel(const float* __restrict__ g,
+                                                       const int8_t* __restrict__ moment_q,
+                                                       const uint16_t* __restrict__ moment_scale, Params p,
+                                                       Work w) {
   __shared__ double red[kThreads / kWave];
   const float sqrt_mean = w.scalars[0];
-  double acc = 0.0;
+  const int lane = threadIdx.x & (kWave - 1);
+  double acc = 0.0, msq = 0.0;
   for (int64_t r = blockIdx.x; r < p.rows; r += gridDim.x) {
     const float rf = row_factor_of(sqrt_mean, w.new_row[r]);
     if (threadIdx.x == 0) w.row_factor[r] = rf;
@@ -253,13 +268,35 @@ __global__ __launch_bounds__(kThreads) void usq_kernel(const float* __restrict__
     if (p.vec) {
       const float4* l4 = reinterpret_cast<const float4*>(line);
       const float4* cf4 = reinterpret_cast<const float4*>(w.col_factor);
+      const uint32_t* q4p = reinterpret_cast<const uint32_t*>(moment_q + r * p.cols);
       for (int64_t q = threadIdx.x; q < p.cols / 4; q += kThreads) {
         const float4 v = l4[q], cf = cf4[q];
-        const float u0 = normalized(v.x, rf, cf.x), u1 = normalized(v.y, rf, cf.y);
-        const float u2 = normalized(v.z, rf, cf.z), u3 = normalized(v.w, rf, cf.w);
-        const float s0 = u0 * u0, s1 = u1 * u1, s2 = u2 * u2, s3 = u3 * u3;
+        uint32_t q4 = 0;
+        float s_old = 0.0f;
+        const int64_t blk = (r * p.cols + 4 * q) >> p.block_shift;
+        if (p.spec) {
+          q4 = q4p[q];
+          s_old = f16_to_f32(moment_scale[blk]);
+        }
+        const float u[4] = {normalized(v.x, rf, cf.x), normalized(v.y, rf, cf.y), normalized(v.z, rf, cf.z),
+                            normalized(v.w, rf, cf.w)};
+        const float s0 = u[0] * u[0], s1 = u[1] * u[1], s2 = u[2] * u[2], s3 = u[3] * u[3];
         acc += (static_cast<double>(s0) + static_cast<double>(s1)) +
                (static_cast<double>(s2) + static_cast<double>(s3));
+        if (p.spec) {
+          float amax = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float prev = static_cast<float>(static_cast<int8_t>(q4 >> (8 * e)));
+            const float m = moment_of(u[e], prev, s_old, p);
+            amax = fmaxf(amax, fabsf(m));
+            const float sq = m * m;
+            msq += static_cast<double>(sq);
+          }
+          // maximum over the block's block_size / 4 lanes
+          for (int o = 1; o < static_cast<int>(p.block_size >> 2); o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+          if ((lane & ((p.block_size >> 2) - 1)) == 0) w.s_new[blk] = f32_to_f16(fmaxf(amax, 1e-6f) / 127.0f);
+        }
       }
     } else {
       for (int64_t c = threadIdx.x; c < p.cols; c += kThreads) {
@@ -271,6 +308,11 @@ __global__ __launch_bounds__(kThreads) void usq_kernel(const float* __restrict__
   }
   acc = block_sum(acc, red);
   if (threadIdx.x == 0) w.usq_part[blockIdx.x] = acc;
+  if (p.spec) {
+    __syncthreads();
+    msq = block_sum(msq, red);
+    if (threadIdx.x == 0) w.msq_part[blockIdx.x] = msq;
+  }
 }
 
 __device__ __forceinline__ float divisor_of(const double* usq_part, int64_t parts, int64_t count,
@@ -293,6 +335,8 @@ __global__ __launch_bounds__(kThreads) void moment_kernel(const float* __restric
   __shared__ double wsum[kThreads / kWave];
   const float divisor = divisor_of(w.usq_part, kUsqGroups, p.count, p.clip, red);
   if (blockIdx.x == 0 && threadIdx.x == 0) w.scalars[1] = divisor;
+  // the usq pass's momentum assumed a divisor of 1: exact if it is
+  if (p.spec && divisor == 1.0f) return;
   const float rdiv = 1.0f / divisor;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -516,6 +560,117 @@ __global__ __launch_bounds__(kThreads) void final_kernel(const float* __restrict
   if (threadIdx.x == 0) w.flips_part[blockIdx.x] = on ? flips : 0;
 }
 
+// Vector path of the final pass (cols % 8 == 0, block_size >= 8, aligned
+// pointers): one packed byte per thread per iteration, straight-line code
+// for its 8 elements, the same arithmetic as final_byte.  With a clip
+// divisor of exactly 1 the correction U / div is the identity and is
+// skipped (a uniform choice per workgroup).
+template <bool DIV1>
+__device__ __forceinline__ int64_t final_vec_loop(const float* __restrict__ g, int8_t* __restrict__ coord,
+                                                  uint8_t* __restrict__ packed, int8_t* __restrict__ moment_q,
+                                                  const uint16_t* __restrict__ moment_scale, const Params& p,
+                                                  const Work& w, float divisor, float rdiv, float step_size,
+                                                  uint32_t combined, bool on) {
+  const int64_t stride = p.cols >> 3;
+  const int64_t total = p.rows * stride;
+  int64_t flips = 0;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * kThreads) {
+    int64_t r, b;
+    if (p.small) {
+      const uint32_t ii = static_cast<uint32_t>(idx), ss = static_cast<uint32_t>(stride);
+      const uint32_t rr = ii / ss;
+      r = rr;
+      b = ii - rr * ss;
+    } else {
+      r = idx / stride;
+      b = idx - r * stride;
+    }
+    const int64_t c0 = b * 8;
+    const int64_t i0 = r * p.cols + c0;
+    const float4 ga = *reinterpret_cast<const float4*>(g + i0);
+    const float4 gb = *reinterpret_cast<const float4*>(g + i0 + 4);
+    const float4 ca = *reinterpret_cast<const float4*>(w.col_factor + c0);
+    const float4 cb = *reinterpret_cast<const float4*>(w.col_factor + c0 + 4);
+    const uint64_t q8 = *reinterpret_cast<const uint64_t*>(moment_q + i0);
+    const uint64_t c8 = *reinterpret_cast<const uint64_t*>(coord + i0);
+    const uint32_t old_byte = packed[idx];
+    const float rf = w.row_factor[r];
+    const int64_t blk = i0 >> p.block_shift;  // block_size >= 8: one block for the byte
+    const float s_old = f16_to_f32(moment_scale[blk]);
+    const float decode = fmaxf(f16_to_f32(w.s_new[blk]), 1e-12f);
+    const float rdec = 1.0f / decode;
+    const float gv[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+    const float cv[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
+    uint32_t byte = 0, cn_lo = 0, cn_hi = 0, qn_lo = 0, qn_hi = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float u2 = normalized(gv[j], rf, cv[j]);
+      if (!DIV1) u2 = div_by(u2, divisor, rdiv);
+      const float prev = static_cast<float>(static_cast<int8_t>(q8 >> (8 * j)));
+      const float cur = static_cast<float>(static_cast<int8_t>(c8 >> (8 * j)));
+      const float m = moment_of(u2, prev, s_old, p);
+      const float delta = m * step_size;
+      const float target = cur - delta;
+      const float lower = floorf(target);
+      const float u = static_cast<float>(scramble(static_cast<uint32_t>(i0 + j) ^ combined)) *
+                      (1.0f / 4294967296.0f);
+      const float frac = target - lower;
+      float rounded = lower + (u < frac ? 1.0f : 0.0f);
+      rounded = fminf(127.0f, fmaxf(-127.0f, rounded));
+      float q = rintf(div_by(m, decode, rdec));
+      q = fminf(127.0f, fmaxf(-127.0f, q));
+      const uint32_t cb8 = static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(rounded)));
+      const uint32_t qb8 = static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(q)));
+      if (j < 4) {
+        cn_lo |= cb8 << (8 * j);
+        qn_lo |= qb8 << (8 * j);
+      } else {
+        cn_hi |= cb8 << (8 * (j - 4));
+        qn_hi |= qb8 << (8 * (j - 4));
+      }
+      byte |= (rounded >= 0.0f ? 1u : 0u) << j;
+    }
+    if (on) {
+      *reinterpret_cast<uint64_t*>(coord + i0) = (static_cast<uint64_t>(cn_hi) << 32) | cn_lo;
+      *reinterpret_cast<uint64_t*>(moment_q + i0) = (static_cast<uint64_t>(qn_hi) << 32) | qn_lo;
+      packed[idx] = static_cast<uint8_t>(byte);
+    }
+    flips += __popc(old_byte ^ byte);
+  }
+  return flips;
+}
+
+__global__ __launch_bounds__(kThreads) void final_vec_kernel(const float* __restrict__ g,
+                                                             int8_t* __restrict__ coord,
+                                                             uint8_t* __restrict__ packed,
+                                                             int8_t* __restrict__ moment_q,
+                                                             const uint16_t* __restrict__ moment_scale,
+                                                             Params p, Work w) {
+  __shared__ double red[kThreads / kWave];
+  __shared__ int64_t ired[kThreads / kWave];
+  double acc = 0.0;
+  for (int64_t i = threadIdx.x; i < kMomentGroups; i += kThreads) acc += w.msq_part[i];
+  acc = block_sum(acc, red);
+  const float padded = static_cast<float>(p.blocks * p.block_size);
+  float mrms = sqrtf(static_cast<float>(acc) / padded);
+  mrms = fmaxf(mrms, 1e-8f);
+  const float step_size = p.lr / mrms;
+  if (blockIdx.x == 0 && threadIdx.x == 0) w.scalars[2] = step_size;
+  const float divisor = w.scalars[1];
+  const float rdiv = 1.0f / divisor;
+  const int64_t step = p.step_device ? *p.step_device : p.step;
+  const uint32_t combined = p.seed_part ^ step_hash(step);
+  const bool on = enabled(p);
+  const int64_t flips =
+      divisor == 1.0f
+          ? final_vec_loop<true>(g, coord, packed, moment_q, moment_scale, p, w, divisor, rdiv, step_size, combined, on)
+          : final_vec_loop<false>(g, coord, packed, moment_q, moment_scale, p, w, divisor, rdiv, step_size, combined,
+                                  on);
+  const int64_t total = block_sum(flips, ired);
+  if (threadIdx.x == 0) w.flips_part[blockIdx.x] = on ? total : 0;
+}
+
 __global__ __launch_bounds__(kThreads) void finish_kernel(uint16_t* __restrict__ moment_scale,
                                                           int64_t* __restrict__ flips_out, Params p, Work w) {
   __shared__ int64_t red[kThreads / kWave];
@@ -632,6 +787,11 @@ int launch_coordinate_update(const float* g, int8_t* coord, uint8_t* packed, int
           (reinterpret_cast<uintptr_t>(coord) & 7) == 0 && (reinterpret_cast<uintptr_t>(moment_q) & 7) == 0;
   p.small = p.count < (int64_t{1} << 32) && p.blocks * p.block_size < (int64_t{1} << 32);
   p.bpr = (p.small && cols % block_size == 0) ? static_cast<uint32_t>(cols / block_size) : 0u;
+  // the usq pass guesses the momentum only where the guess usually holds:
+  // the clip divisor is 1 once the second-moment EMA has warmed up (rms(U)
+  // falls towards 1), not in the first tens of steps from a fresh state
+  p.spec = p.vec && cols % 256 == 0 && block_size >= 4 && block_size <= 256 &&
+           (reinterpret_cast<uintptr_t>(moment_q) & 3) == 0 && step_device == nullptr && step_ >= 64;
 
   int rc;
   stats_kernel<<<dim3(static_cast<unsigned>(w.nchunks), static_cast<unsigned>(w.nstrips)), kThreads, 0,
@@ -641,11 +801,14 @@ int launch_coordinate_update(const float* g, int8_t* coord, uint8_t* packed, int
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
   cols_kernel<<<ceil_div(cols, 64), kThreads, 0, stream>>>(col_v, p, w, kRowsGroups);
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
-  usq_kernel<<<kUsqGroups, kThreads, 0, stream>>>(g, p, w);
+  usq_kernel<<<kUsqGroups, kThreads, 0, stream>>>(g, moment_q, moment_scale, p, w);
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
   moment_kernel<<<kMomentGroups, kThreads, 0, stream>>>(g, moment_q, moment_scale, p, w);
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
-  final_kernel<<<kFinalGroups, kThreads, 0, stream>>>(g, coord, packed, moment_q, moment_scale, p, w);
+  if (p.vec)
+    final_vec_kernel<<<kFinalGroups, kThreads, 0, stream>>>(g, coord, packed, moment_q, moment_scale, p, w);
+  else
+    final_kernel<<<kFinalGroups, kThreads, 0, stream>>>(g, coord, packed, moment_q, moment_scale, p, w);
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
   finish_kernel<<<ceil_div(p.blocks, kThreads) < 1024 ? ceil_div(p.blocks, kThreads) : 1024, kThreads, 0,
                   stream>>>(moment_scale, flips_out, p, w);

@@ -281,6 +281,28 @@ def test_coordinate_update_matches_oracle(rows, cols, block):
         assert flips == oflips
 
 
+@pytest.mark.parametrize("clip", [0.05, 1e6])
+def test_coordinate_update_clip_regimes(clip):
+    """Both sides of the RMS clip on a shape where the usq pass also computes
+    the momentum as if the clip divisor were 1: with the clip engaged that
+    guess is thrown away and the momentum pass recomputes; with it idle
+    (divisor exactly 1) the guess is the result.  Bit-exact either way."""
+
+    rows, cols, block = 96, 1024, 256
+    rng = np.random.default_rng(11)
+    coord = rng.integers(-127, 128, size=(rows, cols)).astype(np.int8)
+    state = oracle.fresh_state(coord, block)
+    gstate = _to_gpu_state(state)
+    for step in range(4):
+        ev = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+        kw = dict(beta1=0.9, beta2=0.99, update_clip=clip, coordinate_lr=1.0, block_size=block,
+                  seed=17, step=step)
+        flips = _gpu_step(ev, gstate, **kw)
+        oflips = oracle.coordinate_update(ev, state, **kw)
+        _assert_state_equal(gstate, state, (clip, step))
+        assert flips == oflips
+
+
 def test_coordinate_update_device_step_flips_and_gate():
     rows, cols, block = 64, 96, 64
     rng = np.random.default_rng(5)
