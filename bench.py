@@ -47,7 +47,42 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip per-kernel, step and GEMV timing")
     ap.add_argument("--cpu-tokens", type=int, default=256)
+    ap.add_argument("--pmc-calibrate", action="store_true",
+                    help="one launch of each GEMM kind at the gate-layer shape plus a plain device copy of "
+                         "COPY_BYTES, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
     return ap.parse_args()
+
+
+COPY_BYTES = 256 << 20  # the known-size copy the traffic counters are scaled by
+TRAFFIC_FILE = ROOT / "profiles" / "gemm_traffic.txt"
+
+
+def read_traffic():
+    """HBM bytes per launch of each GEMM kind, from the committed counter summary.
+
+    The file's `traffic <kind> <bytes>` lines are FETCH_SIZE + WRITE_SIZE per
+    dispatch, scaled by what the same counters read for a plain copy of known
+    size (the summary states the command and the factor)."""
+
+    out = {}
+    if TRAFFIC_FILE.exists():
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic":
+                out[parts[1]] = float(parts[2])
+    return out
+
+
+def pmc_calibrate(T, d, ffn, device):
+    import torch
+
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=device).fill_(7)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    kernels_t, _ = gemm_kernels(T, d, ffn, device, iters=1)
+    print(json.dumps({"copy_bytes": COPY_BYTES, "gemm_shape": [T, ffn, d], "kernels": kernels_t}), flush=True)
 
 
 def make_layer(rows, cols, seed, device, scale_std=0.01):
@@ -95,7 +130,7 @@ def timed_events(fn, iters, stream=None):
     return start.elapsed_time(stop) / iters
 
 
-def gemm_kernels(T, d, ffn, device):
+def gemm_kernels(T, d, ffn, device, iters=5):
     """Per-launch time of each product kind at the gate-layer shape."""
 
     import torch
@@ -118,7 +153,7 @@ def gemm_kernels(T, d, ffn, device):
         "evidence": lambda: kernels.evidence_from_packed(dy, xbits, d, row_scale=xs),
     }
     for name, fn in runs.items():
-        ms = timed_events(fn, 5)
+        ms = timed_events(fn, iters)
         out[name] = {"ms": round(ms, 4), "tflops": round(flop / ms / 1e9, 2),
                      "frac_of_mfma_peak": round(flop / (ms * 1e-3) / MFMA_BF16_PEAK, 4)}
     del oracle
@@ -234,6 +269,9 @@ def main():
         sys.exit(2)
     device = torch.device("cuda:0")
     T, d, ffn = args.tokens, args.d, args.ffn
+    if args.pmc_calibrate:
+        pmc_calibrate(T, d, ffn, device)
+        return
 
     mlp = SwiGLU(d, ffn, device)
     coords = qste.QSTEOptimizer(list(qste.surfaces(mlp.modules)))
@@ -279,9 +317,11 @@ def main():
         kernels_t, kflop = gemm_kernels(T, d, ffn, device)
         dominant = max(kernels_t, key=lambda k: kernels_t[k]["ms"])
         dk = kernels_t[dominant]
+        traffic = read_traffic().get(dominant)
         line["roofline"] = {"bound": "mfma", "kernel": dominant, "achieved": dk["tflops"],
                             "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
-                            "frac": round(dk["tflops"] * 1e12 / MFMA_BF16_PEAK, 4), "traffic": None}
+                            "frac": round(dk["tflops"] * 1e12 / MFMA_BF16_PEAK, 4),
+                            "traffic": None if traffic is None else int(traffic)}
         line["kernels"] = kernels_t
         line["coordinate_step"] = step_bandwidth(ffn, d, device)
         line["decode_gemv"] = decode_gemv(device)
