@@ -12,7 +12,8 @@ backward as in the reference.  ``value`` = 6 * T * sum(R*C) / step time.
 
 Alongside, measured live with HIP events on the stream the kernels run on:
 each GEMM kind at the gate-layer shape (the dominant kernel is reported as
-``roofline``), the coordinate step of one 14336 x 4096 surface (HBM), and
+``roofline``), torch.matmul (hipBLASLt) on dense bf16 operands of the same
+shapes for comparison, the coordinate step of one 14336 x 4096 surface (HBM), and
 the skinny-M decode GEMV of config 5 (K=8192, N=28672, M in {1, 4, 16}) over
 rotated weight copies larger than the 256 MB Infinity Cache.  The CPU
 baseline is the reference's CPU algorithm (oracle/cpu_baseline.py) timed on
@@ -158,6 +159,30 @@ def gemm_kernels(T, d, ffn, device, iters=5):
                      "frac_of_mfma_peak": round(flop / (ms * 1e-3) / MFMA_BF16_PEAK, 4)}
     del oracle
     return out, flop
+
+
+def vendor_dense(T, d, ffn, device, iters=5):
+    """torch.matmul (hipBLASLt) on dense bf16 operands of each product's shape,
+    as the products store them: the practical GEMM rate of this box, for
+    comparison with the packed-sign kernels (which also expand the signs)."""
+
+    import torch
+
+    g = torch.Generator(device=device).manual_seed(3)
+    x = torch.randn(T, d, generator=g, device=device).to(torch.bfloat16)
+    dy = torch.randn(T, ffn, generator=g, device=device).to(torch.bfloat16)
+    w = torch.randn(ffn, d, generator=g, device=device).to(torch.bfloat16)
+    runs = {
+        "forward": lambda: torch.matmul(x, w.t()),
+        "dgrad": lambda: torch.matmul(dy, w),
+        "evidence": lambda: torch.matmul(dy.t(), x),
+    }
+    flop = 2.0 * T * ffn * d
+    out = {}
+    for name, fn in runs.items():
+        ms = timed_events(fn, iters)
+        out[name] = {"ms": round(ms, 4), "tflops": round(flop / ms / 1e9, 2)}
+    return out
 
 
 def step_bandwidth(rows, cols, device):
@@ -323,6 +348,7 @@ def main():
                             "frac": round(dk["tflops"] * 1e12 / MFMA_BF16_PEAK, 4),
                             "traffic": None if traffic is None else int(traffic)}
         line["kernels"] = kernels_t
+        line["vendor_dense_bf16_gemm"] = vendor_dense(T, d, ffn, device)
         line["coordinate_step"] = step_bandwidth(ffn, d, device)
         line["decode_gemv"] = decode_gemv(device)
     if not args.no_cpu_baseline:
