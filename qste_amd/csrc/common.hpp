@@ -88,6 +88,19 @@ __host__ __device__ __forceinline__ uint32_t scramble(uint32_t v) {
   return v;
 }
 
+// scramble split after its first step: for j < 2^16, scramble(x ^ j) ==
+// scramble_tail(scramble_head(x) ^ j), since j never reaches x >> 16.  The
+// eight elements of one packed byte (flat indices i0 + j, i0 % 8 == 0) share
+// one head.
+__host__ __device__ __forceinline__ uint32_t scramble_head(uint32_t x) { return (x ^ 61u) ^ (x >> 16); }
+__host__ __device__ __forceinline__ uint32_t scramble_tail(uint32_t v) {
+  v = v + (v << 3);
+  v = v ^ (v >> 4);
+  v = v * kMultiplier;
+  v = v ^ (v >> 15);
+  return v;
+}
+
 __host__ __device__ __forceinline__ uint32_t seed_hash(int64_t seed) {
   return scramble(static_cast<uint32_t>(static_cast<uint64_t>(seed)));
 }

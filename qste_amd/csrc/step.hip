@@ -5,14 +5,16 @@
 // the new momentum -- so it runs as a short chain of passes over the fp32
 // evidence, none of which writes the evidence:
 //
-//   stats    one workgroup per strip of rows: row sums of g^2 + 1e-12 (so
-//            the row EMA, fp16 row_v and the clamped row statistic are
-//            finished here), column partial sums per strip
-//   cols     column EMA, fp16 col_v, column factor; block 0 also finishes
-//            the mean row statistic
-//   usq      sum of U^2, U = g * rf * cf, per workgroup; on the vector path
-//            also the momentum m = q*S*b1 + (1-b1)*U as if the clip divisor
-//            were 1: new fp16 block scales and sum of m^2
+//   stats    one workgroup per strip of rows and chunk of 1024 columns: row
+//            sums of g^2 + 1e-12 (finished here when one chunk holds the
+//            row), column partial sums per strip
+//   colrow   column EMA, fp16 col_v, column factor; its last workgroups
+//            finish rows split over chunks (row EMA, fp16 row_v) and sum
+//            the clamped row statistic
+//   usq      (prologue: mean row statistic) sum of U^2, U = g * rf * cf,
+//            per workgroup; on the vector path also the momentum
+//            m = q*S*b1 + (1-b1)*U as if the clip divisor were 1: new fp16
+//            block scales and sum of m^2
 //   moment   (prologue: RMS clip divisor) returns at once when the divisor
 //            is exactly 1 (then U / div == U and the usq pass's momentum is
 //            the exact result, which is the usual case: the clip engages
@@ -28,12 +30,16 @@
 // element-wise product and sum rounds in fp32 (this file is compiled with
 // -ffp-contract=off), torch's `add_(x, alpha=a)` is a fused multiply-add
 // (fmaf), divisions and square roots are correctly rounded.  Reductions
-// accumulate in double in a fixed order and round once, so results do not
-// depend on launch geometry and equal the correctly rounded sums but in
-// vanishingly rare cases.
+// accumulate in double, each in a fixed order, and round once, so results
+// equal the correctly rounded sums but in vanishingly rare cases, whichever
+// kernel (and so whichever order) a shape takes.
 //
 // Fast paths (vector loads) need cols % 8 == 0 and block_size >= 8; other
-// shapes take scalar code with the same arithmetic.
+// shapes take scalar code with the same arithmetic.  Shapes with cols % 256
+// == 0 and block_size <= 256 take the row kernels for the stats, usq and
+// momentum passes: a wave owns a 1024-column chunk of one row at a time,
+// keeps its column factors in registers, and finds a momentum block's
+// maximum among block_size / 4 consecutive lanes with DPP lane moves.
 #include "common.hpp"
 
 namespace qste {
@@ -44,8 +50,9 @@ constexpr int kThreads = 256;
 constexpr int kStrip = 64;        // rows per stats workgroup
 constexpr int kColChunk = 1024;   // columns per stats workgroup (4 per thread)
 constexpr int kUsqGroups = 1024;
-constexpr int kMomentGroups = 1024;
+constexpr int kMomentGroups = kUsqGroups;  // the momentum partials share the usq layout
 constexpr int kFinalGroups = 2048;
+constexpr int kRowsGroups = 64;   // workgroups finishing the row statistics
 
 struct Params {
   float b1, a1, b2, a2, clip, lr;
@@ -76,7 +83,7 @@ __device__ __forceinline__ void row_col(int64_t i, const Params& p, int64_t& r, 
 
 struct Work {
   double* col_part;    // [nstrips][cols]
-  double* clamp_part;  // [nstrips * nchunks] partial sums of max(new_row, 1e-10)
+  double* clamp_part;  // [kRowsGroups] partial sums of max(new_row, 1e-10)
   double* row_part;    // [nchunks][rows]
   float* new_row;      // [rows]
   float* row_factor;   // [rows] (written by the usq pass)
@@ -86,8 +93,11 @@ struct Work {
   double* msq_part;    // [kMomentGroups]
   float* scalars;      // [0] sqrt(mean row stat), [1] divisor, [2] step size
   uint16_t* s_new;     // [blocks]
+  float* s_rcp;        // [blocks] 1 / max(s_new, 1e-12), correctly rounded (row path)
   int64_t* flips_part; // [kFinalGroups]
   int64_t nstrips, nchunks;
+  int64_t parts;       // slots of usq_part and msq_part written (<= kUsqGroups)
+  int64_t fparts;      // slots of flips_part written (<= kFinalGroups)
 };
 
 __device__ __forceinline__ bool enabled(const Params& p) {
@@ -125,10 +135,60 @@ __device__ __forceinline__ float moment_of(float u2, float prev, float s_old, co
   return fmaf(u2, p.a1, decoded);
 }
 
+// DPP lane moves (v_mov_b32 with a data-parallel-primitive control): lane i
+// receives the value of the lane CTRL names; a lane whose source lies outside
+// its row of 16 lanes, or whose row is not in ROWS, receives 0.
+constexpr int kShr1 = 0x111, kShr2 = 0x112, kShr4 = 0x114, kShr8 = 0x118;  // row_shr:n
+constexpr int kBcast15 = 0x142, kBcast31 = 0x143;                         // row_bcast:15, :31
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROWS, 0xF, true));
+}
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __uint_as_float(dpp_u32<CTRL, ROWS>(__float_as_uint(v)));
+}
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t b = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint64_t lo = dpp_u32<CTRL, ROWS>(static_cast<uint32_t>(b));
+  const uint64_t hi = dpp_u32<CTRL, ROWS>(static_cast<uint32_t>(b >> 32));
+  return __longlong_as_double(static_cast<long long>((hi << 32) | lo));
+}
+
+// Maximum of nonnegative values over aligned groups of n lanes (n a power of
+// two, 1..64): after the shift by 2^j every lane holds the maximum of the
+// 2^(j+1) lanes ending at it within its row; the broadcasts join rows.  The
+// last lane of each group receives the group's maximum.
+__device__ __forceinline__ float group_max_last(float v, int n) {
+  if (n >= 2) v = fmaxf(v, dpp_f32<kShr1>(v));
+  if (n >= 4) v = fmaxf(v, dpp_f32<kShr2>(v));
+  if (n >= 8) v = fmaxf(v, dpp_f32<kShr4>(v));
+  if (n >= 16) v = fmaxf(v, dpp_f32<kShr8>(v));
+  if (n >= 32) v = fmaxf(v, dpp_f32<kBcast15, 0xA>(v));
+  if (n >= 64) v = fmaxf(v, dpp_f32<kBcast31, 0xC>(v));
+  return v;
+}
+
+// Sum over the wave in a fixed tree (the same shifts and broadcasts), read
+// back from the last lane: every lane receives the total.
+__device__ __forceinline__ double wave_total(double v) {
+  v += dpp_f64<kShr1>(v);
+  v += dpp_f64<kShr2>(v);
+  v += dpp_f64<kShr4>(v);
+  v += dpp_f64<kShr8>(v);
+  v += dpp_f64<kBcast15, 0xA>(v);
+  v += dpp_f64<kBcast31, 0xC>(v);
+  const uint64_t b = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(b)), 63));
+  const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(b >> 32)), 63));
+  return __longlong_as_double(static_cast<long long>((hi << 32) | lo));
+}
+
 // -- stats: strip of rows x chunk of columns --------------------------------
 // Thread t owns columns c0 + 4t .. c0 + 4t + 3 of the chunk.  When the whole
 // row fits one chunk (cols <= 1024) the row sums complete here; otherwise
-// per-chunk row partials go to row_part and are combined in `cols`.
+// per-chunk row partials go to row_part and are combined in `colrow`.
 __global__ __launch_bounds__(kThreads) void stats_kernel(const float* __restrict__ g,
                                                          uint16_t* __restrict__ row_v, Params p,
                                                          Work w) {
@@ -194,58 +254,66 @@ __global__ __launch_bounds__(kThreads) void stats_kernel(const float* __restrict
     if (c0 + j < p.cols) w.col_part[static_cast<int64_t>(blockIdx.y) * p.cols + c0 + j] = col_acc[j];
 }
 
-// Rows whose sums were split over chunks; also the clamped row statistic.
-__global__ __launch_bounds__(kThreads) void rows_kernel(uint16_t* __restrict__ row_v, Params p, Work w) {
-  __shared__ double red[kThreads / kWave];
-  double acc = 0.0;
+// -- column statistics and the rows split over chunks --------------------------
+// Workgroups below `col_groups` own 16 columns each: thread t sums strips
+// t/16, t/16 + 16, ... of column 16 b + t % 16 and a column's 16 partials
+// are combined in a fixed order.  The kRowsGroups workgroups after them
+// finish rows whose sums were split over chunks and sum the clamped row
+// statistic (finished by the next pass).
+__global__ __launch_bounds__(kThreads) void colrow_kernel(uint16_t* __restrict__ col_v,
+                                                          uint16_t* __restrict__ row_v, Params p, Work w,
+                                                          int col_groups) {
   const bool on = enabled(p);
-  for (int64_t r = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; r < p.rows;
-       r += static_cast<int64_t>(gridDim.x) * kThreads) {
-    float nr;
-    if (w.nchunks > 1) {
-      double s = 0.0;
-      for (int64_t k = 0; k < w.nchunks; ++k) s += w.row_part[k * p.rows + r];
-      const float mean = static_cast<float>(s) / static_cast<float>(p.cols);
-      nr = fmaf(mean, p.a2, f16_to_f32(row_v[r]) * p.b2);
-      w.new_row[r] = nr;
-      if (on) row_v[r] = f32_to_f16(nr);
-    } else {
-      nr = w.new_row[r];
+  if (static_cast<int>(blockIdx.x) >= col_groups) {
+    __shared__ double red[kThreads / kWave];
+    const int64_t group = static_cast<int64_t>(blockIdx.x) - col_groups;
+    double acc = 0.0;
+    for (int64_t r = group * kThreads + threadIdx.x; r < p.rows; r += static_cast<int64_t>(kRowsGroups) * kThreads) {
+      float nr;
+      if (w.nchunks > 1) {
+        double s = 0.0;
+        for (int64_t k = 0; k < w.nchunks; ++k) s += w.row_part[k * p.rows + r];
+        const float mean = static_cast<float>(s) / static_cast<float>(p.cols);
+        nr = fmaf(mean, p.a2, f16_to_f32(row_v[r]) * p.b2);
+        w.new_row[r] = nr;
+        if (on) row_v[r] = f32_to_f16(nr);
+      } else {
+        nr = w.new_row[r];
+      }
+      acc += static_cast<double>(fmaxf(nr, 1e-10f));
     }
-    acc += static_cast<double>(fmaxf(nr, 1e-10f));
+    acc = block_sum(acc, red);
+    if (threadIdx.x == 0) w.clamp_part[group] = acc;
+    return;
   }
-  acc = block_sum(acc, red);
-  if (threadIdx.x == 0) w.clamp_part[blockIdx.x] = acc;
-}
-
-// -- column statistics; block 0 also finishes the mean row statistic --------
-// A workgroup owns 64 columns; its 4 waves sum interleaved subsets of the
-// strips and the 4 partials are combined in a fixed order.
-__global__ __launch_bounds__(kThreads) void cols_kernel(uint16_t* __restrict__ col_v, Params p, Work w,
-                                                        int64_t clamp_parts) {
-  __shared__ double part[4][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t c = blockIdx.x * 64ll + lane;
+  __shared__ double part[16][17];
+  const int cl = threadIdx.x & 15, sg = threadIdx.x >> 4;
+  const int64_t c = blockIdx.x * 16ll + cl;
   double s = 0.0;
   if (c < p.cols)
-    for (int64_t k = wave; k < w.nstrips; k += 4) s += w.col_part[k * p.cols + c];
-  part[wave][lane] = s;
+    for (int64_t k = sg; k < w.nstrips; k += 16) s += w.col_part[k * p.cols + c];
+  part[sg][cl] = s;
   __syncthreads();
-  if (wave == 0 && c < p.cols) {
-    const double t = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
+  if (threadIdx.x < 16 && c < p.cols) {
+    double t = 0.0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) t += part[k][cl];
     const float mean = static_cast<float>(t) / static_cast<float>(p.rows);
     const float nc = fmaf(mean, p.a2, f16_to_f32(col_v[c]) * p.b2);
     w.new_col[c] = nc;
     w.col_factor[c] = 1.0f / sqrtf(fmaxf(nc, 1e-10f));
-    if (enabled(p)) col_v[c] = f32_to_f16(nc);
+    if (on) col_v[c] = f32_to_f16(nc);
   }
-  if (blockIdx.x == 0) {
-    __shared__ double red[kThreads / kWave];
-    double acc = 0.0;
-    for (int64_t i = threadIdx.x; i < clamp_parts; i += kThreads) acc += w.clamp_part[i];
-    acc = block_sum(acc, red);
-    if (threadIdx.x == 0) w.scalars[0] = sqrtf(static_cast<float>(acc) / static_cast<float>(p.rows));
-  }
+}
+
+// sqrt of the mean clamped row statistic (the same value in every workgroup)
+__device__ __forceinline__ float sqrt_mean_of(const Params& p, const Work& w, double* red) {
+  double acc = 0.0;
+  for (int64_t i = threadIdx.x; i < kRowsGroups; i += kThreads) acc += w.clamp_part[i];
+  acc = block_sum(acc, red);
+  const float v = sqrtf(static_cast<float>(acc) / static_cast<float>(p.rows));
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) w.scalars[0] = v;
+  return v;
 }
 
 // -- sum of U^2, one row at a time per workgroup -----------------------------
@@ -258,7 +326,7 @@ __global__ __launch_bounds__(kThreads) void usq_kernel(const float* __restrict__
                                                        const uint16_t* __restrict__ moment_scale, Params p,
                                                        Work w) {
   __shared__ double red[kThreads / kWave];
-  const float sqrt_mean = w.scalars[0];
+  const float sqrt_mean = sqrt_mean_of(p, w, red);
   const int lane = threadIdx.x & (kWave - 1);
   double acc = 0.0, msq = 0.0;
   for (int64_t r = blockIdx.x; r < p.rows; r += gridDim.x) {
@@ -333,7 +401,7 @@ __global__ __launch_bounds__(kThreads) void moment_kernel(const float* __restric
                                                           Params p, Work w) {
   __shared__ double red[kThreads / kWave];
   __shared__ double wsum[kThreads / kWave];
-  const float divisor = divisor_of(w.usq_part, kUsqGroups, p.count, p.clip, red);
+  const float divisor = divisor_of(w.usq_part, w.parts, p.count, p.clip, red);
   if (blockIdx.x == 0 && threadIdx.x == 0) w.scalars[1] = divisor;
   // the usq pass's momentum assumed a divisor of 1: exact if it is
   if (p.spec && divisor == 1.0f) return;
@@ -423,6 +491,200 @@ __global__ __launch_bounds__(kThreads) void moment_kernel(const float* __restric
     double t = 0.0;
     for (int k = 0; k < kThreads / kWave; ++k) t += wsum[k];
     w.msq_part[blockIdx.x] = t;
+  }
+}
+
+// -- row path --------------------------------------------------------------------
+// cols % 256 == 0, block_size 8..256, vector-aligned operands.  A wave owns a
+// kRowChunk-column chunk of one row at a time: lane l holds the float4
+// slots at columns c0 + 4 l + 256 k, k = 0..3, and a slot is present in
+// every lane or in none (chunk_slots).  A momentum block of block_size
+// columns is then block_size / 4 consecutive lanes of one slot.
+constexpr int kRowChunk = kColChunk;
+
+__device__ __forceinline__ int chunk_slots(int64_t cols, int64_t c0) {
+  const int64_t left = (cols - c0) >> 8;
+  return left >= 4 ? 4 : static_cast<int>(left);
+}
+
+// stats on the row path: workgroup (chunk, strip); wave w takes rows w,
+// w + 4, ... of the strip, two rows' loads in flight before either is
+// reduced; one wave sum per row and chunk, the column partials of the four
+// waves combined through LDS.  Same outputs as stats_kernel.
+__global__ __launch_bounds__(kThreads) void stats_row_kernel(const float* __restrict__ g,
+                                                             uint16_t* __restrict__ row_v, Params p, Work w) {
+  __shared__ double colsum[kThreads / kWave][kRowChunk];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t chunk = blockIdx.x;
+  const int64_t c0 = chunk * kRowChunk;
+  const int ns = chunk_slots(p.cols, c0);
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kStrip;
+  const int rows_here = static_cast<int>(p.rows - r0 < kStrip ? p.rows - r0 : kStrip);
+  const float* base = g + r0 * p.cols + c0 + 4 * lane;
+  double col[4][4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) col[k][e] = 0.0;
+  constexpr int U = 2;  // rows per wave iteration
+  for (int rr = wave; rr < rows_here; rr += 4 * U) {
+    float4 v[U][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = rr + 4 * u;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        v[u][k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (row < rows_here && k < ns)
+          v[u][k] = *reinterpret_cast<const float4*>(base + row * p.cols + 256 * k);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int row = rr + 4 * u;
+      if (row >= rows_here) break;
+      double rp = 0.0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (k < ns) {
+          const double d0 = square_eps(v[u][k].x), d1 = square_eps(v[u][k].y);
+          const double d2 = square_eps(v[u][k].z), d3 = square_eps(v[u][k].w);
+          col[k][0] += d0; col[k][1] += d1; col[k][2] += d2; col[k][3] += d3;
+          rp += (d0 + d1) + (d2 + d3);
+        }
+      }
+      rp = wave_total(rp);
+      if (lane == 0) {
+        const int64_t r = r0 + row;
+        if (w.nchunks == 1) {
+          const float mean = static_cast<float>(rp) / static_cast<float>(p.cols);
+          const float nr = fmaf(mean, p.a2, f16_to_f32(row_v[r]) * p.b2);
+          w.new_row[r] = nr;
+          if (enabled(p)) row_v[r] = f32_to_f16(nr);
+        } else {
+          w.row_part[chunk * p.rows + r] = rp;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) colsum[wave][256 * k + 4 * lane + e] = col[k][e];
+  __syncthreads();
+  for (int c = threadIdx.x; c < 256 * ns; c += kThreads)
+    w.col_part[static_cast<int64_t>(blockIdx.y) * p.cols + c0 + c] =
+        (colsum[0][c] + colsum[1][c]) + (colsum[2][c] + colsum[3][c]);
+}
+
+// usq (MOMENT false) and momentum (MOMENT true) passes on the row path:
+// workgroup (b, chunk) takes rows 4 b + wave, + 4 gridDim.x, ... of its
+// chunk and writes partial slot chunk * gridDim.x + b.  The usq pass also
+// computes the momentum when p.spec is set (as usq_kernel does), the
+// momentum pass returns at once when that result stands.
+template <bool MOMENT>
+__global__ __launch_bounds__(kThreads) void elem_row_kernel(const float* __restrict__ g,
+                                                            const int8_t* __restrict__ moment_q,
+                                                            const uint16_t* __restrict__ moment_scale,
+                                                            Params p, Work w) {
+  __shared__ double red[kThreads / kWave];
+  float divisor = 1.0f, sqrt_mean = 0.0f;
+  if (MOMENT) {
+    divisor = divisor_of(w.usq_part, w.parts, p.count, p.clip, red);
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) w.scalars[1] = divisor;
+    if (p.spec && divisor == 1.0f) return;
+  } else {
+    sqrt_mean = sqrt_mean_of(p, w, red);
+  }
+  const bool with_m = MOMENT || p.spec;
+  const float rdiv = 1.0f / divisor;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t chunk = blockIdx.y;
+  const int64_t c0 = chunk * kRowChunk;
+  const int ns = chunk_slots(p.cols, c0);
+  const int gsize = static_cast<int>(p.block_size >> 2);  // lanes per momentum block
+  // loads are unconditional (straight-line code keeps the compiler's waits
+  // per load): slots past the chunk's end re-read its last slot, and those
+  // results are dropped
+  int64_t sc[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) sc[k] = c0 + 4 * lane + 256 * (k < ns ? k : ns - 1);
+  float4 cf[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) cf[k] = *reinterpret_cast<const float4*>(w.col_factor + sc[k]);
+  double acc = 0.0, msq = 0.0;
+  const int64_t rstep = static_cast<int64_t>(gridDim.x) * (kThreads / kWave);
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + wave; r < p.rows; r += rstep) {
+    float rf;
+    if (MOMENT) {
+      rf = w.row_factor[r];
+    } else {
+      rf = row_factor_of(sqrt_mean, w.new_row[r]);
+      if (chunk == 0 && lane == 0) w.row_factor[r] = rf;
+    }
+    const int64_t rb = r * p.cols;
+    float4 v[4];
+    uint32_t q4[4];
+    float so[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[k] = *reinterpret_cast<const float4*>(g + rb + sc[k]);
+      if (with_m) {
+        q4[k] = *reinterpret_cast<const uint32_t*>(moment_q + rb + sc[k]);
+        so[k] = f16_to_f32(moment_scale[(rb + sc[k]) >> p.block_shift]);
+      } else {
+        q4[k] = 0u;
+        so[k] = 0.f;
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the arithmetic
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (k >= ns) break;
+      const float gv[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+      const float cv[4] = {cf[k].x, cf[k].y, cf[k].z, cf[k].w};
+      float uu[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uu[e] = normalized(gv[e], rf, cv[e]);
+        if (MOMENT) uu[e] = div_by(uu[e], divisor, rdiv);
+      }
+      if (!MOMENT) {
+        const float s0 = uu[0] * uu[0], s1 = uu[1] * uu[1], s2 = uu[2] * uu[2], s3 = uu[3] * uu[3];
+        acc += (static_cast<double>(s0) + static_cast<double>(s1)) +
+               (static_cast<double>(s2) + static_cast<double>(s3));
+      }
+      if (with_m) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float prev = static_cast<float>(static_cast<int8_t>(q4[k] >> (8 * e)));
+          const float m = moment_of(uu[e], prev, so[k], p);
+          amax = fmaxf(amax, fabsf(m));
+          const float sq = m * m;
+          msq += static_cast<double>(sq);
+        }
+        amax = group_max_last(amax, gsize);
+        if ((lane & (gsize - 1)) == gsize - 1) {
+          const int64_t blk = (rb + sc[k]) >> p.block_shift;
+          const uint16_t s16 = f32_to_f16(fmaxf(amax, 1e-6f) / 127.0f);
+          w.s_new[blk] = s16;
+          w.s_rcp[blk] = 1.0f / fmaxf(f16_to_f32(s16), 1e-12f);
+        }
+      }
+    }
+  }
+  const int64_t slot = chunk * gridDim.x + blockIdx.x;
+  if (!MOMENT) {
+    acc = block_sum(acc, red);
+    if (threadIdx.x == 0) w.usq_part[slot] = acc;
+  }
+  if (with_m) {
+    __syncthreads();
+    msq = block_sum(msq, red);
+    if (threadIdx.x == 0) w.msq_part[slot] = msq;
   }
 }
 
@@ -518,7 +780,7 @@ __global__ __launch_bounds__(kThreads) void final_kernel(const float* __restrict
   __shared__ int64_t ired[kThreads / kWave];
   // step size from the momentum RMS
   double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < kMomentGroups; i += kThreads) acc += w.msq_part[i];
+  for (int64_t i = threadIdx.x; i < w.parts; i += kThreads) acc += w.msq_part[i];
   acc = block_sum(acc, red);
   const float padded = static_cast<float>(p.blocks * p.block_size);
   float mrms = sqrtf(static_cast<float>(acc) / padded);
@@ -650,7 +912,7 @@ __global__ __launch_bounds__(kThreads) void final_vec_kernel(const float* __rest
   __shared__ double red[kThreads / kWave];
   __shared__ int64_t ired[kThreads / kWave];
   double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < kMomentGroups; i += kThreads) acc += w.msq_part[i];
+  for (int64_t i = threadIdx.x; i < w.parts; i += kThreads) acc += w.msq_part[i];
   acc = block_sum(acc, red);
   const float padded = static_cast<float>(p.blocks * p.block_size);
   float mrms = sqrtf(static_cast<float>(acc) / padded);
@@ -671,6 +933,141 @@ __global__ __launch_bounds__(kThreads) void final_vec_kernel(const float* __rest
   if (threadIdx.x == 0) w.flips_part[blockIdx.x] = on ? total : 0;
 }
 
+// Final pass on the row path: workgroup (b, chunk) takes kFinalChunk
+// columns of rows 4 b + wave, + 4 gridDim.x, ..., two rows per iteration;
+// lane l owns the packed byte of columns c0 + 8 l .. + 7 (lanes past the
+// row's end idle).  Column factors stay in registers, the row factor is one
+// load per row, the block scale's reciprocal comes from the momentum pass,
+// and the eight elements of a byte share the first step of their hash.
+// The same arithmetic as final_byte.
+constexpr int kFinalChunk = 512;
+constexpr int kFinalRows = 1;  // rows per wave iteration
+
+template <bool DIV1>
+__device__ __forceinline__ int64_t final_row_loop(const float* __restrict__ g, int8_t* __restrict__ coord,
+                                                  uint8_t* __restrict__ packed, int8_t* __restrict__ moment_q,
+                                                  const uint16_t* __restrict__ moment_scale, const Params& p,
+                                                  const Work& w, float divisor, float rdiv, float step_size,
+                                                  uint32_t combined, bool on) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kFinalChunk + 8 * lane;
+  const bool lane_on = c0 < p.cols;
+  const int64_t stride = p.cols >> 3;
+  float cv[8];
+  {
+    const int64_t cl = lane_on ? c0 : p.cols - 8;
+    const float4 ca = *reinterpret_cast<const float4*>(w.col_factor + cl);
+    const float4 cb = *reinterpret_cast<const float4*>(w.col_factor + cl + 4);
+    cv[0] = ca.x; cv[1] = ca.y; cv[2] = ca.z; cv[3] = ca.w; cv[4] = cb.x; cv[5] = cb.y; cv[6] = cb.z; cv[7] = cb.w;
+  }
+  int64_t flips = 0;
+  const int64_t rstep = static_cast<int64_t>(gridDim.x) * (kThreads / kWave);
+  // loads are unconditional (straight-line code keeps the compiler's waits
+  // per load): idle lanes read their row's last byte, rows past the end the
+  // last row, and those results are dropped
+  const int64_t cc = lane_on ? c0 : p.cols - 8;
+  constexpr int U = kFinalRows;
+  for (int64_t r0 = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + wave; r0 < p.rows; r0 += U * rstep) {
+    float4 ga[U], gb[U];
+    uint64_t q8[U], c8[U];
+    uint32_t old_byte[U];
+    float rf[U], s_old[U], decode[U], rdec[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t rr = r0 + u * rstep;
+      const int64_t r = rr < p.rows ? rr : p.rows - 1;
+      const int64_t i0 = r * p.cols + cc;
+      ga[u] = *reinterpret_cast<const float4*>(g + i0);
+      gb[u] = *reinterpret_cast<const float4*>(g + i0 + 4);
+      q8[u] = *reinterpret_cast<const uint64_t*>(moment_q + i0);
+      c8[u] = *reinterpret_cast<const uint64_t*>(coord + i0);
+      old_byte[u] = packed[r * stride + (cc >> 3)];
+      rf[u] = w.row_factor[r];
+      const int64_t blk = i0 >> p.block_shift;  // block_size >= 8: one block for the byte
+      s_old[u] = f16_to_f32(moment_scale[blk]);
+      decode[u] = fmaxf(f16_to_f32(w.s_new[blk]), 1e-12f);
+      rdec[u] = w.s_rcp[blk];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the arithmetic
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t r = r0 + u * rstep;
+      if (r >= p.rows) break;
+      const int64_t i0 = r * p.cols + cc;
+      const uint32_t head = scramble_head(static_cast<uint32_t>(i0) ^ combined);
+      const float gv[8] = {ga[u].x, ga[u].y, ga[u].z, ga[u].w, gb[u].x, gb[u].y, gb[u].z, gb[u].w};
+      uint32_t byte = 0, cn_lo = 0, cn_hi = 0, qn_lo = 0, qn_hi = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float u2 = normalized(gv[j], rf[u], cv[j]);
+        if (!DIV1) u2 = div_by(u2, divisor, rdiv);
+        const float prev = static_cast<float>(static_cast<int8_t>(q8[u] >> (8 * j)));
+        const float cur = static_cast<float>(static_cast<int8_t>(c8[u] >> (8 * j)));
+        const float m = moment_of(u2, prev, s_old[u], p);
+        const float delta = m * step_size;
+        const float target = cur - delta;
+        const float lower = floorf(target);
+        const float uu = static_cast<float>(scramble_tail(head ^ static_cast<uint32_t>(j))) * (1.0f / 4294967296.0f);
+        const float frac = target - lower;
+        float rounded = lower + (uu < frac ? 1.0f : 0.0f);
+        rounded = fminf(127.0f, fmaxf(-127.0f, rounded));
+        float q = rintf(div_by(m, decode[u], rdec[u]));
+        q = fminf(127.0f, fmaxf(-127.0f, q));
+        const uint32_t cb8 = static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(rounded)));
+        const uint32_t qb8 = static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(q)));
+        if (j < 4) {
+          cn_lo |= cb8 << (8 * j);
+          qn_lo |= qb8 << (8 * j);
+        } else {
+          cn_hi |= cb8 << (8 * (j - 4));
+          qn_hi |= qb8 << (8 * (j - 4));
+        }
+        byte |= (rounded >= 0.0f ? 1u : 0u) << j;
+      }
+      if (lane_on) {
+        if (on) {
+          *reinterpret_cast<uint64_t*>(coord + i0) = (static_cast<uint64_t>(cn_hi) << 32) | cn_lo;
+          *reinterpret_cast<uint64_t*>(moment_q + i0) = (static_cast<uint64_t>(qn_hi) << 32) | qn_lo;
+          packed[r * stride + (cc >> 3)] = static_cast<uint8_t>(byte);
+        }
+        flips += __popc(old_byte[u] ^ byte);
+      }
+    }
+  }
+  return flips;
+}
+
+__global__ __launch_bounds__(kThreads) void final_row_kernel(const float* __restrict__ g,
+                                                             int8_t* __restrict__ coord,
+                                                             uint8_t* __restrict__ packed,
+                                                             int8_t* __restrict__ moment_q,
+                                                             const uint16_t* __restrict__ moment_scale,
+                                                             Params p, Work w) {
+  __shared__ double red[kThreads / kWave];
+  __shared__ int64_t ired[kThreads / kWave];
+  double acc = 0.0;
+  for (int64_t i = threadIdx.x; i < w.parts; i += kThreads) acc += w.msq_part[i];
+  acc = block_sum(acc, red);
+  const float padded = static_cast<float>(p.blocks * p.block_size);
+  float mrms = sqrtf(static_cast<float>(acc) / padded);
+  mrms = fmaxf(mrms, 1e-8f);
+  const float step_size = p.lr / mrms;
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) w.scalars[2] = step_size;
+  const float divisor = w.scalars[1];
+  const float rdiv = 1.0f / divisor;
+  const int64_t step = p.step_device ? *p.step_device : p.step;
+  const uint32_t combined = p.seed_part ^ step_hash(step);
+  const bool on = enabled(p);
+  const int64_t flips =
+      divisor == 1.0f
+          ? final_row_loop<true>(g, coord, packed, moment_q, moment_scale, p, w, divisor, rdiv, step_size, combined, on)
+          : final_row_loop<false>(g, coord, packed, moment_q, moment_scale, p, w, divisor, rdiv, step_size, combined,
+                                  on);
+  const int64_t total = block_sum(flips, ired);
+  if (threadIdx.x == 0) w.flips_part[static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x] = on ? total : 0;
+}
+
 __global__ __launch_bounds__(kThreads) void finish_kernel(uint16_t* __restrict__ moment_scale,
                                                           int64_t* __restrict__ flips_out, Params p, Work w) {
   __shared__ int64_t red[kThreads / kWave];
@@ -681,15 +1078,14 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(uint16_t* __restrict__
   }
   if (blockIdx.x == 0 && flips_out) {
     int64_t acc = 0;
-    for (int64_t i = threadIdx.x; i < kFinalGroups; i += kThreads) acc += w.flips_part[i];
+    for (int64_t i = threadIdx.x; i < w.fparts; i += kThreads) acc += w.flips_part[i];
     acc = block_sum(acc, red);
     if (threadIdx.x == 0) *flips_out = acc;
   }
 }
 
 // -- plan ------------------------------------------------------------------------
-constexpr int kSegments = 12;
-constexpr int kRowsGroups = 64;
+constexpr int kSegments = 13;
 
 struct Layout {
   size_t off[kSegments];
@@ -716,6 +1112,7 @@ static Layout layout(int64_t rows, int64_t cols, int64_t block_size, Work* w) {
       sizeof(float) * 4,
       sizeof(uint16_t) * static_cast<size_t>(blocks),
       sizeof(int64_t) * kFinalGroups,
+      sizeof(float) * static_cast<size_t>(blocks),
   };
   Layout l{};
   size_t at = 0;
@@ -763,6 +1160,7 @@ int launch_coordinate_update(const float* g, int8_t* coord, uint8_t* packed, int
   w.scalars = reinterpret_cast<float*>(base + l.off[9]);
   w.s_new = reinterpret_cast<uint16_t*>(base + l.off[10]);
   w.flips_part = reinterpret_cast<int64_t*>(base + l.off[11]);
+  w.s_rcp = reinterpret_cast<float*>(base + l.off[12]);
 
   Params p{};
   p.b1 = static_cast<float>(beta1);
@@ -793,19 +1191,41 @@ int launch_coordinate_update(const float* g, int8_t* coord, uint8_t* packed, int
   p.spec = p.vec && cols % 256 == 0 && block_size >= 4 && block_size <= 256 &&
            (reinterpret_cast<uintptr_t>(moment_q) & 3) == 0 && step_device == nullptr && step_ >= 64;
 
+  // row path: whole 256-column slots, momentum blocks inside one slot, and
+  // at least one usq workgroup per chunk
+  const bool row_path = p.vec && cols % 256 == 0 && block_size <= 256 && w.nchunks <= kUsqGroups;
+  const unsigned row_groups = static_cast<unsigned>(kUsqGroups / w.nchunks);
+  w.parts = row_path ? static_cast<int64_t>(row_groups) * w.nchunks : kUsqGroups;
+
   int rc;
-  stats_kernel<<<dim3(static_cast<unsigned>(w.nchunks), static_cast<unsigned>(w.nstrips)), kThreads, 0,
-                 stream>>>(g, row_v, p, w);
+  const dim3 stats_grid(static_cast<unsigned>(w.nchunks), static_cast<unsigned>(w.nstrips));
+  if (row_path)
+    stats_row_kernel<<<stats_grid, kThreads, 0, stream>>>(g, row_v, p, w);
+  else
+    stats_kernel<<<stats_grid, kThreads, 0, stream>>>(g, row_v, p, w);
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
-  rows_kernel<<<kRowsGroups, kThreads, 0, stream>>>(row_v, p, w);
+  const int col_groups = ceil_div(cols, 16);
+  colrow_kernel<<<col_groups + kRowsGroups, kThreads, 0, stream>>>(col_v, row_v, p, w, col_groups);
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
-  cols_kernel<<<ceil_div(cols, 64), kThreads, 0, stream>>>(col_v, p, w, kRowsGroups);
+  if (row_path) {
+    const dim3 grid(row_groups, static_cast<unsigned>(w.nchunks));
+    elem_row_kernel<false><<<grid, kThreads, 0, stream>>>(g, moment_q, moment_scale, p, w);
+    if ((rc = static_cast<int>(hipGetLastError()))) return rc;
+    elem_row_kernel<true><<<grid, kThreads, 0, stream>>>(g, moment_q, moment_scale, p, w);
+  } else {
+    usq_kernel<<<kUsqGroups, kThreads, 0, stream>>>(g, moment_q, moment_scale, p, w);
+    if ((rc = static_cast<int>(hipGetLastError()))) return rc;
+    moment_kernel<<<kMomentGroups, kThreads, 0, stream>>>(g, moment_q, moment_scale, p, w);
+  }
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
-  usq_kernel<<<kUsqGroups, kThreads, 0, stream>>>(g, moment_q, moment_scale, p, w);
-  if ((rc = static_cast<int>(hipGetLastError()))) return rc;
-  moment_kernel<<<kMomentGroups, kThreads, 0, stream>>>(g, moment_q, moment_scale, p, w);
-  if ((rc = static_cast<int>(hipGetLastError()))) return rc;
-  if (p.vec)
+  const int64_t fchunks = (cols + kFinalChunk - 1) / kFinalChunk;
+  const bool final_rows = row_path && fchunks <= kFinalGroups;
+  const unsigned final_groups = static_cast<unsigned>(kFinalGroups / fchunks);
+  w.fparts = final_rows ? static_cast<int64_t>(final_groups) * fchunks : kFinalGroups;
+  if (final_rows)
+    final_row_kernel<<<dim3(final_groups, static_cast<unsigned>(fchunks)), kThreads, 0, stream>>>(
+        g, coord, packed, moment_q, moment_scale, p, w);
+  else if (p.vec)
     final_vec_kernel<<<kFinalGroups, kThreads, 0, stream>>>(g, coord, packed, moment_q, moment_scale, p, w);
   else
     final_kernel<<<kFinalGroups, kThreads, 0, stream>>>(g, coord, packed, moment_q, moment_scale, p, w);

@@ -264,8 +264,17 @@ def test_coordinate_update_reference_vectors(golden):
         assert not np.any(bad & (tm >= 2.0 ** -16)), name
 
 
+# Shapes with cols % 256 == 0 and block <= 256 take the row kernels (a wave
+# per 1024-column chunk, momentum blocks as lane groups): every block size
+# 8..256, a last chunk of 1, 2 or 3 slots, fewer rows than waves, and one
+# chunk for a whole row (the row sums finish in the stats pass).  The rest
+# take the generic kernels.
+ROW_PATH = [(64, 1280, 8), (33, 2304, 16), (130, 512, 32), (3, 256, 64), (200, 3072, 128), (70, 1792, 256),
+            (64, 1024, 512)]
+
+
 @pytest.mark.parametrize("rows,cols,block", [(16, 32, 64), (37, 45, 64), (256, 1024, 256), (1024, 384, 256),
-                                             (200, 200, 128), (3, 5000, 256), (512, 4096, 256)])
+                                             (200, 200, 128), (3, 5000, 256), (512, 4096, 256)] + ROW_PATH)
 def test_coordinate_update_matches_oracle(rows, cols, block):
     rng = np.random.default_rng(rows * cols)
     coord = rng.integers(-127, 128, size=(rows, cols)).astype(np.int8)
