@@ -507,66 +507,66 @@ __device__ __forceinline__ int chunk_slots(int64_t cols, int64_t c0) {
   return left >= 4 ? 4 : static_cast<int>(left);
 }
 
-// stats on the row path: workgroup (chunk, strip); wave w takes rows w,
-// w + 4, ... of the strip, two rows' loads in flight before either is
-// reduced; one wave sum per row and chunk, the column partials of the four
-// waves combined through LDS.  Same outputs as stats_kernel.
+// stats on the row path: workgroup (b, chunk) takes rows 4 b + wave,
+// + 4 gridDim.x, ... of its chunk, the next row's loads issued before the
+// current row is reduced; one wave sum per row and chunk, and the column
+// partials of the four waves combined through LDS into strip b.  Same
+// outputs as stats_kernel with gridDim.x strips.
 __global__ __launch_bounds__(kThreads) void stats_row_kernel(const float* __restrict__ g,
                                                              uint16_t* __restrict__ row_v, Params p, Work w) {
   __shared__ double colsum[kThreads / kWave][kRowChunk];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int64_t chunk = blockIdx.x;
+  const int64_t chunk = blockIdx.y;
   const int64_t c0 = chunk * kRowChunk;
   const int ns = chunk_slots(p.cols, c0);
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kStrip;
-  const int rows_here = static_cast<int>(p.rows - r0 < kStrip ? p.rows - r0 : kStrip);
-  const float* base = g + r0 * p.cols + c0 + 4 * lane;
+  // slots past the chunk's end re-read its last slot (results dropped)
+  int64_t sc[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) sc[k] = c0 + 4 * lane + 256 * (k < ns ? k : ns - 1);
   double col[4][4];
 #pragma unroll
   for (int k = 0; k < 4; ++k)
 #pragma unroll
     for (int e = 0; e < 4; ++e) col[k][e] = 0.0;
-  constexpr int U = 2;  // rows per wave iteration
-  for (int rr = wave; rr < rows_here; rr += 4 * U) {
-    float4 v[U][4];
+  const int64_t rstep = static_cast<int64_t>(gridDim.x) * (kThreads / kWave);
+  int64_t r = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + wave;
+  float4 cur[4];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int row = rr + 4 * u;
+  for (int k = 0; k < 4; ++k) cur[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (r < p.rows) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        v[u][k] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (row < rows_here && k < ns)
-          v[u][k] = *reinterpret_cast<const float4*>(base + row * p.cols + 256 * k);
+    for (int k = 0; k < 4; ++k) cur[k] = *reinterpret_cast<const float4*>(g + r * p.cols + sc[k]);
+  }
+  for (; r < p.rows; r += rstep) {
+    // the last row re-reads itself (a cache hit) rather than branch
+    const int64_t rn = r + rstep < p.rows ? r + rstep : r;
+    float4 nxt[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) nxt[k] = *reinterpret_cast<const float4*>(g + rn * p.cols + sc[k]);
+    __builtin_amdgcn_sched_barrier(0);  // the next row's loads in flight during this row's arithmetic
+    double rp = 0.0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (k >= ns) break;
+      const double d0 = square_eps(cur[k].x), d1 = square_eps(cur[k].y);
+      const double d2 = square_eps(cur[k].z), d3 = square_eps(cur[k].w);
+      col[k][0] += d0; col[k][1] += d1; col[k][2] += d2; col[k][3] += d3;
+      rp += (d0 + d1) + (d2 + d3);
+    }
+    rp = wave_total(rp);
+    if (lane == 0) {
+      if (w.nchunks == 1) {
+        const float mean = static_cast<float>(rp) / static_cast<float>(p.cols);
+        const float nr = fmaf(mean, p.a2, f16_to_f32(row_v[r]) * p.b2);
+        w.new_row[r] = nr;
+        if (enabled(p)) row_v[r] = f32_to_f16(nr);
+      } else {
+        w.row_part[chunk * p.rows + r] = rp;
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int row = rr + 4 * u;
-      if (row >= rows_here) break;
-      double rp = 0.0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        if (k < ns) {
-          const double d0 = square_eps(v[u][k].x), d1 = square_eps(v[u][k].y);
-          const double d2 = square_eps(v[u][k].z), d3 = square_eps(v[u][k].w);
-          col[k][0] += d0; col[k][1] += d1; col[k][2] += d2; col[k][3] += d3;
-          rp += (d0 + d1) + (d2 + d3);
-        }
-      }
-      rp = wave_total(rp);
-      if (lane == 0) {
-        const int64_t r = r0 + row;
-        if (w.nchunks == 1) {
-          const float mean = static_cast<float>(rp) / static_cast<float>(p.cols);
-          const float nr = fmaf(mean, p.a2, f16_to_f32(row_v[r]) * p.b2);
-          w.new_row[r] = nr;
-          if (enabled(p)) row_v[r] = f32_to_f16(nr);
-        } else {
-          w.row_part[chunk * p.rows + r] = rp;
-        }
-      }
-    }
+    for (int k = 0; k < 4; ++k) cur[k] = nxt[k];
   }
 #pragma unroll
   for (int k = 0; k < 4; ++k)
@@ -574,7 +574,7 @@ __global__ __launch_bounds__(kThreads) void stats_row_kernel(const float* __rest
     for (int e = 0; e < 4; ++e) colsum[wave][256 * k + 4 * lane + e] = col[k][e];
   __syncthreads();
   for (int c = threadIdx.x; c < 256 * ns; c += kThreads)
-    w.col_part[static_cast<int64_t>(blockIdx.y) * p.cols + c0 + c] =
+    w.col_part[static_cast<int64_t>(blockIdx.x) * p.cols + c0 + c] =
         (colsum[0][c] + colsum[1][c]) + (colsum[2][c] + colsum[3][c]);
 }
 
@@ -934,14 +934,14 @@ __global__ __launch_bounds__(kThreads) void final_vec_kernel(const float* __rest
 }
 
 // Final pass on the row path: workgroup (b, chunk) takes kFinalChunk
-// columns of rows 4 b + wave, + 4 gridDim.x, ..., two rows per iteration;
+// columns of rows 4 b + wave, + 4 gridDim.x, ..., the next row's loads
+// issued before the current row's arithmetic;
 // lane l owns the packed byte of columns c0 + 8 l .. + 7 (lanes past the
 // row's end idle).  Column factors stay in registers, the row factor is one
 // load per row, the block scale's reciprocal comes from the momentum pass,
 // and the eight elements of a byte share the first step of their hash.
 // The same arithmetic as final_byte.
 constexpr int kFinalChunk = 512;
-constexpr int kFinalRows = 1;  // rows per wave iteration
 
 template <bool DIV1>
 __device__ __forceinline__ int64_t final_row_loop(const float* __restrict__ g, int8_t* __restrict__ coord,
@@ -967,73 +967,74 @@ __device__ __forceinline__ int64_t final_row_loop(const float* __restrict__ g, i
   // per load): idle lanes read their row's last byte, rows past the end the
   // last row, and those results are dropped
   const int64_t cc = lane_on ? c0 : p.cols - 8;
-  constexpr int U = kFinalRows;
-  for (int64_t r0 = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + wave; r0 < p.rows; r0 += U * rstep) {
-    float4 ga[U], gb[U];
-    uint64_t q8[U], c8[U];
-    uint32_t old_byte[U];
-    float rf[U], s_old[U], decode[U], rdec[U];
+  struct RowIn {
+    float4 ga, gb;
+    uint64_t q8, c8;
+    uint32_t old_byte;
+    float rf, s_old, decode, rdec;
+  };
+  auto load_row = [&](int64_t r, RowIn& in) {
+    const int64_t i0 = r * p.cols + cc;
+    in.ga = *reinterpret_cast<const float4*>(g + i0);
+    in.gb = *reinterpret_cast<const float4*>(g + i0 + 4);
+    in.q8 = *reinterpret_cast<const uint64_t*>(moment_q + i0);
+    in.c8 = *reinterpret_cast<const uint64_t*>(coord + i0);
+    in.old_byte = packed[r * stride + (cc >> 3)];
+    in.rf = w.row_factor[r];
+    const int64_t blk = i0 >> p.block_shift;  // block_size >= 8: one block for the byte
+    in.s_old = f16_to_f32(moment_scale[blk]);
+    in.decode = fmaxf(f16_to_f32(w.s_new[blk]), 1e-12f);
+    in.rdec = w.s_rcp[blk];
+  };
+  int64_t r = static_cast<int64_t>(blockIdx.x) * (kThreads / kWave) + wave;
+  RowIn cur;
+  load_row(r < p.rows ? r : 0, cur);
+  for (; r < p.rows; r += rstep) {
+    // the next row's loads in flight during this row's arithmetic; the last
+    // row re-reads itself (a cache hit) rather than branch
+    RowIn nxt;
+    load_row(r + rstep < p.rows ? r + rstep : r, nxt);
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t i0 = r * p.cols + cc;
+    const uint32_t head = scramble_head(static_cast<uint32_t>(i0) ^ combined);
+    const float gv[8] = {cur.ga.x, cur.ga.y, cur.ga.z, cur.ga.w, cur.gb.x, cur.gb.y, cur.gb.z, cur.gb.w};
+    uint32_t byte = 0, cn_lo = 0, cn_hi = 0, qn_lo = 0, qn_hi = 0;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t rr = r0 + u * rstep;
-      const int64_t r = rr < p.rows ? rr : p.rows - 1;
-      const int64_t i0 = r * p.cols + cc;
-      ga[u] = *reinterpret_cast<const float4*>(g + i0);
-      gb[u] = *reinterpret_cast<const float4*>(g + i0 + 4);
-      q8[u] = *reinterpret_cast<const uint64_t*>(moment_q + i0);
-      c8[u] = *reinterpret_cast<const uint64_t*>(coord + i0);
-      old_byte[u] = packed[r * stride + (cc >> 3)];
-      rf[u] = w.row_factor[r];
-      const int64_t blk = i0 >> p.block_shift;  // block_size >= 8: one block for the byte
-      s_old[u] = f16_to_f32(moment_scale[blk]);
-      decode[u] = fmaxf(f16_to_f32(w.s_new[blk]), 1e-12f);
-      rdec[u] = w.s_rcp[blk];
-    }
-    __builtin_amdgcn_sched_barrier(0);  // every load issued before the arithmetic
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t r = r0 + u * rstep;
-      if (r >= p.rows) break;
-      const int64_t i0 = r * p.cols + cc;
-      const uint32_t head = scramble_head(static_cast<uint32_t>(i0) ^ combined);
-      const float gv[8] = {ga[u].x, ga[u].y, ga[u].z, ga[u].w, gb[u].x, gb[u].y, gb[u].z, gb[u].w};
-      uint32_t byte = 0, cn_lo = 0, cn_hi = 0, qn_lo = 0, qn_hi = 0;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float u2 = normalized(gv[j], rf[u], cv[j]);
-        if (!DIV1) u2 = div_by(u2, divisor, rdiv);
-        const float prev = static_cast<float>(static_cast<int8_t>(q8[u] >> (8 * j)));
-        const float cur = static_cast<float>(static_cast<int8_t>(c8[u] >> (8 * j)));
-        const float m = moment_of(u2, prev, s_old[u], p);
-        const float delta = m * step_size;
-        const float target = cur - delta;
-        const float lower = floorf(target);
-        const float uu = static_cast<float>(scramble_tail(head ^ static_cast<uint32_t>(j))) * (1.0f / 4294967296.0f);
-        const float frac = target - lower;
-        float rounded = lower + (uu < frac ? 1.0f : 0.0f);
-        rounded = fminf(127.0f, fmaxf(-127.0f, rounded));
-        float q = rintf(div_by(m, decode[u], rdec[u]));
-        q = fminf(127.0f, fmaxf(-127.0f, q));
-        const uint32_t cb8 = static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(rounded)));
-        const uint32_t qb8 = static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(q)));
-        if (j < 4) {
-          cn_lo |= cb8 << (8 * j);
-          qn_lo |= qb8 << (8 * j);
-        } else {
-          cn_hi |= cb8 << (8 * (j - 4));
-          qn_hi |= qb8 << (8 * (j - 4));
-        }
-        byte |= (rounded >= 0.0f ? 1u : 0u) << j;
+    for (int j = 0; j < 8; ++j) {
+      float u2 = normalized(gv[j], cur.rf, cv[j]);
+      if (!DIV1) u2 = div_by(u2, divisor, rdiv);
+      const float prev = static_cast<float>(static_cast<int8_t>(cur.q8 >> (8 * j)));
+      const float cval = static_cast<float>(static_cast<int8_t>(cur.c8 >> (8 * j)));
+      const float m = moment_of(u2, prev, cur.s_old, p);
+      const float delta = m * step_size;
+      const float target = cval - delta;
+      const float lower = floorf(target);
+      const float uu = static_cast<float>(scramble_tail(head ^ static_cast<uint32_t>(j))) * (1.0f / 4294967296.0f);
+      const float frac = target - lower;
+      float rounded = lower + (uu < frac ? 1.0f : 0.0f);
+      rounded = fminf(127.0f, fmaxf(-127.0f, rounded));
+      float q = rintf(div_by(m, cur.decode, cur.rdec));
+      q = fminf(127.0f, fmaxf(-127.0f, q));
+      const uint32_t cb8 = static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(rounded)));
+      const uint32_t qb8 = static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(q)));
+      if (j < 4) {
+        cn_lo |= cb8 << (8 * j);
+        qn_lo |= qb8 << (8 * j);
+      } else {
+        cn_hi |= cb8 << (8 * (j - 4));
+        qn_hi |= qb8 << (8 * (j - 4));
       }
-      if (lane_on) {
-        if (on) {
-          *reinterpret_cast<uint64_t*>(coord + i0) = (static_cast<uint64_t>(cn_hi) << 32) | cn_lo;
-          *reinterpret_cast<uint64_t*>(moment_q + i0) = (static_cast<uint64_t>(qn_hi) << 32) | qn_lo;
-          packed[r * stride + (cc >> 3)] = static_cast<uint8_t>(byte);
-        }
-        flips += __popc(old_byte[u] ^ byte);
-      }
+      byte |= (rounded >= 0.0f ? 1u : 0u) << j;
     }
+    if (lane_on) {
+      if (on) {
+        *reinterpret_cast<uint64_t*>(coord + i0) = (static_cast<uint64_t>(cn_hi) << 32) | cn_lo;
+        *reinterpret_cast<uint64_t*>(moment_q + i0) = (static_cast<uint64_t>(qn_hi) << 32) | qn_lo;
+        packed[r * stride + (cc >> 3)] = static_cast<uint8_t>(byte);
+      }
+      flips += __popc(cur.old_byte ^ byte);
+    }
+    cur = nxt;
   }
   return flips;
 }
@@ -1097,10 +1098,12 @@ static size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255);
 static Layout layout(int64_t rows, int64_t cols, int64_t block_size, Work* w) {
   const int64_t nchunks = (cols + kColChunk - 1) / kColChunk;
   const int64_t nstrips = (rows + kStrip - 1) / kStrip;
+  // the row path's stats pass writes one strip per usq workgroup of a chunk
+  const int64_t row_strips = nchunks <= kUsqGroups ? kUsqGroups / nchunks : 0;
   const int64_t count = rows * cols;
   const int64_t blocks = (count + block_size - 1) / block_size;
   const size_t sizes[kSegments] = {
-      sizeof(double) * static_cast<size_t>(nstrips * cols),
+      sizeof(double) * static_cast<size_t>((nstrips > row_strips ? nstrips : row_strips) * cols),
       sizeof(double) * kRowsGroups,
       sizeof(double) * static_cast<size_t>(nchunks > 1 ? nchunks * rows : 1),
       sizeof(float) * static_cast<size_t>(rows),
@@ -1129,6 +1132,24 @@ static Layout layout(int64_t rows, int64_t cols, int64_t block_size, Work* w) {
 }
 
 }  // namespace step
+
+// Workgroups of final_row_kernel resident at once on the current device
+// (compute units x workgroups per unit at its register use), cached per
+// device; 0 when the runtime cannot say.
+static int64_t resident_final_groups() {
+  static int64_t cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, step::final_row_kernel, step::kThreads, 0) !=
+            hipSuccess)
+      return 0;
+    cache[dev] = static_cast<int64_t>(cus) * per_cu;
+  }
+  return cache[dev];
+}
 
 size_t coordinate_update_workspace(int64_t rows, int64_t cols, int64_t block_size) {
   if (rows <= 0 || cols <= 0 || block_size <= 0) return 0;
@@ -1198,11 +1219,13 @@ int launch_coordinate_update(const float* g, int8_t* coord, uint8_t* packed, int
   w.parts = row_path ? static_cast<int64_t>(row_groups) * w.nchunks : kUsqGroups;
 
   int rc;
-  const dim3 stats_grid(static_cast<unsigned>(w.nchunks), static_cast<unsigned>(w.nstrips));
-  if (row_path)
-    stats_row_kernel<<<stats_grid, kThreads, 0, stream>>>(g, row_v, p, w);
-  else
-    stats_kernel<<<stats_grid, kThreads, 0, stream>>>(g, row_v, p, w);
+  if (row_path) {
+    w.nstrips = row_groups;
+    stats_row_kernel<<<dim3(row_groups, static_cast<unsigned>(w.nchunks)), kThreads, 0, stream>>>(g, row_v, p, w);
+  } else {
+    stats_kernel<<<dim3(static_cast<unsigned>(w.nchunks), static_cast<unsigned>(w.nstrips)), kThreads, 0, stream>>>(
+        g, row_v, p, w);
+  }
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
   const int col_groups = ceil_div(cols, 16);
   colrow_kernel<<<col_groups + kRowsGroups, kThreads, 0, stream>>>(col_v, row_v, p, w, col_groups);
@@ -1220,7 +1243,11 @@ int launch_coordinate_update(const float* g, int8_t* coord, uint8_t* packed, int
   if ((rc = static_cast<int>(hipGetLastError()))) return rc;
   const int64_t fchunks = (cols + kFinalChunk - 1) / kFinalChunk;
   const bool final_rows = row_path && fchunks <= kFinalGroups;
-  const unsigned final_groups = static_cast<unsigned>(kFinalGroups / fchunks);
+  // as many workgroups as the device holds at once (one round, no tail),
+  // at most kFinalGroups in all
+  const int64_t fit = resident_final_groups();
+  const int64_t per_chunk = (fit > 0 ? (fit < kFinalGroups ? fit : kFinalGroups) : kFinalGroups) / fchunks;
+  const unsigned final_groups = static_cast<unsigned>(per_chunk > 0 ? per_chunk : 1);
   w.fparts = final_rows ? static_cast<int64_t>(final_groups) * fchunks : kFinalGroups;
   if (final_rows)
     final_row_kernel<<<dim3(final_groups, static_cast<unsigned>(fchunks)), kThreads, 0, stream>>>(
