@@ -157,6 +157,12 @@ def gemm_kernels(T, d, ffn, device, iters=5):
         ms = timed_events(fn, iters)
         out[name] = {"ms": round(ms, 4), "tflops": round(flop / ms / 1e9, 2),
                      "frac_of_mfma_peak": round(flop / (ms * 1e-3) / MFMA_BF16_PEAK, 4)}
+    # the training path's backward of one layer: one C-ABI call, dX and the
+    # evidence in one kernel launch plus its sign transposes, scale copies and
+    # column sums (two products' FLOPs)
+    ms = timed_events(lambda: kernels.linear_backward(dy, xbits, off, xs, packed, scale, d, need_bias=False), iters)
+    out["backward_call"] = {"ms": round(ms, 4), "tflops": round(2 * flop / ms / 1e9, 2),
+                            "frac_of_mfma_peak": round(2 * flop / (ms * 1e-3) / MFMA_BF16_PEAK, 4)}
     del oracle
     return out, flop
 
@@ -340,7 +346,7 @@ def main():
     }
     if not args.no_extras:
         kernels_t, kflop = gemm_kernels(T, d, ffn, device)
-        dominant = max(kernels_t, key=lambda k: kernels_t[k]["ms"])
+        dominant = max((k for k in kernels_t if k != "backward_call"), key=lambda k: kernels_t[k]["ms"])
         dk = kernels_t[dominant]
         traffic = read_traffic().get(dominant)
         line["roofline"] = {"bound": "mfma", "kernel": dominant, "achieved": dk["tflops"],

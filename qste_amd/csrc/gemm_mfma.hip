@@ -357,24 +357,26 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
       }
     }
   };
-  // bits along K: this lane's 64 k-bits of each of its 4 columns
+  // bits along K: this lane's 64 k-bits of each of its columns, as stored
+  // (a set bit is +1); the expansions invert them, so no arithmetic waits on
+  // these reads (LDS reads complete in order: a use right after this read
+  // would also wait for every dense-fragment read issued before it)
   auto load_bits = [&](const uint8_t* Bs) {
     if (BKIND != B_BITS_ALONG_N) {
 #pragma unroll
-      for (int nb = 0; nb < NBN; ++nb)
-        bits[nb] = ~*reinterpret_cast<const uint64_t*>(Bs + 8 * (WNC * wn + 32 * nb + l32));
+      for (int nb = 0; nb < NBN; ++nb) bits[nb] = *reinterpret_cast<const uint64_t*>(Bs + 8 * (WNC * wn + 32 * nb + l32));
     }
   };
+  // the inverted byte of k-bits of substep s (a set bit is -1)
+  auto neg_byte = [&](int nb, int s) { return ~static_cast<uint32_t>(bits[nb] >> (8 * (2 * s + kg))) & 0xFFu; };
   auto expand_b = [&](const uint8_t* Bs, const uint16_t* Ss, int s, bf16x8* dst) {
     if (BKIND == B_BITS_ALONG_K) {
 #pragma unroll
-      for (int nb = 0; nb < NBN; ++nb)
-        dst[nb] = signs_along_k(static_cast<uint32_t>(bits[nb] >> (8 * (2 * s + kg))) & 0xFFu, one);
+      for (int nb = 0; nb < NBN; ++nb) dst[nb] = signs_along_k(neg_byte(nb, s), one);
     } else if (BKIND == B_BITS_ALONG_K_SCALED) {
       const uint4 sc = *reinterpret_cast<const uint4*>(Ss + 16 * s + 8 * kg);
 #pragma unroll
-      for (int nb = 0; nb < NBN; ++nb)
-        dst[nb] = scaled_signs_along_k(static_cast<uint32_t>(bits[nb] >> (8 * (2 * s + kg))) & 0xFFu, sc);
+      for (int nb = 0; nb < NBN; ++nb) dst[nb] = scaled_signs_along_k(neg_byte(nb, s), sc);
     } else {
       const int kk = 16 * s + 8 * kg;
       const uint4 sc = *reinterpret_cast<const uint4*>(Ss + kk);
@@ -398,10 +400,10 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   };
   auto expand_b1 = [&](const uint8_t* Bs, const uint16_t* Ss, int s, int nb, bf16x8* dst) {
     if (BKIND == B_BITS_ALONG_K) {
-      dst[nb] = signs_along_k(static_cast<uint32_t>(bits[nb] >> (8 * (2 * s + kg))) & 0xFFu, one);
+      dst[nb] = signs_along_k(neg_byte(nb, s), one);
     } else if (BKIND == B_BITS_ALONG_K_SCALED) {
       const uint4 sc = *reinterpret_cast<const uint4*>(Ss + 16 * s + 8 * kg);
-      dst[nb] = scaled_signs_along_k(static_cast<uint32_t>(bits[nb] >> (8 * (2 * s + kg))) & 0xFFu, sc);
+      dst[nb] = scaled_signs_along_k(neg_byte(nb, s), sc);
     } else {
       const int kk = 16 * s + 8 * kg;
       const uint4 sc = *reinterpret_cast<const uint4*>(Ss + kk);
@@ -459,11 +461,11 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
     mfma_row(3, 0);
     __builtin_amdgcn_sched_barrier(0);
     issue(it + 3, N3a, N3b, N3s, 1);
+    load_bits(N1b);
     load_a(N1a, 0, a[0]);
     mfma_row(3, 1);
     __builtin_amdgcn_sched_barrier(0);
     issue(it + 3, N3a, N3b, N3s, 2);
-    load_bits(N1b);
     mfma_row(3, 2);
     __builtin_amdgcn_sched_barrier(0);
     issue(it + 3, N3a, N3b, N3s, 3);
@@ -490,8 +492,8 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   }
   issue(2, A2, B2, S2);
   stage_barrier<BKIND != B_BITS_ALONG_N ? 2 * NL : NL>();  // along K: steps 0, 1 complete; along N: step 0, 1
-  load_a(A0, 0, a[0]);
   load_bits(B0);
+  load_a(A0, 0, a[0]);
   expand_b(B0, S0, 0, b[0]);
   int it = 0;
   for (; it + 4 <= nk; it += 4) {
