@@ -150,6 +150,89 @@ int qste_coordinate_update(const float* evidence, int8_t* coordinate, uint8_t* p
                            const uint8_t* update_enabled, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/* ---- packed activations (src/qste/nn.py) ------------------------------- */
+
+/* masked-activation kinds of qste_masked_activation */
+#define QSTE_MASK_CLAMP 0    /* ReLU, ReLU6, Hardtanh: out = clamp(x), bit = lower < out (< upper) */
+#define QSTE_MASK_LEAKY 1    /* LeakyReLU: out = x > 0 ? x : x * slope, bit = x > 0 */
+#define QSTE_MASK_INTERVAL 2 /* Hardsigmoid: bit = lower < x (< upper) only; out unused */
+
+/* smooth-activation kinds of qste_smooth_activation */
+#define QSTE_ACT_GELU 0
+#define QSTE_ACT_GELU_TANH 1
+#define QSTE_ACT_SILU 2
+#define QSTE_ACT_TANH 3
+#define QSTE_ACT_SIGMOID 4
+#define QSTE_ACT_ELU 5        /* param = alpha */
+#define QSTE_ACT_CELU 6       /* param = alpha */
+#define QSTE_ACT_SELU 7
+#define QSTE_ACT_SOFTPLUS 8   /* param = beta (threshold 20) */
+#define QSTE_ACT_MISH 9
+#define QSTE_ACT_HARDSWISH 10
+#define QSTE_ACT_RELU_SQUARE 11 /* relu(x)^2; uint8 payload of relu(x) */
+#define QSTE_ACT_PROVIDED 12  /* derivative handed in as fp32 [rows, cols] */
+
+/* One bit per element of a byte mask (nonzero -> 1), LSB first:
+ * mask uint8 [rows, cols] -> packed uint8 [rows, (cols+7)/8], pad bits 0.
+ * Replaces qste.kernels.pack_bits (src/qste/kernels/loader.py:256-260;
+ * fallback.py:32-47). */
+int qste_pack_bits(const uint8_t* mask, uint8_t* packed, int64_t rows, int64_t cols,
+                   void* stream);
+
+/* The 0/1 companion of unpack_rows: out [rows, cols] in out_dtype.
+ * Replaces qste.kernels.unpack_bits (loader.py:270-273; fallback.py:50-54). */
+int qste_unpack_bits(const uint8_t* packed, void* out, int out_dtype, int64_t rows,
+                     int64_t cols, void* stream);
+
+/* out = values where the bit is set, +0 where it is not (the GPU
+ * reference's select, cuda.py:158-178).
+ * Replaces qste.kernels.apply_bits (loader.py:263-267; fallback.py:57-70). */
+int qste_apply_bits(const void* values, int dtype, const uint8_t* packed, void* out,
+                    int64_t rows, int64_t cols, void* stream);
+
+/* Backward of every one-bit activation: kept = bit ? grad : 0, then
+ * out = kept * inside when outside == 0, else
+ * out = grad * outside + kept * diff (each product and the sum rounded to the
+ * dtype).  Replaces the backward bodies of _MaskedFn, _PiecewiseFn, _LeakyFn
+ * and _DropoutFn (src/qste/nn.py:133-136, 168-181, 278-282, 364-368), which
+ * call apply_bits and then scale in torch. */
+int qste_masked_backward(const void* grad, int dtype, const uint8_t* packed, void* out,
+                         int64_t rows, int64_t cols, float inside, float outside, float diff,
+                         void* stream);
+
+/* Forward of a one-bit activation and its mask in one pass (kind
+ * QSTE_MASK_*; upper ignored unless has_upper).  out and x may not overlap.
+ * Replaces the forward bodies of _MaskedFn, _LeakyFn and _PiecewiseFn
+ * (src/qste/nn.py:119-131, 152-166, 271-276): torch's clamp / leaky_relu
+ * followed by pack_bits. */
+int qste_masked_activation(const void* x, int dtype, int kind, float lower, float upper,
+                           int has_upper, float slope, void* out, uint8_t* packed,
+                           int64_t rows, int64_t cols, void* stream);
+
+/* Smooth activation with its derivative retained as a row-quantized byte.
+ * Per row r: d = f'(x) in fp32 (from x and from y = f(x) rounded to the
+ * dtype), scale[r] = max(amax_c |d|, 1e-8) / 127, payload int8 =
+ * clamp(round_half_even(d / scale), -127, 127).
+ *   y_given == 0: y = f(x) is computed here and written to y (y may be NULL)
+ *   y_given != 0: y holds the forward output already and is read
+ *   kind QSTE_ACT_PROVIDED: `derivative` (fp32 [rows, cols]) is quantized;
+ *                 x and y are unused
+ *   kind QSTE_ACT_RELU_SQUARE: y = relu(x)^2; the payload is uint8 of relu(x)
+ *                 against max(amax, 1e-8) / 255, that arithmetic in the dtype
+ * Replaces _SmoothFn.forward, _ReluSquareFn.forward and
+ * _AnyElementwiseFn.forward (src/qste/nn.py:487-502, 315-323, 531-548). */
+int qste_smooth_activation(const void* x, int dtype, int kind, float param, void* y,
+                           int y_given, const float* derivative, void* payload, float* scale,
+                           int64_t rows, int64_t cols, void* stream);
+
+/* out = grad * (payload * scale[r]) (products rounded to the dtype); with
+ * unsigned_payload, out = grad * 2 * (payload * scale[r]) (relu(x)^2).
+ * Replaces _SmoothFn.backward / _ReluSquareFn.backward /
+ * _AnyElementwiseFn.backward (src/qste/nn.py:504-507, 325-330, 550-555). */
+int qste_smooth_backward(const void* grad, int dtype, const void* payload,
+                         int unsigned_payload, const float* scale, void* out, int64_t rows,
+                         int64_t cols, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

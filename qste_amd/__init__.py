@@ -20,6 +20,8 @@ from .convert import (continuous_parameters, convert, export_packed, memory_repo
                       surfaces)
 from .functional import QSTELinearFn, qste_linear, qste_weight
 from .modules import PackedLinear, QSTELinear
+from . import nn
+from .nn import packed_activations
 from .optim import QSTEOptimizer
 from .surface import Surface
 
@@ -38,6 +40,8 @@ __all__ = [
     "export_packed",
     "kernel_status",
     "memory_report",
+    "nn",
+    "packed_activations",
     "qste_linear",
     "qste_weight",
     "surfaces",

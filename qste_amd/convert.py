@@ -5,10 +5,13 @@ shell-style globs over qualified module names (``include`` then
 ``exclude``), ``ValueError`` when nothing is selected, tied weights sharing
 one ``Surface``, the config recorded on the model as ``_qste_config``.
 
-Not in this build: binary embeddings (``QSTEEmbedding``) and the packed
-activation modules of ``qste.nn``.  Selecting an ``nn.Embedding`` raises
-``NotImplementedError``; ``activations`` is validated as in the reference
-but activation modules are left as they are.
+With ``activations`` set, activation modules are swapped for the packed
+ones of ``qste_amd.nn`` (``convert.py:246-274``): ``True`` / ``"all"`` take
+every replacement, ``"exact"`` only the one-bit (value- and
+gradient-identical) ones.
+
+Not in this build: binary embeddings (``QSTEEmbedding``).  Selecting an
+``nn.Embedding`` raises ``NotImplementedError``.
 """
 
 from __future__ import annotations
@@ -85,9 +88,34 @@ def convert(
         if verbose:
             print(f"converted {name}: {replacement.out_features} x {replacement.in_features}")
 
+    if activations:
+        converted.extend(_convert_activations(model, activations))
+
     model._qste_config = cfg
     model._qste_converted = tuple(converted)
     return model
+
+
+def _convert_activations(model: nn.Module, mode: bool | str) -> list[str]:
+    """Swap activation modules for packed ones; returns the names replaced.
+
+    Idempotent: the packed classes are not keys of the replacement tables.
+    """
+
+    from . import nn as packed
+
+    table = packed.EXACT_REPLACEMENTS if mode == "exact" else packed.REPLACEMENTS
+    replaced: list[str] = []
+    for name, module in list(model.named_modules()):
+        if not name or type(module) not in table:
+            continue
+        substitute = packed.replace(module)
+        if substitute is None:
+            continue
+        substitute.training = module.training
+        _set_submodule(model, name, substitute)
+        replaced.append(name)
+    return replaced
 
 
 def surfaces(model: nn.Module) -> list[Surface]:

@@ -1,0 +1,688 @@
+// Packed activations: what backward keeps of an activation, in bits or bytes.
+//
+// Reference behaviour (BleedingXiko/QSTE):
+//   pack_bits / unpack_bits / apply_bits -- src/qste/kernels/fallback.py:32-70,
+//       GPU select semantics of cuda.py:158-195 (a cleared bit gives +0)
+//   masked activations (ReLU, ReLU6, Hardtanh, LeakyReLU, Hardsigmoid,
+//       Dropout)                                      -- src/qste/nn.py:116-186, 267-282, 352-368
+//   smooth activations, int8 derivative per row       -- src/qste/nn.py:392-507
+//   relu(x)^2 with an unsigned byte per element       -- src/qste/nn.py:292-330
+//   any elementwise function (derivative handed in)   -- src/qste/nn.py:510-555
+//
+// All of it is HBM-bound element work.  The bit kernels give one thread one
+// packed byte (eight elements), so no two threads write the same byte.  The
+// smooth forward gives each row to one wave or one workgroup: the row's
+// derivative is computed once, held in registers while the row maximum is
+// reduced, then quantized, so the input is read from HBM once.
+//
+// Arithmetic follows the reference's tensor expressions operation by
+// operation in fp32 (the library is built without FMA contraction), with a
+// rounding to the tensor dtype wherever the reference's expression produces a
+// tensor of that dtype.
+#include <math.h>
+
+#include "common.hpp"
+
+namespace qste {
+namespace act {
+
+constexpr int kThreads = 256;
+
+// ---------------------------------------------------------------------------
+// 8-element chunks: element c of a row lives in chunk c / 8.  A chunk is read
+// with one vector load when the row is a whole number of chunks.
+// ---------------------------------------------------------------------------
+
+template <int DT>
+struct Chunk;
+
+template <>
+struct Chunk<QSTE_F32> {
+  __device__ __forceinline__ static void load(const float* p, int n, bool vec, float v[8]) {
+    if (vec && n == 8) {
+      const float4 a = reinterpret_cast<const float4*>(p)[0];
+      const float4 b = reinterpret_cast<const float4*>(p)[1];
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+      v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = j < n ? p[j] : 0.0f;
+    }
+  }
+  __device__ __forceinline__ static void store(float* p, int n, bool vec, const float v[8]) {
+    if (vec && n == 8) {
+      reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+      reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j < n) p[j] = v[j];
+    }
+  }
+};
+
+template <int DT>
+struct Chunk16 {
+  using E = Elem<DT>;
+  __device__ __forceinline__ static void load(const uint16_t* p, int n, bool vec, float v[8]) {
+    if (vec && n == 8) {
+      const uint4 q = *reinterpret_cast<const uint4*>(p);
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint16_t lo = static_cast<uint16_t>(w[j] & 0xFFFFu);
+        const uint16_t hi = static_cast<uint16_t>(w[j] >> 16);
+        v[2 * j] = E::load(&lo, 0);
+        v[2 * j + 1] = E::load(&hi, 0);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = j < n ? E::load(p, j) : 0.0f;
+    }
+  }
+  __device__ __forceinline__ static void store(uint16_t* p, int n, bool vec, const float v[8]) {
+    if (vec && n == 8) {
+      uint16_t h[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) E::store(h, j, v[j]);
+      uint4 q;
+      q.x = h[0] | (static_cast<uint32_t>(h[1]) << 16);
+      q.y = h[2] | (static_cast<uint32_t>(h[3]) << 16);
+      q.z = h[4] | (static_cast<uint32_t>(h[5]) << 16);
+      q.w = h[6] | (static_cast<uint32_t>(h[7]) << 16);
+      *reinterpret_cast<uint4*>(p) = q;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j < n) E::store(p, j, v[j]);
+    }
+  }
+};
+
+template <>
+struct Chunk<QSTE_F16> : Chunk16<QSTE_F16> {};
+template <>
+struct Chunk<QSTE_BF16> : Chunk16<QSTE_BF16> {};
+
+// ---------------------------------------------------------------------------
+// pack_bits / unpack_bits
+// ---------------------------------------------------------------------------
+
+__global__ void pack_bits_kernel(const uint8_t* __restrict__ mask, uint8_t* __restrict__ packed,
+                                 int64_t rows, int64_t cols, int64_t pb) {
+  const int64_t total = rows * pb;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = idx / pb;
+    const int64_t b = idx - r * pb;
+    const uint8_t* src = mask + r * cols + b * 8;
+    const int64_t n = cols - b * 8 < 8 ? cols - b * 8 : 8;
+    uint32_t byte = 0;
+    if (n == 8 && (cols & 7) == 0) {
+      const uint64_t w = *reinterpret_cast<const uint64_t*>(src);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) byte |= (((w >> (8 * j)) & 0xFFu) != 0 ? 1u : 0u) << j;
+    } else {
+      for (int j = 0; j < n; ++j) byte |= (src[j] != 0 ? 1u : 0u) << j;
+    }
+    packed[idx] = static_cast<uint8_t>(byte);
+  }
+}
+
+template <int DT>
+__global__ void unpack_bits_kernel(const uint8_t* __restrict__ packed, typename Elem<DT>::T* __restrict__ out,
+                                   int64_t rows, int64_t cols, int64_t pb) {
+  const int64_t total = rows * pb;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = idx / pb;
+    const int64_t b = idx - r * pb;
+    const int n = static_cast<int>(cols - b * 8 < 8 ? cols - b * 8 : 8);
+    const uint32_t byte = packed[idx];
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = static_cast<float>((byte >> j) & 1u);
+    typename Elem<DT>::T* dst = out + r * cols + b * 8;
+    Chunk<DT>::store(dst, n, (cols & 7) == 0, v);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Masked backward: one formula for every one-bit activation.
+//   kept = bit ? g : 0
+//   outside == 0:  out = kept * inside                     (ReLU family: inside 1;
+//                                                            Dropout: inside = gain;
+//                                                            Hardsigmoid: 1/6)
+//   otherwise:     out = g * outside + kept * diff         (LeakyReLU, nn.py:278-282)
+// each product and the sum rounded to the dtype, as the tensor expressions are.
+// ---------------------------------------------------------------------------
+
+template <int DT>
+__global__ void masked_backward_kernel(const typename Elem<DT>::T* __restrict__ grad,
+                                       const uint8_t* __restrict__ packed,
+                                       typename Elem<DT>::T* __restrict__ out, int64_t rows, int64_t cols,
+                                       int64_t pb, float inside, float outside, float diff) {
+  using E = Elem<DT>;
+  const int64_t total = rows * pb;
+  const bool whole = (cols & 7) == 0;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = idx / pb;
+    const int64_t b = idx - r * pb;
+    const int n = static_cast<int>(cols - b * 8 < 8 ? cols - b * 8 : 8);
+    const int64_t off = r * cols + b * 8;
+    float g[8], o[8];
+    const uint32_t byte = packed[idx];
+    Chunk<DT>::load(grad + off, n, whole, g);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float kept = ((byte >> j) & 1u) ? g[j] : 0.0f;
+      if (outside == 0.0f) {
+        o[j] = kept * inside;
+      } else {
+        o[j] = E::round(E::round(g[j] * outside) + E::round(kept * diff));
+      }
+    }
+    Chunk<DT>::store(out + off, n, whole, o);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Masked forward.
+//   CLAMP   out = clamp(x, lower, upper) (upper first, nn.py:121-122),
+//           bit = lower < out (< upper)            (ReLU, ReLU6, Hardtanh)
+//   LEAKY   out = x > 0 ? x : x * slope, bit = x > 0           (LeakyReLU)
+//   INTERVAL bit = lower < x (< upper); out not written       (Hardsigmoid)
+// Bounds compare against their value rounded to the dtype, as a comparison of
+// a tensor of that dtype with a Python scalar does.
+// ---------------------------------------------------------------------------
+
+template <int DT>
+__global__ void masked_forward_kernel(const typename Elem<DT>::T* __restrict__ x,
+                                      typename Elem<DT>::T* __restrict__ out, uint8_t* __restrict__ packed,
+                                      int64_t rows, int64_t cols, int64_t pb, int kind, float lower,
+                                      float upper, int has_upper, float slope) {
+  using E = Elem<DT>;
+  const int64_t total = rows * pb;
+  const bool whole = (cols & 7) == 0;
+  const float lo_d = E::round(lower);
+  const float hi_d = E::round(upper);
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = idx / pb;
+    const int64_t b = idx - r * pb;
+    const int n = static_cast<int>(cols - b * 8 < 8 ? cols - b * 8 : 8);
+    const int64_t off = r * cols + b * 8;
+    float v[8], o[8];
+    Chunk<DT>::load(x + off, n, whole, v);
+    uint32_t byte = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      bool keep;
+      if (kind == QSTE_MASK_CLAMP) {
+        float t = v[j];
+        if (has_upper && t > upper) t = hi_d;
+        if (t < lower) t = lo_d;
+        o[j] = t;
+        keep = t > lo_d && (!has_upper || t < hi_d);
+      } else if (kind == QSTE_MASK_LEAKY) {
+        keep = v[j] > 0.0f;
+        o[j] = keep ? v[j] : E::round(v[j] * slope);
+      } else {
+        keep = v[j] > lo_d && (!has_upper || v[j] < hi_d);
+        o[j] = 0.0f;
+      }
+      byte |= (keep && j < n ? 1u : 0u) << j;
+    }
+    if (out != nullptr && kind != QSTE_MASK_INTERVAL) Chunk<DT>::store(out + off, n, whole, o);
+    packed[idx] = static_cast<uint8_t>(byte);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Smooth activations.
+// ---------------------------------------------------------------------------
+
+struct SmoothParams {
+  int kind;
+  float a;  // alpha (ELU, CELU) or beta (Softplus)
+};
+
+constexpr double kSqrt2 = 1.4142135623730951;
+constexpr double kInvSqrt2Pi = 0.3989422804014327;   // 1 / sqrt(2 pi)
+constexpr double kSqrt2OverPi = 0.7978845608028654;  // sqrt(2 / pi)
+constexpr double kTanhCoefficient = 0.044715;
+constexpr double kSeluAlpha = 1.6732632423543772;
+constexpr double kSeluScale = 1.0507009873554805;
+
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float softplus_f(float x, float beta) {
+  const float bx = x * beta;
+  return bx > 20.0f ? x : log1pf(expf(bx)) / beta;
+}
+
+// f(x) in fp32 (the value torch's activation computes before its rounding to
+// the dtype).
+__device__ __forceinline__ float smooth_value(const SmoothParams& p, float x) {
+  switch (p.kind) {
+    case QSTE_ACT_GELU:
+      return x * 0.5f * (1.0f + erff(x * static_cast<float>(0.70710678118654752440)));
+    case QSTE_ACT_GELU_TANH: {
+      const float beta = static_cast<float>(kSqrt2 * 1.12837916709551257390 * 0.5);
+      const float kappa = static_cast<float>(kTanhCoefficient);
+      const float cube = x * x * x;
+      const float inner = beta * (x + kappa * cube);
+      return 0.5f * x * (1.0f + tanhf(inner));
+    }
+    case QSTE_ACT_SILU: return x / (1.0f + expf(-x));
+    case QSTE_ACT_TANH: return tanhf(x);
+    case QSTE_ACT_SIGMOID: return 1.0f / (1.0f + expf(-x));
+    case QSTE_ACT_ELU: return x <= 0.0f ? expm1f(x) * p.a : x;
+    case QSTE_ACT_CELU: return x <= 0.0f ? expm1f(x * (1.0f / p.a)) * p.a : x;
+    case QSTE_ACT_SELU: {
+      const float scale = static_cast<float>(kSeluScale);
+      const float neg = static_cast<float>(kSeluAlpha) * scale;
+      return x <= 0.0f ? expm1f(x) * neg : x * scale;
+    }
+    case QSTE_ACT_SOFTPLUS: return softplus_f(x, p.a);
+    case QSTE_ACT_MISH: return x * tanhf(log1pf(expf(x)));
+    case QSTE_ACT_HARDSWISH: return x * fminf(fmaxf(x + 3.0f, 0.0f), 6.0f) / 6.0f;
+    case QSTE_ACT_RELU_SQUARE: {
+      const float a = x < 0.0f ? 0.0f : x;
+      return a * a;
+    }
+    default: return 0.0f;
+  }
+}
+
+// The derivative the reference retains (nn.py:392-440, 456-481), from the
+// input x and the output y as a tensor of the dtype (y already rounded).
+__device__ __forceinline__ float smooth_derivative(const SmoothParams& p, float x, float y) {
+  switch (p.kind) {
+    case QSTE_ACT_GELU: {
+      const float cumulative = 0.5f * (1.0f + erff(x / static_cast<float>(kSqrt2)));
+      const float e = expf(-0.5f * x * x);
+      return cumulative + x * e * static_cast<float>(kInvSqrt2Pi);
+    }
+    case QSTE_ACT_GELU_TANH: {
+      const float s = static_cast<float>(kSqrt2OverPi);
+      const float cube = x * x * x;
+      const float inner = s * (x + static_cast<float>(kTanhCoefficient) * cube);
+      const float t = tanhf(inner);
+      const float left = 0.5f * (1.0f + t);
+      const float right = 0.5f * x * (1.0f - t * t) * s *
+                          (1.0f + static_cast<float>(3.0 * kTanhCoefficient) * x * x);
+      return left + right;
+    }
+    case QSTE_ACT_SILU: {
+      const float s = sigmoid_f(x);
+      return s * (1.0f + x * (1.0f - s));
+    }
+    case QSTE_ACT_TANH: return 1.0f - y * y;
+    case QSTE_ACT_SIGMOID: return y * (1.0f - y);
+    case QSTE_ACT_ELU: return x > 0.0f ? 1.0f : y + p.a;
+    case QSTE_ACT_CELU: return x > 0.0f ? 1.0f : y / p.a + 1.0f;
+    case QSTE_ACT_SELU:
+      return x > 0.0f ? static_cast<float>(kSeluScale) : y + static_cast<float>(kSeluScale * kSeluAlpha);
+    case QSTE_ACT_SOFTPLUS: return sigmoid_f(p.a * x);
+    case QSTE_ACT_MISH: {
+      const float t = tanhf(softplus_f(x, 1.0f));
+      return t + x * (1.0f - t * t) * sigmoid_f(x);
+    }
+    case QSTE_ACT_HARDSWISH:
+      return x <= -3.0f ? 0.0f : (x >= 3.0f ? 1.0f : (2.0f * x + 3.0f) / 6.0f);
+    case QSTE_ACT_RELU_SQUARE: return x < 0.0f ? 0.0f : x;  // the retained quantity: relu(x)
+    default: return 0.0f;
+  }
+}
+
+template <int G>
+__device__ __forceinline__ float group_max(float v, float* red) {
+  v = wave_max(v);
+  if (G == kWave) return v;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float m = red[0];
+#pragma unroll
+  for (int w = 1; w < kThreads / kWave; ++w) m = fmaxf(m, red[w]);
+  return m;
+}
+
+// fmaxf drops a NaN; the reference's amax keeps it.  Track NaN separately.
+__device__ __forceinline__ float nan_max(float m, float v) { return (v != v || m != m) ? __builtin_nanf("") : fmaxf(m, v); }
+
+// One row per group of G threads (G = 64: a wave, four rows per workgroup;
+// G = 256: the workgroup).
+//
+// mode: 0 -- compute y = f(x), store it (when y != NULL), derive from it
+//       1 -- y holds the forward output already (computed elsewhere); read it
+//       2 -- `provided` holds the fp32 derivative (x, y unused)
+template <int DT, int G, bool CACHED>
+__global__ __launch_bounds__(kThreads) void smooth_rows_kernel(
+    const typename Elem<DT>::T* __restrict__ x, typename Elem<DT>::T* __restrict__ y,
+    const float* __restrict__ provided, int mode, SmoothParams p, void* __restrict__ payload,
+    float* __restrict__ scale, int64_t rows, int64_t cols) {
+  using E = Elem<DT>;
+  __shared__ float red[kThreads / kWave];
+  constexpr int kRowsPerBlock = kThreads / G;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / G;
+  const int t = threadIdx.x % G;
+  const bool live = row < rows;
+  const int64_t nch = (cols + 7) / 8;
+  const bool whole = (cols & 7) == 0;
+  const bool usq = p.kind == QSTE_ACT_RELU_SQUARE;
+  const int64_t base = (live ? row : 0) * cols;
+
+  auto derive = [&](int64_t q, float d[8], bool write_y) {
+    const int n = static_cast<int>(cols - q * 8 < 8 ? cols - q * 8 : 8);
+    if (mode == 2) {
+      Chunk<QSTE_F32>::load(provided + base + q * 8, n, whole, d);
+      for (int j = n; j < 8; ++j) d[j] = 0.0f;
+      return;
+    }
+    float xv[8], yv[8];
+    Chunk<DT>::load(x + base + q * 8, n, whole, xv);
+    if (mode == 1) {
+      Chunk<DT>::load(y + base + q * 8, n, whole, yv);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) yv[j] = E::round(smooth_value(p, xv[j]));
+      if (write_y && y != nullptr) Chunk<DT>::store(y + base + q * 8, n, whole, yv);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      // relu(x)^2 retains relu(x) itself, a tensor of the dtype
+      d[j] = j < n ? (usq ? E::round(smooth_derivative(p, xv[j], yv[j]))
+                          : smooth_derivative(p, xv[j], yv[j]))
+                   : 0.0f;
+    }
+  };
+
+  auto quantize = [&](int64_t q, const float d[8], float s) {
+    const int n = static_cast<int>(cols - q * 8 < 8 ? cols - q * 8 : 8);
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint32_t byte;
+      if (usq) {
+        float v = rintf(E::round(d[j] / s));
+        v = v != v ? 0.0f : fminf(fmaxf(v, 0.0f), 255.0f);
+        byte = static_cast<uint32_t>(v);
+      } else {
+        float v = rintf(d[j] / s);
+        v = v != v ? 0.0f : fminf(fmaxf(v, -127.0f), 127.0f);
+        byte = static_cast<uint32_t>(static_cast<int32_t>(v)) & 0xFFu;
+      }
+      if (j < 4) lo |= byte << (8 * j);
+      else hi |= byte << (8 * (j - 4));
+    }
+    uint8_t* dst = static_cast<uint8_t*>(payload) + base + q * 8;
+    if (whole) {
+      *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+    } else {
+      for (int j = 0; j < n; ++j) dst[j] = static_cast<uint8_t>(((j < 4 ? lo : hi) >> (8 * (j & 3))) & 0xFFu);
+    }
+  };
+
+  // CACHED: the row's derivatives wait in LDS (each thread reads back only
+  // what it wrote) between the maximum and the quantization; otherwise they
+  // are recomputed from the input, which is still in L2.
+  extern __shared__ float dcache[];
+  float* mine = dcache + (CACHED ? (threadIdx.x / G) * nch * 8 : 0);
+  float amax = 0.0f;
+  if (live) {
+    for (int64_t q = t; q < nch; q += G) {
+      float d[8];
+      derive(q, d, true);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = nan_max(amax, fabsf(d[j]));
+      if constexpr (CACHED) {
+        reinterpret_cast<float4*>(mine + q * 8)[0] = make_float4(d[0], d[1], d[2], d[3]);
+        reinterpret_cast<float4*>(mine + q * 8)[1] = make_float4(d[4], d[5], d[6], d[7]);
+      }
+    }
+  }
+  // the reference's amax keeps a NaN: carry it through the reduction as the
+  // largest key, then tell NaN from an infinite derivative
+  float key = amax != amax ? __builtin_inff() : amax;
+  key = group_max<G>(key, red);
+  float nan_flag = (amax != amax) ? 1.0f : 0.0f;
+  if (key == __builtin_inff()) nan_flag = group_max<G>(nan_flag, red);
+  if (!live) return;
+  float s;
+  if (usq) {
+    // relu(x)^2: maximum, clamp and division in the dtype (nn.py:316-318)
+    s = E::round(E::round(fmaxf(key, 1e-8f)) / 255.0f);
+  } else {
+    s = fmaxf(key, 1e-8f) / 127.0f;
+  }
+  if (nan_flag > 0.0f) s = __builtin_nanf("");
+  for (int64_t q = t; q < nch; q += G) {
+    float d[8];
+    if constexpr (CACHED) {
+      const float4 a = reinterpret_cast<const float4*>(mine + q * 8)[0];
+      const float4 b = reinterpret_cast<const float4*>(mine + q * 8)[1];
+      d[0] = a.x; d[1] = a.y; d[2] = a.z; d[3] = a.w;
+      d[4] = b.x; d[5] = b.y; d[6] = b.z; d[7] = b.w;
+    } else {
+      derive(q, d, false);
+    }
+    quantize(q, d, s);
+  }
+  if (t == 0) scale[row] = s;
+}
+
+// grad * (payload * scale), each product rounded to the dtype
+// (nn.py:504-507; relu(x)^2: grad * 2 * (payload * scale), nn.py:325-330).
+template <int DT>
+__global__ void smooth_backward_kernel(const typename Elem<DT>::T* __restrict__ grad,
+                                       const void* __restrict__ payload, const float* __restrict__ scale,
+                                       typename Elem<DT>::T* __restrict__ out, int64_t rows, int64_t cols,
+                                       int unsigned_payload) {
+  using E = Elem<DT>;
+  const int64_t nch = (cols + 7) / 8;
+  const int64_t total = rows * nch;
+  const bool whole = (cols & 7) == 0;
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = idx / nch;
+    const int64_t q = idx - r * nch;
+    const int n = static_cast<int>(cols - q * 8 < 8 ? cols - q * 8 : 8);
+    const int64_t off = r * cols + q * 8;
+    const float s = E::round(scale[r]);
+    float g[8], o[8];
+    Chunk<DT>::load(grad + off, n, whole, g);
+    const uint8_t* src = static_cast<const uint8_t*>(payload) + off;
+    uint32_t lo = 0, hi = 0;
+    if (whole) {
+      const uint2 w = *reinterpret_cast<const uint2*>(src);
+      lo = w.x;
+      hi = w.y;
+    } else {
+      for (int j = 0; j < n; ++j) (j < 4 ? lo : hi) |= static_cast<uint32_t>(src[j]) << (8 * (j & 3));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t byte = ((j < 4 ? lo : hi) >> (8 * (j & 3))) & 0xFFu;
+      const float pv = unsigned_payload ? static_cast<float>(byte)
+                                        : static_cast<float>(static_cast<int8_t>(static_cast<uint8_t>(byte)));
+      const float d = E::round(pv * s);
+      o[j] = unsigned_payload ? E::round(E::round(g[j] * 2.0f) * d) : E::round(g[j] * d);
+    }
+    Chunk<DT>::store(out + off, n, whole, o);
+  }
+}
+
+inline int grid_for(int64_t items) {
+  int64_t blocks = (items + kThreads - 1) / kThreads;
+  if (blocks > 65536) blocks = 65536;
+  return static_cast<int>(blocks < 1 ? 1 : blocks);
+}
+
+inline bool dtype_ok(int d) { return d == QSTE_F32 || d == QSTE_F16 || d == QSTE_BF16; }
+
+}  // namespace act
+}  // namespace qste
+
+using namespace qste;
+using namespace qste::act;
+
+namespace {
+
+#define QSTE_DT_SWITCH(dtype, ...)                                  \
+  switch (dtype) {                                                 \
+    case QSTE_F32: { constexpr int DT = QSTE_F32; __VA_ARGS__; } break;  \
+    case QSTE_F16: { constexpr int DT = QSTE_F16; __VA_ARGS__; } break;  \
+    case QSTE_BF16: { constexpr int DT = QSTE_BF16; __VA_ARGS__; } break; \
+    default: return QSTE_E_DTYPE;                                  \
+  }
+
+bool chunk_aligned(const void* p, int dtype) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  (void)dtype;
+  return (a % 16) == 0;
+}
+
+// LDS cache per workgroup: (rows per workgroup) x (row rounded up to whole
+// chunks) fp32 derivatives; rows longer than kMaxCachedCols recompute.
+constexpr int64_t kMaxCachedCols = 15360;  // 60 KiB of LDS per workgroup at most
+
+template <int DT, int G, bool CACHED>
+int smooth_launch(const void* x, void* y, const float* provided, int mode, SmoothParams p, void* payload,
+                  float* scale, int64_t rows, int64_t cols, hipStream_t s) {
+  using T = typename Elem<DT>::T;
+  constexpr int kRows = kThreads / G;
+  const int64_t blocks = (rows + kRows - 1) / kRows;
+  const size_t lds = CACHED ? sizeof(float) * static_cast<size_t>(kRows * ((cols + 7) / 8) * 8) : 0;
+  smooth_rows_kernel<DT, G, CACHED><<<static_cast<unsigned>(blocks), kThreads, lds, s>>>(
+      static_cast<const T*>(x), static_cast<T*>(y), provided, mode, p, payload, scale, rows, cols);
+  return static_cast<int>(hipGetLastError());
+}
+
+template <int DT>
+int smooth_dispatch(const void* x, void* y, const float* provided, int mode, SmoothParams p, void* payload,
+                    float* scale, int64_t rows, int64_t cols, hipStream_t s) {
+  if (cols <= 2048) return smooth_launch<DT, 64, true>(x, y, provided, mode, p, payload, scale, rows, cols, s);
+  if (cols <= kMaxCachedCols)
+    return smooth_launch<DT, 256, true>(x, y, provided, mode, p, payload, scale, rows, cols, s);
+  return smooth_launch<DT, 256, false>(x, y, provided, mode, p, payload, scale, rows, cols, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int qste_pack_bits(const uint8_t* mask, uint8_t* packed, int64_t rows, int64_t cols, void* stream) {
+  if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  const int64_t pb = (cols + 7) / 8;
+  if (rows * pb == 0) return 0;
+  if (!mask || !packed) return QSTE_E_NULL;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  pack_bits_kernel<<<grid_for(rows * pb), kThreads, 0, s>>>(mask, packed, rows, cols, pb);
+  return static_cast<int>(hipGetLastError());
+}
+
+int qste_unpack_bits(const uint8_t* packed, void* out, int out_dtype, int64_t rows, int64_t cols,
+                     void* stream) {
+  if (!act::dtype_ok(out_dtype)) return QSTE_E_DTYPE;
+  if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  const int64_t pb = (cols + 7) / 8;
+  if (rows * pb == 0) return 0;
+  if (!packed || !out) return QSTE_E_NULL;
+  if ((cols & 7) == 0 && !chunk_aligned(out, out_dtype)) return QSTE_E_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  QSTE_DT_SWITCH(out_dtype, unpack_bits_kernel<DT><<<grid_for(rows * pb), kThreads, 0, s>>>(
+                                packed, static_cast<typename Elem<DT>::T*>(out), rows, cols, pb));
+  return static_cast<int>(hipGetLastError());
+}
+
+int qste_masked_backward(const void* grad, int dtype, const uint8_t* packed, void* out, int64_t rows,
+                         int64_t cols, float inside, float outside, float diff, void* stream) {
+  if (!act::dtype_ok(dtype)) return QSTE_E_DTYPE;
+  if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  const int64_t pb = (cols + 7) / 8;
+  if (rows * pb == 0) return 0;
+  if (!grad || !packed || !out) return QSTE_E_NULL;
+  if ((cols & 7) == 0 && (!chunk_aligned(grad, dtype) || !chunk_aligned(out, dtype))) return QSTE_E_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  QSTE_DT_SWITCH(dtype, masked_backward_kernel<DT><<<grid_for(rows * pb), kThreads, 0, s>>>(
+                            static_cast<const typename Elem<DT>::T*>(grad), packed,
+                            static_cast<typename Elem<DT>::T*>(out), rows, cols, pb, inside, outside, diff));
+  return static_cast<int>(hipGetLastError());
+}
+
+int qste_apply_bits(const void* values, int dtype, const uint8_t* packed, void* out, int64_t rows,
+                    int64_t cols, void* stream) {
+  return qste_masked_backward(values, dtype, packed, out, rows, cols, 1.0f, 0.0f, 0.0f, stream);
+}
+
+int qste_masked_activation(const void* x, int dtype, int kind, float lower, float upper, int has_upper,
+                           float slope, void* out, uint8_t* packed, int64_t rows, int64_t cols,
+                           void* stream) {
+  if (!act::dtype_ok(dtype)) return QSTE_E_DTYPE;
+  if (kind != QSTE_MASK_CLAMP && kind != QSTE_MASK_LEAKY && kind != QSTE_MASK_INTERVAL) return QSTE_E_SHAPE;
+  if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  const int64_t pb = (cols + 7) / 8;
+  if (rows * pb == 0) return 0;
+  if (!x || !packed || (kind != QSTE_MASK_INTERVAL && !out)) return QSTE_E_NULL;
+  if ((cols & 7) == 0 && (!chunk_aligned(x, dtype) || (out && !chunk_aligned(out, dtype)))) return QSTE_E_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  QSTE_DT_SWITCH(dtype, masked_forward_kernel<DT><<<grid_for(rows * pb), kThreads, 0, s>>>(
+                            static_cast<const typename Elem<DT>::T*>(x), static_cast<typename Elem<DT>::T*>(out),
+                            packed, rows, cols, pb, kind, lower, upper, has_upper, slope));
+  return static_cast<int>(hipGetLastError());
+}
+
+int qste_smooth_activation(const void* x, int dtype, int kind, float param, void* y, int y_given,
+                           const float* derivative, void* payload, float* scale, int64_t rows, int64_t cols,
+                           void* stream) {
+  if (!act::dtype_ok(dtype)) return QSTE_E_DTYPE;
+  if (kind < QSTE_ACT_GELU || kind > QSTE_ACT_PROVIDED) return QSTE_E_SHAPE;
+  if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  if (rows == 0) return 0;
+  if (!payload || !scale) return QSTE_E_NULL;
+  int mode = 0;
+  if (kind == QSTE_ACT_PROVIDED) {
+    if (!derivative && cols > 0) return QSTE_E_NULL;
+    mode = 2;
+  } else {
+    if (!x && cols > 0) return QSTE_E_NULL;
+    if (y_given) {
+      if (!y && cols > 0) return QSTE_E_NULL;
+      mode = 1;
+    }
+  }
+  if ((cols & 7) == 0 && cols > 0) {
+    if (mode == 2 && !chunk_aligned(derivative, QSTE_F32)) return QSTE_E_ALIGN;
+    if (mode != 2 && (!chunk_aligned(x, dtype) || (y && !chunk_aligned(y, dtype)))) return QSTE_E_ALIGN;
+    if ((reinterpret_cast<uintptr_t>(payload) & 7) != 0) return QSTE_E_ALIGN;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  SmoothParams p{kind, param};
+  const int d = mode == 2 ? QSTE_F32 : dtype;
+  QSTE_DT_SWITCH(d, return smooth_dispatch<DT>(x, y, derivative, mode, p, payload, scale, rows, cols, s));
+  return 0;
+}
+
+int qste_smooth_backward(const void* grad, int dtype, const void* payload, int unsigned_payload,
+                         const float* scale, void* out, int64_t rows, int64_t cols, void* stream) {
+  if (!act::dtype_ok(dtype)) return QSTE_E_DTYPE;
+  if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  if (rows * cols == 0) return 0;
+  if (!grad || !payload || !scale || !out) return QSTE_E_NULL;
+  if ((cols & 7) == 0 && (!chunk_aligned(grad, dtype) || !chunk_aligned(out, dtype) ||
+                          (reinterpret_cast<uintptr_t>(payload) & 7) != 0))
+    return QSTE_E_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t nch = (cols + 7) / 8;
+  QSTE_DT_SWITCH(dtype, smooth_backward_kernel<DT><<<grid_for(rows * nch), kThreads, 0, s>>>(
+                            static_cast<const typename Elem<DT>::T*>(grad), payload, scale,
+                            static_cast<typename Elem<DT>::T*>(out), rows, cols, unsigned_payload));
+  return static_cast<int>(hipGetLastError());
+}
+
+}  // extern "C"

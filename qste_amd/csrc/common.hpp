@@ -30,7 +30,12 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
 
+// The empty asm keeps the backend from folding a preceding fp32 multiply or
+// add into a mixed-precision instruction that rounds once, straight to fp16:
+// the value is rounded to fp32 first, then to fp16, as a tensor expression
+// evaluated in fp32 and stored as fp16 is.
 __device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  asm volatile("" : "+v"(f));
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
 

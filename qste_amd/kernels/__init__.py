@@ -23,6 +23,13 @@ _DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 __all__ = [
     "KernelError",
+    "apply_bits",
+    "masked_activation",
+    "masked_backward",
+    "pack_bits",
+    "smooth_activation",
+    "smooth_backward",
+    "unpack_bits",
     "coordinate_update",
     "cuda_available",
     "evidence_from_packed",
@@ -98,6 +105,19 @@ def _f32(t: Tensor | None) -> Tensor | None:
     if t is None:
         return None
     return t.detach().to(torch.float32).contiguous()
+
+
+def _aligned(t: Tensor) -> Tensor:
+    """Contiguous, with the 16-byte start the vector paths need."""
+
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _rows2d(t: Tensor, what: str) -> Tensor:
+    if t.dim() != 2:
+        raise ValueError(f"{what} expects a rank-2 tensor")
+    return _aligned(t)
 
 
 def _workspace(nbytes: int, device: torch.device) -> Tensor:
@@ -379,3 +399,153 @@ def coordinate_update(
     if out_dev is not flips:
         flips.copy_(out_dev)
     return flips
+
+
+# ---------------------------------------------------------------------------
+# packed activations (reference: loader.py:256-273, src/qste/nn.py)
+# ---------------------------------------------------------------------------
+
+# kinds of masked_activation / smooth_activation (include/qste_hip.h)
+MASK_CLAMP, MASK_LEAKY, MASK_INTERVAL = 0, 1, 2
+SMOOTH_KINDS = {
+    "gelu": 0, "gelu_tanh": 1, "silu": 2, "tanh": 3, "sigmoid": 4, "elu": 5, "celu": 6,
+    "selu": 7, "softplus": 8, "mish": 9, "hardswish": 10, "relu_square": 11, "provided": 12,
+}
+
+
+def pack_bits(mask: Tensor) -> Tensor:
+    """One bit per element of a rank-2 mask, LSB first (fallback.py:32-47)."""
+
+    device = _require_gpu(mask)
+    if mask.dim() != 2:
+        raise ValueError("packing expects a rank-2 tensor")
+    if mask.dtype == torch.bool:
+        mask = mask.contiguous().view(torch.uint8)
+    elif mask.dtype != torch.uint8:
+        mask = (mask != 0).view(torch.uint8)
+    mask = _aligned(mask)
+    rows, cols = mask.shape
+    packed = torch.empty(rows, _packed_width(cols), dtype=torch.uint8, device=device)
+    code = _lib.load().qste_pack_bits(_ptr(mask), _ptr(packed), rows, cols, _stream(device))
+    _lib.check(code, "pack_bits")
+    return packed
+
+
+def unpack_bits(packed: Tensor, columns: int, *, dtype: torch.dtype | None = None) -> Tensor:
+    """0/1 matrix of packed bits, pad columns dropped (fallback.py:50-54)."""
+
+    dtype = dtype or torch.float32
+    device = _require_gpu(packed)
+    packed = _check_packed(packed, columns)
+    out = torch.empty(packed.shape[0], int(columns), dtype=dtype, device=device)
+    code = _lib.load().qste_unpack_bits(
+        _ptr(packed), _ptr(out), _dtype_code(out), packed.shape[0], int(columns), _stream(device))
+    _lib.check(code, "unpack_bits")
+    return out
+
+
+def apply_bits(values: Tensor, packed: Tensor, columns: int) -> Tensor:
+    """``values`` where the bit is set, zero where it is not (fallback.py:57-70)."""
+
+    return masked_backward(values, packed, columns)
+
+
+def masked_backward(grad: Tensor, packed: Tensor, columns: int, *, inside: float = 1.0,
+                    outside: float = 0.0) -> Tensor:
+    """Backward of a one-bit activation (src/qste/nn.py:133-136, 168-181, 278-282, 364-368).
+
+    ``kept = bit ? grad : 0``; ``kept * inside`` when ``outside == 0``, else
+    ``grad * outside + kept * (inside - outside)``, each product rounded to
+    the dtype like the reference's tensor expressions.
+    """
+
+    device = _require_gpu(grad, packed)
+    grad = _rows2d(grad, "masked_backward")
+    rows, cols = grad.shape
+    if cols != columns:
+        raise ValueError(f"value width {cols} does not match {columns} columns")
+    packed = _check_packed(packed, columns, rows)
+    out = torch.empty_like(grad)
+    code = _lib.load().qste_masked_backward(
+        _ptr(grad), _dtype_code(grad), _ptr(packed), _ptr(out), rows, cols, float(inside),
+        float(outside), float(inside - outside), _stream(device))
+    _lib.check(code, "masked_backward")
+    return out
+
+
+def masked_activation(x: Tensor, kind: int, *, lower: float = 0.0, upper: float | None = None,
+                      slope: float = 0.0, want_output: bool = True) -> tuple[Tensor | None, Tensor]:
+    """Forward of a one-bit activation and its packed mask, in one pass.
+
+    ``x`` is rank 2; returns ``(output or None, packed)``.
+    """
+
+    device = _require_gpu(x)
+    x = _rows2d(x, "masked_activation")
+    rows, cols = x.shape
+    out = torch.empty_like(x) if (want_output and kind != MASK_INTERVAL) else None
+    packed = torch.empty(rows, _packed_width(cols), dtype=torch.uint8, device=device)
+    code = _lib.load().qste_masked_activation(
+        _ptr(x), _dtype_code(x), int(kind), float(lower), float(0.0 if upper is None else upper),
+        0 if upper is None else 1, float(slope), _ptr(out), _ptr(packed), rows, cols,
+        _stream(device))
+    _lib.check(code, "masked_activation")
+    return out, packed
+
+
+def smooth_activation(x: Tensor | None, kind: str, param: float = 0.0, *,
+                      output: Tensor | None = None,
+                      derivative: Tensor | None = None) -> tuple[Tensor | None, Tensor, Tensor]:
+    """Smooth activation with its row-quantized derivative (src/qste/nn.py:487-502).
+
+    ``x`` rank 2.  When ``output`` is given it holds f(x) already and is read;
+    otherwise f(x) is computed and returned.  ``kind == "provided"`` quantizes
+    ``derivative`` (fp32) instead.  Returns ``(output, payload, scale)``:
+    payload int8 (uint8 for ``relu_square``) ``[rows, cols]``, scale fp32 ``[rows]``.
+    """
+
+    code_kind = SMOOTH_KINDS[kind]
+    if kind == "provided":
+        device = _require_gpu(derivative)
+        derivative = _rows2d(derivative.float(), "smooth_activation")
+        rows, cols = derivative.shape
+        dtype_code, x_ptr, y_ptr, y_given = 0, None, None, 0
+        out = None
+    else:
+        device = _require_gpu(x, output)
+        x = _rows2d(x, "smooth_activation")
+        rows, cols = x.shape
+        dtype_code = _dtype_code(x)
+        if output is not None:
+            output = _rows2d(output, "smooth_activation")
+            if output.shape != x.shape or output.dtype != x.dtype:
+                raise ValueError("output must match the input's shape and dtype")
+            out, y_given = output, 1
+        else:
+            out, y_given = torch.empty_like(x), 0
+        x_ptr, y_ptr = _ptr(x), _ptr(out)
+    payload = torch.empty(rows, cols, dtype=torch.uint8 if kind == "relu_square" else torch.int8,
+                          device=device)
+    scale = torch.empty(rows, dtype=torch.float32, device=device)
+    code = _lib.load().qste_smooth_activation(
+        x_ptr, dtype_code, code_kind, float(param), y_ptr, y_given, _ptr(derivative),
+        _ptr(payload), _ptr(scale), rows, cols, _stream(device))
+    _lib.check(code, "smooth_activation")
+    return out, payload, scale
+
+
+def smooth_backward(grad: Tensor, payload: Tensor, scale: Tensor) -> Tensor:
+    """``grad * (payload * scale)`` per row (src/qste/nn.py:504-507, 325-330)."""
+
+    device = _require_gpu(grad, payload, scale)
+    grad = _rows2d(grad, "smooth_backward")
+    rows, cols = grad.shape
+    if payload.shape != grad.shape or scale.shape != (rows,):
+        raise ValueError("payload/scale do not match the gradient's shape")
+    payload = _aligned(payload)
+    out = torch.empty_like(grad)
+    code = _lib.load().qste_smooth_backward(
+        _ptr(grad), _dtype_code(grad), _ptr(payload), 1 if payload.dtype == torch.uint8 else 0,
+        _ptr(_f32(scale)), _ptr(out), rows, cols, _stream(device))
+    _lib.check(code, "smooth_backward")
+    return out

@@ -25,6 +25,7 @@ _int = ctypes.c_int
 _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
 _dbl = ctypes.c_double
+_flt = ctypes.c_float
 
 # name -> (restype, argtypes); mirrors include/qste_hip.h
 SIGNATURES = {
@@ -43,6 +44,15 @@ SIGNATURES = {
     "qste_coordinate_update_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "qste_coordinate_update": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _dbl, _dbl,
                                       _dbl, _dbl, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "qste_pack_bits": (_int, [_vp, _vp, _i64, _i64, _vp]),
+    "qste_unpack_bits": (_int, [_vp, _vp, _int, _i64, _i64, _vp]),
+    "qste_apply_bits": (_int, [_vp, _int, _vp, _vp, _i64, _i64, _vp]),
+    "qste_masked_backward": (_int, [_vp, _int, _vp, _vp, _i64, _i64, _flt, _flt, _flt, _vp]),
+    "qste_masked_activation": (_int, [_vp, _int, _int, _flt, _flt, _int, _flt, _vp, _vp, _i64, _i64,
+                                      _vp]),
+    "qste_smooth_activation": (_int, [_vp, _int, _int, _flt, _vp, _int, _vp, _vp, _vp, _i64, _i64,
+                                      _vp]),
+    "qste_smooth_backward": (_int, [_vp, _int, _vp, _int, _vp, _vp, _i64, _i64, _vp]),
 }
 
 

@@ -14,6 +14,7 @@ from torch import Tensor
 from . import kernels
 from .config import QSTEConfig, coerce_config
 from .functional import qste_linear, qste_weight
+from .nn import _mark_activation_input
 from .surface import Surface
 
 
@@ -50,7 +51,8 @@ class QSTELinear(nn.Module):
         return qste_weight(self.surface)
 
     def forward(self, inputs: Tensor) -> Tensor:
-        return qste_linear(inputs, self.surface, self.bias)
+        # tagged so packed_activations() packs an activation applied to it
+        return _mark_activation_input(qste_linear(inputs, self.surface, self.bias))
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "

@@ -26,6 +26,7 @@ import torch
 import torch.nn as nn
 
 import oracle
+from oracle import activations as oa
 
 ROOT = Path(__file__).resolve().parents[1]
 
@@ -139,6 +140,50 @@ class OracleKernels:
             return flips
         return n
 
+    # packed activations (oracle/activations.py)
+    @staticmethod
+    def _dt(t):
+        return {torch.float32: "float32", torch.bfloat16: "bfloat16", torch.float16: "float16"}[t.dtype]
+
+    def pack_bits(self, mask):
+        return torch.from_numpy(oa.pack_bits(mask.numpy()))
+
+    def unpack_bits(self, packed, columns, *, dtype=None):
+        return torch.from_numpy(oa.unpack_bits(packed.numpy(), columns)).to(dtype or torch.float32)
+
+    def masked_backward(self, grad, packed, columns, *, inside=1.0, outside=0.0):
+        out = oa.masked_backward(grad.float().numpy(), packed.numpy(), inside, outside, self._dt(grad))
+        return torch.from_numpy(out).to(grad.dtype)
+
+    def masked_activation(self, x, kind, *, lower=0.0, upper=None, slope=0.0, want_output=True):
+        from qste_amd import kernels
+
+        v, name = x.float().numpy(), self._dt(x)
+        if kind == kernels.MASK_CLAMP:
+            out, packed = oa.clamp_forward(v, lower, upper, name)
+        elif kind == kernels.MASK_LEAKY:
+            out, packed = oa.leaky_forward(v, slope, name)
+        else:
+            return None, torch.from_numpy(oa.interval_bits(v, lower, upper, name))
+        return torch.from_numpy(out).to(x.dtype), torch.from_numpy(packed)
+
+    def smooth_activation(self, x, kind, param=0.0, *, output=None, derivative=None):
+        if kind == "provided":
+            payload, scale = oa.quantize_rows(derivative.float().numpy())
+            return None, torch.from_numpy(payload), torch.from_numpy(scale)
+        name = self._dt(x)
+        y = None if output is None else output.float().numpy()
+        y, payload, scale = oa.smooth_forward(kind, x.float().numpy(), param, name, y=y)
+        return torch.from_numpy(y).to(x.dtype), torch.from_numpy(payload), torch.from_numpy(scale)
+
+    def smooth_backward(self, grad, payload, scale):
+        out = oa.smooth_backward(grad.float().numpy(), payload.numpy(), scale.numpy(), self._dt(grad))
+        return torch.from_numpy(out).to(grad.dtype)
+
+
+ACTIVATION_OPS = ("pack_bits", "unpack_bits", "masked_backward", "masked_activation",
+                  "smooth_activation", "smooth_backward")
+
 
 @pytest.fixture
 def fake(monkeypatch):
@@ -147,7 +192,7 @@ def fake(monkeypatch):
 
     ok = OracleKernels()
     for name in ("pack_coordinate", "unpack_rows", "pack_affine_rows", "packed_linear_affine",
-                 "packed_row_inner", "linear_backward", "coordinate_update"):
+                 "packed_row_inner", "linear_backward", "coordinate_update") + ACTIVATION_OPS:
         monkeypatch.setattr(kernels, name, getattr(ok, name))
     monkeypatch.setattr(surface, "_on_gpu", lambda fn, t, *a, **k: fn(t, *a, **k))
     return ok
@@ -336,3 +381,83 @@ def test_multirank_group_requires_an_explicit_reducer(monkeypatch, fake):
     with pytest.raises(RuntimeError, match="gradient_reducer"):
         qste.QSTEOptimizer(model)
     assert qste.QSTEOptimizer(model, gradient_reducer=False).gradient_reducer is None
+
+
+# ---------------------------------------------------------------------------
+# packed activations: orchestration (src/qste/nn.py, convert.py:246-274)
+# ---------------------------------------------------------------------------
+
+
+def test_convert_swaps_activation_modules_by_mode(fake):
+    import qste_amd as qste
+
+    def model():
+        return nn.Sequential(nn.Linear(8, 16), nn.GELU(approximate="tanh"), nn.Linear(16, 8),
+                             nn.LeakyReLU(0.2), nn.Dropout(0.3), nn.Softplus(2.0))
+
+    m = qste.convert(model())
+    assert isinstance(m[1], qste.nn.GELU) and m[1].approximate == "tanh"
+    assert isinstance(m[3], qste.nn.LeakyReLU) and m[3].negative_slope == 0.2
+    assert isinstance(m[4], qste.nn.Dropout) and m[4].p == 0.3
+    assert isinstance(m[5], qste.nn.Softplus) and m[5].beta == 2.0
+    assert {"1", "3", "4", "5"} <= set(m._qste_converted)
+    m = qste.convert(model(), activations="exact")
+    assert type(m[1]) is nn.GELU and isinstance(m[3], qste.nn.LeakyReLU)
+    m = qste.convert(model(), activations=False)
+    assert type(m[1]) is nn.GELU and type(m[3]) is nn.LeakyReLU
+    # idempotent
+    m = qste.convert(model())
+    again = qste.convert(m)
+    assert isinstance(again[1], qste.nn.GELU)
+
+
+def test_packed_activation_autograd_composition(fake):
+    from qste_amd import nn as qnn
+
+    x = torch.randn(6, 40, requires_grad=True)
+    g = torch.randn(6, 40)
+    qnn.relu(x).backward(g)
+    assert torch.equal(x.grad, torch.where(x > 0, g, torch.zeros_like(g)))
+    x.grad = None
+    y = qnn.silu(x)
+    assert torch.allclose(y, torch.nn.functional.silu(x), rtol=1e-6, atol=1e-6)
+    y.backward(g)
+    xs = x.detach()
+    d = torch.sigmoid(xs) * (1 + xs * (1 - torch.sigmoid(xs)))
+    scale = d.abs().amax(1, keepdim=True) / 127
+    assert torch.allclose(x.grad, g * d, atol=float(scale.max() * g.abs().max()) * 0.51)
+    # 0-d and 1-d inputs keep their shapes
+    s = torch.tensor(0.5, requires_grad=True)
+    assert qnn.gelu(s).shape == ()
+    v = torch.randn(9, requires_grad=True)
+    qnn.tanh(v).sum().backward()
+    assert v.grad.shape == (9,)
+
+
+def test_packed_activations_context_routes_marked_outputs_only(fake):
+    import qste_amd as qste
+    import torch.nn.functional as F
+
+    model = qste.convert(nn.Sequential(nn.Linear(16, 24)), include=["0"])
+    x = torch.randn(5, 16)
+    seen = []
+
+    def pack(t):
+        seen.append(t.dtype)
+        return t
+
+    with qste.packed_activations():
+        assert F.gelu is not qste.nn._TORCH_GELU
+        hidden = model(x)
+        with torch.autograd.graph.saved_tensors_hooks(pack, lambda t: t):
+            F.gelu(hidden)
+        assert torch.int8 in seen
+        seen.clear()
+        with torch.autograd.graph.saved_tensors_hooks(pack, lambda t: t):
+            F.gelu(torch.randn(5, 24, requires_grad=True))
+        assert torch.int8 not in seen
+        # relu(...).square() fuses into one uint8-retaining op
+        fused = qste.nn.relu(hidden).square()
+        assert torch.allclose(fused, torch.relu(hidden).square())
+        assert fused.grad_fn is not None and "ReluSquare" in type(fused.grad_fn).__name__
+    assert F.gelu is qste.nn._TORCH_GELU and torch.relu is qste.nn._TORCH_TORCH_RELU
