@@ -215,6 +215,36 @@ def step_bandwidth(rows, cols, device):
             "gbps": round(nbytes / ms / 1e6, 1), "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / HBM_PEAK, 4)}
 
 
+def packed_activation_bandwidth(T, ffn, device):
+    """HBM rate of the packed-activation kernels on the MLP's hidden [T, ffn] bf16."""
+
+    import torch
+
+    from qste_amd import kernels
+
+    g = torch.Generator(device=device).manual_seed(7)
+    h = torch.randn(T, ffn, generator=g, device=device).to(torch.bfloat16)
+    grad = torch.randn(T, ffn, generator=g, device=device).to(torch.bfloat16)
+    n = T * ffn
+    out = {}
+
+    def rate(name, fn, nbytes):
+        ms = timed_events(fn, 5)
+        out[name] = {"ms": round(ms, 4), "algorithmic_bytes": nbytes, "gbps": round(nbytes / ms / 1e6, 1),
+                     "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / HBM_PEAK, 4)}
+
+    # SiLU value + int8 derivative + fp32 row scale: read x, write y and the payload
+    rate("silu_forward", lambda: kernels.smooth_activation(h, "silu"), n * (2 + 2 + 1) + 4 * T)
+    _, payload, scale = kernels.smooth_activation(h, "silu")
+    # grad * (payload * scale): read grad and payload, write the input gradient
+    rate("smooth_backward", lambda: kernels.smooth_backward(grad, payload, scale), n * (2 + 1 + 2) + 4 * T)
+    # ReLU value + bit mask; its backward reads grad and bits, writes the gradient
+    rate("relu_forward", lambda: kernels.masked_activation(h, kernels.MASK_CLAMP), n * (2 + 2) + n // 8)
+    _, bits = kernels.masked_activation(h, kernels.MASK_CLAMP)
+    rate("relu_backward", lambda: kernels.masked_backward(grad, bits, ffn), n * (2 + 2) + n // 8)
+    return out
+
+
 def decode_gemv(device, K=8192, N=28672, copies=10):
     import torch
 
@@ -316,6 +346,12 @@ def main():
         y.backward(dy)
         return coords.step()
 
+    def packed_step():
+        with qste.packed_activations():
+            y = mlp(x)
+        y.backward(dy)
+        return coords.step()
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -357,6 +393,15 @@ def main():
         line["vendor_dense_bf16_gemm"] = vendor_dense(T, d, ffn, device)
         line["coordinate_step"] = step_bandwidth(ffn, d, device)
         line["decode_gemv"] = decode_gemv(device)
+        line["packed_activations"] = packed_activation_bandwidth(T, ffn, device)
+        # the same step with the SiLU retaining its int8 derivative (qste.packed_activations())
+        packed_step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(3):
+            packed_step()
+        torch.cuda.synchronize()
+        line["packed_activations"]["step_ms"] = round((time.perf_counter() - t1) / 3 * 1e3, 3)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(d, ffn, args.cpu_tokens)
     print(json.dumps(line), flush=True)

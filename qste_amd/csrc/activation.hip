@@ -262,81 +262,159 @@ __device__ __forceinline__ float softplus_f(float x, float beta) {
   return bx > 20.0f ? x : log1pf(expf(bx)) / beta;
 }
 
-// f(x) in fp32 (the value torch's activation computes before its rounding to
-// the dtype).
-__device__ __forceinline__ float smooth_value(const SmoothParams& p, float x) {
-  switch (p.kind) {
-    case QSTE_ACT_GELU:
-      return x * 0.5f * (1.0f + erff(x * static_cast<float>(0.70710678118654752440)));
-    case QSTE_ACT_GELU_TANH: {
-      const float beta = static_cast<float>(kSqrt2 * 1.12837916709551257390 * 0.5);
-      const float kappa = static_cast<float>(kTanhCoefficient);
-      const float cube = x * x * x;
-      const float inner = beta * (x + kappa * cube);
-      return 0.5f * x * (1.0f + tanhf(inner));
-    }
-    case QSTE_ACT_SILU: return x / (1.0f + expf(-x));
-    case QSTE_ACT_TANH: return tanhf(x);
-    case QSTE_ACT_SIGMOID: return 1.0f / (1.0f + expf(-x));
-    case QSTE_ACT_ELU: return x <= 0.0f ? expm1f(x) * p.a : x;
-    case QSTE_ACT_CELU: return x <= 0.0f ? expm1f(x * (1.0f / p.a)) * p.a : x;
-    case QSTE_ACT_SELU: {
-      const float scale = static_cast<float>(kSeluScale);
-      const float neg = static_cast<float>(kSeluAlpha) * scale;
-      return x <= 0.0f ? expm1f(x) * neg : x * scale;
-    }
-    case QSTE_ACT_SOFTPLUS: return softplus_f(x, p.a);
-    case QSTE_ACT_MISH: return x * tanhf(log1pf(expf(x)));
-    case QSTE_ACT_HARDSWISH: return x * fminf(fmaxf(x + 3.0f, 0.0f), 6.0f) / 6.0f;
-    case QSTE_ACT_RELU_SQUARE: {
-      const float a = x < 0.0f ? 0.0f : x;
-      return a * a;
-    }
-    default: return 0.0f;
+// f(x) in fp32: the value torch's activation computes before its rounding to
+// the dtype.
+template <int KIND>
+__device__ __forceinline__ float value_of(float x, float a) {
+  if constexpr (KIND == QSTE_ACT_GELU) {
+    return x * 0.5f * (1.0f + erff(x * static_cast<float>(0.70710678118654752440)));
+  } else if constexpr (KIND == QSTE_ACT_GELU_TANH) {
+    const float beta = static_cast<float>(kSqrt2 * 1.12837916709551257390 * 0.5);
+    const float kappa = static_cast<float>(kTanhCoefficient);
+    const float cube = x * x * x;
+    const float inner = beta * (x + kappa * cube);
+    return 0.5f * x * (1.0f + tanhf(inner));
+  } else if constexpr (KIND == QSTE_ACT_SILU) {
+    return x / (1.0f + expf(-x));
+  } else if constexpr (KIND == QSTE_ACT_TANH) {
+    return tanhf(x);
+  } else if constexpr (KIND == QSTE_ACT_SIGMOID) {
+    return 1.0f / (1.0f + expf(-x));
+  } else if constexpr (KIND == QSTE_ACT_ELU) {
+    return x <= 0.0f ? expm1f(x) * a : x;
+  } else if constexpr (KIND == QSTE_ACT_CELU) {
+    return x <= 0.0f ? expm1f(x * (1.0f / a)) * a : x;
+  } else if constexpr (KIND == QSTE_ACT_SELU) {
+    const float scale = static_cast<float>(kSeluScale);
+    const float neg = static_cast<float>(kSeluAlpha) * scale;
+    return x <= 0.0f ? expm1f(x) * neg : x * scale;
+  } else if constexpr (KIND == QSTE_ACT_SOFTPLUS) {
+    return softplus_f(x, a);
+  } else if constexpr (KIND == QSTE_ACT_MISH) {
+    return x * tanhf(log1pf(expf(x)));
+  } else if constexpr (KIND == QSTE_ACT_HARDSWISH) {
+    return x * fminf(fmaxf(x + 3.0f, 0.0f), 6.0f) / 6.0f;
+  } else if constexpr (KIND == QSTE_ACT_RELU_SQUARE) {
+    const float r = x < 0.0f ? 0.0f : x;
+    return r * r;
+  } else {
+    return 0.0f;
   }
 }
 
 // The derivative the reference retains (nn.py:392-440, 456-481), from the
 // input x and the output y as a tensor of the dtype (y already rounded).
-__device__ __forceinline__ float smooth_derivative(const SmoothParams& p, float x, float y) {
-  switch (p.kind) {
-    case QSTE_ACT_GELU: {
-      const float cumulative = 0.5f * (1.0f + erff(x / static_cast<float>(kSqrt2)));
-      const float e = expf(-0.5f * x * x);
-      return cumulative + x * e * static_cast<float>(kInvSqrt2Pi);
-    }
-    case QSTE_ACT_GELU_TANH: {
-      const float s = static_cast<float>(kSqrt2OverPi);
-      const float cube = x * x * x;
-      const float inner = s * (x + static_cast<float>(kTanhCoefficient) * cube);
-      const float t = tanhf(inner);
-      const float left = 0.5f * (1.0f + t);
-      const float right = 0.5f * x * (1.0f - t * t) * s *
-                          (1.0f + static_cast<float>(3.0 * kTanhCoefficient) * x * x);
-      return left + right;
-    }
-    case QSTE_ACT_SILU: {
-      const float s = sigmoid_f(x);
-      return s * (1.0f + x * (1.0f - s));
-    }
-    case QSTE_ACT_TANH: return 1.0f - y * y;
-    case QSTE_ACT_SIGMOID: return y * (1.0f - y);
-    case QSTE_ACT_ELU: return x > 0.0f ? 1.0f : y + p.a;
-    case QSTE_ACT_CELU: return x > 0.0f ? 1.0f : y / p.a + 1.0f;
-    case QSTE_ACT_SELU:
-      return x > 0.0f ? static_cast<float>(kSeluScale) : y + static_cast<float>(kSeluScale * kSeluAlpha);
-    case QSTE_ACT_SOFTPLUS: return sigmoid_f(p.a * x);
-    case QSTE_ACT_MISH: {
-      const float t = tanhf(softplus_f(x, 1.0f));
-      return t + x * (1.0f - t * t) * sigmoid_f(x);
-    }
-    case QSTE_ACT_HARDSWISH:
-      return x <= -3.0f ? 0.0f : (x >= 3.0f ? 1.0f : (2.0f * x + 3.0f) / 6.0f);
-    case QSTE_ACT_RELU_SQUARE: return x < 0.0f ? 0.0f : x;  // the retained quantity: relu(x)
-    default: return 0.0f;
+template <int KIND>
+__device__ __forceinline__ float derivative_of(float x, float y, float a) {
+  if constexpr (KIND == QSTE_ACT_GELU) {
+    // x / sqrt(2) through the correctly rounded reciprocal (same quotient)
+    constexpr float kS2 = static_cast<float>(kSqrt2);
+    constexpr float kInvS2 = 1.0f / kS2;
+    const float cumulative = 0.5f * (1.0f + erff(div_by(x, kS2, kInvS2)));
+    const float e = expf(-0.5f * x * x);
+    return cumulative + x * e * static_cast<float>(kInvSqrt2Pi);
+  } else if constexpr (KIND == QSTE_ACT_GELU_TANH) {
+    const float s = static_cast<float>(kSqrt2OverPi);
+    const float cube = x * x * x;
+    const float inner = s * (x + static_cast<float>(kTanhCoefficient) * cube);
+    const float t = tanhf(inner);
+    const float left = 0.5f * (1.0f + t);
+    const float right = 0.5f * x * (1.0f - t * t) * s * (1.0f + static_cast<float>(3.0 * kTanhCoefficient) * x * x);
+    return left + right;
+  } else if constexpr (KIND == QSTE_ACT_SILU) {
+    const float s = sigmoid_f(x);
+    return s * (1.0f + x * (1.0f - s));
+  } else if constexpr (KIND == QSTE_ACT_TANH) {
+    return 1.0f - y * y;
+  } else if constexpr (KIND == QSTE_ACT_SIGMOID) {
+    return y * (1.0f - y);
+  } else if constexpr (KIND == QSTE_ACT_ELU) {
+    return x > 0.0f ? 1.0f : y + a;
+  } else if constexpr (KIND == QSTE_ACT_CELU) {
+    return x > 0.0f ? 1.0f : y / a + 1.0f;
+  } else if constexpr (KIND == QSTE_ACT_SELU) {
+    return x > 0.0f ? static_cast<float>(kSeluScale) : y + static_cast<float>(kSeluScale * kSeluAlpha);
+  } else if constexpr (KIND == QSTE_ACT_SOFTPLUS) {
+    return sigmoid_f(a * x);
+  } else if constexpr (KIND == QSTE_ACT_MISH) {
+    const float t = tanhf(softplus_f(x, 1.0f));
+    return t + x * (1.0f - t * t) * sigmoid_f(x);
+  } else if constexpr (KIND == QSTE_ACT_HARDSWISH) {
+    return x <= -3.0f ? 0.0f : (x >= 3.0f ? 1.0f : (2.0f * x + 3.0f) / 6.0f);
+  } else if constexpr (KIND == QSTE_ACT_RELU_SQUARE) {
+    return x < 0.0f ? 0.0f : x;  // the retained quantity: relu(x), a tensor of the dtype
+  } else {
+    return 0.0f;
   }
 }
 
+// Value (rounded to the dtype) and derivative of one element, sharing the
+// subexpressions the two formulas have in common; every shared value is the
+// one each formula computes on its own, so the results are unchanged.
+template <int KIND, int DT>
+__device__ __forceinline__ void value_and_derivative(float x, float a, float& y, float& d) {
+  using E = Elem<DT>;
+  if constexpr (KIND == QSTE_ACT_SILU) {
+    const float denom = 1.0f + expf(-x);  // torch's silu and sigmoid share it
+    const float s = 1.0f / denom;         // sigmoid(x) = RN(1 / denom)
+    // x / denom from that reciprocal while it stays a normal number
+    y = E::round(denom < 0x1p60f ? div_by(x, denom, s) : x / denom);
+    d = s * (1.0f + x * (1.0f - s));
+  } else if constexpr (KIND == QSTE_ACT_MISH) {
+    const float e = expf(x);
+    const float t = tanhf(log1pf(e));  // softplus below its threshold is log1p(exp(x))
+    y = E::round(x * t);
+    const float t2 = x > 20.0f ? tanhf(x) : t;
+    d = t2 + x * (1.0f - t2 * t2) * sigmoid_f(x);
+  } else if constexpr (KIND == QSTE_ACT_RELU_SQUARE) {
+    y = E::round(value_of<KIND>(x, a));
+    d = E::round(derivative_of<KIND>(x, y, a));
+  } else {
+    y = E::round(value_of<KIND>(x, a));
+    d = derivative_of<KIND>(x, y, a);
+  }
+}
+
+// Any kind chosen at run time (the generic path; the hot kinds also have
+// specialised instantiations).
+constexpr int kDynamic = -1;
+
+template <int KIND, int DT>
+__device__ __forceinline__ void value_and_derivative_any(int kind, float x, float a, float& y, float& d) {
+  if constexpr (KIND != kDynamic) {
+    value_and_derivative<KIND, DT>(x, a, y, d);
+  } else {
+    switch (kind) {
+#define QSTE_VD(K) case K: value_and_derivative<K, DT>(x, a, y, d); break;
+      QSTE_VD(QSTE_ACT_GELU) QSTE_VD(QSTE_ACT_GELU_TANH) QSTE_VD(QSTE_ACT_SILU) QSTE_VD(QSTE_ACT_TANH)
+      QSTE_VD(QSTE_ACT_SIGMOID) QSTE_VD(QSTE_ACT_ELU) QSTE_VD(QSTE_ACT_CELU) QSTE_VD(QSTE_ACT_SELU)
+      QSTE_VD(QSTE_ACT_SOFTPLUS) QSTE_VD(QSTE_ACT_MISH) QSTE_VD(QSTE_ACT_HARDSWISH) QSTE_VD(QSTE_ACT_RELU_SQUARE)
+#undef QSTE_VD
+      default: y = 0.0f; d = 0.0f;
+    }
+  }
+}
+
+template <int KIND, int DT>
+__device__ __forceinline__ float derivative_any(int kind, float x, float y, float a) {
+  using E = Elem<DT>;
+  if constexpr (KIND != kDynamic) {
+    return KIND == QSTE_ACT_RELU_SQUARE ? E::round(derivative_of<KIND>(x, y, a)) : derivative_of<KIND>(x, y, a);
+  } else {
+    switch (kind) {
+#define QSTE_D(K) case K: return derivative_of<K>(x, y, a);
+      QSTE_D(QSTE_ACT_GELU) QSTE_D(QSTE_ACT_GELU_TANH) QSTE_D(QSTE_ACT_SILU) QSTE_D(QSTE_ACT_TANH)
+      QSTE_D(QSTE_ACT_SIGMOID) QSTE_D(QSTE_ACT_ELU) QSTE_D(QSTE_ACT_CELU) QSTE_D(QSTE_ACT_SELU)
+      QSTE_D(QSTE_ACT_SOFTPLUS) QSTE_D(QSTE_ACT_MISH) QSTE_D(QSTE_ACT_HARDSWISH)
+#undef QSTE_D
+      case QSTE_ACT_RELU_SQUARE: return E::round(derivative_of<QSTE_ACT_RELU_SQUARE>(x, y, a));
+      default: return 0.0f;
+    }
+  }
+}
+
+// Maximum over a row's G threads (G = 64: within the wave; otherwise G is the
+// whole workgroup).
 template <int G>
 __device__ __forceinline__ float group_max(float v, float* red) {
   v = wave_max(v);
@@ -348,72 +426,82 @@ __device__ __forceinline__ float group_max(float v, float* red) {
   __syncthreads();
   float m = red[0];
 #pragma unroll
-  for (int w = 1; w < kThreads / kWave; ++w) m = fmaxf(m, red[w]);
+  for (int w = 1; w < G / kWave; ++w) m = fmaxf(m, red[w]);
   return m;
 }
 
-// fmaxf drops a NaN; the reference's amax keeps it.  Track NaN separately.
+// fmaxf drops a NaN; the reference's amax keeps it.
 __device__ __forceinline__ float nan_max(float m, float v) { return (v != v || m != m) ? __builtin_nanf("") : fmaxf(m, v); }
 
-// One row per group of G threads (G = 64: a wave, four rows per workgroup;
-// G = 256: the workgroup).
+// One row per group of G threads: G = 64 is a wave (BLOCK / 64 rows per
+// workgroup), G = BLOCK a whole workgroup.  Thread t owns the 8-element
+// chunks t, t + G, ...  With CH > 0 a row has at most G * CH chunks and each
+// thread's derivatives stay in registers (unrolled, constant indices) between
+// the row maximum and the quantization, so the input is read once; with
+// CH == 0 (longer rows) they are recomputed from the input, still in L2.
+// KIND == kDynamic takes the kind from `kind` at run time.
 //
 // mode: 0 -- compute y = f(x), store it (when y != NULL), derive from it
 //       1 -- y holds the forward output already (computed elsewhere); read it
 //       2 -- `provided` holds the fp32 derivative (x, y unused)
-template <int DT, int G, bool CACHED>
-__global__ __launch_bounds__(kThreads) void smooth_rows_kernel(
-    const typename Elem<DT>::T* __restrict__ x, typename Elem<DT>::T* __restrict__ y,
-    const float* __restrict__ provided, int mode, SmoothParams p, void* __restrict__ payload,
-    float* __restrict__ scale, int64_t rows, int64_t cols) {
+template <int DT, int G, int CH, int KIND, int BLOCK>
+__device__ __forceinline__ void smooth_row(const typename Elem<DT>::T* __restrict__ x,
+                                           typename Elem<DT>::T* __restrict__ y,
+                                           const float* __restrict__ provided, int mode, int kind, float a,
+                                           void* __restrict__ payload, float* __restrict__ scale,
+                                           int64_t rows, int64_t cols, float* red) {
   using E = Elem<DT>;
-  __shared__ float red[kThreads / kWave];
-  constexpr int kRowsPerBlock = kThreads / G;
+  const bool kUsq = (KIND == kDynamic ? kind : KIND) == QSTE_ACT_RELU_SQUARE;
+  constexpr int kRowsPerBlock = BLOCK / G;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / G;
   const int t = threadIdx.x % G;
   const bool live = row < rows;
   const int64_t nch = (cols + 7) / 8;
   const bool whole = (cols & 7) == 0;
-  const bool usq = p.kind == QSTE_ACT_RELU_SQUARE;
   const int64_t base = (live ? row : 0) * cols;
 
-  auto derive = [&](int64_t q, float d[8], bool write_y) {
+  auto derive = [&](int64_t q, float d[8], bool write_y) __attribute__((always_inline)) {
     const int n = static_cast<int>(cols - q * 8 < 8 ? cols - q * 8 : 8);
     if (mode == 2) {
       Chunk<QSTE_F32>::load(provided + base + q * 8, n, whole, d);
-      for (int j = n; j < 8; ++j) d[j] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) d[j] = j < n ? d[j] : 0.0f;
       return;
     }
     float xv[8], yv[8];
     Chunk<DT>::load(x + base + q * 8, n, whole, xv);
     if (mode == 1) {
       Chunk<DT>::load(y + base + q * 8, n, whole, yv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float v = derivative_any<KIND, DT>(kind, xv[j], yv[j], a);
+        d[j] = j < n ? v : 0.0f;
+      }
     } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) yv[j] = E::round(smooth_value(p, xv[j]));
+      for (int j = 0; j < 8; ++j) {
+        value_and_derivative_any<KIND, DT>(kind, xv[j], a, yv[j], d[j]);
+        d[j] = j < n ? d[j] : 0.0f;
+      }
       if (write_y && y != nullptr) Chunk<DT>::store(y + base + q * 8, n, whole, yv);
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      // relu(x)^2 retains relu(x) itself, a tensor of the dtype
-      d[j] = j < n ? (usq ? E::round(smooth_derivative(p, xv[j], yv[j]))
-                          : smooth_derivative(p, xv[j], yv[j]))
-                   : 0.0f;
     }
   };
 
-  auto quantize = [&](int64_t q, const float d[8], float s) {
+  // d / s through r = RN(1 / s): the row scale lies in [1e-8 / 255, amax / 127]
+  // and |d / s| <= 255, so no step leaves the normal range (a NaN or infinite
+  // scale gives a NaN quotient, stored as 0, as the division would)
+  auto quantize = [&](int64_t q, const float d[8], float s, float r) __attribute__((always_inline)) {
     const int n = static_cast<int>(cols - q * 8 < 8 ? cols - q * 8 : 8);
     uint32_t lo = 0, hi = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       uint32_t byte;
-      if (usq) {
-        float v = rintf(E::round(d[j] / s));
+      if (kUsq) {
+        float v = rintf(E::round(div_by(d[j], s, r)));
         v = v != v ? 0.0f : fminf(fmaxf(v, 0.0f), 255.0f);
         byte = static_cast<uint32_t>(v);
       } else {
-        float v = rintf(d[j] / s);
+        float v = rintf(div_by(d[j], s, r));
         v = v != v ? 0.0f : fminf(fmaxf(v, -127.0f), 127.0f);
         byte = static_cast<uint32_t>(static_cast<int32_t>(v)) & 0xFFu;
       }
@@ -428,22 +516,24 @@ __global__ __launch_bounds__(kThreads) void smooth_rows_kernel(
     }
   };
 
-  // CACHED: the row's derivatives wait in LDS (each thread reads back only
-  // what it wrote) between the maximum and the quantization; otherwise they
-  // are recomputed from the input, which is still in L2.
-  extern __shared__ float dcache[];
-  float* mine = dcache + (CACHED ? (threadIdx.x / G) * nch * 8 : 0);
+  float cache[CH > 0 ? CH : 1][8];
   float amax = 0.0f;
-  if (live) {
+  if constexpr (CH > 0) {
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int64_t q = t + static_cast<int64_t>(k) * G;
+      if (live && q < nch) {
+        derive(q, cache[k], true);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = nan_max(amax, fabsf(cache[k][j]));
+      }
+    }
+  } else if (live) {
     for (int64_t q = t; q < nch; q += G) {
       float d[8];
       derive(q, d, true);
 #pragma unroll
       for (int j = 0; j < 8; ++j) amax = nan_max(amax, fabsf(d[j]));
-      if constexpr (CACHED) {
-        reinterpret_cast<float4*>(mine + q * 8)[0] = make_float4(d[0], d[1], d[2], d[3]);
-        reinterpret_cast<float4*>(mine + q * 8)[1] = make_float4(d[4], d[5], d[6], d[7]);
-      }
     }
   }
   // the reference's amax keeps a NaN: carry it through the reduction as the
@@ -454,26 +544,37 @@ __global__ __launch_bounds__(kThreads) void smooth_rows_kernel(
   if (key == __builtin_inff()) nan_flag = group_max<G>(nan_flag, red);
   if (!live) return;
   float s;
-  if (usq) {
+  if (kUsq) {
     // relu(x)^2: maximum, clamp and division in the dtype (nn.py:316-318)
     s = E::round(E::round(fmaxf(key, 1e-8f)) / 255.0f);
   } else {
     s = fmaxf(key, 1e-8f) / 127.0f;
   }
   if (nan_flag > 0.0f) s = __builtin_nanf("");
-  for (int64_t q = t; q < nch; q += G) {
-    float d[8];
-    if constexpr (CACHED) {
-      const float4 a = reinterpret_cast<const float4*>(mine + q * 8)[0];
-      const float4 b = reinterpret_cast<const float4*>(mine + q * 8)[1];
-      d[0] = a.x; d[1] = a.y; d[2] = a.z; d[3] = a.w;
-      d[4] = b.x; d[5] = b.y; d[6] = b.z; d[7] = b.w;
-    } else {
-      derive(q, d, false);
+  const float r = 1.0f / s;
+  if constexpr (CH > 0) {
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int64_t q = t + static_cast<int64_t>(k) * G;
+      if (q < nch) quantize(q, cache[k], s, r);
     }
-    quantize(q, d, s);
+  } else {
+    for (int64_t q = t; q < nch; q += G) {
+      float d[8];
+      derive(q, d, false);
+      quantize(q, d, s, r);
+    }
   }
   if (t == 0) scale[row] = s;
+}
+
+template <int DT, int G, int CH, int KIND, int BLOCK>
+__global__ __launch_bounds__(BLOCK) void smooth_rows_kernel(
+    const typename Elem<DT>::T* __restrict__ x, typename Elem<DT>::T* __restrict__ y,
+    const float* __restrict__ provided, int mode, SmoothParams p, void* __restrict__ payload,
+    float* __restrict__ scale, int64_t rows, int64_t cols) {
+  __shared__ float red[BLOCK / kWave];
+  smooth_row<DT, G, CH, KIND, BLOCK>(x, y, provided, mode, p.kind, p.a, payload, scale, rows, cols, red);
 }
 
 // grad * (payload * scale), each product rounded to the dtype
@@ -547,29 +648,47 @@ bool chunk_aligned(const void* p, int dtype) {
   return (a % 16) == 0;
 }
 
-// LDS cache per workgroup: (rows per workgroup) x (row rounded up to whole
-// chunks) fp32 derivatives; rows longer than kMaxCachedCols recompute.
-constexpr int64_t kMaxCachedCols = 15360;  // 60 KiB of LDS per workgroup at most
-
-template <int DT, int G, bool CACHED>
+template <int DT, int G, int CH, int KIND, int BLOCK>
 int smooth_launch(const void* x, void* y, const float* provided, int mode, SmoothParams p, void* payload,
                   float* scale, int64_t rows, int64_t cols, hipStream_t s) {
   using T = typename Elem<DT>::T;
-  constexpr int kRows = kThreads / G;
+  constexpr int kRows = BLOCK / G;
   const int64_t blocks = (rows + kRows - 1) / kRows;
-  const size_t lds = CACHED ? sizeof(float) * static_cast<size_t>(kRows * ((cols + 7) / 8) * 8) : 0;
-  smooth_rows_kernel<DT, G, CACHED><<<static_cast<unsigned>(blocks), kThreads, lds, s>>>(
+  smooth_rows_kernel<DT, G, CH, KIND, BLOCK><<<static_cast<unsigned>(blocks), BLOCK, 0, s>>>(
       static_cast<const T*>(x), static_cast<T*>(y), provided, mode, p, payload, scale, rows, cols);
   return static_cast<int>(hipGetLastError());
 }
 
+// Row length -> threads per row, at most two register-cached chunks each:
+// <= 1024 columns a wave (4 rows per workgroup), <= 4096 a 256-thread
+// workgroup, <= 16384 a 1024-thread workgroup; longer rows recompute.
+template <int DT, int KIND>
+int smooth_shapes(const void* x, void* y, const float* provided, int mode, SmoothParams p, void* payload,
+                  float* scale, int64_t rows, int64_t cols, hipStream_t s) {
+  if constexpr (KIND == kDynamic) {
+    // every kind in one kernel: derivatives recomputed, no unrolled cache
+    if (cols <= 1024) return smooth_launch<DT, 64, 0, KIND, 256>(x, y, provided, mode, p, payload, scale, rows, cols, s);
+    if (cols <= 4096) return smooth_launch<DT, 256, 0, KIND, 256>(x, y, provided, mode, p, payload, scale, rows, cols, s);
+    return smooth_launch<DT, 1024, 0, KIND, 1024>(x, y, provided, mode, p, payload, scale, rows, cols, s);
+  } else {
+    if (cols <= 1024) return smooth_launch<DT, 64, 2, KIND, 256>(x, y, provided, mode, p, payload, scale, rows, cols, s);
+    if (cols <= 4096) return smooth_launch<DT, 256, 2, KIND, 256>(x, y, provided, mode, p, payload, scale, rows, cols, s);
+    if (cols <= 16384)
+      return smooth_launch<DT, 1024, 2, KIND, 1024>(x, y, provided, mode, p, payload, scale, rows, cols, s);
+    return smooth_launch<DT, 1024, 0, KIND, 1024>(x, y, provided, mode, p, payload, scale, rows, cols, s);
+  }
+}
+
+// GELU and SiLU (the MLP activations) computing their own value get kernels
+// of their own; every other case runs the run-time-kind kernel.
 template <int DT>
 int smooth_dispatch(const void* x, void* y, const float* provided, int mode, SmoothParams p, void* payload,
                     float* scale, int64_t rows, int64_t cols, hipStream_t s) {
-  if (cols <= 2048) return smooth_launch<DT, 64, true>(x, y, provided, mode, p, payload, scale, rows, cols, s);
-  if (cols <= kMaxCachedCols)
-    return smooth_launch<DT, 256, true>(x, y, provided, mode, p, payload, scale, rows, cols, s);
-  return smooth_launch<DT, 256, false>(x, y, provided, mode, p, payload, scale, rows, cols, s);
+  if (mode == 0 && p.kind == QSTE_ACT_SILU)
+    return smooth_shapes<DT, QSTE_ACT_SILU>(x, y, provided, mode, p, payload, scale, rows, cols, s);
+  if (mode == 0 && p.kind == QSTE_ACT_GELU)
+    return smooth_shapes<DT, QSTE_ACT_GELU>(x, y, provided, mode, p, payload, scale, rows, cols, s);
+  return smooth_shapes<DT, kDynamic>(x, y, provided, mode, p, payload, scale, rows, cols, s);
 }
 
 }  // namespace

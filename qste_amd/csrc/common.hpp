@@ -147,6 +147,18 @@ __device__ __forceinline__ T block_sum(T v, T* scratch) {
   return total;
 }
 
+// x / d, correctly rounded, for a divisor shared by many quotients: with
+// r = RN(1/d) and q0 = RN(x r) within one ulp of x/d, the residual
+// x - q0 d is exact under FMA and RN(q0 + r (x - q0 d)) is the correctly
+// rounded quotient (Markstein's correction step).  Three operations instead
+// of a full IEEE division per element.  Valid while no step overflows or
+// underflows (callers keep d and x in the normal range).
+__device__ __forceinline__ float div_by(float x, float d, float r) {
+  const float q0 = x * r;
+  const float e = fmaf(-q0, d, x);
+  return fmaf(e, r, q0);
+}
+
 inline int ceil_div(int64_t a, int64_t b) { return static_cast<int>((a + b - 1) / b); }
 
 }  // namespace qste

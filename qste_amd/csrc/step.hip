@@ -118,17 +118,6 @@ __device__ __forceinline__ float row_factor_of(float sqrt_mean, float new_row) {
   return sqrt_mean / sqrtf(fmaxf(new_row, 1e-10f));
 }
 
-// x / d, correctly rounded, for a divisor shared by many quotients: with
-// r = RN(1/d) and q0 = RN(x r) within one ulp of x/d, the residual
-// x - q0 d is exact under FMA and RN(q0 + r (x - q0 d)) is the correctly
-// rounded quotient (Markstein's correction step).  Three operations instead
-// of a full IEEE division per element.
-__device__ __forceinline__ float div_by(float x, float d, float r) {
-  const float q0 = x * r;
-  const float e = fmaf(-q0, d, x);
-  return fmaf(e, r, q0);
-}
-
 __device__ __forceinline__ float moment_of(float u2, float prev, float s_old, const Params& p) {
   float decoded = prev * s_old;
   decoded = decoded * p.b1;
