@@ -461,3 +461,28 @@ def test_packed_activations_context_routes_marked_outputs_only(fake):
         assert torch.allclose(fused, torch.relu(hidden).square())
         assert fused.grad_fn is not None and "ReluSquare" in type(fused.grad_fn).__name__
     assert F.gelu is qste.nn._TORCH_GELU and torch.relu is qste.nn._TORCH_TORCH_RELU
+
+
+def test_checkpoint_layout_matches_the_reference(fake):
+    """State-dict keys, dtypes and shapes of surface.py:67-74 / optim.py:212-232."""
+
+    import qste_amd as qste
+
+    model = qste.convert(nn.Sequential(nn.Linear(20, 12), nn.ReLU(), nn.Linear(12, 5, bias=False)))
+    coords = qste.QSTEOptimizer(model)
+    sd = model.state_dict()
+    assert set(sd) == {"0.surface.coordinate", "0.surface.packed_sign", "0.surface.log_scale", "0.bias",
+                       "2.surface.coordinate", "2.surface.packed_sign", "2.surface.log_scale"}
+    assert (sd["0.surface.coordinate"].dtype, tuple(sd["0.surface.coordinate"].shape)) == (torch.int8, (12, 20))
+    assert (sd["0.surface.packed_sign"].dtype, tuple(sd["0.surface.packed_sign"].shape)) == (torch.uint8, (12, 3))
+    assert sd["0.surface.log_scale"].dtype == torch.float32
+    osd = coords.state_dict()
+    assert sorted(osd) == ["config", "step_number", "surfaces"]
+    assert osd["config"] == qste.QSTEConfig().metadata()
+    assert [sorted(e) for e in osd["surfaces"]] == [["col_v", "moment_q", "moment_scale", "row_v"]] * 2
+    assert osd["surfaces"][1]["moment_scale"].shape == ((5 * 12 + 255) // 256,)
+    restored = qste.convert(nn.Sequential(nn.Linear(20, 12), nn.ReLU(), nn.Linear(12, 5, bias=False)))
+    restored.load_state_dict(sd)
+    again = qste.QSTEOptimizer(restored)
+    again.load_state_dict(osd)
+    assert again.step_number == coords.step_number
