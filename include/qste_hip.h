@@ -233,6 +233,34 @@ int qste_smooth_backward(const void* grad, int dtype, const void* payload,
                          int unsigned_payload, const float* scale, void* out, int64_t rows,
                          int64_t cols, void* stream);
 
+/* ---- binary embedding (src/qste/modules.py:68-100) ---------------------- */
+
+/* out [count, cols] (out_dtype) = sign(packed[ids[n]]) * scale[ids[n]];
+ * ids int64 [count] must lie in [0, rows) (an id outside gives a zero row;
+ * the Python layer rejects such ids before the call).
+ * Replaces qste.kernels.packed_embedding (cuda.py:1691-1702;
+ * fallback.py:151-155). */
+int qste_packed_embedding(const int64_t* ids, int64_t count, const uint8_t* packed,
+                          const float* scale, void* out, int out_dtype, int64_t rows,
+                          int64_t cols, void* stream);
+
+/* Backward of the embedding (QSTEEmbeddingFn.backward,
+ * src/qste/functional.py:274-286) in one call:
+ *   E0 [rows, cols] = zeros.index_add_(0, ids, grad), each row summed in
+ *                     ascending token order (a sequential index_add_'s fp32
+ *                     sums, bit for bit)
+ *   grad_scale fp32 [rows] = sum_c E0 * sign
+ *   evidence fp32 [rows, cols] = E0 * scale[r]  (every row written)
+ * grad [count, cols] in dtype.  Needs
+ * qste_embedding_backward_workspace_bytes(count, rows) bytes of workspace.
+ * No single counterpart in the reference: it fuses index_add_, packed_row_inner
+ * and the scaling. */
+size_t qste_embedding_backward_workspace_bytes(int64_t count, int64_t rows);
+int qste_embedding_backward(const int64_t* ids, int64_t count, const void* grad, int dtype,
+                            const uint8_t* packed, const float* scale, float* evidence,
+                            float* grad_scale, int64_t rows, int64_t cols, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

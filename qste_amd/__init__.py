@@ -18,8 +18,8 @@ Forward, backward and the coordinate step run as hand-written HIP kernels in
 from .config import QSTEConfig, coerce_config
 from .convert import (continuous_parameters, convert, export_packed, memory_report,
                       surfaces)
-from .functional import QSTELinearFn, qste_linear, qste_weight
-from .modules import PackedLinear, QSTELinear
+from .functional import QSTEEmbeddingFn, QSTELinearFn, qste_embedding, qste_linear, qste_weight
+from .modules import PackedEmbedding, PackedLinear, QSTEEmbedding, QSTELinear
 from . import nn
 from .nn import packed_activations
 from .optim import QSTEOptimizer
@@ -28,7 +28,10 @@ from .surface import Surface
 __version__ = "0.1.0"
 
 __all__ = [
+    "PackedEmbedding",
     "PackedLinear",
+    "QSTEEmbedding",
+    "QSTEEmbeddingFn",
     "QSTEConfig",
     "QSTELinear",
     "QSTELinearFn",
@@ -42,6 +45,7 @@ __all__ = [
     "memory_report",
     "nn",
     "packed_activations",
+    "qste_embedding",
     "qste_linear",
     "qste_weight",
     "surfaces",

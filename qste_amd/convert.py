@@ -10,8 +10,8 @@ ones of ``qste_amd.nn`` (``convert.py:246-274``): ``True`` / ``"all"`` take
 every replacement, ``"exact"`` only the one-bit (value- and
 gradient-identical) ones.
 
-Not in this build: binary embeddings (``QSTEEmbedding``).  Selecting an
-``nn.Embedding`` raises ``NotImplementedError``.
+``nn.Embedding`` layers become ``QSTEEmbedding``; ``export_packed`` turns
+them into ``PackedEmbedding`` (``convert.py:327-357``).
 """
 
 from __future__ import annotations
@@ -23,7 +23,7 @@ from typing import Iterator, Sequence
 import torch.nn as nn
 
 from .config import QSTEConfig, coerce_config
-from .modules import PackedLinear, QSTELinear
+from .modules import PackedEmbedding, PackedLinear, QSTEEmbedding, QSTELinear
 from .surface import Surface
 
 DEFAULT_TYPES = (nn.Linear, nn.Embedding)
@@ -36,10 +36,11 @@ def _selected(name: str, include: Sequence[str] | None, exclude: Sequence[str] |
 
 
 def _candidates(model: nn.Module, types: tuple[type, ...]) -> Iterator[tuple[str, nn.Module]]:
+    converted = (QSTELinear, QSTEEmbedding)
     for name, module in model.named_modules():
-        if name and isinstance(module, types + (QSTELinear,)):
-            weight = None if isinstance(module, QSTELinear) else getattr(module, "weight", None)
-            if isinstance(module, QSTELinear) or (weight is not None and weight.ndim == 2):
+        if name and isinstance(module, types + converted):
+            weight = None if isinstance(module, converted) else getattr(module, "weight", None)
+            if isinstance(module, converted) or (weight is not None and weight.ndim == 2):
                 yield name, module
 
 
@@ -74,14 +75,13 @@ def convert(
     shared: dict[int, Surface] = {}
     converted = list(getattr(model, "_qste_converted", ()))
     for name, module in targets:
-        if isinstance(module, QSTELinear):
-            continue
-        if isinstance(module, nn.Embedding):
-            raise NotImplementedError(
-                f"{name}: binary embeddings are not part of qste_amd; exclude it or "
-                "narrow `include` to linear layers")
+        if isinstance(module, (QSTELinear, QSTEEmbedding)):
+            continue  # already binary
         surface = shared.get(id(module.weight))
-        replacement = QSTELinear.from_linear(module, cfg, surface)
+        if isinstance(module, nn.Embedding):
+            replacement = QSTEEmbedding.from_embedding(module, cfg, surface)
+        else:
+            replacement = QSTELinear.from_linear(module, cfg, surface)
         shared[id(module.weight)] = replacement.surface
         _set_submodule(model, name, replacement)
         converted.append(name)
@@ -164,4 +164,8 @@ def export_packed(model: nn.Module, *, inplace: bool = False) -> nn.Module:
             _set_submodule(target, name, PackedLinear(
                 s.packed_sign.data.clone(), s.scale.detach().clone(), s.columns,
                 None if module.bias is None else module.bias.detach().clone()))
+        elif isinstance(module, QSTEEmbedding):
+            s = module.surface
+            _set_submodule(target, name, PackedEmbedding(
+                s.packed_sign.data.clone(), s.scale.detach().clone(), s.columns))
     return target

@@ -103,3 +103,29 @@ class QSTEWeightFn(Function):
 def qste_weight(surface: Surface) -> Tensor:
     surface.note_forward()
     return QSTEWeightFn.apply(surface.packed_sign, surface.scale, surface)
+
+
+class QSTEEmbeddingFn(Function):
+    """Binary embedding lookup; its backward is the surface's evidence (functional.py:260-282)."""
+
+    @staticmethod
+    def forward(ctx, ids, packed, scale, surface: Surface):
+        output = kernels.packed_embedding(ids, packed, scale, surface.columns)
+        ctx.save_for_backward(ids, packed, scale)
+        ctx.surface = surface
+        return output
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        ids, packed, scale = ctx.saved_tensors
+        evidence, grad_scale = kernels.embedding_backward(
+            ids, grad_output, packed, scale.detach(), ctx.surface.columns)
+        ctx.surface.consume_evidence(evidence)
+        return None, None, grad_scale.to(scale.dtype), None
+
+
+def qste_embedding(ids: Tensor, surface: Surface) -> Tensor:
+    """Functional binary embedding (functional.py:285-287)."""
+
+    surface.note_forward()
+    return QSTEEmbeddingFn.apply(ids, surface.packed_sign, surface.scale, surface)

@@ -32,6 +32,8 @@ __all__ = [
     "unpack_bits",
     "coordinate_update",
     "cuda_available",
+    "embedding_backward",
+    "packed_embedding",
     "evidence_from_packed",
     "linear_backward",
     "native_available",
@@ -549,3 +551,62 @@ def smooth_backward(grad: Tensor, payload: Tensor, scale: Tensor) -> Tensor:
         _ptr(_f32(scale)), _ptr(out), rows, cols, _stream(device))
     _lib.check(code, "smooth_backward")
     return out
+
+
+# ---------------------------------------------------------------------------
+# binary embedding (reference: cuda.py:1691-1702, functional.py:260-287)
+# ---------------------------------------------------------------------------
+
+
+def _check_ids(ids: Tensor, rows: int) -> Tensor:
+    flat = ids.reshape(-1).to(torch.int64).contiguous()
+    if flat.numel() and (int(flat.min()) < 0 or int(flat.max()) >= rows):
+        raise IndexError(f"embedding id out of range for {rows} rows")
+    return flat
+
+
+def packed_embedding(ids: Tensor, packed: Tensor, scale: Tensor, columns: int) -> Tensor:
+    """``sign(packed[ids]) * scale[ids]``, shape ``ids.shape + (columns,)``, in scale's dtype.
+
+    fallback.py:151-155.
+    """
+
+    device = _require_gpu(ids, packed, scale)
+    packed = _check_packed(packed, columns)
+    rows = packed.shape[0]
+    if scale.shape != (rows,):
+        raise ValueError(f"scale has shape {tuple(scale.shape)}, expected ({rows},)")
+    flat = _check_ids(ids, rows)
+    out_dtype = scale.dtype if scale.dtype in _DTYPES else torch.float32
+    out = torch.empty(flat.numel(), int(columns), dtype=out_dtype, device=device)
+    code = _lib.load().qste_packed_embedding(
+        _ptr(flat), flat.numel(), _ptr(packed), _ptr(_f32(scale)), _ptr(out), _dtype_code(out), rows,
+        int(columns), _stream(device))
+    _lib.check(code, "packed_embedding")
+    return out.view(*ids.shape, int(columns)).to(scale.dtype)
+
+
+def embedding_backward(ids: Tensor, grad: Tensor, packed: Tensor, scale: Tensor,
+                       columns: int) -> tuple[Tensor, Tensor]:
+    """``(evidence, grad_scale)`` of an embedding (functional.py:274-286).
+
+    ``evidence = zeros(R, C).index_add_(0, ids, grad) * scale[r]`` (fp32,
+    token-order sums) and ``grad_scale = row_inner(index_add_, signs)``.
+    """
+
+    device = _require_gpu(ids, grad, packed, scale)
+    packed = _check_packed(packed, columns)
+    rows = packed.shape[0]
+    flat = _check_ids(ids, rows)
+    g = grad.reshape(-1, int(columns)).contiguous()
+    if g.shape[0] != flat.numel():
+        raise ValueError("gradient rows do not match the number of ids")
+    evidence = torch.empty(rows, int(columns), dtype=torch.float32, device=device)
+    grad_scale = torch.empty(rows, dtype=torch.float32, device=device)
+    lib = _lib.load()
+    ws = _workspace(lib.qste_embedding_backward_workspace_bytes(flat.numel(), rows), device)
+    code = lib.qste_embedding_backward(
+        _ptr(flat), flat.numel(), _ptr(g), _dtype_code(g), _ptr(packed), _ptr(_f32(scale)),
+        _ptr(evidence), _ptr(grad_scale), rows, int(columns), _ptr(ws), ws.numel(), _stream(device))
+    _lib.check(code, "embedding_backward")
+    return evidence, grad_scale

@@ -1,4 +1,5 @@
-"""Drop-in modules: ``QSTELinear`` (training) and ``PackedLinear`` (inference).
+"""Drop-in modules: ``QSTELinear`` / ``QSTEEmbedding`` (training) and
+``PackedLinear`` / ``PackedEmbedding`` (inference).
 
 Constructor attributes, ``weight``/``bias`` surface and call signature follow
 the reference (``src/qste/modules.py:21-123``) so code that introspects an
@@ -13,7 +14,7 @@ from torch import Tensor
 
 from . import kernels
 from .config import QSTEConfig, coerce_config
-from .functional import qste_linear, qste_weight
+from .functional import qste_embedding, qste_linear, qste_weight
 from .nn import _mark_activation_input
 from .surface import Surface
 
@@ -83,3 +84,55 @@ class PackedLinear(nn.Module):
 
     def extra_repr(self) -> str:
         return f"in_features={self.in_features}, out_features={self.out_features}"
+
+
+class QSTEEmbedding(nn.Module):
+    """Binary embedding table: a row of packed signs times the row scale (modules.py:68-97)."""
+
+    def __init__(self, surface: Surface, padding_idx: int | None = None):
+        super().__init__()
+        self.surface = surface
+        self.num_embeddings = surface.rows
+        self.embedding_dim = surface.columns
+        self.padding_idx = padding_idx
+
+    @classmethod
+    def from_embedding(cls, module: nn.Embedding, cfg: QSTEConfig | None = None,
+                       surface: Surface | None = None) -> "QSTEEmbedding":
+        return cls(surface or Surface(module.weight, coerce_config(cfg)), getattr(module, "padding_idx", None))
+
+    @property
+    def scale(self) -> Tensor:
+        return self.surface.scale
+
+    @property
+    def packed_sign(self) -> Tensor:
+        return self.surface.packed_sign
+
+    @property
+    def weight(self) -> Tensor:
+        return qste_weight(self.surface)
+
+    def forward(self, ids: Tensor) -> Tensor:
+        return _mark_activation_input(qste_embedding(ids, self.surface))
+
+    def extra_repr(self) -> str:
+        return f"num_embeddings={self.num_embeddings}, embedding_dim={self.embedding_dim}"
+
+
+class PackedEmbedding(nn.Module):
+    """Inference-only embedding over packed signs (modules.py:126-143)."""
+
+    def __init__(self, packed: Tensor, scale: Tensor, columns: int):
+        super().__init__()
+        self.register_buffer("packed_sign", packed)
+        self.register_buffer("scale", scale)
+        self.num_embeddings = packed.shape[0]
+        self.embedding_dim = columns
+
+    @torch.no_grad()
+    def forward(self, ids: Tensor) -> Tensor:
+        return kernels.packed_embedding(ids, self.packed_sign, self.scale, self.embedding_dim)
+
+    def extra_repr(self) -> str:
+        return f"num_embeddings={self.num_embeddings}, embedding_dim={self.embedding_dim}"

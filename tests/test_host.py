@@ -27,6 +27,7 @@ import torch.nn as nn
 
 import oracle
 from oracle import activations as oa
+from oracle import embedding as oe
 
 ROOT = Path(__file__).resolve().parents[1]
 
@@ -181,8 +182,18 @@ class OracleKernels:
         return torch.from_numpy(out).to(grad.dtype)
 
 
+    # binary embedding (oracle/embedding.py)
+    def packed_embedding(self, ids, packed, scale, columns):
+        out = oe.lookup(ids.numpy(), packed.numpy(), scale.detach().float().numpy(), columns)
+        return torch.from_numpy(out).to(scale.dtype)
+
+    def embedding_backward(self, ids, grad, packed, scale, columns):
+        ev, gs = oe.backward(ids.numpy(), grad.float().numpy(), packed.numpy(), scale.float().numpy(), columns)
+        return torch.from_numpy(ev), torch.from_numpy(gs)
+
+
 ACTIVATION_OPS = ("pack_bits", "unpack_bits", "masked_backward", "masked_activation",
-                  "smooth_activation", "smooth_backward")
+                  "smooth_activation", "smooth_backward", "packed_embedding", "embedding_backward")
 
 
 @pytest.fixture
@@ -224,8 +235,8 @@ def test_convert_selects_by_glob_and_records_config(fake):
     assert model.fc1.bias.dtype == torch.float32
     with pytest.raises(ValueError):
         qste.convert(Block(), include=["nothing*"])
-    with pytest.raises(NotImplementedError):
-        qste.convert(Block(), include=["emb"])
+    emb = qste.convert(Block(), include=["emb"]).emb
+    assert isinstance(emb, qste.QSTEEmbedding) and emb.num_embeddings == 10 and emb.embedding_dim == 16
     with pytest.raises(ValueError):
         qste.convert(Block(), include=["fc1"], activations="sometimes")
 
@@ -486,3 +497,39 @@ def test_checkpoint_layout_matches_the_reference(fake):
     again = qste.QSTEOptimizer(restored)
     again.load_state_dict(osd)
     assert again.step_number == coords.step_number
+
+
+def test_embedding_forward_and_evidence(fake):
+    """functional.py:260-287 composition (the reference's test_autograd.py:231-245)."""
+
+    import qste_amd as qste
+
+    torch.manual_seed(12)
+    surface = qste.Surface(torch.randn(40, 16))
+    captured = []
+    surface._immediate = lambda _, evidence: captured.append(evidence.clone())
+    ids = torch.randint(0, 40, (3, 5))
+    grad = torch.randn(3, 5, 16)
+    out = qste.qste_embedding(ids, surface)
+    dense = torch.where(surface.coordinate >= 0, 1.0, -1.0) * surface.scale.detach()[:, None]
+    assert torch.allclose(out, dense[ids], atol=1e-6)
+    (out * grad).sum().backward()
+    expected = torch.zeros(40, 16).index_add_(0, ids.reshape(-1), grad.reshape(-1, 16))
+    assert len(captured) == 1
+    assert torch.equal(captured[0], expected * surface.scale.detach()[:, None])
+    inner = (expected.double() * torch.where(surface.coordinate >= 0, 1.0, -1.0).double()).sum(1).float()
+    assert torch.allclose(surface.log_scale.grad, inner * surface.scale.detach(), rtol=1e-6, atol=1e-7)
+
+
+def test_export_packed_turns_embeddings_into_packed_embeddings(fake):
+    import qste_amd as qste
+
+    torch.manual_seed(3)
+    model = qste.convert(nn.Sequential(nn.Embedding(30, 8), nn.Linear(8, 4)))
+    ids = torch.randint(0, 30, (2, 6))
+    with torch.no_grad():
+        expected = model(ids)
+    exported = qste.export_packed(model)
+    assert isinstance(exported[0], qste.PackedEmbedding) and isinstance(exported[1], qste.PackedLinear)
+    with torch.no_grad():
+        assert torch.allclose(exported(ids), expected, atol=1e-5)
