@@ -15,7 +15,10 @@ each GEMM kind at the gate-layer shape (the dominant kernel is reported as
 ``roofline``), torch.matmul (hipBLASLt) on dense bf16 operands of the same
 shapes for comparison, the coordinate step of one 14336 x 4096 surface (HBM), and
 the skinny-M decode GEMV of config 5 (K=8192, N=28672, M in {1, 4, 16}) over
-rotated weight copies larger than the 256 MB Infinity Cache.  The CPU
+rotated weight copies larger than the 256 MB Infinity Cache, the packed
+activation kernels at the MLP's hidden shape, and the step times of config 2
+(ReLU MLP, d=1024, 8192 tokens) and config 3 (GPT-2 small, batch 8 x 1024,
+AdamW + QSTEOptimizer).  The CPU
 baseline is the reference's CPU algorithm (oracle/cpu_baseline.py) timed on
 this host on a token sample of the same layers.
 """
@@ -113,6 +116,146 @@ class SwiGLU:
         return self.down(F.silu(self.gate(x)) * self.up(x))
 
 
+def relu_mlp(d=1024, ratio=4, device="cuda"):
+    """Config 2: fc1 d -> ratio*d, ReLU, fc2 back, both QSTE (convert), bf16."""
+
+    import torch
+    import torch.nn as nn
+
+    import qste_amd as qste
+
+    torch.manual_seed(0)
+    model = nn.Sequential(nn.Linear(d, ratio * d), nn.ReLU(), nn.Linear(ratio * d, d))
+    return qste.convert(model).to(device=device, dtype=torch.bfloat16)
+
+
+class GPT2Small:
+    """Config 3: a GPT-2-small-shaped decoder (12 layers, d=768, 12 heads, MLP
+    ratio 4, vocab 50257, context 1024, tied embedding), random init, bf16.
+    Only the MLPs are converted to QSTE (their tanh-GELU becomes the packed
+    one); attention stays float, its two batched products run in fp32."""
+
+    def __new__(cls, device="cuda", layers=12, d=768, heads=12, vocab=50257, context=1024):
+        import math
+
+        import torch
+        import torch.nn as nn
+        import torch.nn.functional as F
+
+        import qste_amd as qste
+
+        class Block(nn.Module):
+            def __init__(self):
+                super().__init__()
+                self.ln1 = nn.LayerNorm(d)
+                self.qkv = nn.Linear(d, 3 * d)
+                self.proj = nn.Linear(d, d)
+                self.ln2 = nn.LayerNorm(d)
+                self.mlp = nn.Sequential(nn.Linear(d, 4 * d), nn.GELU(approximate="tanh"), nn.Linear(4 * d, d))
+
+            def attention(self, x):
+                b, s, _ = x.shape
+                q, k, v = self.qkv(x).split(d, dim=-1)
+                q, k, v = (t.reshape(b, s, heads, d // heads).transpose(1, 2).float() for t in (q, k, v))
+                att = torch.matmul(q, k.transpose(-1, -2).contiguous()) * (1.0 / math.sqrt(d // heads))
+                mask = torch.ones(s, s, dtype=torch.bool, device=x.device).triu(1)
+                att = att.masked_fill(mask, float("-inf")).softmax(-1)
+                y = torch.matmul(att, v.contiguous()).to(x.dtype)
+                return self.proj(y.transpose(1, 2).reshape(b, s, d))
+
+            def forward(self, x):
+                x = x + self.attention(self.ln1(x))
+                return x + self.mlp(self.ln2(x))
+
+        class Model(nn.Module):
+            def __init__(self):
+                super().__init__()
+                self.wte = nn.Embedding(vocab, d)
+                self.wpe = nn.Embedding(context, d)
+                self.blocks = nn.ModuleList(Block() for _ in range(layers))
+                self.ln_f = nn.LayerNorm(d)
+
+            def forward(self, ids):
+                pos = torch.arange(ids.shape[1], device=ids.device)
+                x = self.wte(ids) + self.wpe(pos)
+                for block in self.blocks:
+                    x = block(x)
+                return F.linear(self.ln_f(x), self.wte.weight)
+
+        torch.manual_seed(0)
+        model = Model()
+        for module in model.modules():  # GPT-2's initialisation
+            if isinstance(module, (nn.Linear, nn.Embedding)):
+                nn.init.normal_(module.weight, 0.0, 0.02)
+            if isinstance(module, nn.Linear) and module.bias is not None:
+                nn.init.zeros_(module.bias)
+        qste.convert(model, include=["blocks.*.mlp.*"])
+        return model.to(device=device, dtype=torch.bfloat16)
+
+
+def config_steps(device):
+    """Configs 2 and 3 (fwd+bwd+step), reported beside the headline."""
+
+    import torch
+    import torch.nn.functional as F
+
+    import qste_amd as qste
+
+    out = {}
+    # config 2: 8192 tokens through the ReLU MLP, upstream gradient N(0,1)
+    model = relu_mlp(device=device)
+    coords = qste.QSTEOptimizer(model)
+    g = torch.Generator(device=device).manual_seed(0)
+    x = torch.randn(8192, 1024, generator=g, device=device).to(torch.bfloat16)
+    dy = torch.randn(8192, 1024, generator=g, device=device).to(torch.bfloat16)
+
+    def step2():
+        model(x).backward(dy)
+        coords.step()
+
+    ms = timed_wall(step2, 10)
+    flop = 6.0 * 8192 * (2 * 4096 * 1024)
+    out["cfg2_relu_mlp"] = {"ms_per_step": round(ms, 3), "tflops": round(flop / ms / 1e9, 2),
+                            "frac_of_mfma_peak": round(flop / (ms * 1e-3) / MFMA_BF16_PEAK, 4),
+                            "tokens": 8192, "d": 1024, "ffn": 4096}
+    del model, coords, x, dy
+    # config 3: GPT-2 small, batch 8 x 1024 random ids, AdamW + QSTEOptimizer
+    model = GPT2Small(device=device)
+    adam = torch.optim.AdamW(list(qste.continuous_parameters(model)), lr=1e-4)
+    coords = qste.QSTEOptimizer(model)
+    ids = torch.randint(0, 50257, (8, 1024), generator=g, device=device)
+
+    def step3():
+        logits = model(ids[:, :-1])
+        F.cross_entropy(logits.reshape(-1, logits.shape[-1]).float(), ids[:, 1:].reshape(-1)).backward()
+        adam.step()
+        coords.step()
+        adam.zero_grad(set_to_none=True)
+
+    ms = timed_wall(step3, 5)
+    tokens = 8 * 1023
+    mlp_flop = 6.0 * tokens * 12 * (2 * 3072 * 768)
+    out["cfg3_gpt2_small"] = {"ms_per_step": round(ms, 3), "tokens_per_s": round(tokens / ms * 1e3, 1),
+                              "mlp_fwd_bwd_flop": mlp_flop, "batch": 8, "seq": 1024,
+                              "note": "whole training step; MLPs QSTE with packed tanh-GELU, attention float"}
+    return out
+
+
+def timed_wall(fn, iters, warmup=2):
+    """Average milliseconds of ``fn`` by the host clock, synchronized around."""
+
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / iters * 1e3
+
+
 def timed_events(fn, iters, stream=None):
     """Average milliseconds of ``fn`` over ``iters`` calls, by HIP events."""
 
@@ -136,7 +279,6 @@ def gemm_kernels(T, d, ffn, device, iters=5):
 
     import torch
 
-    import oracle
     from qste_amd import kernels
 
     g = torch.Generator(device=device).manual_seed(7)
@@ -163,7 +305,6 @@ def gemm_kernels(T, d, ffn, device, iters=5):
     ms = timed_events(lambda: kernels.linear_backward(dy, xbits, off, xs, packed, scale, d, need_bias=False), iters)
     out["backward_call"] = {"ms": round(ms, 4), "tflops": round(2 * flop / ms / 1e9, 2),
                             "frac_of_mfma_peak": round(2 * flop / (ms * 1e-3) / MFMA_BF16_PEAK, 4)}
-    del oracle
     return out, flop
 
 
@@ -402,6 +543,7 @@ def main():
             packed_step()
         torch.cuda.synchronize()
         line["packed_activations"]["step_ms"] = round((time.perf_counter() - t1) / 3 * 1e3, 3)
+        line["configs"] = config_steps(device)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(d, ffn, args.cpu_tokens)
     print(json.dumps(line), flush=True)

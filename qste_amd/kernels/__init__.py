@@ -104,6 +104,12 @@ def _check_packed(packed: Tensor, columns: int, rows: int | None = None) -> Tens
 
 
 def _f32(t: Tensor | None) -> Tensor | None:
+    """``t`` as contiguous fp32 (a new tensor unless it already is one).
+
+    Bind the result to a name that lives until the C call returns: a
+    temporary passed straight to ``_ptr`` is freed before the launch, and the
+    caching allocator hands its block to the next allocation."""
+
     if t is None:
         return None
     return t.detach().to(torch.float32).contiguous()
@@ -181,8 +187,9 @@ def unpack_rows(packed: Tensor, columns: int, *, dtype: torch.dtype | None = Non
     device = _require_gpu(packed, row_scale)
     packed = _check_packed(packed, columns)
     out = torch.empty(packed.shape[0], int(columns), dtype=dtype, device=device)
+    row_scale_f32 = _f32(row_scale)  # held until the launch is queued
     code = _lib.load().qste_unpack_rows(
-        _ptr(packed), _ptr(_f32(row_scale)), _ptr(out), _dtype_code(out), packed.shape[0],
+        _ptr(packed), _ptr(row_scale_f32), _ptr(out), _dtype_code(out), packed.shape[0],
         int(columns), _stream(device))
     _lib.check(code, "unpack_rows")
     return out
@@ -226,8 +233,10 @@ def packed_linear_affine(inputs: Tensor, packed: Tensor, scale: Tensor, bias: Te
         raise ValueError("bias must have one entry per output row")
     flat = inputs.reshape(-1, columns).contiguous()
     out = torch.empty(flat.shape[0], rows, dtype=inputs.dtype, device=device)
+    scale_f32 = _f32(scale)  # held until the launch is queued
+    bias_f32 = _f32(bias)  # held until the launch is queued
     code = _lib.load().qste_packed_linear_affine(
-        _ptr(flat), _dtype_code(flat), _ptr(packed), _ptr(_f32(scale)), _ptr(_f32(bias)),
+        _ptr(flat), _dtype_code(flat), _ptr(packed), _ptr(scale_f32), _ptr(bias_f32),
         _ptr(out), flat.shape[0], rows, int(columns), _stream(device))
     _lib.check(code, "packed_linear_affine")
     return out.view(*inputs.shape[:-1], rows)
@@ -246,8 +255,9 @@ def packed_transpose(inputs: Tensor, packed: Tensor, columns: int,
         raise ValueError("transpose row scale must have one entry per packed row")
     flat = inputs.reshape(-1, rows).contiguous()
     out = torch.empty(flat.shape[0], int(columns), dtype=inputs.dtype, device=device)
+    row_scale_f32 = _f32(row_scale)  # held until the launch is queued
     code = _lib.load().qste_packed_transpose(
-        _ptr(flat), _dtype_code(flat), _ptr(packed), _ptr(_f32(row_scale)), _ptr(out),
+        _ptr(flat), _dtype_code(flat), _ptr(packed), _ptr(row_scale_f32), _ptr(out),
         flat.shape[0], rows, int(columns), _stream(device))
     _lib.check(code, "packed_transpose")
     return out.view(*inputs.shape[:-1], int(columns))
@@ -268,8 +278,9 @@ def evidence_from_packed(grad: Tensor, packed: Tensor, columns: int,
         raise ValueError("evidence row scale must have one entry per sample")
     grad = grad.contiguous()
     out = torch.empty(rows, int(columns), dtype=torch.float32, device=device)
+    row_scale_f32 = _f32(row_scale)  # held until the launch is queued
     code = _lib.load().qste_evidence_from_packed(
-        _ptr(grad), _dtype_code(grad), _ptr(packed), _ptr(_f32(row_scale)), _ptr(out), samples,
+        _ptr(grad), _dtype_code(grad), _ptr(packed), _ptr(row_scale_f32), _ptr(out), samples,
         rows, int(columns), _stream(device))
     _lib.check(code, "evidence_from_packed")
     return out
@@ -311,9 +322,12 @@ def linear_backward(grad: Tensor, packed_x: Tensor, x_offset: Tensor, x_scale: T
     grad_bias = torch.empty(rows, dtype=torch.float32, device=device) if need_bias else None
     nbytes = lib.qste_linear_backward_workspace_bytes(samples, rows, int(columns))
     work = _workspace(nbytes, device)
+    x_offset_f32 = _f32(x_offset)  # held until the launch is queued
+    x_scale_f32 = _f32(x_scale)  # held until the launch is queued
+    scale_f32 = _f32(scale)  # held until the launch is queued
     code = lib.qste_linear_backward(
-        _ptr(grad), _dtype_code(grad), _ptr(packed_x), _ptr(_f32(x_offset)), _ptr(_f32(x_scale)),
-        _ptr(packed_w), _ptr(_f32(scale)), _ptr(dx), _ptr(evidence), _ptr(grad_scale),
+        _ptr(grad), _dtype_code(grad), _ptr(packed_x), _ptr(x_offset_f32), _ptr(x_scale_f32),
+        _ptr(packed_w), _ptr(scale_f32), _ptr(dx), _ptr(evidence), _ptr(grad_scale),
         _ptr(grad_bias), samples, rows, int(columns), _ptr(work), work.numel(), _stream(device))
     _lib.check(code, "linear_backward")
     return dx, evidence, grad_scale, grad_bias
@@ -546,9 +560,10 @@ def smooth_backward(grad: Tensor, payload: Tensor, scale: Tensor) -> Tensor:
         raise ValueError("payload/scale do not match the gradient's shape")
     payload = _aligned(payload)
     out = torch.empty_like(grad)
+    scale_f32 = _f32(scale)  # held until the launch is queued
     code = _lib.load().qste_smooth_backward(
         _ptr(grad), _dtype_code(grad), _ptr(payload), 1 if payload.dtype == torch.uint8 else 0,
-        _ptr(_f32(scale)), _ptr(out), rows, cols, _stream(device))
+        _ptr(scale_f32), _ptr(out), rows, cols, _stream(device))
     _lib.check(code, "smooth_backward")
     return out
 
@@ -579,8 +594,9 @@ def packed_embedding(ids: Tensor, packed: Tensor, scale: Tensor, columns: int) -
     flat = _check_ids(ids, rows)
     out_dtype = scale.dtype if scale.dtype in _DTYPES else torch.float32
     out = torch.empty(flat.numel(), int(columns), dtype=out_dtype, device=device)
+    scale_f32 = _f32(scale)  # held until the launch is queued
     code = _lib.load().qste_packed_embedding(
-        _ptr(flat), flat.numel(), _ptr(packed), _ptr(_f32(scale)), _ptr(out), _dtype_code(out), rows,
+        _ptr(flat), flat.numel(), _ptr(packed), _ptr(scale_f32), _ptr(out), _dtype_code(out), rows,
         int(columns), _stream(device))
     _lib.check(code, "packed_embedding")
     return out.view(*ids.shape, int(columns)).to(scale.dtype)
@@ -605,8 +621,9 @@ def embedding_backward(ids: Tensor, grad: Tensor, packed: Tensor, scale: Tensor,
     grad_scale = torch.empty(rows, dtype=torch.float32, device=device)
     lib = _lib.load()
     ws = _workspace(lib.qste_embedding_backward_workspace_bytes(flat.numel(), rows), device)
+    scale_f32 = _f32(scale)  # held until the launch is queued
     code = lib.qste_embedding_backward(
-        _ptr(flat), flat.numel(), _ptr(g), _dtype_code(g), _ptr(packed), _ptr(_f32(scale)),
+        _ptr(flat), flat.numel(), _ptr(g), _dtype_code(g), _ptr(packed), _ptr(scale_f32),
         _ptr(evidence), _ptr(grad_scale), rows, int(columns), _ptr(ws), ws.numel(), _stream(device))
     _lib.check(code, "embedding_backward")
     return evidence, grad_scale

@@ -181,3 +181,30 @@ def test_full_size_step_properties():
         assert torch.equal(a.view(torch.uint8) if a.dtype == torch.float16 else a,
                            b.view(torch.uint8) if b.dtype == torch.float16 else b)
     assert outs[0][5] == outs[1][5]
+
+
+def test_bf16_parameters_reach_the_kernels_intact():
+    """Regression: a bf16 scale and bias (a model cast with .to(bfloat16)) are
+    converted to fp32 copies for the C call; those copies must outlive the
+    launch, or the allocator reuses one's block for the next (the bias) and
+    the kernel reads the wrong values."""
+
+    import qste_amd as qste
+
+    torch.manual_seed(0)
+    model = qste.convert(torch.nn.Sequential(torch.nn.Linear(256, 384)))[0].to(device="cuda", dtype=torch.bfloat16)
+    x = torch.randn(64, 256, device="cuda").to(torch.bfloat16)
+    sign = torch.where(model.surface.coordinate >= 0, 1.0, -1.0).double()
+    ref = (x.double() @ sign.t()) * model.scale.detach().double() + model.bias.detach().double()
+    with torch.no_grad():
+        y = model(x)
+    # against the exact product rounded to the output dtype, as the bf16
+    # forward parity is stated
+    ref16 = ref.to(torch.bfloat16).double()
+    rel = float((y.double() - ref16).norm() / ref16.norm())
+    assert rel <= 1e-3, rel
+    dy = torch.randn(64, 384, device="cuda").to(torch.bfloat16)
+    xr = x.clone().requires_grad_(True)
+    model(xr).backward(dy)
+    ref_dx = dy.double() @ (sign * model.scale.detach().double()[:, None])
+    assert float((xr.grad.double() - ref_dx).norm() / ref_dx.norm()) <= 5e-3

@@ -1,0 +1,123 @@
+"""The BASELINE configurations 2 and 3 end to end, at their real shapes.
+
+* config 2 -- the converted ReLU MLP (1024 -> 4096 -> 1024, bf16, 8192
+  tokens): each layer's forward against a float64 product over the same signs
+  and scales rounded to bf16 (rel-L2 <= 1e-3), the input gradient of the whole
+  block against float32 autograd through the dense weights, and one
+  fwd+bwd+coordinate step that moves the coordinates with packed == pack(coord);
+* config 3 -- GPT-2 small (12 layers, d=768, vocab 50257, batch 8 x 1024),
+  MLPs converted: one AdamW + QSTEOptimizer training step with a finite loss,
+  every MLP surface moved and its packed signs consistent, attention weights
+  updated, and the first MLP layer's forward at the real shape against float64.
+
+The workloads are bench.py's own (``relu_mlp``, ``GPT2Small``).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def _rel(a, b):
+    a, b = a.double(), b.double()
+    return float((a - b).norm() / b.norm())
+
+
+def _dense(layer):
+    sign = torch.where(layer.surface.coordinate >= 0, 1.0, -1.0).double()
+    return sign * layer.scale.detach().double()[:, None]
+
+
+def _reference_linear(layer, x):
+    y = x.double() @ _dense(layer).t()
+    if layer.bias is not None:
+        y = y + layer.bias.detach().double()
+    return y
+
+
+def _packed_of(coord):
+    from qste_amd import kernels
+
+    return kernels.pack_coordinate(coord)
+
+
+def test_config2_relu_mlp():
+    import qste_amd as qste
+    from bench import relu_mlp
+
+    model = relu_mlp(device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(0)
+    x = torch.randn(8192, 1024, generator=g, device=DEV).to(torch.bfloat16)
+    dy = torch.randn(8192, 1024, generator=g, device=DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        h = model[0](x)
+        ref_h = _reference_linear(model[0], x)
+        assert _rel(h, ref_h.to(torch.bfloat16)) <= 1e-3
+        y = model[2](torch.relu(h))
+        assert _rel(y, _reference_linear(model[2], torch.relu(h)).to(torch.bfloat16)) <= 1e-3
+
+    # input gradient of the block against float32 autograd through dense weights
+    xr = x.float().requires_grad_(True)
+    w1, w2 = _dense(model[0]).float(), _dense(model[2]).float()
+    b1, b2 = model[0].bias.detach().float(), model[2].bias.detach().float()
+    (F.linear(torch.relu(F.linear(xr, w1, b1)), w2, b2) * dy.float()).sum().backward()
+
+    coords = qste.QSTEOptimizer(model)
+    surfaces = qste.surfaces(model)
+    before = [s.coordinate.clone() for s in surfaces]
+    xq = x.clone().requires_grad_(True)
+    model(xq).backward(dy)
+    assert _rel(xq.grad, xr.grad) <= 1.5e-2
+    flips = coords.step()
+    assert flips > 0
+    for s, b in zip(surfaces, before):
+        assert not torch.equal(s.coordinate, b)
+        assert torch.equal(s.packed_sign, _packed_of(s.coordinate))
+        assert int(s.coordinate.abs().max()) <= 127
+
+
+def test_config3_gpt2_small_training_step():
+    import qste_amd as qste
+    from bench import GPT2Small
+
+    model = GPT2Small(device=DEV)
+    mlp_layers = [m for m in model.modules() if isinstance(m, qste.QSTELinear)]
+    assert len(mlp_layers) == 24
+    assert all(isinstance(b.mlp[1], qste.nn.GELU) for b in model.blocks)
+    adam = torch.optim.AdamW(list(qste.continuous_parameters(model)), lr=1e-3)
+    coords = qste.QSTEOptimizer(model)
+    g = torch.Generator(device=DEV).manual_seed(1)
+    ids = torch.randint(0, 50257, (8, 1024), generator=g, device=DEV)
+
+    # the first MLP layer at its real shape (8192 x 768 -> 3072)
+    with torch.no_grad():
+        x = torch.randn(8192, 768, generator=g, device=DEV).to(torch.bfloat16)
+        fc = model.blocks[0].mlp[0]
+        assert _rel(fc(x), _reference_linear(fc, x).to(torch.bfloat16)) <= 1e-3
+
+    before = [s.coordinate.clone() for s in qste.surfaces(model)]
+    qkv_before = model.blocks[0].qkv.weight.detach().clone()
+    logits = model(ids[:, :-1])
+    loss = F.cross_entropy(logits.reshape(-1, logits.shape[-1]).float(), ids[:, 1:].reshape(-1))
+    assert torch.isfinite(loss)
+    assert abs(float(loss) - 10.8) < 1.5  # ~log(50257) at random init
+    loss.backward()
+    adam.step()
+    flips = coords.step()
+    assert flips > 0
+    for s, b in zip(qste.surfaces(model), before):
+        assert not torch.equal(s.coordinate, b)
+        assert torch.equal(s.packed_sign, _packed_of(s.coordinate))
+    assert not torch.equal(model.blocks[0].qkv.weight, qkv_before)
