@@ -52,7 +52,8 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int WAVES = 8;
 constexpr int THREADS = 64 * WAVES;
 constexpr int CHUNK_K = 512;  // columns per wave chunk (4 lane groups x 128)
-constexpr int DEPTH = 16;     // weight loads in flight per wave (all of a wave's, for K <= 8192)
+constexpr int DEPTH = 2;      // weight loads in flight per wave (swept 2-16: fewer requests per wave keep the
+                              // CUs' streams interleaved; 2 is fastest at M = 4 and 16)
 constexpr uint32_t kRsrcWord3 = 0x00020000u;
 constexpr uint32_t kOob = 0x80000000u;  // an offset past every buffer: reads zero
 
@@ -358,7 +359,7 @@ __device__ __forceinline__ f32x4 mma_f8f4(const i32x8& a, u32x4 b, f32x4 c) {
 constexpr int F4_WAVES = 4;
 constexpr int F4_THREADS = 64 * F4_WAVES;
 constexpr int F4_CHUNKS = FP4_MAX_K / CHUNK_K / F4_WAVES;  // chunks per wave
-constexpr int F4_DEPTH = 16;                               // weight loads in flight per wave
+constexpr int F4_DEPTH = 8;   // weight loads in flight per wave (swept: 8 beats 4-6 and 12-28)
 
 template <int NBW>
 struct SmemF4 {
