@@ -14,6 +14,8 @@ inside ``loss.backward()``.
 
 from __future__ import annotations
 
+import weakref
+
 import torch
 from torch import Tensor
 from torch.autograd import Function
@@ -38,13 +40,37 @@ def encode_activation(flat: Tensor) -> tuple[Tensor, Tensor]:
     return packed, torch.stack((offset, scale))
 
 
+# Layers that read the same input in one forward (a SwiGLU's gate and up
+# projections) share its encoding: the last input encoded, held weakly, with
+# its version counter and address.  Any backward clears it, so a reuse never
+# spans a training step.
+_last_encoding: tuple | None = None
+
+
+def _encoding_of(inputs: Tensor, flat: Tensor, columns: int) -> tuple[Tensor, Tensor]:
+    global _last_encoding
+    key = (inputs._version, inputs.data_ptr(), tuple(inputs.shape), inputs.dtype, columns)
+    if _last_encoding is not None:
+        ref, last_key, payload, aux = _last_encoding
+        if ref() is inputs and last_key == key:
+            return payload, aux
+    payload, aux = encode_activation(flat)
+    _last_encoding = (weakref.ref(inputs), key, payload, aux)
+    return payload, aux
+
+
+def forget_encodings() -> None:
+    global _last_encoding
+    _last_encoding = None
+
+
 class QSTELinearFn(Function):
     @staticmethod
     def forward(ctx, inputs, packed, scale, bias, surface: Surface):
         columns = surface.columns
         output = kernels.packed_linear_affine(inputs, packed, scale, bias, columns)
         flat = inputs.reshape(-1, columns)
-        payload, aux = encode_activation(flat)
+        payload, aux = _encoding_of(inputs, flat, columns)
         ctx.save_for_backward(payload, aux, packed, scale)
         ctx.surface = surface
         ctx.columns = columns
@@ -55,6 +81,7 @@ class QSTELinearFn(Function):
 
     @staticmethod
     def backward(ctx, grad_output):
+        forget_encodings()
         payload, aux, packed, scale = ctx.saved_tensors
         grad2 = grad_output.reshape(-1, grad_output.shape[-1])
         grad_inputs, evidence, grad_scale, grad_bias = kernels.linear_backward(

@@ -533,3 +533,34 @@ def test_export_packed_turns_embeddings_into_packed_embeddings(fake):
     assert isinstance(exported[0], qste.PackedEmbedding) and isinstance(exported[1], qste.PackedLinear)
     with torch.no_grad():
         assert torch.allclose(exported(ids), expected, atol=1e-5)
+
+
+def test_layers_reading_one_input_share_its_encoding(fake, monkeypatch):
+    """A SwiGLU's gate and up projections read the same x: it is encoded once
+    per forward, and again after a backward (no reuse across steps)."""
+
+    import qste_amd as qste
+    from qste_amd import kernels
+
+    calls = []
+    original = kernels.pack_affine_rows
+    monkeypatch.setattr(kernels, "pack_affine_rows", lambda v: calls.append(v.shape) or original(v))
+    model = qste.convert(nn.ModuleDict({"gate": nn.Linear(8, 16), "up": nn.Linear(8, 16),
+                                        "down": nn.Linear(16, 8)}))
+    x = torch.randn(5, 8)
+
+    def forward():
+        return model["down"](torch.nn.functional.silu(model["gate"](x)) * model["up"](x))
+
+    out = forward()
+    assert calls == [(5, 8), (5, 16)]
+    out.sum().backward()
+    calls.clear()
+    forward()
+    assert calls == [(5, 8), (5, 16)]
+    # an in-place change of x invalidates the shared encoding
+    calls.clear()
+    model["gate"](x)
+    x.add_(1.0)
+    model["up"](x)
+    assert calls == [(5, 8), (5, 8)]
