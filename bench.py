@@ -50,6 +50,7 @@ def parse():
     ap.add_argument("--ffn", type=int, default=14336)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip per-kernel, step and GEMV timing")
+    ap.add_argument("--no-configs", action="store_true", help="skip the config 2 and config 3 step lines")
     ap.add_argument("--cpu-tokens", type=int, default=256)
     ap.add_argument("--pmc-calibrate", action="store_true",
                     help="one launch of each GEMM kind at the gate-layer shape plus a plain device copy of "
@@ -543,7 +544,8 @@ def main():
             packed_step()
         torch.cuda.synchronize()
         line["packed_activations"]["step_ms"] = round((time.perf_counter() - t1) / 3 * 1e3, 3)
-        line["configs"] = config_steps(device)
+        if not args.no_configs:
+            line["configs"] = config_steps(device)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(d, ffn, args.cpu_tokens)
     print(json.dumps(line), flush=True)

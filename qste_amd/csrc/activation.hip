@@ -379,6 +379,12 @@ __device__ __forceinline__ void value_and_derivative(float x, float a, float& y,
 // specialised instantiations).
 constexpr int kDynamic = -1;
 
+// Kinds whose retained derivative reads the output y (the others need only x).
+__host__ __device__ constexpr bool derivative_reads_y(int kind) {
+  return kind == QSTE_ACT_TANH || kind == QSTE_ACT_SIGMOID || kind == QSTE_ACT_ELU || kind == QSTE_ACT_CELU ||
+         kind == QSTE_ACT_SELU;
+}
+
 template <int KIND, int DT>
 __device__ __forceinline__ void value_and_derivative_any(int kind, float x, float a, float& y, float& d) {
   if constexpr (KIND != kDynamic) {
@@ -471,7 +477,13 @@ __device__ __forceinline__ void smooth_row(const typename Elem<DT>::T* __restric
     float xv[8], yv[8];
     Chunk<DT>::load(x + base + q * 8, n, whole, xv);
     if (mode == 1) {
-      Chunk<DT>::load(y + base + q * 8, n, whole, yv);
+      const bool reads_y = KIND == kDynamic ? derivative_reads_y(kind) : derivative_reads_y(KIND);
+      if (reads_y) {
+        Chunk<DT>::load(y + base + q * 8, n, whole, yv);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) yv[j] = 0.0f;
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float v = derivative_any<KIND, DT>(kind, xv[j], yv[j], a);
@@ -679,8 +691,9 @@ int smooth_shapes(const void* x, void* y, const float* provided, int mode, Smoot
   }
 }
 
-// GELU and SiLU (the MLP activations) computing their own value get kernels
-// of their own; every other case runs the run-time-kind kernel.
+// The MLP activations get kernels of their own: GELU and SiLU computing their
+// value, tanh-GELU and Hardswish deriving from torch's (which they cannot
+// reproduce bit for bit); every other case runs the run-time-kind kernel.
 template <int DT>
 int smooth_dispatch(const void* x, void* y, const float* provided, int mode, SmoothParams p, void* payload,
                     float* scale, int64_t rows, int64_t cols, hipStream_t s) {
@@ -688,6 +701,10 @@ int smooth_dispatch(const void* x, void* y, const float* provided, int mode, Smo
     return smooth_shapes<DT, QSTE_ACT_SILU>(x, y, provided, mode, p, payload, scale, rows, cols, s);
   if (mode == 0 && p.kind == QSTE_ACT_GELU)
     return smooth_shapes<DT, QSTE_ACT_GELU>(x, y, provided, mode, p, payload, scale, rows, cols, s);
+  if (mode == 1 && p.kind == QSTE_ACT_GELU_TANH)
+    return smooth_shapes<DT, QSTE_ACT_GELU_TANH>(x, y, provided, mode, p, payload, scale, rows, cols, s);
+  if (mode == 1 && p.kind == QSTE_ACT_HARDSWISH)
+    return smooth_shapes<DT, QSTE_ACT_HARDSWISH>(x, y, provided, mode, p, payload, scale, rows, cols, s);
   return smooth_shapes<DT, kDynamic>(x, y, provided, mode, p, payload, scale, rows, cols, s);
 }
 
