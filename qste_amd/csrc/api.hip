@@ -36,7 +36,7 @@ int mfma_backward_pair(const void*, int, const uint8_t*, int64_t, const uint16_t
                        const uint16_t*, const uint8_t*, void*, int64_t, int64_t, int64_t, const float*,
                        const float*, float*, hipStream_t);
 int launch_transpose_bits(const uint8_t*, uint8_t*, int64_t, int64_t, int64_t, int64_t, hipStream_t);
-int launch_f32_to_bf16(const float*, uint16_t*, int64_t, int64_t, hipStream_t);
+int launch_f32_to_16(const float*, uint16_t*, int64_t, int64_t, int, hipStream_t);
 int gemv_linear_forward(const void*, int, const uint8_t*, const float*, const float*, void*, int64_t,
                         int64_t, int64_t, hipStream_t);
 }  // namespace qste
@@ -241,8 +241,8 @@ int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x, con
       const int64_t pb = (cols + 7) / 8;
       if ((rc = launch_transpose_bits(packed_w, w_t, rows, cols, pb, l.w_t_pitch, s))) return rc;
       if ((rc = launch_transpose_bits(packed_x, x_t, samples, cols, pb, l.x_t_pitch, s))) return rc;
-      if ((rc = launch_f32_to_bf16(scale, s16, rows, (rows + 63) / 64 * 64, s))) return rc;
-      if ((rc = launch_f32_to_bf16(x_scale, xs16, samples, (samples + 63) / 64 * 64, s))) return rc;
+      if ((rc = launch_f32_to_16(scale, s16, rows, (rows + 63) / 64 * 64, dtype, s))) return rc;
+      if ((rc = launch_f32_to_16(x_scale, xs16, samples, (samples + 63) / 64 * 64, dtype, s))) return rc;
       rc = mfma_backward_pair(dy, dtype, x_t, l.x_t_pitch, xs16, evidence, w_t, l.w_t_pitch, s16, packed_w, dx,
                               samples, rows, cols, v, scale, gs_part, s);
       if (rc == 0) return launch_sum_partials(gs_part, mfma_evidence_tiles(cols), rows, grad_scale, s);

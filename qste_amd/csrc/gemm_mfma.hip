@@ -1,4 +1,4 @@
-// bf16 MFMA products over packed signs for gfx950 (CDNA4).
+// bf16 / fp16 MFMA products over packed signs for gfx950 (CDNA4).
 //
 // All three products of a binary linear layer are GEMMs whose one operand
 // is a matrix of +-1 (times a per-k scale in the backward ones) held as
@@ -122,6 +122,40 @@ __device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// The same products on fp16 operands: the 16-bit fragments are only
+// reinterpreted (a sign insertion into a nonnegative 16-bit value is the same
+// bit operation in both formats); only the +1 pattern, the MFMA and the
+// rounding of scales and outputs depend on DT.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+template <int DT>
+__device__ __forceinline__ f32x16 mma_dt(bf16x8 a, bf16x8 b, f32x16 c) {
+  if constexpr (DT == QSTE_F16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  } else {
+    return mma(a, b, c);
+  }
+}
+
+// a pair of +1.0 in DT (bf16 0x3F80, fp16 0x3C00), held in a VGPR
+template <int DT>
+__device__ __forceinline__ uint32_t one_pair() {
+  if constexpr (DT == QSTE_F16) {
+    uint32_t v;
+    asm volatile("v_mov_b32 %0, 0x3C003C00" : "=v"(v));
+    return v;
+  } else {
+    return bf16_one_pair();
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ uint16_t round16(float f) {
+  if constexpr (DT == QSTE_F16) return f32_to_f16(f);
+  else return f32_to_bf16(f);
+}
+
 // Workgroup -> output tile.  Consecutive workgroup ids land on different
 // XCDs (round-robin), so ids are first regrouped so each XCD gets a
 // contiguous range, then walked in column-major groups of 2 M-tiles, so the
@@ -209,7 +243,7 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 // One output tile; the LDS stages are the caller's (one __shared__ array per
 // stage, so that the compiler tracks each stage's direct loads separately
 // and waits only where this code says).
-template <int AKIND, int BKIND, int EPI>
+template <int AKIND, int BKIND, int EPI, int DT>
 __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0, uint8_t* A1, uint8_t* A2,
                                           uint8_t* A3, uint8_t* B0, uint8_t* B1, uint8_t* B2, uint8_t* B3,
                                           uint16_t* Sc) {
@@ -223,7 +257,7 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   int tm, tn;
   tile_of(pid, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
-  const uint32_t one = bf16_one_pair();
+  const uint32_t one = one_pair<DT>();
   const int nk = static_cast<int>((p.K + BK - 1) / BK);  // K % BK != 0 only for A as rows of K
 
   // A (rows of M, K contiguous): the buffer starts at row m0, so rows past
@@ -322,7 +356,7 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
 #pragma unroll
         for (int i = 0; i < 4; ++i) Bs[(4 * g + i) * LDB_N + k] = static_cast<uint8_t>(neg >> (8 * i));
       }
-      if (tid < BK) Ss[tid] = f32_to_bf16(p.kscale ? __uint_as_float(bsv) : balt);
+      if (tid < BK) Ss[tid] = round16<DT>(p.kscale ? __uint_as_float(bsv) : balt);
     }
   };
 
@@ -415,13 +449,13 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   auto mfma_row = [&](int s, int q) {
 #pragma unroll
     for (int i = 4 * q; i < 4 * q + 4; ++i)
-      acc[i / NBN][i % NBN] = mma(a[s & 1][i / NBN], b[s & 1][i % NBN], acc[i / NBN][i % NBN]);
+      acc[i / NBN][i % NBN] = mma_dt<DT>(a[s & 1][i / NBN], b[s & 1][i % NBN], acc[i / NBN][i % NBN]);
   };
   auto mfmas = [&](int s) {
 #pragma unroll
     for (int mb = 0; mb < MBN; ++mb)
 #pragma unroll
-      for (int nb = 0; nb < NBN; ++nb) acc[mb][nb] = mma(a[s & 1][mb], b[s & 1][nb], acc[mb][nb]);
+      for (int nb = 0; nb < NBN; ++nb) acc[mb][nb] = mma_dt<DT>(a[s & 1][mb], b[s & 1][nb], acc[mb][nb]);
   };
 
   // K step `it` on stage (As, Bs, Ss); substep 0's fragments are in buffer 0.
@@ -618,7 +652,7 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
           const float lo = odd ? recv : v0;
           const float hi = odd ? v1 : recv;
           const uint32_t word =
-              static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+              static_cast<uint32_t>(round16<DT>(lo)) | (static_cast<uint32_t>(round16<DT>(hi)) << 16);
           const int row = 8 * (r >> 2) + 4 * kg + (r & 3) + (odd ? 1 : 0) - EPR * h;
           *reinterpret_cast<uint32_t*>(stg + row * EPL + 2 * (32 * nb + (l32 & ~1))) = word;
         }
@@ -664,11 +698,11 @@ struct StageSizes {
   __shared__ __attribute__((aligned(16))) uint8_t B3[BSZ];       \
   __shared__ __attribute__((aligned(16))) uint16_t Sc[SSZ];
 
-template <int AKIND, int BKIND, int EPI>
+template <int AKIND, int BKIND, int EPI, int DT>
 __global__ __launch_bounds__(THREADS, 1) void wide_kernel(Params p) {
   using SZ = StageSizes<AKIND, BKIND>;
   QSTE_WIDE_STAGES(SZ::a, SZ::b, SZ::s)
-  wide_tile<AKIND, BKIND, EPI>(p, blockIdx.x, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
+  wide_tile<AKIND, BKIND, EPI, DT>(p, blockIdx.x, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
 }
 
 // The two large products of a layer's backward in one launch: evidence
@@ -676,13 +710,15 @@ __global__ __launch_bounds__(THREADS, 1) void wide_kernel(Params p) {
 // of one product is filled by the other instead of leaving CUs idle.  Both
 // take their signs as transposed copies (bits along K) with bf16 per-k
 // scales, prepared by the caller.
+template <int DT>
 __global__ __launch_bounds__(THREADS, 1) void backward_pair_kernel(Params pe, Params pd, int tiles_e) {
   QSTE_WIDE_STAGES(A_STAGE_K, B_STAGE, 4 * BK)
   if (static_cast<int>(blockIdx.x) < tiles_e)
-    wide_tile<A_ROWS_K, B_BITS_ALONG_K_SCALED, EPI_EVIDENCE>(pe, blockIdx.x, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
+    wide_tile<A_ROWS_K, B_BITS_ALONG_K_SCALED, EPI_EVIDENCE, DT>(pe, blockIdx.x, A0, A1, A2, A3, B0, B1, B2, B3,
+                                                                 Sc);
   else
-    wide_tile<A_ROWS_M, B_BITS_ALONG_K_SCALED, EPI_PLAIN>(pd, blockIdx.x - tiles_e, A0, A1, A2, A3, B0, B1, B2,
-                                                          B3, Sc);
+    wide_tile<A_ROWS_M, B_BITS_ALONG_K_SCALED, EPI_PLAIN, DT>(pd, blockIdx.x - tiles_e, A0, A1, A2, A3, B0, B1, B2,
+                                                              B3, Sc);
 }
 #undef QSTE_WIDE_STAGES
 }  // namespace wide
@@ -694,6 +730,9 @@ __global__ __launch_bounds__(THREADS, 1) void backward_pair_kernel(Params pe, Pa
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// bf16 and fp16 take the MFMA path (fp32 stays on the fp32 SIMT kernel)
+static bool mfma_dtype(int dtype) { return dtype == QSTE_BF16 || dtype == QSTE_F16; }
+
 // Buffer offsets are 32-bit: every operand must stay under 4 GiB.
 static bool fits32(int64_t bytes) { return bytes < (int64_t{1} << 32); }
 
@@ -702,16 +741,16 @@ static int wide_grid(int64_t M, int64_t N) {
 }
 
 static bool forward_ok(const void* x, int dtype, const uint8_t* packed, int64_t m, int64_t rows, int64_t cols) {
-  return dtype == QSTE_BF16 && cols % 64 == 0 && cols > 0 && m > 0 && rows > 0 && aligned16(x) &&
+  return mfma_dtype(dtype) && cols % 64 == 0 && cols > 0 && m > 0 && rows > 0 && aligned16(x) &&
          aligned16(packed) && fits32(m * cols * 2) && fits32(rows * cols / 8);
 }
 static bool dgrad_ok(const void* dy, int dtype, const uint8_t* packed, int64_t m, int64_t rows, int64_t cols) {
-  return dtype == QSTE_BF16 && cols % 64 == 0 && rows % 64 == 0 && rows > 0 && cols > 0 && m > 0 &&
+  return mfma_dtype(dtype) && cols % 64 == 0 && rows % 64 == 0 && rows > 0 && cols > 0 && m > 0 &&
          aligned16(dy) && aligned16(packed) && fits32(m * rows * 2) && fits32(rows * cols / 8);
 }
 static bool evidence_ok(const void* dy, int dtype, const uint8_t* packed_x, int64_t samples, int64_t rows,
                         int64_t cols) {
-  return dtype == QSTE_BF16 && cols % 64 == 0 && rows % 64 == 0 && rows > 0 && cols > 0 && samples > 0 &&
+  return mfma_dtype(dtype) && cols % 64 == 0 && rows % 64 == 0 && rows > 0 && cols > 0 && samples > 0 &&
          aligned16(dy) && aligned16(packed_x) && fits32(samples * rows * 2) && fits32(samples * cols / 8);
 }
 
@@ -755,8 +794,12 @@ int mfma_linear_forward(const void* x, int dtype, const uint8_t* packed, const f
   p.lda = cols; p.pb = cols / 8;
   p.a_rows = m; p.bit_rows = rows;
   p.n_scale = scale; p.n_bias = bias;
-  mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD>
-      <<<wide_grid(m, rows), mfma::wide::THREADS, 0, stream>>>(p);
+  if (dtype == QSTE_F16)
+    mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD, QSTE_F16>
+        <<<wide_grid(m, rows), mfma::wide::THREADS, 0, stream>>>(p);
+  else
+    mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD, QSTE_BF16>
+        <<<wide_grid(m, rows), mfma::wide::THREADS, 0, stream>>>(p);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -764,8 +807,12 @@ int mfma_linear_dgrad(const void* dy, int dtype, const uint8_t* packed, const fl
                       int64_t m, int64_t rows, int64_t cols, hipStream_t stream) {
   if (!dgrad_ok(dy, dtype, packed, m, rows, cols)) return 1;
   const mfma::Params p = dgrad_params(dy, packed, row_scale, dx, m, rows, cols);
-  mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_N, mfma::EPI_PLAIN>
-      <<<wide_grid(m, cols), mfma::wide::THREADS, 0, stream>>>(p);
+  if (dtype == QSTE_F16)
+    mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_N, mfma::EPI_PLAIN, QSTE_F16>
+        <<<wide_grid(m, cols), mfma::wide::THREADS, 0, stream>>>(p);
+  else
+    mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_N, mfma::EPI_PLAIN, QSTE_BF16>
+        <<<wide_grid(m, cols), mfma::wide::THREADS, 0, stream>>>(p);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -777,15 +824,19 @@ int mfma_evidence(const void* dy, int dtype, const uint8_t* packed_x, const floa
   if (!evidence_ok(dy, dtype, packed_x, samples, rows, cols)) return 1;
   const mfma::Params p =
       evidence_params(dy, packed_x, x_scale, ev, samples, rows, cols, m_add, m_scale, w_bits, gs_partial);
-  mfma::wide::wide_kernel<mfma::A_ROWS_K, mfma::B_BITS_ALONG_N, mfma::EPI_EVIDENCE>
-      <<<wide_grid(rows, cols), mfma::wide::THREADS, 0, stream>>>(p);
+  if (dtype == QSTE_F16)
+    mfma::wide::wide_kernel<mfma::A_ROWS_K, mfma::B_BITS_ALONG_N, mfma::EPI_EVIDENCE, QSTE_F16>
+        <<<wide_grid(rows, cols), mfma::wide::THREADS, 0, stream>>>(p);
+  else
+    mfma::wide::wide_kernel<mfma::A_ROWS_K, mfma::B_BITS_ALONG_N, mfma::EPI_EVIDENCE, QSTE_BF16>
+        <<<wide_grid(rows, cols), mfma::wide::THREADS, 0, stream>>>(p);
   return static_cast<int>(hipGetLastError());
 }
 
 // Whether mfma_backward_pair takes a call (workspace copies are 256-byte
 // aligned, so only the caller's operands are checked here).
 bool mfma_pair_ok(const void* dy, int dtype, int64_t samples, int64_t rows, int64_t cols) {
-  return dtype == QSTE_BF16 && cols % 64 == 0 && rows % 64 == 0 && rows > 0 && cols > 0 && samples > 0 &&
+  return mfma_dtype(dtype) && cols % 64 == 0 && rows % 64 == 0 && rows > 0 && cols > 0 && samples > 0 &&
          aligned16(dy) && fits32(samples * rows * 2) && fits32(samples * cols / 8) && fits32(rows * cols / 8);
 }
 
@@ -820,7 +871,10 @@ int mfma_backward_pair(const void* dy, int dtype, const uint8_t* x_t, int64_t x_
   pd.lda = rows; pd.pb = w_t_pitch;
   pd.a_rows = samples; pd.bit_rows = cols;
   const int te = wide_grid(rows, cols), td = wide_grid(samples, cols);
-  mfma::wide::backward_pair_kernel<<<te + td, mfma::wide::THREADS, 0, stream>>>(pe, pd, te);
+  if (dtype == QSTE_F16)
+    mfma::wide::backward_pair_kernel<QSTE_F16><<<te + td, mfma::wide::THREADS, 0, stream>>>(pe, pd, te);
+  else
+    mfma::wide::backward_pair_kernel<QSTE_BF16><<<te + td, mfma::wide::THREADS, 0, stream>>>(pe, pd, te);
   return static_cast<int>(hipGetLastError());
 }
 

@@ -233,10 +233,11 @@ __global__ __launch_bounds__(256) void transpose_bits_kernel(const uint8_t* __re
   }
 }
 
-__global__ void f32_to_bf16_kernel(const float* __restrict__ in, uint16_t* __restrict__ out, int64_t n,
-                                   int64_t padded) {
+template <int DT>
+__global__ void f32_to_16_kernel(const float* __restrict__ in, uint16_t* __restrict__ out, int64_t n,
+                                 int64_t padded) {
   const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-  if (i < padded) out[i] = i < n ? f32_to_bf16(in[i]) : 0;
+  if (i < padded) out[i] = i < n ? (DT == QSTE_F16 ? f32_to_f16(in[i]) : f32_to_bf16(in[i])) : 0;
 }
 
 int launch_transpose_bits(const uint8_t* in, uint8_t* out, int64_t rows, int64_t cols, int64_t in_pitch,
@@ -250,9 +251,13 @@ int launch_transpose_bits(const uint8_t* in, uint8_t* out, int64_t rows, int64_t
   return static_cast<int>(hipGetLastError());
 }
 
-int launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, int64_t padded, hipStream_t stream) {
+// fp32 -> the 16-bit operand dtype (bf16 or fp16), zero-padded to `padded`
+int launch_f32_to_16(const float* in, uint16_t* out, int64_t n, int64_t padded, int dtype, hipStream_t stream) {
   if (padded == 0) return 0;
-  f32_to_bf16_kernel<<<ceil_div(padded, 256), 256, 0, stream>>>(in, out, n, padded);
+  if (dtype == QSTE_F16)
+    f32_to_16_kernel<QSTE_F16><<<ceil_div(padded, 256), 256, 0, stream>>>(in, out, n, padded);
+  else
+    f32_to_16_kernel<QSTE_BF16><<<ceil_div(padded, 256), 256, 0, stream>>>(in, out, n, padded);
   return static_cast<int>(hipGetLastError());
 }
 

@@ -352,20 +352,22 @@ def test_coordinate_update_rejects_bad_block():
 MFMA_SHAPES = [(576, 320, 300), (1024, 2048, 1000), (128, 64, 17), (256, 512, 2), (4096, 1024, 257)]
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("rows,cols,m", MFMA_SHAPES)
-def test_mfma_products_ragged(rows, cols, m):
-    packed, x, scale, bias, dy = _problem(rows, cols, m, "bf16", rows * 3 + m)
-    bf = torch.bfloat16
-    y = f32(K().packed_linear_affine(t(x, bf), t(packed), t(scale), t(bias), cols))
-    assert rel_l2(y, round_out(oracle.linear_fwd(x, packed, scale, bias, cols), "bf16")) <= 1e-3
-    dx = f32(K().packed_transpose(t(dy, bf), t(packed), cols, row_scale=t(scale)))
-    assert rel_l2(dx, round_out(oracle.linear_dgrad(dy, packed, cols, round_scale(scale, "bf16")), "bf16")) <= 1e-3
+def test_mfma_products_ragged(rows, cols, m, dt):
+    print(f"mfma {rows}x{cols} m={m} {dt}", flush=True)
+    packed, x, scale, bias, dy = _problem(rows, cols, m, dt, rows * 3 + m)
+    tdt = DT[dt]
+    y = f32(K().packed_linear_affine(t(x, tdt), t(packed), t(scale), t(bias), cols))
+    assert rel_l2(y, round_out(oracle.linear_fwd(x, packed, scale, bias, cols), dt)) <= 1e-3
+    dx = f32(K().packed_transpose(t(dy, tdt), t(packed), cols, row_scale=t(scale)))
+    assert rel_l2(dx, round_out(oracle.linear_dgrad(dy, packed, cols, round_scale(scale, dt)), dt)) <= 1e-3
     xbits, off, xs = oracle.pack_affine_rows(x)
-    ev = K().evidence_from_packed(t(dy, bf), t(xbits), cols, row_scale=t(xs)).cpu().numpy()
-    assert rel_l2(ev, oracle.evidence(dy, xbits, cols, round_scale(xs, "bf16"))) <= 1e-5
-    dxf, evf, gs, db = K().linear_backward(t(dy, bf), t(xbits), t(off), t(xs), t(packed), t(scale), cols,
+    ev = K().evidence_from_packed(t(dy, tdt), t(xbits), cols, row_scale=t(xs)).cpu().numpy()
+    assert rel_l2(ev, oracle.evidence(dy, xbits, cols, round_scale(xs, dt))) <= 1e-5
+    dxf, evf, gs, db = K().linear_backward(t(dy, tdt), t(xbits), t(off), t(xs), t(packed), t(scale), cols,
                                            need_bias=True)
-    e0 = oracle.evidence(dy, xbits, cols, round_scale(xs, "bf16")) + oracle.offset_correction(dy, off)[:, None]
+    e0 = oracle.evidence(dy, xbits, cols, round_scale(xs, dt)) + oracle.offset_correction(dy, off)[:, None]
     assert rel_l2(evf.cpu().numpy(), e0 * scale[:, None]) <= 1e-5
     assert rel_l2(gs.cpu().numpy(), oracle.row_inner(e0.astype(np.float32), packed, cols)) <= 1e-4
     assert rel_l2(f32(dxf), dx) == 0.0
