@@ -1,0 +1,143 @@
+"""Graph capture and deferred evidence, on the GPU.
+
+* The coordinate step records into a HIP graph with a device step counter,
+  a device flip count and an enable flag (the reference's capture contract,
+  ``cuda.py:1724-1729``, ``tests/test_gpu.py:519-553``).  Each replay --
+  with eager work and a step increment between replays -- is compared bit for
+  bit with the same step run eagerly on a copy of the state (coordinates,
+  packed signs, int8 momentum, fp16 scales and statistics, flips); a replay
+  with the flag cleared writes nothing.
+* Gradient accumulation (``prepare_accumulation``, ``optim.py:120-135``):
+  four microbatches leave the evidence one batch gives, to summation order,
+  and coordinates within one step of it (the reference's
+  ``tests/test_learning.py:174-212``); ``unscale_`` divides the held evidence.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn as nn
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def _state(rows, cols, seed):
+    from qste_amd import kernels
+
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    coord = torch.randint(-100, 100, (rows, cols), generator=g, device=DEV, dtype=torch.int32).to(torch.int8)
+    return {
+        "coordinate": coord,
+        "packed": kernels.pack_coordinate(coord),
+        "moment_q": torch.zeros_like(coord),
+        "moment_scale": torch.full(((rows * cols + 255) // 256,), 1 / 127, dtype=torch.float16, device=DEV),
+        "row_v": torch.zeros(rows, dtype=torch.float16, device=DEV),
+        "col_v": torch.zeros(cols, dtype=torch.float16, device=DEV),
+    }
+
+
+def _update(st, grad, step, flips, enabled=None):
+    from qste_amd import kernels
+
+    return kernels.coordinate_update(
+        grad, st["coordinate"], st["packed"], st["moment_q"], st["moment_scale"], st["row_v"], st["col_v"],
+        beta1=0.9, beta2=0.99, update_clip=2.0, coordinate_lr=1.0, block_size=256, seed=1, step=step,
+        flips=flips, update_enabled=enabled)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 128), (256, 1024)])
+def test_graph_replays_equal_eager_steps(rows, cols):
+    g = torch.Generator(device=DEV).manual_seed(7)
+    grad = torch.randn(rows, cols, generator=g, device=DEV)
+    st = _state(rows, cols, 3)
+    ref = {k: v.clone() for k, v in st.items()}
+    step = torch.zeros((), dtype=torch.int64, device=DEV)
+    flips = torch.zeros((), dtype=torch.int64, device=DEV)
+    enabled = torch.ones((), dtype=torch.uint8, device=DEV)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm up off the capture
+        warm = {k: v.clone() for k, v in st.items()}
+        _update(warm, grad, step, flips, enabled)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _update(st, grad, step, flips, enabled)
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        expected_flips = _update(ref, grad, i, None)
+        for key in st:
+            assert torch.equal(st[key], ref[key]), (i, key)
+        assert int(flips) == expected_flips
+        # eager work between replays, then the next step number
+        _ = (grad * 2).sum().item()
+        step.add_(1)
+    # the enable flag cleared: a replay writes no state
+    before = {k: v.clone() for k, v in st.items()}
+    enabled.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    for key in st:
+        assert torch.equal(st[key], before[key]), key
+    assert int(flips) == 0
+
+
+@pytest.mark.parametrize("accum,tol", [("fp32", 1e-5), ("fp16", 2e-3)])
+def test_gradient_accumulation_matches_one_large_batch(accum, tol):
+    import qste_amd as qste
+
+    def run(microbatches):
+        torch.manual_seed(10)
+        # the accumulation buffer takes the surface's config (convert's), as
+        # in the reference (surface.py:197-206)
+        cfg = {"coordinate_lr": 4.0, "evidence_accum_dtype": accum}
+        model = qste.convert(nn.Sequential(nn.Linear(256, 128, bias=False)), config=cfg).to(DEV)
+        coords = qste.QSTEOptimizer(model, config=cfg)
+        coords.prepare_accumulation()
+        data = torch.randn(512, 256, generator=torch.Generator().manual_seed(11)).to(DEV)
+        for chunk in data.chunk(microbatches):
+            (model(chunk).square().sum() / len(data)).backward()
+        surface = qste.surfaces(model)[0]
+        evidence = surface._evidence.float().clone()
+        coords.step()
+        return evidence, surface.coordinate.clone()
+
+    one_e, one_c = run(1)
+    many_e, many_c = run(4)
+    scale = one_e.pow(2).mean().sqrt().clamp_min(1e-12)
+    assert float((one_e - many_e).pow(2).mean().sqrt() / scale) < tol
+    diff = (one_c.int() - many_c.int()).abs()
+    assert int(diff.max()) <= 1
+    assert float((diff > 0).float().mean()) < 0.01
+
+
+def test_unscale_divides_the_held_evidence():
+    import qste_amd as qste
+
+    torch.manual_seed(2)
+    cfg = {"evidence_accum_dtype": "fp32"}
+    model = qste.convert(nn.Sequential(nn.Linear(64, 32, bias=False)), config=cfg).to(DEV)
+    coords = qste.QSTEOptimizer(model, config=cfg)
+    coords.defer()
+    x = torch.randn(16, 64, device=DEV)
+    (model(x).sum() * 1024.0).backward()
+    surface = qste.surfaces(model)[0]
+    held = surface._evidence.float().clone()
+    coords.unscale_(1024.0)
+    assert torch.allclose(surface._evidence.float(), held / 1024.0, rtol=1e-6, atol=0)
+    assert coords.step() >= 0
+    # deferred mode keeps the buffer for the next accumulation, emptied
+    assert surface._evidence is not None and not surface._evidence.any()
