@@ -156,6 +156,14 @@ __device__ __forceinline__ uint16_t round16(float f) {
   else return f32_to_bf16(f);
 }
 
+// two outputs to a 16-bit pair (lo in bits 0..15)
+template <int DT>
+__device__ __forceinline__ uint32_t round16x2(float lo, float hi) {
+  if constexpr (DT == QSTE_F16)
+    return static_cast<uint32_t>(f32_to_f16(lo)) | (static_cast<uint32_t>(f32_to_f16(hi)) << 16);
+  else return f32x2_to_bf16x2(lo, hi);
+}
+
 // Workgroup -> output tile.  Consecutive workgroup ids land on different
 // XCDs (round-robin), so ids are first regrouped so each XCD gets a
 // contiguous range, then walked in column-major groups of 2 M-tiles, so the
@@ -651,8 +659,7 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
               __builtin_amdgcn_update_dpp(0, __float_as_int(send), 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
           const float lo = odd ? recv : v0;
           const float hi = odd ? v1 : recv;
-          const uint32_t word =
-              static_cast<uint32_t>(round16<DT>(lo)) | (static_cast<uint32_t>(round16<DT>(hi)) << 16);
+          const uint32_t word = round16x2<DT>(lo, hi);
           const int row = 8 * (r >> 2) + 4 * kg + (r & 3) + (odd ? 1 : 0) - EPR * h;
           *reinterpret_cast<uint32_t*>(stg + row * EPL + 2 * (32 * nb + (l32 & ~1))) = word;
         }
