@@ -102,7 +102,8 @@ def test_unpack_rows_exact(cols, dt):
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("rows,cols", [(9, 7), (17, 64), (16, 1024), (8, 4096), (5, 1001), (3, 14336)])
+@pytest.mark.parametrize("rows,cols", [(9, 7), (17, 64), (16, 1024), (8, 4096), (4, 4104), (5, 1001), (3, 14336),
+                                       (2, 16384), (2, 16392)])
 def test_pack_affine_rows_bit_exact(dt, rows, cols):
     rng = np.random.default_rng(rows * 31 + cols)
     x = as_dtype_values((rng.standard_normal((rows, cols)) * 2 + 0.3).astype(np.float32), dt)
