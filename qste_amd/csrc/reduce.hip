@@ -66,61 +66,91 @@ __global__ void colsum_partial_kernel(const typename Elem<DT>::T* __restrict__ d
 }
 
 // bf16 / f16 with rows % 8 == 0: each lane reduces 8 adjacent columns (one
-// 16-byte load per sample), a wave 512 columns, over kColChunk samples,
-// with UNROLL loads in flight; same per-column order as the scalar kernel.
+// 16-byte load per sample), so a wave covers 512 columns.  The chunk's
+// kColChunk samples are split over the workgroup's kColWaves waves (a
+// contiguous quarter each, UNROLL loads in flight), and the waves' sums are
+// added in wave order through LDS: a fixed order, so the result does not
+// depend on scheduling.  Four waves per chunk keep ~28 waves resident per CU
+// at 16384 x 14336, where one wave per chunk left the loads latency-bound.
+constexpr int kColWaves = 4;
+constexpr int kColThreads = kColWaves * kWave;
+
 template <int DT>
-__global__ __launch_bounds__(64) void colsum_partial_x8_kernel(const uint16_t* __restrict__ dy,
-                                                              const float* __restrict__ offset,
-                                                              int64_t samples, int64_t rows,
-                                                              float* __restrict__ v_part,
-                                                              float* __restrict__ db_part) {
+__global__ __launch_bounds__(kColThreads) void colsum_partial_x8_kernel(
+    const uint16_t* __restrict__ dy, const float* __restrict__ offset, int64_t samples, int64_t rows,
+    float* __restrict__ v_part, float* __restrict__ db_part) {
   constexpr int UNROLL = 8;
-  const int64_t r = (blockIdx.x * static_cast<int64_t>(64) + threadIdx.x) * 8;
-  if (r >= rows) return;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kColChunk;
-  const int64_t t1 = t0 + kColChunk < samples ? t0 + kColChunk : samples;
+  constexpr int kPad = 17;  // 16 sums per lane, padded against bank conflicts
+  __shared__ float red[kColWaves * kWave * kPad];
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kWave * 8);
+  const int64_t r = base + lane * 8;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kColChunk;
+  const int64_t c1 = c0 + kColChunk < samples ? c0 + kColChunk : samples;
+  constexpr int kPer = kColChunk / kColWaves;
+  const int64_t t0 = c0 + wave * kPer < c1 ? c0 + wave * kPer : c1;
+  const int64_t t1 = t0 + kPer < c1 ? t0 + kPer : c1;
   float v[8], db[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) v[i] = db[i] = 0.0f;
-  const uint16_t* col = dy + r;
-  int64_t t = t0;
-  for (; t + UNROLL <= t1; t += UNROLL) {
-    uint4 q[UNROLL];
-    float o[UNROLL];
+  if (r < rows) {
+    const uint16_t* col = dy + r;
+    int64_t t = t0;
+    for (; t + UNROLL <= t1; t += UNROLL) {
+      uint4 q[UNROLL];
+      float o[UNROLL];
 #pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      q[u] = *reinterpret_cast<const uint4*>(col + (t + u) * rows);
-      o[u] = offset[t + u];
+      for (int u = 0; u < UNROLL; ++u) {
+        q[u] = *reinterpret_cast<const uint4*>(col + (t + u) * rows);
+        o[u] = offset[t + u];
+      }
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const uint16_t* e = reinterpret_cast<const uint16_t*>(&q[u]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float g = Elem<DT>::load(e, i);
+          v[i] = fmaf(g, o[u], v[i]);
+          db[i] += g;
+        }
+      }
     }
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      const uint16_t* e = reinterpret_cast<const uint16_t*>(&q[u]);
+    for (; t < t1; ++t) {
+      const uint4 q = *reinterpret_cast<const uint4*>(col + t * rows);
+      const float o = offset[t];
+      const uint16_t* e = reinterpret_cast<const uint16_t*>(&q);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float g = Elem<DT>::load(e, i);
-        v[i] = fmaf(g, o[u], v[i]);
+        v[i] = fmaf(g, o, v[i]);
         db[i] += g;
       }
     }
   }
-  for (; t < t1; ++t) {
-    const uint4 q = *reinterpret_cast<const uint4*>(col + t * rows);
-    const float o = offset[t];
-    const uint16_t* e = reinterpret_cast<const uint16_t*>(&q);
+  float* mine = red + (wave * kWave + lane) * kPad;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float g = Elem<DT>::load(e, i);
-      v[i] = fmaf(g, o, v[i]);
-      db[i] += g;
-    }
+  for (int i = 0; i < 8; ++i) {
+    mine[i] = v[i];
+    mine[8 + i] = db[i];
   }
-  float* vp = v_part + blockIdx.y * rows + r;
+  __syncthreads();
+  // 1024 results per workgroup (512 columns of v, then of db), consecutive
+  // threads on consecutive columns; waves summed in order 0..kColWaves-1.
+  const int64_t part = static_cast<int64_t>(blockIdx.y) * rows;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) vp[i] = v[i];
-  if (db_part) {
-    float* dp = db_part + blockIdx.y * rows + r;
+  for (int j = threadIdx.x; j < 2 * kWave * 8; j += kColThreads) {
+    const int which = j / (kWave * 8);
+    const int c = j % (kWave * 8);
+    const int64_t rc = base + c;
+    const int slot = (c / 8) * kPad + which * 8 + c % 8;
+    float s = red[slot];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) dp[i] = db[i];
+    for (int w = 1; w < kColWaves; ++w) s += red[w * kWave * kPad + slot];
+    if (rc < rows) {
+      if (which == 0) v_part[part + rc] = s;
+      else if (db_part) db_part[part + rc] = s;
+    }
   }
 }
 
@@ -149,13 +179,13 @@ int launch_colsums(const void* dy, int dtype, const float* offset, int64_t sampl
   const bool x8 = (dtype == QSTE_BF16 || dtype == QSTE_F16) && rows % 8 == 0 &&
                   (reinterpret_cast<uintptr_t>(dy) & 15) == 0;
   if (chunks > 0 && x8) {
-    dim3 grid(ceil_div(rows, 512), chunks);
+    dim3 grid(ceil_div(rows, kWave * 8), chunks);
     if (dtype == QSTE_BF16)
-      colsum_partial_x8_kernel<QSTE_BF16><<<grid, 64, 0, stream>>>(static_cast<const uint16_t*>(dy), offset,
-                                                                    samples, rows, v_part, db_part);
+      colsum_partial_x8_kernel<QSTE_BF16><<<grid, kColThreads, 0, stream>>>(
+          static_cast<const uint16_t*>(dy), offset, samples, rows, v_part, db_part);
     else
-      colsum_partial_x8_kernel<QSTE_F16><<<grid, 64, 0, stream>>>(static_cast<const uint16_t*>(dy), offset,
-                                                                   samples, rows, v_part, db_part);
+      colsum_partial_x8_kernel<QSTE_F16><<<grid, kColThreads, 0, stream>>>(
+          static_cast<const uint16_t*>(dy), offset, samples, rows, v_part, db_part);
     int rc = static_cast<int>(hipGetLastError());
     if (rc) return rc;
   } else if (chunks > 0) {
