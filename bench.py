@@ -207,10 +207,11 @@ def config_steps(device):
     model = relu_mlp(device=device)
     coords = qste.QSTEOptimizer(model)
     g = torch.Generator(device=device).manual_seed(0)
-    x = torch.randn(8192, 1024, generator=g, device=device).to(torch.bfloat16)
+    x = torch.randn(8192, 1024, generator=g, device=device).to(torch.bfloat16).requires_grad_(True)
     dy = torch.randn(8192, 1024, generator=g, device=device).to(torch.bfloat16)
 
     def step2():
+        x.grad = None  # both layers form their input gradient (the FLOPs counted)
         model(x).backward(dy)
         coords.step()
 
@@ -484,16 +485,20 @@ def main():
     mlp = SwiGLU(d, ffn, device)
     coords = qste.QSTEOptimizer(list(qste.surfaces(mlp.modules)))
     g = torch.Generator(device=device).manual_seed(0)
-    x = torch.randn(T, d, generator=g, device=device).to(torch.bfloat16).requires_grad_(False)
+    # the block's input takes a gradient, as inside a network: every layer
+    # forms its input gradient, so the step does the 6*T*sum(R*C) FLOPs counted
+    x = torch.randn(T, d, generator=g, device=device).to(torch.bfloat16).requires_grad_(True)
     g4 = torch.Generator(device=device).manual_seed(4)
     dy = torch.randn(T, d, generator=g4, device=device).to(torch.bfloat16)
 
     def step():
+        x.grad = None
         y = mlp(x)
         y.backward(dy)
         return coords.step()
 
     def packed_step():
+        x.grad = None
         with qste.packed_activations():
             y = mlp(x)
         y.backward(dy)

@@ -115,6 +115,11 @@ int qste_packed_row_inner(const float* matrix, const uint8_t* packed, float* out
  *   evidence fp32 [rows, cols] = E0 * scale[r]           (functional.py:190)
  *   grad_bias fp32 [rows] = sum_t dy  (written when grad_bias != NULL)
  * x_offset / x_scale are the fp32 [samples] rows of the saved aux.
+ * dx may be NULL when no input gradient is wanted (autograd's
+ * needs_input_grad); then that product is not computed.
+ * Where the evidence has few output tiles for its K (= samples), its K
+ * range is split over several workgroups and summed in a fixed order in
+ * the workspace, so results do not depend on scheduling.
  * Needs qste_linear_backward_workspace_bytes() bytes of workspace.
  * No counterpart as a single call in the reference: it fuses five of its
  * calls (cuda.py:1568-1688, functional.py:143, 193). */

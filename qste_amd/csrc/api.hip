@@ -32,9 +32,10 @@ int mfma_evidence(const void*, int, const uint8_t*, const float*, float*, int64_
                   const float*, const float*, const uint8_t*, float*, hipStream_t);
 int64_t mfma_evidence_tiles(int64_t cols);
 bool mfma_pair_ok(const void*, int, int64_t, int64_t, int64_t);
+EvidenceSplit mfma_evidence_split(int64_t, int64_t, int64_t, bool);
 int mfma_backward_pair(const void*, int, const uint8_t*, int64_t, const uint16_t*, float*, const uint8_t*, int64_t,
                        const uint16_t*, const uint8_t*, void*, int64_t, int64_t, int64_t, const float*,
-                       const float*, float*, hipStream_t);
+                       const float*, float*, EvidenceSplit, float*, hipStream_t);
 int launch_transpose_bits(const uint8_t*, uint8_t*, int64_t, int64_t, int64_t, int64_t, hipStream_t);
 int launch_f32_to_16(const float*, uint16_t*, int64_t, int64_t, int, hipStream_t);
 int gemv_linear_forward(const void*, int, const uint8_t*, const float*, const float*, void*, int64_t,
@@ -50,7 +51,7 @@ inline bool dtype_ok(int d) { return d == QSTE_F32 || d == QSTE_F16 || d == QSTE
 inline size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 struct BackwardLayout {
-  size_t v_part, db_part, v, gs_part, w_t, x_t, s16, xs16, total;
+  size_t v_part, db_part, v, gs_part, w_t, x_t, s16, xs16, partial, total;
   int64_t chunks, tiles;
   int64_t w_t_pitch, x_t_pitch;  // bytes per row of the transposed sign copies
 };
@@ -75,6 +76,12 @@ BackwardLayout backward_layout(int64_t samples, int64_t rows, int64_t cols) {
   l.x_t = at; at += align_up(static_cast<size_t>(cols * l.x_t_pitch));
   l.s16 = at; at += align_up(sizeof(uint16_t) * static_cast<size_t>((rows + 63) / 64 * 64));
   l.xs16 = at; at += align_up(sizeof(uint16_t) * static_cast<size_t>((samples + 63) / 64 * 64));
+  // split-K partials of the evidence: room for the larger of the plans with
+  // and without the input gradient
+  int64_t splits = mfma_evidence_split(samples, rows, cols, true).splits;
+  const int64_t alone = mfma_evidence_split(samples, rows, cols, false).splits;
+  if (alone > splits) splits = alone;
+  l.partial = at; at += splits > 1 ? align_up(sizeof(float) * static_cast<size_t>(splits * rows * cols)) : 0;
   l.total = at;
   return l;
 }
@@ -216,7 +223,7 @@ int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x, con
                          void* stream) {
   if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
   if (samples < 0 || rows <= 0 || cols <= 0) return QSTE_E_SHAPE;
-  if (!dx || !evidence || !grad_scale || !scale || !packed_w) return QSTE_E_NULL;
+  if (!evidence || !grad_scale || !scale || !packed_w) return QSTE_E_NULL;
   if (samples > 0 && (!dy || !packed_x || !x_offset || !x_scale)) return QSTE_E_NULL;
   const BackwardLayout l = backward_layout(samples, rows, cols);
   if (!workspace || workspace_bytes < l.total) return QSTE_E_WORKSPACE;
@@ -231,24 +238,29 @@ int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x, con
     if ((rc = launch_colsums(dy, dtype, x_offset, samples, rows, v_part, grad_bias ? db_part : nullptr, v,
                              grad_bias, s)))
       return rc;
-    // evidence and dgrad together when both take the MFMA path, from
-    // transposed copies of the signs and bf16 copies of the scales
+    // evidence and dgrad (when dx is wanted) together when both take the
+    // MFMA path, from transposed copies of the signs and bf16 copies of the
+    // scales; the evidence split over K ranges where that shortens the launch
     if (mfma_pair_ok(dy, dtype, samples, rows, cols)) {
       uint8_t* w_t = reinterpret_cast<uint8_t*>(base + l.w_t);
       uint8_t* x_t = reinterpret_cast<uint8_t*>(base + l.x_t);
       uint16_t* s16 = reinterpret_cast<uint16_t*>(base + l.s16);
       uint16_t* xs16 = reinterpret_cast<uint16_t*>(base + l.xs16);
+      float* partial = reinterpret_cast<float*>(base + l.partial);
       const int64_t pb = (cols + 7) / 8;
-      if ((rc = launch_transpose_bits(packed_w, w_t, rows, cols, pb, l.w_t_pitch, s))) return rc;
+      if (dx) {
+        if ((rc = launch_transpose_bits(packed_w, w_t, rows, cols, pb, l.w_t_pitch, s))) return rc;
+        if ((rc = launch_f32_to_16(scale, s16, rows, (rows + 63) / 64 * 64, dtype, s))) return rc;
+      }
       if ((rc = launch_transpose_bits(packed_x, x_t, samples, cols, pb, l.x_t_pitch, s))) return rc;
-      if ((rc = launch_f32_to_16(scale, s16, rows, (rows + 63) / 64 * 64, dtype, s))) return rc;
       if ((rc = launch_f32_to_16(x_scale, xs16, samples, (samples + 63) / 64 * 64, dtype, s))) return rc;
+      const EvidenceSplit split = mfma_evidence_split(samples, rows, cols, dx != nullptr);
       rc = mfma_backward_pair(dy, dtype, x_t, l.x_t_pitch, xs16, evidence, w_t, l.w_t_pitch, s16, packed_w, dx,
-                              samples, rows, cols, v, scale, gs_part, s);
+                              samples, rows, cols, v, scale, gs_part, split, partial, s);
       if (rc == 0) return launch_sum_partials(gs_part, mfma_evidence_tiles(cols), rows, grad_scale, s);
       if (rc != 1) return rc;
     }
-    if ((rc = dgrad_dispatch(dy, dtype, packed_w, scale, dx, samples, rows, cols, s))) return rc;
+    if (dx && (rc = dgrad_dispatch(dy, dtype, packed_w, scale, dx, samples, rows, cols, s))) return rc;
   } else {
     if ((rc = fill_zero(v, rows, s))) return rc;
     if (grad_bias && (rc = fill_zero(grad_bias, rows, s))) return rc;

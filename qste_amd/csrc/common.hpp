@@ -8,6 +8,13 @@
 
 namespace qste {
 
+// Split-K plan of the backward launch's evidence (gemm_mfma.hip): `splits`
+// K ranges of `ks_steps` 64-sample steps each (the last may be shorter).
+struct EvidenceSplit {
+  int splits;
+  int ks_steps;
+};
+
 constexpr int kWave = 64;
 
 // ---------------------------------------------------------------------------

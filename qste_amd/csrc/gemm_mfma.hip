@@ -21,6 +21,8 @@
 // MFMA 32x32x16 bf16 operand layout used here: lane l holds A[l%32][8(l/32)
 // + i] and B[8(l/32) + i][l%32], i = 0..7; the accumulator's register r
 // holds D[8(r/4) + 4(l/32) + r%4][l%32].
+#include <map>
+
 #include "common.hpp"
 
 namespace qste {
@@ -37,7 +39,9 @@ enum { A_ROWS_M = 0, A_ROWS_K = 1 };        // A[m][k] stored with k (or m) cont
 // B_BITS_ALONG_K_SCALED: bits along K (a transposed copy of the signs) and
 // a per-k bf16 scale, both brought in by direct loads.
 enum { B_BITS_ALONG_K = 0, B_BITS_ALONG_N = 1, B_BITS_ALONG_K_SCALED = 2 };
-enum { EPI_FORWARD = 0, EPI_PLAIN = 1, EPI_EVIDENCE = 2 };
+// EPI_PARTIAL: the bare fp32 accumulators of one K range of a split-K
+// evidence, finished by evidence_combine_kernel
+enum { EPI_FORWARD = 0, EPI_PLAIN = 1, EPI_EVIDENCE = 2, EPI_PARTIAL = 3 };
 
 struct Params {
   const uint16_t* a;     // bf16 dense operand (x or dy)
@@ -459,12 +463,6 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
     for (int i = 4 * q; i < 4 * q + 4; ++i)
       acc[i / NBN][i % NBN] = mma_dt<DT>(a[s & 1][i / NBN], b[s & 1][i % NBN], acc[i / NBN][i % NBN]);
   };
-  auto mfmas = [&](int s) {
-#pragma unroll
-    for (int mb = 0; mb < MBN; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < NBN; ++nb) acc[mb][nb] = mma_dt<DT>(a[s & 1][mb], b[s & 1][nb], acc[mb][nb]);
-  };
 
   // K step `it` on stage (As, Bs, Ss); substep 0's fragments are in buffer 0.
   // After substep 2 every wave has finished step it-1, so step it+3 may
@@ -550,6 +548,23 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
 
   // every in-flight load has landed (the stages are free for the epilogue)
   stage_barrier<0>();
+
+  if (EPI == EPI_PARTIAL) {
+    // 32 lanes x 4 bytes per row per store, as the evidence epilogue
+    float* part = static_cast<float*>(p.out);
+#pragma unroll
+    for (int mb = 0; mb < MBN; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + WMR * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
+#pragma unroll
+        for (int nb = 0; nb < NBN; ++nb) {
+          const int64_t col = n0 + WNC * wn + 32 * nb + l32;
+          if (row < p.M && col < p.N) part[row * p.N + col] = acc[mb][nb][r];
+        }
+      }
+    return;
+  }
 
   if (EPI == EPI_EVIDENCE) {
     // E0 = acc + v[m]; E = E0 * s[m] (fp32, 32 lanes x 4 bytes per row per
@@ -716,16 +731,66 @@ __global__ __launch_bounds__(THREADS, 1) void wide_kernel(Params p) {
 // tiles first (the longer ones), then dgrad tiles, so the grid's last wave
 // of one product is filled by the other instead of leaving CUs idle.  Both
 // take their signs as transposed copies (bits along K) with bf16 per-k
-// scales, prepared by the caller.
-template <int DT>
-__global__ __launch_bounds__(THREADS, 1) void backward_pair_kernel(Params pe, Params pd, int tiles_e) {
+// scales, prepared by the caller.  SPLIT: the evidence's K range is cut
+// into `splits` ranges of ks_steps K steps; workgroup e covers tile
+// e % tiles_e over range e / tiles_e and stores its bare accumulators in
+// partial[range] ([M][N] fp32 each) for evidence_combine_kernel.
+template <int DT, bool SPLIT>
+__global__ __launch_bounds__(THREADS, 1) void backward_pair_kernel(Params pe, Params pd, int tiles_e, int splits,
+                                                                   int ks_steps, float* partial) {
   QSTE_WIDE_STAGES(A_STAGE_K, B_STAGE, 4 * BK)
-  if (static_cast<int>(blockIdx.x) < tiles_e)
-    wide_tile<A_ROWS_K, B_BITS_ALONG_K_SCALED, EPI_EVIDENCE, DT>(pe, blockIdx.x, A0, A1, A2, A3, B0, B1, B2, B3,
-                                                                 Sc);
-  else
-    wide_tile<A_ROWS_M, B_BITS_ALONG_K_SCALED, EPI_PLAIN, DT>(pd, blockIdx.x - tiles_e, A0, A1, A2, A3, B0, B1, B2,
-                                                              B3, Sc);
+  const int e = static_cast<int>(blockIdx.x);
+  if (!SPLIT) {
+    if (e < tiles_e)
+      wide_tile<A_ROWS_K, B_BITS_ALONG_K_SCALED, EPI_EVIDENCE, DT>(pe, e, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
+    else
+      wide_tile<A_ROWS_M, B_BITS_ALONG_K_SCALED, EPI_PLAIN, DT>(pd, e - tiles_e, A0, A1, A2, A3, B0, B1, B2, B3,
+                                                                Sc);
+  } else if (e < tiles_e * splits) {
+    const int j = e / tiles_e;
+    const int64_t k0 = static_cast<int64_t>(j) * ks_steps * BK;
+    Params q = pe;
+    q.a = pe.a + k0 * pe.lda;          // dy rows k0 .. (A as rows of K)
+    q.a_rows = pe.a_rows - k0;
+    q.bits = pe.bits + k0 / 8;         // bit k0 of every transposed row (k0 % 64 == 0)
+    q.kscale16 = pe.kscale16 + k0;
+    const int64_t left = pe.K - k0, span = static_cast<int64_t>(ks_steps) * BK;
+    q.K = left < span ? left : span;   // the host makes every range nonempty
+    q.out = partial + static_cast<int64_t>(j) * pe.M * pe.N;
+    wide_tile<A_ROWS_K, B_BITS_ALONG_K_SCALED, EPI_PARTIAL, DT>(q, e - j * tiles_e, A0, A1, A2, A3, B0, B1, B2, B3,
+                                                                Sc);
+  } else {
+    wide_tile<A_ROWS_M, B_BITS_ALONG_K_SCALED, EPI_PLAIN, DT>(pd, e - tiles_e * splits, A0, A1, A2, A3, B0, B1,
+                                                              B2, B3, Sc);
+  }
+}
+
+// The evidence epilogue over split-K partials: E0 = sum of the ranges'
+// partials (in range order) + m_add[m]; E = E0 * m_scale[m]; and the
+// scale-gradient partials sum_c E0 * sign_w over each 64-column slot, in the
+// slots the fused epilogue writes ([WAVES_N * tiles_n][M], zero past N).
+// One workgroup per (row, 256 columns), one wave per slot.
+__global__ __launch_bounds__(THREADS) void evidence_combine_kernel(const float* __restrict__ partial, int splits,
+                                                                   const float* __restrict__ m_add,
+                                                                   const float* __restrict__ m_scale,
+                                                                   const uint8_t* __restrict__ w_bits, int64_t w_pb,
+                                                                   float* __restrict__ ev,
+                                                                   float* __restrict__ gs_partial, int64_t M,
+                                                                   int64_t N) {
+  const int64_t row = blockIdx.x;
+  const int64_t col = static_cast<int64_t>(blockIdx.y) * BN + threadIdx.x;
+  const int64_t slot = static_cast<int64_t>(blockIdx.y) * WAVES_N + threadIdx.x / kWave;
+  float signed_e0 = 0.0f;
+  if (col < N) {
+    const int64_t at = row * N + col;
+    float s = partial[at];
+    for (int j = 1; j < splits; ++j) s += partial[static_cast<int64_t>(j) * M * N + at];
+    const float e0 = s + (m_add ? m_add[row] : 0.0f);
+    ev[at] = e0 * (m_scale ? m_scale[row] : 1.0f);
+    if (w_bits) signed_e0 = ((w_bits[row * w_pb + (col >> 3)] >> (col & 7)) & 1u) ? e0 : -e0;
+  }
+  const float tot = wave_sum(signed_e0);
+  if (gs_partial && threadIdx.x % kWave == 0) gs_partial[slot * M + row] = tot;
 }
 #undef QSTE_WIDE_STAGES
 }  // namespace wide
@@ -847,19 +912,86 @@ bool mfma_pair_ok(const void* dy, int dtype, int64_t samples, int64_t rows, int6
          aligned16(dy) && fits32(samples * rows * 2) && fits32(samples * cols / 8) && fits32(rows * cols / 8);
 }
 
-// Evidence (with its fused epilogue) and dgrad of one layer in one launch,
-// from transposed sign copies: x_t [cols][x_t_pitch] (bit k of row c = sign
-// of x[k][c]) and w_t [cols][w_t_pitch] (bit r of row c = sign of W[r][c]),
-// both zero past their K, and bf16 copies of x_scale and scale, zero-padded
-// to a multiple of 64 entries.  Returns 1 when either product is not for
-// this path.
+// ---------------------------------------------------------------------------
+// split-K plan for the evidence of the backward launch
+// ---------------------------------------------------------------------------
+// The evidence's K is the token count, usually its longest dimension, and
+// its tile count rows/256 x cols/256 can be far below the CU count (64 tiles
+// at 4096 x 1024): then each tile is a long serial chain while most CUs
+// idle.  The plan picks the number of K ranges S (1, 2, 4 or 8) that
+// minimises an estimate of the launch: list scheduling of S x tiles_e
+// ranges of nk/S steps, then the dgrad tiles, on kCUs CUs (each tile
+// costing kTileOverhead steps more for its prologue and epilogue), plus the
+// combine pass's HBM traffic in step units.  The plan depends only on the
+// shape, so the workspace query and the call agree.
+namespace {
+constexpr int kCUs = 256;              // MI350X / MI355X
+constexpr int64_t kTileOverhead = 14;  // K steps a tile's prologue + epilogue cost
+constexpr double kBytesPerStep = 7.5e6;  // combine traffic per K-step time (~5 TB/s x 1.5 us)
+constexpr int64_t kMaxPartialBytes = int64_t{1} << 30;
+
+// Greedy in-order assignment of `groups` (count, length) onto kCUs CUs that
+// start idle; returns the finish time of the last CU.
+int64_t list_schedule(const int64_t (*groups)[2], int n) {
+  std::map<int64_t, int64_t> free_at{{0, kCUs}};  // time -> idle CUs from then
+  for (int g = 0; g < n; ++g) {
+    int64_t left = groups[g][0];
+    const int64_t len = groups[g][1];
+    while (left > 0) {
+      auto it = free_at.begin();
+      const int64_t t = it->first, c = it->second;
+      const int64_t take = left < c ? left : c;
+      if (take == c) free_at.erase(it);
+      else it->second = c - take;
+      free_at[t + len] += take;
+      left -= take;
+    }
+  }
+  return free_at.rbegin()->first;
+}
+}  // namespace
+
+EvidenceSplit mfma_evidence_split(int64_t samples, int64_t rows, int64_t cols, bool with_dgrad) {
+  EvidenceSplit best{1, 0};
+  if (samples <= 0 || rows <= 0 || cols <= 0) return best;
+  const int64_t nk = (samples + mfma::wide::BK - 1) / mfma::wide::BK;
+  const int64_t te = wide_grid(rows, cols), td = with_dgrad ? wide_grid(samples, cols) : 0;
+  const int64_t nkd = (rows + mfma::wide::BK - 1) / mfma::wide::BK;
+  best.ks_steps = static_cast<int>(nk);
+  double best_cost = 0.0;
+  for (int S = 1; S <= 8; S *= 2) {
+    const int64_t ks = (nk + S - 1) / S;
+    if (S > 1 && ks < 16) break;  // ranges shorter than 16 K steps are mostly overhead
+    const int64_t splits = (nk + ks - 1) / ks;  // every range nonempty
+    if (S > 1 && splits * rows * cols * 4 > kMaxPartialBytes) break;
+    const int64_t groups[2][2] = {{te * splits, ks + kTileOverhead}, {td, nkd + kTileOverhead}};
+    double cost = static_cast<double>(list_schedule(groups, 2));
+    if (splits > 1) cost += static_cast<double>((splits + 1) * rows * cols * 4) / kBytesPerStep + 2.0;
+    if (S == 1 || cost < best_cost) {
+      best_cost = cost;
+      best.splits = static_cast<int>(splits);
+      best.ks_steps = static_cast<int>(ks);
+    }
+  }
+  return best;
+}
+
+// Evidence (with its fused epilogue) and, when dx is given, dgrad of one
+// layer in one launch, from transposed sign copies: x_t [cols][x_t_pitch]
+// (bit k of row c = sign of x[k][c]) and w_t [cols][w_t_pitch] (bit r of
+// row c = sign of W[r][c]), both zero past their K, and bf16 copies of
+// x_scale and scale, zero-padded to a multiple of 64 entries.  `split` is
+// mfma_evidence_split's plan for the shape; with more than one range,
+// `partial` holds split.splits x rows x cols floats.  Returns 1 when either
+// product is not for this path.
 int mfma_backward_pair(const void* dy, int dtype, const uint8_t* x_t, int64_t x_t_pitch, const uint16_t* x_scale16,
                        float* ev, const uint8_t* w_t, int64_t w_t_pitch, const uint16_t* scale16,
                        const uint8_t* packed_w, void* dx, int64_t samples, int64_t rows, int64_t cols,
-                       const float* m_add, const float* scale, float* gs_partial, hipStream_t stream) {
-  if (!evidence_ok(dy, dtype, x_t, samples, rows, cols) || !dgrad_ok(dy, dtype, w_t, samples, rows, cols) ||
-      !fits32(cols * x_t_pitch) || !fits32(cols * w_t_pitch))
-    return 1;
+                       const float* m_add, const float* scale, float* gs_partial, EvidenceSplit split,
+                       float* partial, hipStream_t stream) {
+  if (!evidence_ok(dy, dtype, x_t, samples, rows, cols) || !fits32(cols * x_t_pitch)) return 1;
+  if (dx && (!dgrad_ok(dy, dtype, w_t, samples, rows, cols) || !fits32(cols * w_t_pitch))) return 1;
+  if (split.splits < 1 || (split.splits > 1 && !partial)) return QSTE_E_WORKSPACE;
   mfma::Params pe{};
   pe.a = static_cast<const uint16_t*>(dy);
   pe.bits = x_t;
@@ -877,11 +1009,27 @@ int mfma_backward_pair(const void* dy, int dtype, const uint8_t* x_t, int64_t x_
   pd.M = samples; pd.N = cols; pd.K = rows;
   pd.lda = rows; pd.pb = w_t_pitch;
   pd.a_rows = samples; pd.bit_rows = cols;
-  const int te = wide_grid(rows, cols), td = wide_grid(samples, cols);
-  if (dtype == QSTE_F16)
-    mfma::wide::backward_pair_kernel<QSTE_F16><<<te + td, mfma::wide::THREADS, 0, stream>>>(pe, pd, te);
-  else
-    mfma::wide::backward_pair_kernel<QSTE_BF16><<<te + td, mfma::wide::THREADS, 0, stream>>>(pe, pd, te);
+  const int te = wide_grid(rows, cols), td = dx ? wide_grid(samples, cols) : 0;
+  const int grid = te * split.splits + td;
+  const dim3 g(grid), b(mfma::wide::THREADS);
+  if (dtype == QSTE_F16) {
+    if (split.splits > 1)
+      mfma::wide::backward_pair_kernel<QSTE_F16, true><<<g, b, 0, stream>>>(pe, pd, te, split.splits,
+                                                                           split.ks_steps, partial);
+    else
+      mfma::wide::backward_pair_kernel<QSTE_F16, false><<<g, b, 0, stream>>>(pe, pd, te, 1, 0, nullptr);
+  } else {
+    if (split.splits > 1)
+      mfma::wide::backward_pair_kernel<QSTE_BF16, true><<<g, b, 0, stream>>>(pe, pd, te, split.splits,
+                                                                            split.ks_steps, partial);
+    else
+      mfma::wide::backward_pair_kernel<QSTE_BF16, false><<<g, b, 0, stream>>>(pe, pd, te, 1, 0, nullptr);
+  }
+  int rc = static_cast<int>(hipGetLastError());
+  if (rc || split.splits == 1) return rc;
+  const dim3 cgrid(static_cast<unsigned>(rows), static_cast<unsigned>((cols + mfma::wide::BN - 1) / mfma::wide::BN));
+  mfma::wide::evidence_combine_kernel<<<cgrid, mfma::wide::THREADS, 0, stream>>>(
+      partial, split.splits, m_add, scale, packed_w, cols / 8, ev, gs_partial, rows, cols);
   return static_cast<int>(hipGetLastError());
 }
 

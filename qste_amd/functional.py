@@ -84,11 +84,14 @@ class QSTELinearFn(Function):
         forget_encodings()
         payload, aux, packed, scale = ctx.saved_tensors
         grad2 = grad_output.reshape(-1, grad_output.shape[-1])
+        # the input-gradient product only when autograd wants that gradient
+        # (the reference always forms it, functional.py:180-183)
         grad_inputs, evidence, grad_scale, grad_bias = kernels.linear_backward(
             grad2, payload, aux[0], aux[1], packed, scale.detach(), ctx.columns,
-            need_bias=ctx.bias_dtype is not None)
+            need_bias=ctx.bias_dtype is not None, need_input=ctx.needs_input_grad[0])
         ctx.surface.consume_evidence(evidence)
-        grad_inputs = grad_inputs.reshape(ctx.input_shape).to(ctx.input_dtype)
+        if grad_inputs is not None:
+            grad_inputs = grad_inputs.reshape(ctx.input_shape).to(ctx.input_dtype)
         if grad_bias is not None:
             grad_bias = grad_bias.to(ctx.bias_dtype)
         return grad_inputs, None, grad_scale.to(scale.dtype), grad_bias, None

@@ -302,12 +302,15 @@ def packed_row_inner(matrix: Tensor, packed: Tensor, columns: int) -> Tensor:
 
 
 def linear_backward(grad: Tensor, packed_x: Tensor, x_offset: Tensor, x_scale: Tensor,
-                    packed_w: Tensor, scale: Tensor, columns: int, *, need_bias: bool):
+                    packed_w: Tensor, scale: Tensor, columns: int, *, need_bias: bool,
+                    need_input: bool = True):
     """All of ``QSTELinearFn.backward``'s products in one call (functional.py:173-194).
 
-    Returns ``(grad_input [samples, columns] in grad's dtype, evidence fp32
-    [rows, columns] already multiplied by the row scale, grad_scale fp32
-    [rows], grad_bias fp32 [rows] or None)``.
+    Returns ``(grad_input [samples, columns] in grad's dtype or None,
+    evidence fp32 [rows, columns] already multiplied by the row scale,
+    grad_scale fp32 [rows], grad_bias fp32 [rows] or None)``.  With
+    ``need_input=False`` the input-gradient product is not computed (autograd
+    asks for no gradient of the layer's input) and grad_input is None.
     """
 
     device = _require_gpu(grad, packed_x, x_offset, x_scale, packed_w, scale)
@@ -316,7 +319,7 @@ def linear_backward(grad: Tensor, packed_x: Tensor, x_offset: Tensor, x_scale: T
     packed_w = _check_packed(packed_w, columns, rows)
     packed_x = _check_packed(packed_x, columns, samples)
     lib = _lib.load()
-    dx = torch.empty(samples, int(columns), dtype=grad.dtype, device=device)
+    dx = torch.empty(samples, int(columns), dtype=grad.dtype, device=device) if need_input else None
     evidence = torch.empty(rows, int(columns), dtype=torch.float32, device=device)
     grad_scale = torch.empty(rows, dtype=torch.float32, device=device)
     grad_bias = torch.empty(rows, dtype=torch.float32, device=device) if need_bias else None

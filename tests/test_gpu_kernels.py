@@ -374,6 +374,47 @@ def test_mfma_products_ragged(rows, cols, m, dt):
     assert rel_l2(f32(dxf), dx) == 0.0
 
 
+# Shapes whose evidence has few output tiles for its K (= tokens): the
+# backward launch splits the evidence's K range and finishes it in a combine
+# pass.  (256, 256, 16384): one tile, 8 ranges; (512, 320, 3000): ragged N
+# and a ragged, shorter last range (2 ranges of 24 and 23 K steps);
+# (1024, 4096, 8192) and (4096, 1024, 8192): the config-2 layers, 2 ranges
+# beside the input gradient, 4 without it.
+SPLIT_SHAPES = [(256, 256, 16384), (512, 320, 3000), (1024, 4096, 8192), (4096, 1024, 8192)]
+
+
+@pytest.mark.parametrize("need_input", [True, False])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("rows,cols,m", SPLIT_SHAPES)
+def test_split_evidence_backward(rows, cols, m, dt, need_input):
+    """Split evidence against the oracle (at the config-2 shapes on 256
+    sampled evidence rows); dX bit for bit equal to the standalone dX
+    product, itself checked against the oracle above and below."""
+
+    print(f"split {rows}x{cols} m={m} {dt} need_input={need_input}", flush=True)
+    packed, x, scale, _, dy = _problem(rows, cols, m, dt, rows + 5 * cols + m)
+    xbits, off, xs = oracle.pack_affine_rows(x)
+    dx, ev, gs, db = K().linear_backward(t(dy, DT[dt]), t(xbits), t(off), t(xs), t(packed), t(scale), cols,
+                                         need_bias=True, need_input=need_input)
+    idx = np.arange(rows)
+    if rows * cols * m > 1 << 31:
+        idx = np.sort(np.random.default_rng(rows + cols).choice(rows, 256, replace=False))
+    dys = np.ascontiguousarray(dy[:, idx])
+    e0 = oracle.evidence(dys, xbits, cols, round_scale(xs, dt)) + oracle.offset_correction(dys, off)[:, None]
+    assert rel_l2(ev.cpu().numpy()[idx], e0 * scale[idx, None]) <= 1e-5
+    want_gs = oracle.row_inner(e0.astype(np.float32), np.ascontiguousarray(packed[idx]), cols)
+    assert rel_l2(gs.cpu().numpy()[idx], want_gs) <= 1e-4
+    assert rel_l2(db.cpu().numpy(), dy.astype(np.float64).sum(0)) <= 1e-5
+    if need_input:
+        alone = K().packed_transpose(t(dy, DT[dt]), t(packed), cols, row_scale=t(scale))
+        assert torch.equal(dx, alone)
+        if len(idx) == rows:
+            want_dx = round_out(oracle.linear_dgrad(dy, packed, cols, round_scale(scale, dt)), dt)
+            assert rel_l2(f32(dx), want_dx) <= 1e-3
+    else:
+        assert dx is None
+
+
 @pytest.mark.parametrize("rows,cols", [(14336, 4096), (4096, 14336)])
 def test_full_size_products_sampled_rows(rows, cols):
     """Config-4 layer shapes, 16384 tokens; oracle on a sample of rows."""

@@ -64,6 +64,13 @@ def test_error_codes_and_workspace_queries_need_no_gpu():
     assert lib.qste_coordinate_update_workspace_bytes(4096, 14336, 256) > 0
     assert lib.qste_coordinate_update_workspace_bytes(0, 8, 256) == 0
     assert lib.qste_linear_backward_workspace_bytes(16384, 14336, 4096) > 0
+    # the split-K plan of the backward's evidence: a one-tile evidence over
+    # 16384 tokens takes 8 K ranges (8 fp32 partials of the 256 x 256
+    # output in the workspace); the config-4 layers take none (a partial
+    # would be 235 MB)
+    assert lib.qste_linear_backward_workspace_bytes(16384, 256, 256) > 8 * 256 * 256 * 4
+    assert lib.qste_linear_backward_workspace_bytes(64, 256, 256) < 256 * 256 * 4
+    assert lib.qste_linear_backward_workspace_bytes(16384, 14336, 4096) < 100 << 20
     # argument errors are reported before any device work
     assert lib.qste_packed_linear_affine(None, 7, None, None, None, None, 1, 1, 8, None) == -1
     assert lib.qste_packed_transpose(None, 2, None, None, None, -1, 4, 8, None) == -2
@@ -94,6 +101,7 @@ class OracleKernels:
 
     def __init__(self):
         self.calls = []
+        self.backward_calls = []
 
     def pack_coordinate(self, coord):
         return torch.from_numpy(oracle.pack_coordinate(coord.numpy()))
@@ -116,16 +124,18 @@ class OracleKernels:
     def packed_row_inner(self, matrix, packed, columns):
         return torch.from_numpy(oracle.row_inner(matrix.float().numpy(), packed.numpy(), columns)).float()
 
-    def linear_backward(self, grad, packed_x, x_offset, x_scale, packed_w, scale, columns, *, need_bias):
+    def linear_backward(self, grad, packed_x, x_offset, x_scale, packed_w, scale, columns, *, need_bias,
+                        need_input=True):
         g = grad.float().numpy()
         s = scale.detach().float().numpy()
+        self.backward_calls.append(need_input)
         dx = oracle.linear_dgrad(g, packed_w.numpy(), columns, s)
         e0 = oracle.decoded_evidence(g, packed_x.numpy(), x_offset.numpy(), x_scale.numpy(), columns)
         gs = oracle.row_inner(e0.astype(np.float32), packed_w.numpy(), columns)
         ev = (e0 * s[:, None]).astype(np.float32)
         db = torch.from_numpy(g.astype(np.float64).sum(0)).float() if need_bias else None
-        return (torch.from_numpy(dx).float().to(grad.dtype), torch.from_numpy(ev),
-                torch.from_numpy(gs).float(), db)
+        dx = torch.from_numpy(dx).float().to(grad.dtype) if need_input else None
+        return dx, torch.from_numpy(ev), torch.from_numpy(gs).float(), db
 
     def coordinate_update(self, gradient, coordinate, packed, moment_q, moment_scale, row_v, col_v, *,
                           beta1, beta2, update_clip, coordinate_lr, block_size, seed, step, flips=None,
@@ -307,6 +317,25 @@ def test_forward_backward_composition(fake):
     e0 = oracle.decoded_evidence(dy.numpy(), bits, off, xs, 24)
     gs = oracle.row_inner(e0.astype(np.float32), packed, 24)
     np.testing.assert_allclose(layer.surface.log_scale.grad.numpy(), gs * s, rtol=1e-4, atol=1e-6)
+
+
+def test_input_gradient_only_when_autograd_asks(fake):
+    import qste_amd as qste
+
+    model = _mlp()
+    qste.convert(model, include=["0", "2"])
+    x = torch.randn(5, 24)
+    dy = torch.randn(5, model[2].out_features)
+    # the first layer's input needs no gradient, the second's does
+    model(x).backward(dy)
+    assert fake.backward_calls == [True, False]
+    fake.backward_calls.clear()
+    xg = x.clone().requires_grad_(True)
+    model(xg).backward(dy)
+    assert fake.backward_calls == [True, True]
+    assert xg.grad is not None and xg.grad.shape == x.shape
+    # the evidence of the first layer is the same either way
+    assert model[0].surface.log_scale.grad is not None
 
 
 def test_optimizer_applies_inside_backward_with_reference_seeds(fake):
