@@ -94,11 +94,17 @@ int qste_packed_transpose(const void* dy, int dtype, const uint8_t* packed,
 /* evidence fp32 [rows, cols] = dy[samples, rows]^T @ (row_scale (*) sign_x),
  * sign_x from packed_x uint8 [samples, (cols+7)/8]; row_scale (fp32
  * [samples], may be NULL) is rounded to dy's dtype as in cuda.py:1625.
+ * workspace: NULL, or at least qste_evidence_from_packed_workspace_bytes()
+ * bytes, with which output tiles whose K (= samples) chain is long against
+ * the launch are split over K and summed in a fixed order (the query
+ * returns 0 where no split pays).
  * Replaces qste.kernels.evidence_from_packed (loader.py:306-313;
  * fallback.py:126-138). */
+size_t qste_evidence_from_packed_workspace_bytes(int64_t samples, int64_t rows, int64_t cols);
 int qste_evidence_from_packed(const void* dy, int dtype, const uint8_t* packed_x,
                               const float* row_scale, float* evidence, int64_t samples,
-                              int64_t rows, int64_t cols, void* stream);
+                              int64_t rows, int64_t cols, void* workspace,
+                              size_t workspace_bytes, void* stream);
 
 /* out fp32 [rows] = sum_c matrix[r, c] * sign[r, c], matrix fp32 [rows, cols].
  * Replaces qste.kernels.packed_row_inner (loader.py:315-320;
@@ -117,9 +123,10 @@ int qste_packed_row_inner(const float* matrix, const uint8_t* packed, float* out
  * x_offset / x_scale are the fp32 [samples] rows of the saved aux.
  * dx may be NULL when no input gradient is wanted (autograd's
  * needs_input_grad); then that product is not computed.
- * Where the evidence has few output tiles for its K (= samples), its K
- * range is split over several workgroups and summed in a fixed order in
- * the workspace, so results do not depend on scheduling.
+ * Per shape, evidence and dx run in one launch or as two, and evidence
+ * tiles whose K (= samples) chain is long against the launch are split over
+ * K and summed in a fixed order in the workspace, so results do not depend
+ * on scheduling.
  * Needs qste_linear_backward_workspace_bytes() bytes of workspace.
  * No counterpart as a single call in the reference: it fuses five of its
  * calls (cuda.py:1568-1688, functional.py:143, 193). */

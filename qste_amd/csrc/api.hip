@@ -29,13 +29,13 @@ int mfma_linear_forward(const void*, int, const uint8_t*, const float*, const fl
 int mfma_linear_dgrad(const void*, int, const uint8_t*, const float*, void*, int64_t, int64_t, int64_t,
                       hipStream_t);
 int mfma_evidence(const void*, int, const uint8_t*, const float*, float*, int64_t, int64_t, int64_t,
-                  const float*, const float*, const uint8_t*, float*, hipStream_t);
+                  const float*, const float*, const uint8_t*, float*, const EvidencePlan*, float*, hipStream_t);
 int64_t mfma_evidence_tiles(int64_t cols);
 bool mfma_pair_ok(const void*, int, int64_t, int64_t, int64_t);
-EvidenceSplit mfma_evidence_split(int64_t, int64_t, int64_t, bool);
+EvidencePlan mfma_evidence_plan(int64_t, int64_t, int64_t, bool);
 int mfma_backward_pair(const void*, int, const uint8_t*, int64_t, const uint16_t*, float*, const uint8_t*, int64_t,
                        const uint16_t*, const uint8_t*, void*, int64_t, int64_t, int64_t, const float*,
-                       const float*, float*, EvidenceSplit, float*, hipStream_t);
+                       const float*, float*, const EvidencePlan&, float*, hipStream_t);
 int launch_transpose_bits(const uint8_t*, uint8_t*, int64_t, int64_t, int64_t, int64_t, hipStream_t);
 int launch_f32_to_16(const float*, uint16_t*, int64_t, int64_t, int, hipStream_t);
 int gemv_linear_forward(const void*, int, const uint8_t*, const float*, const float*, void*, int64_t,
@@ -78,10 +78,10 @@ BackwardLayout backward_layout(int64_t samples, int64_t rows, int64_t cols) {
   l.xs16 = at; at += align_up(sizeof(uint16_t) * static_cast<size_t>((samples + 63) / 64 * 64));
   // split-K partials of the evidence: room for the larger of the plans with
   // and without the input gradient
-  int64_t splits = mfma_evidence_split(samples, rows, cols, true).splits;
-  const int64_t alone = mfma_evidence_split(samples, rows, cols, false).splits;
-  if (alone > splits) splits = alone;
-  l.partial = at; at += splits > 1 ? align_up(sizeof(float) * static_cast<size_t>(splits * rows * cols)) : 0;
+  int64_t partial = mfma_evidence_plan(samples, rows, cols, true).partial_bytes;
+  const int64_t alone = mfma_evidence_plan(samples, rows, cols, false).partial_bytes;
+  if (alone > partial) partial = alone;
+  l.partial = at; at += align_up(static_cast<size_t>(partial));
   l.total = at;
   return l;
 }
@@ -104,10 +104,10 @@ int dgrad_dispatch(const void* dy, int dtype, const uint8_t* packed, const float
 
 int evidence_dispatch(const void* dy, int dtype, const uint8_t* packed_x, const float* x_scale,
                       float* ev, int64_t samples, int64_t rows, int64_t cols, const float* m_add,
-                      const float* m_scale, const uint8_t* w_bits, float* gs_part, int64_t* tiles,
-                      hipStream_t s) {
+                      const float* m_scale, const uint8_t* w_bits, float* gs_part, const EvidencePlan* plan,
+                      float* partial, int64_t* tiles, hipStream_t s) {
   int rc = mfma_evidence(dy, dtype, packed_x, x_scale, ev, samples, rows, cols, m_add, m_scale, w_bits,
-                         gs_part, s);
+                         gs_part, plan, partial, s);
   if (rc != 1) {
     *tiles = mfma_evidence_tiles(cols);
     return rc;
@@ -192,15 +192,25 @@ int qste_packed_transpose(const void* dy, int dtype, const uint8_t* packed, cons
   return dgrad_dispatch(dy, dtype, packed, row_scale, dx, m, rows, cols, as_stream(stream));
 }
 
+size_t qste_evidence_from_packed_workspace_bytes(int64_t samples, int64_t rows, int64_t cols) {
+  if (samples <= 0 || rows <= 0 || cols <= 0) return 0;
+  return static_cast<size_t>(mfma_evidence_plan(samples, rows, cols, false).partial_bytes);
+}
+
 int qste_evidence_from_packed(const void* dy, int dtype, const uint8_t* packed_x, const float* row_scale,
-                              float* evidence, int64_t samples, int64_t rows, int64_t cols, void* stream) {
+                              float* evidence, int64_t samples, int64_t rows, int64_t cols, void* workspace,
+                              size_t workspace_bytes, void* stream) {
   if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
   if (samples < 0 || rows < 0 || cols < 0) return QSTE_E_SHAPE;
   if (rows * cols == 0) return 0;
   if (!evidence || (samples > 0 && (!dy || !packed_x))) return QSTE_E_NULL;
+  // without a workspace the evidence runs unsplit
+  EvidencePlan plan = mfma_evidence_plan(samples, rows, cols, false);
+  if (!workspace) plan.splits = 1;
+  else if (workspace_bytes < static_cast<size_t>(plan.partial_bytes)) return QSTE_E_WORKSPACE;
   int64_t tiles = 0;
   return evidence_dispatch(dy, dtype, packed_x, row_scale, evidence, samples, rows, cols, nullptr, nullptr,
-                           nullptr, nullptr, &tiles, as_stream(stream));
+                           nullptr, nullptr, &plan, static_cast<float*>(workspace), &tiles, as_stream(stream));
 }
 
 int qste_packed_row_inner(const float* matrix, const uint8_t* packed, float* out, int64_t rows,
@@ -238,36 +248,46 @@ int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x, con
     if ((rc = launch_colsums(dy, dtype, x_offset, samples, rows, v_part, grad_bias ? db_part : nullptr, v,
                              grad_bias, s)))
       return rc;
-    // evidence and dgrad (when dx is wanted) together when both take the
-    // MFMA path, from transposed copies of the signs and bf16 copies of the
-    // scales; the evidence split over K ranges where that shortens the launch
+    // MFMA path: the plan runs evidence and dgrad in one launch (from
+    // transposed copies of the signs and bf16 copies of the scales) or as
+    // two, and splits evidence tiles over K where that shortens the work
+    bool dgrad_done = false;
     if (mfma_pair_ok(dy, dtype, samples, rows, cols)) {
-      uint8_t* w_t = reinterpret_cast<uint8_t*>(base + l.w_t);
-      uint8_t* x_t = reinterpret_cast<uint8_t*>(base + l.x_t);
-      uint16_t* s16 = reinterpret_cast<uint16_t*>(base + l.s16);
-      uint16_t* xs16 = reinterpret_cast<uint16_t*>(base + l.xs16);
+      const EvidencePlan plan = mfma_evidence_plan(samples, rows, cols, dx != nullptr);
       float* partial = reinterpret_cast<float*>(base + l.partial);
-      const int64_t pb = (cols + 7) / 8;
-      if (dx) {
+      if (plan.pair) {
+        uint8_t* w_t = reinterpret_cast<uint8_t*>(base + l.w_t);
+        uint8_t* x_t = reinterpret_cast<uint8_t*>(base + l.x_t);
+        uint16_t* s16 = reinterpret_cast<uint16_t*>(base + l.s16);
+        uint16_t* xs16 = reinterpret_cast<uint16_t*>(base + l.xs16);
+        const int64_t pb = (cols + 7) / 8;
         if ((rc = launch_transpose_bits(packed_w, w_t, rows, cols, pb, l.w_t_pitch, s))) return rc;
+        if ((rc = launch_transpose_bits(packed_x, x_t, samples, cols, pb, l.x_t_pitch, s))) return rc;
         if ((rc = launch_f32_to_16(scale, s16, rows, (rows + 63) / 64 * 64, dtype, s))) return rc;
+        if ((rc = launch_f32_to_16(x_scale, xs16, samples, (samples + 63) / 64 * 64, dtype, s))) return rc;
+        rc = mfma_backward_pair(dy, dtype, x_t, l.x_t_pitch, xs16, evidence, w_t, l.w_t_pitch, s16, packed_w, dx,
+                                samples, rows, cols, v, scale, gs_part, plan, partial, s);
+        if (rc == 0) return launch_sum_partials(gs_part, mfma_evidence_tiles(cols), rows, grad_scale, s);
+        if (rc != 1) return rc;
+      } else {
+        if (dx && (rc = dgrad_dispatch(dy, dtype, packed_w, scale, dx, samples, rows, cols, s))) return rc;
+        dgrad_done = true;
+        int64_t tiles = 0;
+        if ((rc = evidence_dispatch(dy, dtype, packed_x, x_scale, evidence, samples, rows, cols, v, scale,
+                                    packed_w, gs_part, &plan, partial, &tiles, s)))
+          return rc;
+        return launch_sum_partials(gs_part, tiles, rows, grad_scale, s);
       }
-      if ((rc = launch_transpose_bits(packed_x, x_t, samples, cols, pb, l.x_t_pitch, s))) return rc;
-      if ((rc = launch_f32_to_16(x_scale, xs16, samples, (samples + 63) / 64 * 64, dtype, s))) return rc;
-      const EvidenceSplit split = mfma_evidence_split(samples, rows, cols, dx != nullptr);
-      rc = mfma_backward_pair(dy, dtype, x_t, l.x_t_pitch, xs16, evidence, w_t, l.w_t_pitch, s16, packed_w, dx,
-                              samples, rows, cols, v, scale, gs_part, split, partial, s);
-      if (rc == 0) return launch_sum_partials(gs_part, mfma_evidence_tiles(cols), rows, grad_scale, s);
-      if (rc != 1) return rc;
     }
-    if (dx && (rc = dgrad_dispatch(dy, dtype, packed_w, scale, dx, samples, rows, cols, s))) return rc;
+    if (dx && !dgrad_done && (rc = dgrad_dispatch(dy, dtype, packed_w, scale, dx, samples, rows, cols, s)))
+      return rc;
   } else {
     if ((rc = fill_zero(v, rows, s))) return rc;
     if (grad_bias && (rc = fill_zero(grad_bias, rows, s))) return rc;
   }
   int64_t tiles = 0;
   if ((rc = evidence_dispatch(dy, dtype, packed_x, x_scale, evidence, samples, rows, cols, v, scale, packed_w,
-                              gs_part, &tiles, s)))
+                              gs_part, nullptr, nullptr, &tiles, s)))
     return rc;
   return launch_sum_partials(gs_part, tiles, rows, grad_scale, s);
 }

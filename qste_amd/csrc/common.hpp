@@ -8,11 +8,18 @@
 
 namespace qste {
 
-// Split-K plan of the backward launch's evidence (gemm_mfma.hip): `splits`
-// K ranges of `ks_steps` 64-sample steps each (the last may be shorter).
-struct EvidenceSplit {
+// How the MFMA path runs a layer's evidence (and dgrad) -- gemm_mfma.hip's
+// mfma_evidence_plan: `pair` runs both products in one launch from
+// transposed sign copies, else they run as two launches; evidence tiles
+// [0, tiles_full) are computed whole and the rest over `splits` K ranges
+// of ks_steps 64-sample steps (the last range may be shorter), finished by
+// a combine pass that needs partial_bytes of workspace.
+struct EvidencePlan {
+  int pair;
+  int tiles_full;
   int splits;
   int ks_steps;
+  int64_t partial_bytes;
 };
 
 constexpr int kWave = 64;

@@ -22,6 +22,8 @@
 // + i] and B[8(l/32) + i][l%32], i = 0..7; the accumulator's register r
 // holds D[8(r/4) + 4(l/32) + r%4][l%32].
 #include <map>
+#include <mutex>
+#include <vector>
 
 #include "common.hpp"
 
@@ -550,18 +552,16 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   stage_barrier<0>();
 
   if (EPI == EPI_PARTIAL) {
-    // 32 lanes x 4 bytes per row per store, as the evidence epilogue
+    // the tile's BM x BN accumulators, row-major at p.out (32 lanes x 4
+    // bytes per row per store, as the evidence epilogue)
     float* part = static_cast<float*>(p.out);
 #pragma unroll
     for (int mb = 0; mb < MBN; ++mb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + WMR * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
+        const int lrow = WMR * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
 #pragma unroll
-        for (int nb = 0; nb < NBN; ++nb) {
-          const int64_t col = n0 + WNC * wn + 32 * nb + l32;
-          if (row < p.M && col < p.N) part[row * p.N + col] = acc[mb][nb][r];
-        }
+        for (int nb = 0; nb < NBN; ++nb) part[lrow * BN + WNC * wn + 32 * nb + l32] = acc[mb][nb][r];
       }
     return;
   }
@@ -727,66 +727,115 @@ __global__ __launch_bounds__(THREADS, 1) void wide_kernel(Params p) {
   wide_tile<AKIND, BKIND, EPI, DT>(p, blockIdx.x, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
 }
 
+// Split-K evidence, for tiles whose K chain is long against the launch:
+// workgroups [0, tiles_full) compute tiles 0 .. tiles_full-1 whole; the
+// remaining ns = tiles_e - tiles_full tiles are cut into `splits` K ranges
+// of ks_steps K steps, workgroup tiles_full + j * ns + i covering tile
+// tiles_full + i over range j and storing its bare accumulators in slab
+// j * ns + i of `partial` (BM x BN fp32 each) for evidence_combine_kernel.
+struct Split {
+  int tiles_full, tiles_e, splits, ks_steps;
+  float* partial;
+};
+
+// The evidence Params of K range j (rows of dy and of the K-indexed
+// operands from k0 = j * ks_steps * BK on); bits along N are rows of K,
+// bits along K (scaled) a transposed copy whose bit k0 starts byte k0 / 8.
+template <int BKIND>
+__device__ __forceinline__ Params range_params(const Params& p, int j, int ks_steps) {
+  const int64_t k0 = static_cast<int64_t>(j) * ks_steps * BK;
+  Params q = p;
+  q.a = p.a + k0 * p.lda;  // A as rows of K
+  q.a_rows = p.a_rows - k0;
+  if (BKIND == B_BITS_ALONG_N) {
+    q.bits = p.bits + k0 * p.pb;
+    q.bit_rows = p.bit_rows - k0;
+    q.kscale = p.kscale ? p.kscale + k0 : nullptr;
+  } else {
+    q.bits = p.bits + k0 / 8;  // k0 % 64 == 0
+    q.kscale16 = p.kscale16 + k0;
+  }
+  const int64_t left = p.K - k0, span = static_cast<int64_t>(ks_steps) * BK;
+  q.K = left < span ? left : span;  // the host makes every range nonempty
+  return q;
+}
+
+// Workgroup e >= tiles_full of a split evidence grid: one K range of one tile.
+template <int BKIND, int DT>
+__device__ __forceinline__ void evidence_range(const Params& p, const Split& sp, int e, uint8_t* A0, uint8_t* A1,
+                                               uint8_t* A2, uint8_t* A3, uint8_t* B0, uint8_t* B1, uint8_t* B2,
+                                               uint8_t* B3, uint16_t* Sc) {
+  const int ns = sp.tiles_e - sp.tiles_full, r = e - sp.tiles_full;
+  const int j = r / ns, i = r - j * ns;
+  Params q = range_params<BKIND>(p, j, sp.ks_steps);
+  q.out = sp.partial + (static_cast<int64_t>(j) * ns + i) * (BM * BN);
+  wide_tile<A_ROWS_K, BKIND, EPI_PARTIAL, DT>(q, sp.tiles_full + i, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
+}
+
+// The evidence alone (A = dy^T as stored, bits along N with the fp32 per-k
+// scale), some tiles split over K.
+template <int DT>
+__global__ __launch_bounds__(THREADS, 1) void evidence_split_kernel(Params p, Split sp) {
+  using SZ = StageSizes<A_ROWS_K, B_BITS_ALONG_N>;
+  QSTE_WIDE_STAGES(SZ::a, SZ::b, SZ::s)
+  const int e = static_cast<int>(blockIdx.x);
+  if (e < sp.tiles_full)
+    wide_tile<A_ROWS_K, B_BITS_ALONG_N, EPI_EVIDENCE, DT>(p, e, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
+  else
+    evidence_range<B_BITS_ALONG_N, DT>(p, sp, e, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
+}
+
 // The two large products of a layer's backward in one launch: evidence
 // tiles first (the longer ones), then dgrad tiles, so the grid's last wave
 // of one product is filled by the other instead of leaving CUs idle.  Both
 // take their signs as transposed copies (bits along K) with bf16 per-k
-// scales, prepared by the caller.  SPLIT: the evidence's K range is cut
-// into `splits` ranges of ks_steps K steps; workgroup e covers tile
-// e % tiles_e over range e / tiles_e and stores its bare accumulators in
-// partial[range] ([M][N] fp32 each) for evidence_combine_kernel.
+// scales, prepared by the caller.  SPLIT: every evidence tile is split
+// (tiles_full == 0): tiles_e * splits range workgroups, then dgrad.
 template <int DT, bool SPLIT>
-__global__ __launch_bounds__(THREADS, 1) void backward_pair_kernel(Params pe, Params pd, int tiles_e, int splits,
-                                                                   int ks_steps, float* partial) {
+__global__ __launch_bounds__(THREADS, 1) void backward_pair_kernel(Params pe, Params pd, Split sp) {
   QSTE_WIDE_STAGES(A_STAGE_K, B_STAGE, 4 * BK)
   const int e = static_cast<int>(blockIdx.x);
   if (!SPLIT) {
-    if (e < tiles_e)
+    if (e < sp.tiles_e)
       wide_tile<A_ROWS_K, B_BITS_ALONG_K_SCALED, EPI_EVIDENCE, DT>(pe, e, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
     else
-      wide_tile<A_ROWS_M, B_BITS_ALONG_K_SCALED, EPI_PLAIN, DT>(pd, e - tiles_e, A0, A1, A2, A3, B0, B1, B2, B3,
-                                                                Sc);
-  } else if (e < tiles_e * splits) {
-    const int j = e / tiles_e;
-    const int64_t k0 = static_cast<int64_t>(j) * ks_steps * BK;
-    Params q = pe;
-    q.a = pe.a + k0 * pe.lda;          // dy rows k0 .. (A as rows of K)
-    q.a_rows = pe.a_rows - k0;
-    q.bits = pe.bits + k0 / 8;         // bit k0 of every transposed row (k0 % 64 == 0)
-    q.kscale16 = pe.kscale16 + k0;
-    const int64_t left = pe.K - k0, span = static_cast<int64_t>(ks_steps) * BK;
-    q.K = left < span ? left : span;   // the host makes every range nonempty
-    q.out = partial + static_cast<int64_t>(j) * pe.M * pe.N;
-    wide_tile<A_ROWS_K, B_BITS_ALONG_K_SCALED, EPI_PARTIAL, DT>(q, e - j * tiles_e, A0, A1, A2, A3, B0, B1, B2, B3,
+      wide_tile<A_ROWS_M, B_BITS_ALONG_K_SCALED, EPI_PLAIN, DT>(pd, e - sp.tiles_e, A0, A1, A2, A3, B0, B1, B2, B3,
                                                                 Sc);
   } else {
-    wide_tile<A_ROWS_M, B_BITS_ALONG_K_SCALED, EPI_PLAIN, DT>(pd, e - tiles_e * splits, A0, A1, A2, A3, B0, B1,
-                                                              B2, B3, Sc);
+    const int ge = sp.tiles_e * sp.splits;
+    if (e < ge)
+      evidence_range<B_BITS_ALONG_K_SCALED, DT>(pe, sp, e, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
+    else
+      wide_tile<A_ROWS_M, B_BITS_ALONG_K_SCALED, EPI_PLAIN, DT>(pd, e - ge, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
   }
 }
 
-// The evidence epilogue over split-K partials: E0 = sum of the ranges'
-// partials (in range order) + m_add[m]; E = E0 * m_scale[m]; and the
-// scale-gradient partials sum_c E0 * sign_w over each 64-column slot, in the
-// slots the fused epilogue writes ([WAVES_N * tiles_n][M], zero past N).
-// One workgroup per (row, 256 columns), one wave per slot.
-__global__ __launch_bounds__(THREADS) void evidence_combine_kernel(const float* __restrict__ partial, int splits,
-                                                                   const float* __restrict__ m_add,
+// The evidence epilogue of the split tiles: E0 = the tile's range partials
+// summed in range order + m_add[m]; E = E0 * m_scale[m]; and the
+// scale-gradient partials sum_c E0 * sign_w over each 64-column slot, in
+// the slots the fused epilogue writes ([WAVES_N * tiles_n][M]).  One
+// workgroup per (tile row, split tile), one wave per slot.
+__global__ __launch_bounds__(THREADS) void evidence_combine_kernel(Split sp, const float* __restrict__ m_add,
                                                                    const float* __restrict__ m_scale,
                                                                    const uint8_t* __restrict__ w_bits, int64_t w_pb,
                                                                    float* __restrict__ ev,
                                                                    float* __restrict__ gs_partial, int64_t M,
                                                                    int64_t N) {
-  const int64_t row = blockIdx.x;
-  const int64_t col = static_cast<int64_t>(blockIdx.y) * BN + threadIdx.x;
-  const int64_t slot = static_cast<int64_t>(blockIdx.y) * WAVES_N + threadIdx.x / kWave;
+  const int tiles_m = static_cast<int>((M + BM - 1) / BM), tiles_n = static_cast<int>((N + BN - 1) / BN);
+  const int ns = sp.tiles_e - sp.tiles_full, i = static_cast<int>(blockIdx.y);
+  int tm, tn;
+  tile_of(sp.tiles_full + i, tiles_m, tiles_n, tm, tn);
+  const int64_t row = static_cast<int64_t>(tm) * BM + blockIdx.x;
+  if (row >= M) return;  // the whole workgroup
+  const int64_t col = static_cast<int64_t>(tn) * BN + threadIdx.x;
+  const int64_t slot = static_cast<int64_t>(tn) * WAVES_N + threadIdx.x / kWave;
+  const int64_t at = static_cast<int64_t>(i) * (BM * BN) + static_cast<int64_t>(blockIdx.x) * BN + threadIdx.x;
   float signed_e0 = 0.0f;
   if (col < N) {
-    const int64_t at = row * N + col;
-    float s = partial[at];
-    for (int j = 1; j < splits; ++j) s += partial[static_cast<int64_t>(j) * M * N + at];
+    float s = sp.partial[at];
+    for (int j = 1; j < sp.splits; ++j) s += sp.partial[static_cast<int64_t>(j) * ns * (BM * BN) + at];
     const float e0 = s + (m_add ? m_add[row] : 0.0f);
-    ev[at] = e0 * (m_scale ? m_scale[row] : 1.0f);
+    ev[row * N + col] = e0 * (m_scale ? m_scale[row] : 1.0f);
     if (w_bits) signed_e0 = ((w_bits[row * w_pb + (col >> 3)] >> (col & 7)) & 1u) ? e0 : -e0;
   }
   const float tot = wave_sum(signed_e0);
@@ -854,6 +903,16 @@ static mfma::Params evidence_params(const void* dy, const uint8_t* packed_x, con
   return p;
 }
 
+// The combine pass of a split evidence: one workgroup per (tile row, split tile).
+static int launch_combine(const mfma::wide::Split& sp, const float* m_add, const float* m_scale,
+                          const uint8_t* w_bits, float* ev, float* gs_partial, int64_t rows, int64_t cols,
+                          hipStream_t stream) {
+  const dim3 grid(mfma::wide::BM, static_cast<unsigned>(sp.tiles_e - sp.tiles_full));
+  mfma::wide::evidence_combine_kernel<<<grid, mfma::wide::THREADS, 0, stream>>>(sp, m_add, m_scale, w_bits, cols / 8,
+                                                                               ev, gs_partial, rows, cols);
+  return static_cast<int>(hipGetLastError());
+}
+
 int mfma_linear_forward(const void* x, int dtype, const uint8_t* packed, const float* scale,
                         const float* bias, void* y, int64_t m, int64_t rows, int64_t cols,
                         hipStream_t stream) {
@@ -892,16 +951,30 @@ int64_t mfma_evidence_tiles(int64_t cols) { return mfma::wide::WAVES_N * ((cols 
 
 int mfma_evidence(const void* dy, int dtype, const uint8_t* packed_x, const float* x_scale, float* ev,
                   int64_t samples, int64_t rows, int64_t cols, const float* m_add, const float* m_scale,
-                  const uint8_t* w_bits, float* gs_partial, hipStream_t stream) {
+                  const uint8_t* w_bits, float* gs_partial, const EvidencePlan* plan, float* partial,
+                  hipStream_t stream) {
   if (!evidence_ok(dy, dtype, packed_x, samples, rows, cols)) return 1;
   const mfma::Params p =
       evidence_params(dy, packed_x, x_scale, ev, samples, rows, cols, m_add, m_scale, w_bits, gs_partial);
+  const int te = wide_grid(rows, cols);
+  if (plan && plan->splits > 1) {
+    if (!partial) return QSTE_E_WORKSPACE;
+    const mfma::wide::Split sp{plan->tiles_full, te, plan->splits, plan->ks_steps, partial};
+    const int grid = sp.tiles_full + (te - sp.tiles_full) * sp.splits;
+    if (dtype == QSTE_F16)
+      mfma::wide::evidence_split_kernel<QSTE_F16><<<grid, mfma::wide::THREADS, 0, stream>>>(p, sp);
+    else
+      mfma::wide::evidence_split_kernel<QSTE_BF16><<<grid, mfma::wide::THREADS, 0, stream>>>(p, sp);
+    int rc = static_cast<int>(hipGetLastError());
+    if (rc) return rc;
+    return launch_combine(sp, m_add, m_scale, w_bits, ev, gs_partial, rows, cols, stream);
+  }
   if (dtype == QSTE_F16)
     mfma::wide::wide_kernel<mfma::A_ROWS_K, mfma::B_BITS_ALONG_N, mfma::EPI_EVIDENCE, QSTE_F16>
-        <<<wide_grid(rows, cols), mfma::wide::THREADS, 0, stream>>>(p);
+        <<<te, mfma::wide::THREADS, 0, stream>>>(p);
   else
     mfma::wide::wide_kernel<mfma::A_ROWS_K, mfma::B_BITS_ALONG_N, mfma::EPI_EVIDENCE, QSTE_BF16>
-        <<<wide_grid(rows, cols), mfma::wide::THREADS, 0, stream>>>(p);
+        <<<te, mfma::wide::THREADS, 0, stream>>>(p);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -913,27 +986,33 @@ bool mfma_pair_ok(const void* dy, int dtype, int64_t samples, int64_t rows, int6
 }
 
 // ---------------------------------------------------------------------------
-// split-K plan for the evidence of the backward launch
+// evidence plan: one launch or two, and which tiles split over K
 // ---------------------------------------------------------------------------
 // The evidence's K is the token count, usually its longest dimension, and
-// its tile count rows/256 x cols/256 can be far below the CU count (64 tiles
-// at 4096 x 1024): then each tile is a long serial chain while most CUs
-// idle.  The plan picks the number of K ranges S (1, 2, 4 or 8) that
-// minimises an estimate of the launch: list scheduling of S x tiles_e
-// ranges of nk/S steps, then the dgrad tiles, on kCUs CUs (each tile
-// costing kTileOverhead steps more for its prologue and epilogue), plus the
-// combine pass's HBM traffic in step units.  The plan depends only on the
-// shape, so the workspace query and the call agree.
+// its tile count rows/256 x cols/256 can be small against the CU count (64
+// tiles at 4096 x 1024) or leave a partial last round (896 = 3.5 x 256 at
+// config 4): then long serial tile chains set the launch's length while
+// CUs idle.  The plan cuts the last tiles (or all of them) into S = 2, 4 or
+// 8 K ranges when that shortens the work, and runs dgrad either in the same
+// launch (the backward pair, which fills the evidence's idle CUs) or as a
+// second launch (no sign transposes, and its per-step speed is ~8% higher:
+// measured at config 4's shapes).  The choice minimises an estimate: list
+// scheduling of the tiles on kCUs CUs, in K steps, each tile costing
+// kTileOverhead steps more for its prologue and epilogue, plus the combine
+// pass's HBM traffic in step units.  It depends only on the shape, so the
+// workspace query and the call agree.
 namespace {
-constexpr int kCUs = 256;              // MI350X / MI355X
-constexpr int64_t kTileOverhead = 14;  // K steps a tile's prologue + epilogue cost
-constexpr double kBytesPerStep = 7.5e6;  // combine traffic per K-step time (~5 TB/s x 1.5 us)
+constexpr int64_t kCUs = 256;              // MI350X / MI355X
+constexpr int64_t kTileOverhead = 14;      // K steps a tile's prologue + epilogue cost
+constexpr double kBytesPerStep = 7.5e6;    // combine traffic per K-step time (~5 TB/s x 1.5 us)
+constexpr double kPairFactor = 1.08;       // the pair's K steps are this much slower
 constexpr int64_t kMaxPartialBytes = int64_t{1} << 30;
+constexpr int64_t kTileBytes = int64_t{mfma::wide::BM} * mfma::wide::BN * 4;
 
-// Greedy in-order assignment of `groups` (count, length) onto kCUs CUs that
-// start idle; returns the finish time of the last CU.
+// Greedy in-order assignment of `n` groups of (count, length) items onto
+// kCUs CUs that start idle; returns the finish time of the last CU.
 int64_t list_schedule(const int64_t (*groups)[2], int n) {
-  std::map<int64_t, int64_t> free_at{{0, kCUs}};  // time -> idle CUs from then
+  std::map<int64_t, int64_t> free_at{{0, kCUs}};  // time -> CUs idle from then
   for (int g = 0; g < n; ++g) {
     int64_t left = groups[g][0];
     const int64_t len = groups[g][1];
@@ -951,47 +1030,86 @@ int64_t list_schedule(const int64_t (*groups)[2], int n) {
 }
 }  // namespace
 
-EvidenceSplit mfma_evidence_split(int64_t samples, int64_t rows, int64_t cols, bool with_dgrad) {
-  EvidenceSplit best{1, 0};
-  if (samples <= 0 || rows <= 0 || cols <= 0) return best;
+static EvidencePlan compute_plan(int64_t samples, int64_t rows, int64_t cols, bool with_dgrad) {
   const int64_t nk = (samples + mfma::wide::BK - 1) / mfma::wide::BK;
   const int64_t te = wide_grid(rows, cols), td = with_dgrad ? wide_grid(samples, cols) : 0;
   const int64_t nkd = (rows + mfma::wide::BK - 1) / mfma::wide::BK;
-  best.ks_steps = static_cast<int>(nk);
-  double best_cost = 0.0;
+  EvidencePlan best{0, static_cast<int>(te), 1, static_cast<int>(nk), 0};
+  if (samples <= 0 || rows <= 0 || cols <= 0) return best;
+  const int64_t dgrad[1][2] = {{td, nkd + kTileOverhead}};
+  const double dgrad_alone = td ? static_cast<double>(list_schedule(dgrad, 1)) : 0.0;
+  double best_cost = -1.0;
   for (int S = 1; S <= 8; S *= 2) {
     const int64_t ks = (nk + S - 1) / S;
     if (S > 1 && ks < 16) break;  // ranges shorter than 16 K steps are mostly overhead
     const int64_t splits = (nk + ks - 1) / ks;  // every range nonempty
-    if (S > 1 && splits * rows * cols * 4 > kMaxPartialBytes) break;
-    const int64_t groups[2][2] = {{te * splits, ks + kTileOverhead}, {td, nkd + kTileOverhead}};
-    double cost = static_cast<double>(list_schedule(groups, 2));
-    if (splits > 1) cost += static_cast<double>((splits + 1) * rows * cols * 4) / kBytesPerStep + 2.0;
-    if (S == 1 || cost < best_cost) {
-      best_cost = cost;
-      best.splits = static_cast<int>(splits);
-      best.ks_steps = static_cast<int>(ks);
+    // whole tiles: all (no split), or all of the full rounds, or one round fewer, or none
+    int64_t fulls[3] = {te, -1, -1};
+    if (S > 1) {
+      const int64_t rounds = te / kCUs * kCUs;
+      fulls[0] = 0;
+      fulls[1] = rounds < te && rounds > 0 ? rounds : -1;
+      fulls[2] = rounds - kCUs > 0 && rounds < te ? rounds - kCUs : -1;
+    }
+    for (int64_t F : fulls) {
+      if (F < 0) continue;
+      const int64_t ns = te - F;
+      const int64_t partial = S > 1 ? splits * ns * kTileBytes : 0;
+      if (partial > kMaxPartialBytes) continue;
+      const double combine = S > 1 ? static_cast<double>((splits + 1) * ns * kTileBytes) / kBytesPerStep + 2.0 : 0.0;
+      const int64_t groups[3][2] = {{S > 1 ? F : te, nk + kTileOverhead},
+                                    {S > 1 ? ns * splits : 0, ks + kTileOverhead},
+                                    {td, nkd + kTileOverhead}};
+      // the pair launch splits all of its evidence tiles or none
+      for (int pair = 0; pair <= (td > 0 && (S == 1 || F == 0) ? 1 : 0); ++pair) {
+        const double cost = pair ? static_cast<double>(list_schedule(groups, 3)) * kPairFactor + combine
+                                 : static_cast<double>(list_schedule(groups, 2)) + combine + dgrad_alone;
+        if (best_cost < 0.0 || cost < best_cost) {
+          best_cost = cost;
+          best = EvidencePlan{pair, static_cast<int>(S > 1 ? F : te), static_cast<int>(splits),
+                              static_cast<int>(ks), partial};
+        }
+      }
     }
   }
   return best;
 }
 
-// Evidence (with its fused epilogue) and, when dx is given, dgrad of one
-// layer in one launch, from transposed sign copies: x_t [cols][x_t_pitch]
-// (bit k of row c = sign of x[k][c]) and w_t [cols][w_t_pitch] (bit r of
-// row c = sign of W[r][c]), both zero past their K, and bf16 copies of
-// x_scale and scale, zero-padded to a multiple of 64 entries.  `split` is
-// mfma_evidence_split's plan for the shape; with more than one range,
-// `partial` holds split.splits x rows x cols floats.  Returns 1 when either
-// product is not for this path.
+// Plans are looked up per shape (every training step asks for the same few
+// shapes, each several times per layer).
+EvidencePlan mfma_evidence_plan(int64_t samples, int64_t rows, int64_t cols, bool with_dgrad) {
+  struct Entry {
+    int64_t samples, rows, cols;
+    bool with_dgrad;
+    EvidencePlan plan;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const Entry& e : cache)
+    if (e.samples == samples && e.rows == rows && e.cols == cols && e.with_dgrad == with_dgrad) return e.plan;
+  const EvidencePlan plan = compute_plan(samples, rows, cols, with_dgrad);
+  if (cache.size() >= 256) cache.erase(cache.begin());
+  cache.push_back(Entry{samples, rows, cols, with_dgrad, plan});
+  return plan;
+}
+
+// Evidence (with its fused epilogue) and dgrad of one layer in one launch,
+// from transposed sign copies: x_t [cols][x_t_pitch] (bit k of row c = sign
+// of x[k][c]) and w_t [cols][w_t_pitch] (bit r of row c = sign of W[r][c]),
+// both zero past their K, and bf16 copies of x_scale and scale, zero-padded
+// to a multiple of 64 entries.  `plan` is mfma_evidence_plan's for the
+// shape (with pair set); its split tiles need plan.partial_bytes at
+// `partial`.  Returns 1 when either product is not for this path.
 int mfma_backward_pair(const void* dy, int dtype, const uint8_t* x_t, int64_t x_t_pitch, const uint16_t* x_scale16,
                        float* ev, const uint8_t* w_t, int64_t w_t_pitch, const uint16_t* scale16,
                        const uint8_t* packed_w, void* dx, int64_t samples, int64_t rows, int64_t cols,
-                       const float* m_add, const float* scale, float* gs_partial, EvidenceSplit split,
+                       const float* m_add, const float* scale, float* gs_partial, const EvidencePlan& plan,
                        float* partial, hipStream_t stream) {
-  if (!evidence_ok(dy, dtype, x_t, samples, rows, cols) || !fits32(cols * x_t_pitch)) return 1;
-  if (dx && (!dgrad_ok(dy, dtype, w_t, samples, rows, cols) || !fits32(cols * w_t_pitch))) return 1;
-  if (split.splits < 1 || (split.splits > 1 && !partial)) return QSTE_E_WORKSPACE;
+  if (!evidence_ok(dy, dtype, x_t, samples, rows, cols) || !fits32(cols * x_t_pitch) || !dx ||
+      !dgrad_ok(dy, dtype, w_t, samples, rows, cols) || !fits32(cols * w_t_pitch))
+    return 1;
+  if (plan.splits > 1 && !partial) return QSTE_E_WORKSPACE;
   mfma::Params pe{};
   pe.a = static_cast<const uint16_t*>(dy);
   pe.bits = x_t;
@@ -1009,28 +1127,21 @@ int mfma_backward_pair(const void* dy, int dtype, const uint8_t* x_t, int64_t x_
   pd.M = samples; pd.N = cols; pd.K = rows;
   pd.lda = rows; pd.pb = w_t_pitch;
   pd.a_rows = samples; pd.bit_rows = cols;
-  const int te = wide_grid(rows, cols), td = dx ? wide_grid(samples, cols) : 0;
-  const int grid = te * split.splits + td;
-  const dim3 g(grid), b(mfma::wide::THREADS);
+  const int te = wide_grid(rows, cols), td = wide_grid(samples, cols);
+  const bool split = plan.splits > 1;
+  const mfma::wide::Split sp{split ? plan.tiles_full : te, te, split ? plan.splits : 1, plan.ks_steps,
+                             split ? partial : nullptr};
+  const dim3 g(sp.tiles_full + (te - sp.tiles_full) * sp.splits + td), b(mfma::wide::THREADS);
   if (dtype == QSTE_F16) {
-    if (split.splits > 1)
-      mfma::wide::backward_pair_kernel<QSTE_F16, true><<<g, b, 0, stream>>>(pe, pd, te, split.splits,
-                                                                           split.ks_steps, partial);
-    else
-      mfma::wide::backward_pair_kernel<QSTE_F16, false><<<g, b, 0, stream>>>(pe, pd, te, 1, 0, nullptr);
+    if (split) mfma::wide::backward_pair_kernel<QSTE_F16, true><<<g, b, 0, stream>>>(pe, pd, sp);
+    else mfma::wide::backward_pair_kernel<QSTE_F16, false><<<g, b, 0, stream>>>(pe, pd, sp);
   } else {
-    if (split.splits > 1)
-      mfma::wide::backward_pair_kernel<QSTE_BF16, true><<<g, b, 0, stream>>>(pe, pd, te, split.splits,
-                                                                            split.ks_steps, partial);
-    else
-      mfma::wide::backward_pair_kernel<QSTE_BF16, false><<<g, b, 0, stream>>>(pe, pd, te, 1, 0, nullptr);
+    if (split) mfma::wide::backward_pair_kernel<QSTE_BF16, true><<<g, b, 0, stream>>>(pe, pd, sp);
+    else mfma::wide::backward_pair_kernel<QSTE_BF16, false><<<g, b, 0, stream>>>(pe, pd, sp);
   }
   int rc = static_cast<int>(hipGetLastError());
-  if (rc || split.splits == 1) return rc;
-  const dim3 cgrid(static_cast<unsigned>(rows), static_cast<unsigned>((cols + mfma::wide::BN - 1) / mfma::wide::BN));
-  mfma::wide::evidence_combine_kernel<<<cgrid, mfma::wide::THREADS, 0, stream>>>(
-      partial, split.splits, m_add, scale, packed_w, cols / 8, ev, gs_partial, rows, cols);
-  return static_cast<int>(hipGetLastError());
+  if (rc || !split) return rc;
+  return launch_combine(sp, m_add, scale, packed_w, ev, gs_partial, rows, cols, stream);
 }
 
 }  // namespace qste

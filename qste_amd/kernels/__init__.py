@@ -279,9 +279,12 @@ def evidence_from_packed(grad: Tensor, packed: Tensor, columns: int,
     grad = grad.contiguous()
     out = torch.empty(rows, int(columns), dtype=torch.float32, device=device)
     row_scale_f32 = _f32(row_scale)  # held until the launch is queued
-    code = _lib.load().qste_evidence_from_packed(
+    lib = _lib.load()
+    nbytes = lib.qste_evidence_from_packed_workspace_bytes(samples, rows, int(columns))
+    work = _workspace(nbytes, device) if nbytes else None
+    code = lib.qste_evidence_from_packed(
         _ptr(grad), _dtype_code(grad), _ptr(packed), _ptr(row_scale_f32), _ptr(out), samples,
-        rows, int(columns), _stream(device))
+        rows, int(columns), _ptr(work), 0 if work is None else work.numel(), _stream(device))
     _lib.check(code, "evidence_from_packed")
     return out
 

@@ -36,7 +36,8 @@ SIGNATURES = {
     "qste_pack_affine_rows": (_int, [_vp, _int, _vp, _vp, _vp, _i64, _i64, _vp]),
     "qste_packed_linear_affine": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "qste_packed_transpose": (_int, [_vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
-    "qste_evidence_from_packed": (_int, [_vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "qste_evidence_from_packed_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "qste_evidence_from_packed": (_int, [_vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
     "qste_packed_row_inner": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "qste_linear_backward_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "qste_linear_backward": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,

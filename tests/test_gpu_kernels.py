@@ -374,13 +374,15 @@ def test_mfma_products_ragged(rows, cols, m, dt):
     assert rel_l2(f32(dxf), dx) == 0.0
 
 
-# Shapes whose evidence has few output tiles for its K (= tokens): the
-# backward launch splits the evidence's K range and finishes it in a combine
-# pass.  (256, 256, 16384): one tile, 8 ranges; (512, 320, 3000): ragged N
-# and a ragged, shorter last range (2 ranges of 24 and 23 K steps);
-# (1024, 4096, 8192) and (4096, 1024, 8192): the config-2 layers, 2 ranges
-# beside the input gradient, 4 without it.
-SPLIT_SHAPES = [(256, 256, 16384), (512, 320, 3000), (1024, 4096, 8192), (4096, 1024, 8192)]
+# Shapes whose evidence tiles have long K (= tokens) chains against the
+# launch: tiles split over K ranges, finished by a combine pass.
+# (256, 256, 16384): one tile, 8 ranges; (512, 320, 3000): ragged N and a
+# shorter last range (24 and 23 K steps); (1024, 4096, 8192) and
+# (4096, 1024, 8192): the config-2 layers (all 64 tiles split, beside dX in
+# one launch or alone); (4160, 4096, 2048): 272 tiles, ragged M, the first
+# 256 whole and the last 16 split in two.
+SPLIT_SHAPES = [(256, 256, 16384), (512, 320, 3000), (1024, 4096, 8192), (4096, 1024, 8192),
+                (4160, 4096, 2048)]
 
 
 @pytest.mark.parametrize("need_input", [True, False])
@@ -413,6 +415,23 @@ def test_split_evidence_backward(rows, cols, m, dt, need_input):
             assert rel_l2(f32(dx), want_dx) <= 1e-3
     else:
         assert dx is None
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("rows,cols,m", SPLIT_SHAPES)
+def test_split_evidence_alone(rows, cols, m, dt):
+    """evidence_from_packed with its split workspace, against the oracle
+    (on 256 sampled rows at the larger shapes)."""
+
+    print(f"split evidence {rows}x{cols} m={m} {dt}", flush=True)
+    _, x, _, _, dy = _problem(rows, cols, m, dt, 3 * rows + cols + m)
+    xbits, _, xs = oracle.pack_affine_rows(x)
+    ev = K().evidence_from_packed(t(dy, DT[dt]), t(xbits), cols, row_scale=t(xs)).cpu().numpy()
+    idx = np.arange(rows)
+    if rows * cols * m > 1 << 31:
+        idx = np.sort(np.random.default_rng(rows).choice(rows, 256, replace=False))
+    want = oracle.evidence(np.ascontiguousarray(dy[:, idx]), xbits, cols, round_scale(xs, dt))
+    assert rel_l2(ev[idx], want) <= 1e-5
 
 
 @pytest.mark.parametrize("rows,cols", [(14336, 4096), (4096, 14336)])

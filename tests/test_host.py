@@ -64,13 +64,16 @@ def test_error_codes_and_workspace_queries_need_no_gpu():
     assert lib.qste_coordinate_update_workspace_bytes(4096, 14336, 256) > 0
     assert lib.qste_coordinate_update_workspace_bytes(0, 8, 256) == 0
     assert lib.qste_linear_backward_workspace_bytes(16384, 14336, 4096) > 0
-    # the split-K plan of the backward's evidence: a one-tile evidence over
-    # 16384 tokens takes 8 K ranges (8 fp32 partials of the 256 x 256
-    # output in the workspace); the config-4 layers take none (a partial
-    # would be 235 MB)
-    assert lib.qste_linear_backward_workspace_bytes(16384, 256, 256) > 8 * 256 * 256 * 4
-    assert lib.qste_linear_backward_workspace_bytes(64, 256, 256) < 256 * 256 * 4
-    assert lib.qste_linear_backward_workspace_bytes(16384, 14336, 4096) < 100 << 20
+    # the split-K plan of the evidence (fp32 partials of 256 x 256 tiles in
+    # the workspace): a one-tile evidence over 16384 tokens takes 8 K
+    # ranges; config 4's 896 tiles (3.5 rounds of 256 CUs) split their last
+    # 128 tiles in two; a short K splits nothing
+    tile = 256 * 256 * 4
+    assert lib.qste_evidence_from_packed_workspace_bytes(16384, 256, 256) == 8 * tile
+    assert lib.qste_linear_backward_workspace_bytes(16384, 256, 256) > 8 * tile
+    assert lib.qste_evidence_from_packed_workspace_bytes(16384, 14336, 4096) == 2 * 128 * tile
+    assert lib.qste_evidence_from_packed_workspace_bytes(64, 256, 256) == 0
+    assert lib.qste_linear_backward_workspace_bytes(64, 256, 256) < tile
     # argument errors are reported before any device work
     assert lib.qste_packed_linear_affine(None, 7, None, None, None, None, 1, 1, 8, None) == -1
     assert lib.qste_packed_transpose(None, 2, None, None, None, -1, 4, 8, None) == -2
