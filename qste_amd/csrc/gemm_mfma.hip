@@ -813,33 +813,45 @@ __global__ __launch_bounds__(THREADS, 1) void backward_pair_kernel(Params pe, Pa
 // The evidence epilogue of the split tiles: E0 = the tile's range partials
 // summed in range order + m_add[m]; E = E0 * m_scale[m]; and the
 // scale-gradient partials sum_c E0 * sign_w over each 64-column slot, in
-// the slots the fused epilogue writes ([WAVES_N * tiles_n][M]).  One
-// workgroup per (tile row, split tile), one wave per slot.
+// the slots the fused epilogue writes ([WAVES_N * tiles_n][M]).  One wave
+// per tile row (4 columns per lane, 16-byte accesses; N % 64 == 0 on this
+// path), a 16-lane group per slot; workgroups of 4 rows x split tiles.
 __global__ __launch_bounds__(THREADS) void evidence_combine_kernel(Split sp, const float* __restrict__ m_add,
                                                                    const float* __restrict__ m_scale,
                                                                    const uint8_t* __restrict__ w_bits, int64_t w_pb,
                                                                    float* __restrict__ ev,
                                                                    float* __restrict__ gs_partial, int64_t M,
                                                                    int64_t N) {
+  constexpr int ROWS = THREADS / kWave;
   const int tiles_m = static_cast<int>((M + BM - 1) / BM), tiles_n = static_cast<int>((N + BN - 1) / BN);
   const int ns = sp.tiles_e - sp.tiles_full, i = static_cast<int>(blockIdx.y);
   int tm, tn;
   tile_of(sp.tiles_full + i, tiles_m, tiles_n, tm, tn);
-  const int64_t row = static_cast<int64_t>(tm) * BM + blockIdx.x;
-  if (row >= M) return;  // the whole workgroup
-  const int64_t col = static_cast<int64_t>(tn) * BN + threadIdx.x;
-  const int64_t slot = static_cast<int64_t>(tn) * WAVES_N + threadIdx.x / kWave;
-  const int64_t at = static_cast<int64_t>(i) * (BM * BN) + static_cast<int64_t>(blockIdx.x) * BN + threadIdx.x;
+  const int lane = threadIdx.x % kWave;
+  const int lrow = static_cast<int>(blockIdx.x) * ROWS + static_cast<int>(threadIdx.x) / kWave;
+  const int64_t row = static_cast<int64_t>(tm) * BM + lrow;
+  if (row >= M) return;  // the whole wave
+  const int64_t col = static_cast<int64_t>(tn) * BN + 4 * lane;
   float signed_e0 = 0.0f;
   if (col < N) {
-    float s = sp.partial[at];
-    for (int j = 1; j < sp.splits; ++j) s += sp.partial[static_cast<int64_t>(j) * ns * (BM * BN) + at];
-    const float e0 = s + (m_add ? m_add[row] : 0.0f);
-    ev[row * N + col] = e0 * (m_scale ? m_scale[row] : 1.0f);
-    if (w_bits) signed_e0 = ((w_bits[row * w_pb + (col >> 3)] >> (col & 7)) & 1u) ? e0 : -e0;
+    const int64_t at = static_cast<int64_t>(i) * (BM * BN) + static_cast<int64_t>(lrow) * BN + 4 * lane;
+    float4 acc = *reinterpret_cast<const float4*>(sp.partial + at);
+    for (int j = 1; j < sp.splits; ++j) {
+      const float4 v = *reinterpret_cast<const float4*>(sp.partial + static_cast<int64_t>(j) * ns * (BM * BN) + at);
+      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+    const float add = m_add ? m_add[row] : 0.0f, mul = m_scale ? m_scale[row] : 1.0f;
+    const float e0[4] = {acc.x + add, acc.y + add, acc.z + add, acc.w + add};
+    *reinterpret_cast<float4*>(ev + row * N + col) = make_float4(e0[0] * mul, e0[1] * mul, e0[2] * mul, e0[3] * mul);
+    if (w_bits) {
+      const uint32_t nib = (w_bits[row * w_pb + (col >> 3)] >> (col & 7)) & 0xFu;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) signed_e0 += ((nib >> q) & 1u) ? e0[q] : -e0[q];
+    }
   }
-  const float tot = wave_sum(signed_e0);
-  if (gs_partial && threadIdx.x % kWave == 0) gs_partial[slot * M + row] = tot;
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) signed_e0 += __shfl_xor(signed_e0, o, kWave);
+  if (gs_partial && lane % 16 == 0) gs_partial[(static_cast<int64_t>(tn) * WAVES_N + lane / 16) * M + row] = signed_e0;
 }
 #undef QSTE_WIDE_STAGES
 }  // namespace wide
@@ -903,11 +915,11 @@ static mfma::Params evidence_params(const void* dy, const uint8_t* packed_x, con
   return p;
 }
 
-// The combine pass of a split evidence: one workgroup per (tile row, split tile).
+// The combine pass of a split evidence: workgroups of 4 tile rows x split tiles.
 static int launch_combine(const mfma::wide::Split& sp, const float* m_add, const float* m_scale,
                           const uint8_t* w_bits, float* ev, float* gs_partial, int64_t rows, int64_t cols,
                           hipStream_t stream) {
-  const dim3 grid(mfma::wide::BM, static_cast<unsigned>(sp.tiles_e - sp.tiles_full));
+  const dim3 grid(mfma::wide::BM / (mfma::wide::THREADS / kWave), static_cast<unsigned>(sp.tiles_e - sp.tiles_full));
   mfma::wide::evidence_combine_kernel<<<grid, mfma::wide::THREADS, 0, stream>>>(sp, m_add, m_scale, w_bits, cols / 8,
                                                                                ev, gs_partial, rows, cols);
   return static_cast<int>(hipGetLastError());
@@ -957,7 +969,7 @@ int mfma_evidence(const void* dy, int dtype, const uint8_t* packed_x, const floa
   const mfma::Params p =
       evidence_params(dy, packed_x, x_scale, ev, samples, rows, cols, m_add, m_scale, w_bits, gs_partial);
   const int te = wide_grid(rows, cols);
-  if (plan && plan->splits > 1) {
+  if (plan && plan->splits > 1 && aligned16(ev)) {  // the combine pass stores 16 bytes at a time
     if (!partial) return QSTE_E_WORKSPACE;
     const mfma::wide::Split sp{plan->tiles_full, te, plan->splits, plan->ks_steps, partial};
     const int grid = sp.tiles_full + (te - sp.tiles_full) * sp.splits;
@@ -1128,7 +1140,7 @@ int mfma_backward_pair(const void* dy, int dtype, const uint8_t* x_t, int64_t x_
   pd.lda = rows; pd.pb = w_t_pitch;
   pd.a_rows = samples; pd.bit_rows = cols;
   const int te = wide_grid(rows, cols), td = wide_grid(samples, cols);
-  const bool split = plan.splits > 1;
+  const bool split = plan.splits > 1 && aligned16(ev);  // the combine pass stores 16 bytes at a time
   const mfma::wide::Split sp{split ? plan.tiles_full : te, te, split ? plan.splits : 1, plan.ks_steps,
                              split ? partial : nullptr};
   const dim3 g(sp.tiles_full + (te - sp.tiles_full) * sp.splits + td), b(mfma::wide::THREADS);
