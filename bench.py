@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--no-extras", action="store_true", help="skip per-kernel, step and GEMV timing")
     ap.add_argument("--no-configs", action="store_true", help="skip the config 2 and config 3 step lines")
     ap.add_argument("--cpu-tokens", type=int, default=256)
+    ap.add_argument("--configs-only", action="store_true",
+                    help="only the config 2 and config 3 step lines (for a kernel profile of those workloads)")
     ap.add_argument("--pmc-calibrate", action="store_true",
                     help="one launch of each GEMM kind at the gate-layer shape plus a plain device copy of "
                          "COPY_BYTES, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
@@ -480,6 +482,9 @@ def main():
     T, d, ffn = args.tokens, args.d, args.ffn
     if args.pmc_calibrate:
         pmc_calibrate(T, d, ffn, device)
+        return
+    if args.configs_only:
+        print(json.dumps({"configs": config_steps(device)}), flush=True)
         return
 
     mlp = SwiGLU(d, ffn, device)
