@@ -7,6 +7,10 @@
   bit with the same step run eagerly on a copy of the state (coordinates,
   packed signs, int8 momentum, fp16 scales and statistics, flips); a replay
   with the flag cleared writes nothing.
+* A layer's whole backward (``linear_backward``: column sums, the split-K
+  backward launch and its combine pass, at config 2's shapes) records into a
+  graph; every replay, with eager work between replays, equals an eager call
+  bit for bit (the products are deterministic).
 * Gradient accumulation (``prepare_accumulation``, ``optim.py:120-135``):
   four microbatches leave the evidence one batch gives, to summation order,
   and coordinates within one step of it (the reference's
@@ -93,6 +97,41 @@ def test_graph_replays_equal_eager_steps(rows, cols):
     for key in st:
         assert torch.equal(st[key], before[key]), key
     assert int(flips) == 0
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 1024), (1024, 4096)])
+def test_layer_backward_graph_replays_equal_eager(rows, cols):
+    from qste_amd import kernels
+
+    T = 8192
+    g = torch.Generator(device=DEV).manual_seed(rows)
+    x = torch.randn(T, cols, generator=g, device=DEV).to(torch.bfloat16)
+    dy = torch.randn(T, rows, generator=g, device=DEV).to(torch.bfloat16)
+    coord = torch.randint(-127, 128, (rows, cols), generator=g, device=DEV, dtype=torch.int32).to(torch.int8)
+    packed = kernels.pack_coordinate(coord)
+    scale = torch.rand(rows, generator=g, device=DEV) * 0.02 + 0.005
+    xb, off, xs = kernels.pack_affine_rows(x)
+
+    def call():
+        return kernels.linear_backward(dy, xb, off, xs, packed, scale, cols, need_bias=True)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm up off the capture
+        call()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = call()
+    for i in range(3):
+        dy.mul_(-1.0 if i % 2 else 0.5)  # new gradient values, eager, between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        want = call()
+        for name, got, ref in zip(("dx", "evidence", "grad_scale", "grad_bias"), outs, want):
+            assert torch.equal(got, ref), (i, name)
+        _ = (dy.float() * 2).sum().item()
 
 
 @pytest.mark.parametrize("accum,tol", [("fp32", 1e-5), ("fp16", 2e-3)])
