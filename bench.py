@@ -543,10 +543,15 @@ def main():
                        key=lambda k: kernels_t[k]["ms"])
         dk = kernels_t[dominant]
         traffic = read_traffic().get(dominant)
+        launches = {"forward": "wide_kernel<A_ROWS_M, B_BITS_ALONG_K, EPI_FORWARD>",
+                    "dgrad": "wide_kernel<A_ROWS_M, B_BITS_ALONG_N, EPI_PLAIN>",
+                    "evidence": "evidence_split_kernel + evidence_combine_kernel (the last, partial round of "
+                                "tiles split over K, then summed)"}
         line["roofline"] = {"bound": "mfma", "kernel": dominant, "achieved": dk["tflops"],
                             "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
                             "frac": round(dk["tflops"] * 1e12 / MFMA_BF16_PEAK, 4),
-                            "traffic": None if traffic is None else int(traffic)}
+                            "traffic": None if traffic is None else int(traffic),
+                            "launches": launches[dominant]}
         line["kernels"] = kernels_t
         line["vendor_dense_bf16_gemm"] = vendor_dense(T, d, ffn, device)
         line["coordinate_step"] = step_bandwidth(ffn, d, device)
