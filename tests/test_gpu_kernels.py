@@ -434,6 +434,33 @@ def test_split_evidence_alone(rows, cols, m, dt):
     assert rel_l2(ev[idx], want) <= 1e-5
 
 
+@pytest.mark.parametrize("rows,cols,m", [(256, 256, 16384), (512, 320, 3000)])
+def test_evidence_without_workspace_runs_unsplit(rows, cols, m):
+    """The C entry with a NULL workspace (no split) and with the split
+    workspace agree with the oracle alike."""
+
+    from qste_amd.kernels import _lib
+
+    _, x, _, _, dy = _problem(rows, cols, m, "bf16", rows + m)
+    xbits, _, xs = oracle.pack_affine_rows(x)
+    want = oracle.evidence(dy, xbits, cols, round_scale(xs, "bf16"))
+    g, b, sc = t(dy, torch.bfloat16), t(xbits), t(xs)
+    lib = _lib.load()
+    need = lib.qste_evidence_from_packed_workspace_bytes(m, rows, cols)
+    assert need > 0
+    work = torch.empty(need, dtype=torch.uint8, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for ws, nbytes in ((None, 0), (work.data_ptr(), need)):
+        out = torch.empty(rows, cols, dtype=torch.float32, device=DEV)
+        rc = lib.qste_evidence_from_packed(g.data_ptr(), 2, b.data_ptr(), sc.data_ptr(), out.data_ptr(), m, rows,
+                                           cols, ws, nbytes, stream)
+        assert rc == 0
+        outs.append(out.cpu().numpy())
+    for got in outs:
+        assert rel_l2(got, want) <= 1e-5
+
+
 @pytest.mark.parametrize("rows,cols", [(14336, 4096), (4096, 14336)])
 def test_full_size_products_sampled_rows(rows, cols):
     """Config-4 layer shapes, 16384 tokens; oracle on a sample of rows."""

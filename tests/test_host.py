@@ -74,7 +74,10 @@ def test_error_codes_and_workspace_queries_need_no_gpu():
     assert lib.qste_evidence_from_packed_workspace_bytes(16384, 14336, 4096) == 2 * 128 * tile
     assert lib.qste_evidence_from_packed_workspace_bytes(64, 256, 256) == 0
     assert lib.qste_linear_backward_workspace_bytes(64, 256, 256) < tile
-    # argument errors are reported before any device work
+    # argument errors are reported before any device work; a workspace
+    # smaller than the split plan's is refused (NULL runs unsplit)
+    need = lib.qste_evidence_from_packed_workspace_bytes(16384, 256, 256)
+    assert lib.qste_evidence_from_packed(1, 2, 1, None, 1, 16384, 256, 256, 1, need - 1, None) == -4
     assert lib.qste_packed_linear_affine(None, 7, None, None, None, None, 1, 1, 8, None) == -1
     assert lib.qste_packed_transpose(None, 2, None, None, None, -1, 4, 8, None) == -2
     assert lib.qste_pack_affine_rows(None, 0, None, None, None, 4, 0, None) == -2
