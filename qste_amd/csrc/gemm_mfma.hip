@@ -172,13 +172,15 @@ __device__ __forceinline__ uint32_t round16x2(float lo, float hi) {
 
 // Workgroup -> output tile.  Consecutive workgroup ids land on different
 // XCDs (round-robin), so ids are first regrouped so each XCD gets a
-// contiguous range, then walked in column-major groups of 2 M-tiles, so the
-// workgroups that run together on one XCD share two dense-operand row blocks
-// (the large operand) and many small bit tiles in that XCD's L2.
+// contiguous range, then walked in column-major groups of G M-tiles, so the
+// workgroups that run together on one XCD share G dense-operand row blocks
+// (the large operand) and many small bit tiles in that XCD's L2.  G = 2 for
+// the forward and dX, 1 for the evidence (dense operand as rows of K), as
+// measured fastest for each.
+template <int G>
 __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int total = tiles_m * tiles_n;
   if (total % 8 == 0) pid = (pid % 8) * (total / 8) + pid / 8;
-  constexpr int G = 2;
   const int per_group = G * tiles_n;
   const int group = pid / per_group;
   const int first_m = group * G;
@@ -269,7 +271,7 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   const int tiles_m = static_cast<int>((p.M + BM - 1) / BM);
   const int tiles_n = static_cast<int>((p.N + BN - 1) / BN);
   int tm, tn;
-  tile_of(pid, tiles_m, tiles_n, tm, tn);
+  tile_of<AKIND == A_ROWS_K ? 1 : 2>(pid, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * BM, n0 = static_cast<int64_t>(tn) * BN;
   const uint32_t one = one_pair<DT>();
   const int nk = static_cast<int>((p.K + BK - 1) / BK);  // K % BK != 0 only for A as rows of K
@@ -826,7 +828,7 @@ __global__ __launch_bounds__(THREADS) void evidence_combine_kernel(Split sp, con
   const int tiles_m = static_cast<int>((M + BM - 1) / BM), tiles_n = static_cast<int>((N + BN - 1) / BN);
   const int ns = sp.tiles_e - sp.tiles_full, i = static_cast<int>(blockIdx.y);
   int tm, tn;
-  tile_of(sp.tiles_full + i, tiles_m, tiles_n, tm, tn);
+  tile_of<1>(sp.tiles_full + i, tiles_m, tiles_n, tm, tn);  // the evidence's mapping
   const int lane = threadIdx.x % kWave;
   const int lrow = static_cast<int>(blockIdx.x) * ROWS + static_cast<int>(threadIdx.x) / kWave;
   const int64_t row = static_cast<int64_t>(tm) * BM + lrow;
