@@ -303,9 +303,10 @@ def gemm_kernels(T, d, ffn, device, iters=5):
         ms = timed_events(fn, iters)
         out[name] = {"ms": round(ms, 4), "tflops": round(flop / ms / 1e9, 2),
                      "frac_of_mfma_peak": round(flop / (ms * 1e-3) / MFMA_BF16_PEAK, 4)}
-    # the training path's backward of one layer: one C-ABI call, dX and the
-    # evidence in one kernel launch plus its sign transposes, scale copies and
-    # column sums (two products' FLOPs)
+    # the training path's backward of one layer: one C-ABI call running dX
+    # and the evidence (one launch or two, by the shape's plan) plus the
+    # column sums and whatever sign transposes or combine pass the plan needs
+    # (two products' FLOPs)
     ms = timed_events(lambda: kernels.linear_backward(dy, xbits, off, xs, packed, scale, d, need_bias=False), iters)
     out["backward_call"] = {"ms": round(ms, 4), "tflops": round(2 * flop / ms / 1e9, 2),
                             "frac_of_mfma_peak": round(2 * flop / (ms * 1e-3) / MFMA_BF16_PEAK, 4)}
