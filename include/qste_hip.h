@@ -150,9 +150,15 @@ int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x,
  *   flips_out     device int64, set to the number of sign flips (NULL: skip)
  *   update_enabled device uint8 or NULL; when it holds 0, no state is
  *                 written and flips_out is set to 0 (cuda.py:1724-1729)
- * block_size must be a power of two.  Needs
+ * block_size is any positive size (powers of two take the vector paths).  Needs
  * qste_coordinate_update_workspace_bytes() bytes of workspace. */
 size_t qste_coordinate_update_workspace_bytes(int64_t rows, int64_t cols, int64_t block_size);
+/* Diagnostics of the step above: the byte offset, inside its workspace, of
+ * four fp32 values a completed call leaves there -- sqrt of the mean clamped
+ * row statistic, the RMS-clip divisor, the step size (reciprocal(rms(m)) *
+ * fp32(coordinate_lr), fallback.py:204-206) and rms(m).  Tests compare them
+ * with the specification's.  No counterpart in the reference. */
+size_t qste_coordinate_update_scalars_offset(int64_t rows, int64_t cols, int64_t block_size);
 int qste_coordinate_update(const float* evidence, int8_t* coordinate, uint8_t* packed,
                            int8_t* moment_q, uint16_t* moment_scale, uint16_t* row_v,
                            uint16_t* col_v, int64_t rows, int64_t cols, double beta1,

@@ -84,8 +84,10 @@ def lib():
         handle.qo_coordinate_update.restype = _i64
         handle.qo_coordinate_update.argtypes = [
             _f32p, _i8p, _u8p, _i8p, _u16p, _u16p, _u16p, _i64, _i64,
-            _dbl, _dbl, _dbl, _dbl, _i64, _i64, _i64, _vp, _vp,
+            _dbl, _dbl, _dbl, _dbl, _i64, _i64, _i64, _vp, _vp, _vp,
         ]
+        handle.qo_step_size.restype = ctypes.c_float
+        handle.qo_step_size.argtypes = [ctypes.c_float, _dbl]
         handle.qo_round_bf16.restype = ctypes.c_float
         handle.qo_round_bf16.argtypes = [ctypes.c_float]
         _lib = handle
@@ -220,13 +222,22 @@ def decoded_evidence(dy, bits_x, offset, xs, columns: int) -> np.ndarray:
 # -- coordinate step (fallback.py:158-242) ------------------------------------
 
 
+def step_size(moment_rms: float, coordinate_lr: float) -> np.float32:
+    """``coordinate_lr / moment_rms`` as fallback.py:204-206 evaluates it:
+    ``reciprocal(moment_rms) * fp32(coordinate_lr)``, two fp32 roundings."""
+
+    return np.float32(lib().qo_step_size(float(np.float32(moment_rms)), float(coordinate_lr)))
+
+
 def coordinate_update(grad, state: dict, *, beta1, beta2, update_clip, coordinate_lr,
-                      block_size, seed, step, margins: bool = False):
+                      block_size, seed, step, margins: bool = False, scalars=None):
     """Run the spec step on numpy state in place; returns flips (and margins).
 
     ``state`` holds ``coordinate`` (int8 [R,C]), ``packed`` (uint8 [R,PB]),
     ``moment_q`` (int8 [R,C]), and ``moment_scale`` / ``row_v`` / ``col_v`` as
     float16 arrays (their bit patterns are updated through a uint16 view).
+    ``scalars``, a float32 array of 4, receives sqrt(mean row statistic),
+    the clip divisor, the step size and the momentum RMS.
     """
 
     g = np.array(grad, dtype=np.float32, order="C", copy=True)
@@ -234,6 +245,9 @@ def coordinate_update(grad, state: dict, *, beta1, beta2, update_clip, coordinat
     for key in ("coordinate", "packed", "moment_q", "moment_scale", "row_v", "col_v"):
         if not state[key].flags["C_CONTIGUOUS"]:
             raise ValueError(f"state[{key!r}] must be C-contiguous")
+    if scalars is not None and (scalars.dtype != np.float32 or scalars.size < 4
+                                or not scalars.flags["C_CONTIGUOUS"]):
+        raise ValueError("scalars must be a contiguous float32 array of at least 4")
     tm = np.empty((rows, cols), dtype=np.float32) if margins else None
     mm = np.empty((rows, cols), dtype=np.float32) if margins else None
     flips = lib().qo_coordinate_update(
@@ -241,7 +255,7 @@ def coordinate_update(grad, state: dict, *, beta1, beta2, update_clip, coordinat
         state["moment_scale"].view(np.uint16), state["row_v"].view(np.uint16),
         state["col_v"].view(np.uint16), rows, cols, float(beta1), float(beta2),
         float(update_clip), float(coordinate_lr), int(block_size), _wrap64(seed),
-        _wrap64(step), _ptr(tm), _ptr(mm),
+        _wrap64(step), _ptr(tm), _ptr(mm), _ptr(scalars),
     )
     if margins:
         return int(flips), tm, mm

@@ -249,6 +249,19 @@ void qo_row_inner(const float* mat, const uint8_t* packed, int64_t rows, int64_t
 }
 
 /* ------------------------------------------------------------------------ */
+/* The step size of fallback.py:204-206, `coordinate_lr / moment_rms`, with  */
+/* a Python float over a 0-dim fp32 tensor.  Python hands that division to   */
+/* Tensor.__rtruediv__, which torch defines as `self.reciprocal() * other`:  */
+/* a correctly rounded fp32 reciprocal, then an fp32 product with the float  */
+/* cast to fp32.  Two roundings; for a learning rate that is not a power of  */
+/* two this differs from one fp32 division in about a quarter of cases.      */
+/* ------------------------------------------------------------------------ */
+float qo_step_size(float moment_rms, double coordinate_lr) {
+  const float inverse = 1.0f / moment_rms;
+  return inverse * (float)coordinate_lr;
+}
+
+/* ------------------------------------------------------------------------ */
 /* coordinate_update: fallback.py:158-242, operation by operation.           */
 /*                                                                           */
 /* State arrays are updated in place exactly as the reference mutates them:  */
@@ -264,6 +277,8 @@ void qo_row_inner(const float* mat, const uint8_t* packed, int64_t rows, int64_t
 /* They let a test prove that an integer mismatch against another           */
 /* implementation sits exactly where a one-ulp difference in a reduction can */
 /* move the decision.                                                        */
+/*   scalars_out[0..3] = sqrt(mean clamped row statistic), RMS-clip divisor, */
+/*                      step size (qo_step_size), momentum RMS.              */
 /* ------------------------------------------------------------------------ */
 
 int64_t qo_coordinate_update(float* grad, int8_t* coord, uint8_t* packed, int8_t* moment_q,
@@ -271,7 +286,7 @@ int64_t qo_coordinate_update(float* grad, int8_t* coord, uint8_t* packed, int8_t
                              int64_t rows, int64_t cols, double beta1, double beta2,
                              double update_clip, double coordinate_lr, int64_t block_size,
                              int64_t seed, int64_t step, float* target_margin,
-                             float* moment_margin) {
+                             float* moment_margin, float* scalars_out) {
   const int64_t count = rows * cols;
   const int64_t blocks = (count + block_size - 1) / block_size;
   const int64_t padded = blocks * block_size;
@@ -356,7 +371,13 @@ int64_t qo_coordinate_update(float* grad, int8_t* coord, uint8_t* packed, int8_t
   }
   float mrms = sqrtf((float)msq / (float)padded);
   mrms = fmaxf(mrms, (float)1e-8);
-  const float step_size = (float)coordinate_lr / mrms;
+  const float step_size = qo_step_size(mrms, coordinate_lr);
+  if (scalars_out) {
+    scalars_out[0] = sqrt_mean;
+    scalars_out[1] = divisor;
+    scalars_out[2] = step_size;
+    scalars_out[3] = mrms;
+  }
 
   /* fallback.py:204-225: stochastic rounding of the coordinate target */
   const uint32_t combined = qo_seed_hash(seed) ^ qo_step_hash(step);

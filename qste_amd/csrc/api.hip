@@ -20,6 +20,7 @@ int colsum_chunks(int64_t samples);
 int launch_colsums(const void*, int, const float*, int64_t, int64_t, float*, float*, float*, float*,
                    hipStream_t);
 size_t coordinate_update_workspace(int64_t, int64_t, int64_t);
+size_t coordinate_update_scalars_offset(int64_t, int64_t, int64_t);
 int launch_coordinate_update(const float*, int8_t*, uint8_t*, int8_t*, uint16_t*, uint16_t*, uint16_t*,
                              int64_t, int64_t, double, double, double, double, int64_t, int64_t, int64_t,
                              const int64_t*, int64_t*, const uint8_t*, void*, size_t, hipStream_t);
@@ -135,7 +136,7 @@ int fill_zero(float* p, int64_t n, hipStream_t s) {
 
 extern "C" {
 
-int qste_version(void) { return 1; }
+int qste_version(void) { return 2; }
 
 const char* qste_error_string(int code) {
   switch (code) {
@@ -144,7 +145,7 @@ const char* qste_error_string(int code) {
     case QSTE_E_SHAPE: return "qste: invalid shape (negative size or inconsistent dimensions)";
     case QSTE_E_NULL: return "qste: required pointer is NULL";
     case QSTE_E_WORKSPACE: return "qste: workspace missing or smaller than the *_workspace_bytes query";
-    case QSTE_E_BLOCK: return "qste: momentum block size must be a positive power of two";
+    case QSTE_E_BLOCK: return "qste: momentum block size must be positive";
     case QSTE_E_ALIGN: return "qste: pointer alignment not supported";
     default: return hipGetErrorString(static_cast<hipError_t>(code));
   }
@@ -296,13 +297,17 @@ size_t qste_coordinate_update_workspace_bytes(int64_t rows, int64_t cols, int64_
   return coordinate_update_workspace(rows, cols, block_size);
 }
 
+size_t qste_coordinate_update_scalars_offset(int64_t rows, int64_t cols, int64_t block_size) {
+  return coordinate_update_scalars_offset(rows, cols, block_size);
+}
+
 int qste_coordinate_update(const float* evidence, int8_t* coordinate, uint8_t* packed, int8_t* moment_q,
                            uint16_t* moment_scale, uint16_t* row_v, uint16_t* col_v, int64_t rows,
                            int64_t cols, double beta1, double beta2, double update_clip,
                            double coordinate_lr, int64_t block_size, int64_t seed, int64_t step,
                            const int64_t* step_device, int64_t* flips_out, const uint8_t* update_enabled,
                            void* workspace, size_t workspace_bytes, void* stream) {
-  if (block_size <= 0 || (block_size & (block_size - 1))) return QSTE_E_BLOCK;
+  if (block_size <= 0) return QSTE_E_BLOCK;
   if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
   hipStream_t s = as_stream(stream);
   if (rows == 0 || cols == 0) {

@@ -21,7 +21,7 @@
 //            only when rms(U) > update_clip); otherwise
 //            m = q*S*b1 + (1-b1)*U/div for one momentum block per wave:
 //            new fp16 block scale, sum of m^2
-//   final    (prologue: step size lr / rms(m)) stochastic rounding, momentum
+//   final    (prologue: step size 1/rms(m) * lr) stochastic rounding, momentum
 //            requantization, sign repack and flip count, 8 columns (one
 //            packed byte) per thread
 //   finish   new block scales into place, flip total
@@ -34,8 +34,9 @@
 // equal the correctly rounded sums but in vanishingly rare cases, whichever
 // kernel (and so whichever order) a shape takes.
 //
-// Fast paths (vector loads) need cols % 8 == 0 and block_size >= 8; other
-// shapes take scalar code with the same arithmetic.  Shapes with cols % 256
+// Fast paths (vector loads) need cols % 8 == 0 and a power-of-two
+// block_size >= 8; other shapes and block sizes (any positive size, as the
+// specification allows) take scalar code with the same arithmetic.  Shapes with cols % 256
 // == 0 and block_size <= 256 take the row kernels for the stats, usq and
 // momentum passes: a wave owns a 1024-column chunk of one row at a time,
 // keeps its column factors in registers, and finds a momentum block's
@@ -57,16 +58,21 @@ constexpr int kRowsGroups = 64;   // workgroups finishing the row statistics
 struct Params {
   float b1, a1, b2, a2, clip, lr;
   int64_t rows, cols, count, blocks, block_size;
-  int block_shift;
+  int block_shift;  // log2(block_size), or -1 when block_size is not a power of two
   uint32_t seed_part;
   int64_t step;
   const int64_t* step_device;
   const uint8_t* enabled;
-  bool vec;       // cols % 8 == 0 and block_size >= 8
+  bool vec;       // cols % 8 == 0, block_size a power of two >= 8
   bool small;     // rows * cols < 2^32: 32-bit index arithmetic
   uint32_t bpr;   // momentum blocks per row when cols % block_size == 0, else 0
   bool spec;      // the usq pass also computes the momentum as if the clip divisor were 1
 };
+
+// Momentum block of flat index i.
+__device__ __forceinline__ int64_t block_of(int64_t i, const Params& p) {
+  return p.block_shift >= 0 ? (i >> p.block_shift) : i / p.block_size;
+}
 
 // Row and column of flat index i.
 __device__ __forceinline__ void row_col(int64_t i, const Params& p, int64_t& r, int64_t& c) {
@@ -91,7 +97,7 @@ struct Work {
   float* col_factor;   // [cols]
   double* usq_part;    // [kUsqGroups]
   double* msq_part;    // [kMomentGroups]
-  float* scalars;      // [0] sqrt(mean row stat), [1] divisor, [2] step size
+  float* scalars;      // [0] sqrt(mean row stat), [1] divisor, [2] step size, [3] rms(m)
   uint16_t* s_new;     // [blocks]
   float* s_rcp;        // [blocks] 1 / max(s_new, 1e-12), correctly rounded (row path)
   int64_t* flips_part; // [kFinalGroups]
@@ -678,6 +684,46 @@ __global__ __launch_bounds__(kThreads) void elem_row_kernel(const float* __restr
 }
 
 // -- final element pass: one packed byte (8 columns) per thread ---------------
+
+// Step size of the spec (fallback.py:204-206): `coordinate_lr / moment_rms`
+// divides a Python float by an fp32 tensor, which torch evaluates as
+// Tensor.__rtruediv__, `reciprocal(moment_rms) * fp32(lr)`: two roundings,
+// not one division (they differ for a learning rate that is not a power of
+// two).
+__device__ __forceinline__ float step_size_of(float mrms, float lr) {
+  const float inverse = 1.0f / mrms;
+  return inverse * lr;
+}
+
+struct FinalScalars {
+  float step_size, divisor, rdiv;
+  uint32_t combined;
+  bool on;
+};
+
+// Prologue shared by the final kernels: momentum RMS -> step size (stored in
+// scalars[2] with the RMS in scalars[3] by the first workgroup), the clip
+// divisor of the momentum pass, and the hash key of (seed, step).
+__device__ __forceinline__ FinalScalars final_prologue(const Params& p, const Work& w, double* red) {
+  double acc = 0.0;
+  for (int64_t i = threadIdx.x; i < w.parts; i += kThreads) acc += w.msq_part[i];
+  acc = block_sum(acc, red);
+  const float padded = static_cast<float>(p.blocks * p.block_size);
+  float mrms = sqrtf(static_cast<float>(acc) / padded);
+  mrms = fmaxf(mrms, 1e-8f);
+  FinalScalars f;
+  f.step_size = step_size_of(mrms, p.lr);
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
+    w.scalars[2] = f.step_size;
+    w.scalars[3] = mrms;
+  }
+  f.divisor = w.scalars[1];
+  f.rdiv = 1.0f / f.divisor;
+  const int64_t step = p.step_device ? *p.step_device : p.step;
+  f.combined = p.seed_part ^ step_hash(step);
+  f.on = enabled(p);
+  return f;
+}
 __device__ __forceinline__ uint32_t final_byte(const float* __restrict__ g, int8_t* __restrict__ coord,
                                                int8_t* __restrict__ moment_q,
                                                const uint16_t* __restrict__ moment_scale, const Params& p,
@@ -726,7 +772,7 @@ __device__ __forceinline__ uint32_t final_byte(const float* __restrict__ g, int8
     const int64_t i = i0 + j;
     float so = s_old, sn = s_new;
     if (!p.vec) {
-      const int64_t blk = i >> p.block_shift;
+      const int64_t blk = block_of(i, p);
       so = f16_to_f32(moment_scale[blk]);
       sn = f16_to_f32(w.s_new[blk]);
     }
@@ -767,20 +813,10 @@ __global__ __launch_bounds__(kThreads) void final_kernel(const float* __restrict
                                                          Params p, Work w) {
   __shared__ double red[kThreads / kWave];
   __shared__ int64_t ired[kThreads / kWave];
-  // step size from the momentum RMS
-  double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < w.parts; i += kThreads) acc += w.msq_part[i];
-  acc = block_sum(acc, red);
-  const float padded = static_cast<float>(p.blocks * p.block_size);
-  float mrms = sqrtf(static_cast<float>(acc) / padded);
-  mrms = fmaxf(mrms, 1e-8f);
-  const float step_size = p.lr / mrms;
-  if (blockIdx.x == 0 && threadIdx.x == 0) w.scalars[2] = step_size;
-  const float divisor = w.scalars[1];
-  const float rdiv = 1.0f / divisor;
-  const int64_t step = p.step_device ? *p.step_device : p.step;
-  const uint32_t combined = p.seed_part ^ step_hash(step);
-  const bool on = enabled(p);
+  const FinalScalars f = final_prologue(p, w, red);
+  const float step_size = f.step_size, divisor = f.divisor, rdiv = f.rdiv;
+  const uint32_t combined = f.combined;
+  const bool on = f.on;
 
   const int64_t stride = (p.cols + 7) / 8;
   const int64_t total = p.rows * stride;
@@ -900,19 +936,10 @@ __global__ __launch_bounds__(kThreads) void final_vec_kernel(const float* __rest
                                                              Params p, Work w) {
   __shared__ double red[kThreads / kWave];
   __shared__ int64_t ired[kThreads / kWave];
-  double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < w.parts; i += kThreads) acc += w.msq_part[i];
-  acc = block_sum(acc, red);
-  const float padded = static_cast<float>(p.blocks * p.block_size);
-  float mrms = sqrtf(static_cast<float>(acc) / padded);
-  mrms = fmaxf(mrms, 1e-8f);
-  const float step_size = p.lr / mrms;
-  if (blockIdx.x == 0 && threadIdx.x == 0) w.scalars[2] = step_size;
-  const float divisor = w.scalars[1];
-  const float rdiv = 1.0f / divisor;
-  const int64_t step = p.step_device ? *p.step_device : p.step;
-  const uint32_t combined = p.seed_part ^ step_hash(step);
-  const bool on = enabled(p);
+  const FinalScalars f = final_prologue(p, w, red);
+  const float step_size = f.step_size, divisor = f.divisor, rdiv = f.rdiv;
+  const uint32_t combined = f.combined;
+  const bool on = f.on;
   const int64_t flips =
       divisor == 1.0f
           ? final_vec_loop<true>(g, coord, packed, moment_q, moment_scale, p, w, divisor, rdiv, step_size, combined, on)
@@ -1036,19 +1063,10 @@ __global__ __launch_bounds__(kThreads) void final_row_kernel(const float* __rest
                                                              Params p, Work w) {
   __shared__ double red[kThreads / kWave];
   __shared__ int64_t ired[kThreads / kWave];
-  double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < w.parts; i += kThreads) acc += w.msq_part[i];
-  acc = block_sum(acc, red);
-  const float padded = static_cast<float>(p.blocks * p.block_size);
-  float mrms = sqrtf(static_cast<float>(acc) / padded);
-  mrms = fmaxf(mrms, 1e-8f);
-  const float step_size = p.lr / mrms;
-  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) w.scalars[2] = step_size;
-  const float divisor = w.scalars[1];
-  const float rdiv = 1.0f / divisor;
-  const int64_t step = p.step_device ? *p.step_device : p.step;
-  const uint32_t combined = p.seed_part ^ step_hash(step);
-  const bool on = enabled(p);
+  const FinalScalars f = final_prologue(p, w, red);
+  const float step_size = f.step_size, divisor = f.divisor, rdiv = f.rdiv;
+  const uint32_t combined = f.combined;
+  const bool on = f.on;
   const int64_t flips =
       divisor == 1.0f
           ? final_row_loop<true>(g, coord, packed, moment_q, moment_scale, p, w, divisor, rdiv, step_size, combined, on)
@@ -1145,6 +1163,11 @@ size_t coordinate_update_workspace(int64_t rows, int64_t cols, int64_t block_siz
   return step::layout(rows, cols, block_size, nullptr).total;
 }
 
+size_t coordinate_update_scalars_offset(int64_t rows, int64_t cols, int64_t block_size) {
+  if (rows <= 0 || cols <= 0 || block_size <= 0) return 0;
+  return step::layout(rows, cols, block_size, nullptr).off[9];
+}
+
 int launch_coordinate_update(const float* g, int8_t* coord, uint8_t* packed, int8_t* moment_q,
                              uint16_t* moment_scale, uint16_t* row_v, uint16_t* col_v, int64_t rows,
                              int64_t cols, double beta1, double beta2, double update_clip,
@@ -1186,12 +1209,13 @@ int launch_coordinate_update(const float* g, int8_t* coord, uint8_t* packed, int
   p.blocks = (p.count + block_size - 1) / block_size;
   int shift = 0;
   while ((int64_t{1} << shift) < block_size) ++shift;
-  p.block_shift = shift;
+  const bool pow2 = (int64_t{1} << shift) == block_size;
+  p.block_shift = pow2 ? shift : -1;
   p.seed_part = seed_hash(seed);
   p.step = step_;
   p.step_device = step_device;
   p.enabled = update_enabled;
-  p.vec = (cols % 8 == 0) && block_size >= 8 && (reinterpret_cast<uintptr_t>(g) & 15) == 0 &&
+  p.vec = (cols % 8 == 0) && pow2 && block_size >= 8 && (reinterpret_cast<uintptr_t>(g) & 15) == 0 &&
           (reinterpret_cast<uintptr_t>(coord) & 7) == 0 && (reinterpret_cast<uintptr_t>(moment_q) & 7) == 0;
   p.small = p.count < (int64_t{1} << 32) && p.blocks * p.block_size < (int64_t{1} << 32);
   p.bpr = (p.small && cols % block_size == 0) ? static_cast<uint32_t>(cols / block_size) : 0u;

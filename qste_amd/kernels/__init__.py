@@ -368,8 +368,8 @@ def coordinate_update(
     """
 
     device = _require_gpu(gradient, coordinate, packed, moment_q, moment_scale, row_v, col_v)
-    if block_size <= 0 or block_size & (block_size - 1):
-        raise ValueError("momentum block size must be a positive power of two")
+    if int(block_size) <= 0:
+        raise ValueError("momentum block size must be positive")
     gradient = gradient.detach().to(torch.float32).contiguous()
     rows, cols = gradient.shape
     for name, t, dt in (("coordinate", coordinate, torch.int8), ("packed", packed, torch.uint8),

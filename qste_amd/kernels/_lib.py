@@ -43,6 +43,7 @@ SIGNATURES = {
     "qste_linear_backward": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                     _i64, _i64, _i64, _vp, _sz, _vp]),
     "qste_coordinate_update_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "qste_coordinate_update_scalars_offset": (_sz, [_i64, _i64, _i64]),
     "qste_coordinate_update": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _dbl, _dbl,
                                       _dbl, _dbl, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
     "qste_pack_bits": (_int, [_vp, _vp, _i64, _i64, _vp]),

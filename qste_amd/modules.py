@@ -63,10 +63,13 @@ class QSTELinear(nn.Module):
 class PackedLinear(nn.Module):
     """Inference-only linear over packed signs, a row scale and a bias.
 
-    The reference casts the input to fp32 and the output back
-    (modules.py:114-120). Widening bf16/fp16 to fp32 is exact and the kernel
-    accumulates in fp32 either way, so the input is passed in its own dtype;
-    the output is in the input dtype as in the reference.
+    The reference casts the input to fp32, multiplies in fp32 and rounds the
+    result back to the input dtype (modules.py:114-120).  Widening bf16/fp16
+    to fp32 is exact, so the input goes to the kernel in its own dtype; the
+    kernels multiply exact +-1 operands, accumulate in fp32 and round once to
+    the input dtype.  The decode kernel (bf16, at most 16 rows) accumulates a
+    biased operand and subtracts the bias, which costs a few of fp32's bits
+    relative to sum |x|: well below the output's bf16 rounding.
     """
 
     def __init__(self, packed: Tensor, scale: Tensor, columns: int, bias: Tensor | None):

@@ -1,18 +1,31 @@
 """One binary matrix: its int8 coordinate, packed signs and row scale.
 
-State layout and parameter names match the reference's ``Surface``
-(``src/qste/surface.py:30-79``) so state dicts carry over:
+State layout and parameter names are the reference's ``Surface``
+(``src/qste/surface.py:67-79``), so state dicts load either way:
 
     coordinate   int8  [rows, columns]      training state (optimizer-owned)
     packed_sign  uint8 [rows, ceil(cols/8)] forward weight, LSB-first bits
     log_scale    fp32  [rows]               learned row scale (host optimizer)
 
-Evidence routing (immediate apply inside backward, accumulation for tied or
-deferred surfaces, the forward-count backstop) follows
-``src/qste/surface.py:104-206``.
+Evidence (the fp32 coordinate gradient each backward produces) does not go
+through ``.grad``.  Each surface owns an :class:`EvidenceLedger` that decides
+where it goes; the rules are the reference's (``surface.py:104-206``):
+
+* a surface used once per backward hands its evidence to the optimizer inside
+  that backward, without a buffer;
+* a surface used several times per backward (tied weights) sums the uses, in
+  the configured accumulation dtype, and hands over the sum after the last;
+* while the optimizer is deferred (gradient accumulation, AMP unscaling,
+  capture) evidence is held until ``QSTEOptimizer.step``, in a fixed buffer
+  when one was prepared;
+* the step drains whatever is held, whether or not forward and backward
+  counts balanced (gradient checkpointing runs forwards that never see a
+  backward).
 """
 
 from __future__ import annotations
+
+from typing import Callable, Optional
 
 import torch
 import torch.nn as nn
@@ -22,6 +35,8 @@ from . import kernels
 from .config import QSTEConfig, coerce_config
 
 _ACCUM_DTYPE = {"fp16": torch.float16, "fp32": torch.float32}
+
+Sink = Callable[["Surface", Tensor], None]
 
 
 def _on_gpu(fn, tensor: Tensor, *args, **kwargs) -> Tensor:
@@ -42,28 +57,121 @@ def _on_gpu(fn, tensor: Tensor, *args, **kwargs) -> Tensor:
     return fn(tensor.to("cuda"), *args, **kwargs).to(tensor.device)
 
 
+# Bytes of fp32 temporaries the initial quantization may hold at once; a
+# vocabulary-sized weight is converted in row bands rather than copied whole.
+_INIT_BUDGET = 64 << 20
+
+
 def quantize_weight(weight: Tensor, cfg: QSTEConfig) -> tuple[Tensor, Tensor]:
     """Initial (row scale, int8 coordinate) from a float weight.
 
-    surface.py:41-62: per-row scale = mean |w| (>= 1e-5); latent =
-    clamp(w / scale, +-1.5) / 4; coordinate = round(latent / clip * 127)
-    clamped to +-127, with a zero pushed one step toward the weight's sign.
+    The arithmetic of ``surface.py:41-62``, which fixes the starting
+    coordinates: scale = max(mean |w|, 1e-5) per row; latent =
+    clamp(w / scale, +-1.5) * 0.25; coordinate = round(latent / clip * 127)
+    clamped to +-127, and a zero becomes +-1 after the weight's sign (a zero
+    coordinate would decode to +1 whatever the weight's sign was).
     """
 
     rows, columns = weight.shape
-    row_scale = torch.empty(rows, device=weight.device, dtype=torch.float32)
+    scales = torch.empty(rows, device=weight.device, dtype=torch.float32)
     coordinate = torch.empty(rows, columns, device=weight.device, dtype=torch.int8)
-    chunk = max(1, (32 << 20) // max(1, columns * 12))
-    for start in range(0, rows, chunk):
-        stop = min(start + chunk, rows)
-        value = weight[start:stop].float()
-        scale = value.abs().mean(dim=1).clamp_min(1e-5)
-        latent = (value / scale[:, None]).clamp(-1.5, 1.5) * 0.25
-        q = (latent / cfg.coordinate_clip * 127).round().clamp(-127, 127).to(torch.int8)
-        nudge = torch.where(value >= 0, torch.ones_like(q), -torch.ones_like(q))
-        coordinate[start:stop] = torch.where(q == 0, nudge, q)
-        row_scale[start:stop] = scale
-    return row_scale, coordinate
+    band = max(1, _INIT_BUDGET // max(1, 8 * columns))
+    for r0 in range(0, rows, band):
+        w = weight[r0:r0 + band].float()
+        s = w.abs().mean(dim=1).clamp_min_(1e-5)
+        q = (w / s.unsqueeze(1)).clamp_(-1.5, 1.5).mul_(0.25)
+        q = q.div_(cfg.coordinate_clip).mul_(127).round_().clamp_(-127, 127).to(torch.int8)
+        away = (w >= 0).to(torch.int8).mul_(2).sub_(1)  # +1 / -1 after the sign
+        coordinate[r0:r0 + band] = torch.where(q == 0, away, q)
+        scales[r0:r0 + band] = s
+    return scales, coordinate
+
+
+class EvidenceLedger:
+    """Where one surface's coordinate evidence waits between backward and the step.
+
+    ``open_uses``  forwards run under autograd whose backward has not arrived;
+    ``tied``       the running sum of the current backward's uses while more
+                   are due (accumulation dtype), or None;
+    ``held``       evidence kept across backwards for the step (accumulation
+                   dtype), or None; a prepared buffer keeps its address;
+    ``sink``       the optimizer's apply callback, or None while it defers.
+    """
+
+    __slots__ = ("open_uses", "tied", "held", "sink", "accum")
+
+    def __init__(self, accum: torch.dtype):
+        self.open_uses = 0
+        self.tied: Optional[Tensor] = None
+        self.held: Optional[Tensor] = None
+        self.sink: Optional[Sink] = None
+        self.accum = accum
+
+    def deliver(self, surface: "Surface", evidence: Tensor) -> None:
+        """One use's evidence arrives from backward."""
+
+        self.open_uses = max(0, self.open_uses - 1)
+        last = self.open_uses == 0
+        if last and self.tied is None:
+            if self.sink is not None and self.held is None:
+                self.sink(surface, evidence.detach().float())
+                return
+            if self.sink is None and self.held is not None:
+                self.held.add_(evidence.detach().to(self.held.dtype))
+                return
+        part = evidence.detach().to(self.accum)
+        self.tied = part.clone() if self.tied is None else self.tied.add_(part)
+        if not last:
+            return
+        whole, self.tied = self.tied.float(), None
+        if self.sink is not None:
+            if self.held is not None:
+                whole.add_(self.held.float())
+                self.held = None
+            self.sink(surface, whole)
+        elif self.held is None:
+            self.held = whole.to(self.accum)
+        else:
+            self.held.add_(whole.to(self.accum))
+
+    def drain(self, keep_buffer: bool) -> Optional[Tensor]:
+        """Everything pending as one fp32 tensor (None if nothing is).
+
+        With ``keep_buffer`` a held buffer stays allocated and is cleared;
+        what is returned is then always a copy, never the buffer itself (an
+        fp32 buffer's ``.float()`` would be the buffer, and clearing it would
+        hand the step zeros).
+        """
+
+        total = None
+        if self.tied is not None:
+            total, self.tied = self.tied.float(), None
+        if self.held is not None:
+            mine = self.held.to(torch.float32, copy=keep_buffer)
+            total = mine if total is None else total.add_(mine)
+            if keep_buffer:
+                self.held.zero_()
+            else:
+                self.held = None
+        self.open_uses = 0
+        return total
+
+    def fix_buffer(self, shape: tuple[int, int], device: torch.device) -> None:
+        """A zeroed buffer at a fixed address for accumulation or capture."""
+
+        self.forget_uses()
+        self.held = torch.zeros(shape, device=device, dtype=self.accum)
+
+    def forget_uses(self) -> None:
+        self.tied = None
+        self.open_uses = 0
+
+    def divide(self, divisor: float) -> None:
+        if divisor == 0:
+            raise ValueError("gradient scale must be nonzero")
+        for buffer in (self.held, self.tied):
+            if buffer is not None:
+                buffer.div_(divisor)
 
 
 class Surface(nn.Module):
@@ -74,18 +182,8 @@ class Surface(nn.Module):
         if weight.ndim != 2:
             raise ValueError("a QSTE surface must wrap a rank-2 weight")
         cfg = coerce_config(cfg)
-        source = weight.detach()
-        row_scale, coordinate = quantize_weight(source, cfg)
-        self.cfg = cfg
-        self.rows, self.columns = (int(s) for s in source.shape)
-        self.coordinate = nn.Parameter(coordinate, requires_grad=False)
-        self.packed_sign = nn.Parameter(_on_gpu(kernels.pack_coordinate, coordinate),
-                                        requires_grad=False)
-        self.log_scale = nn.Parameter(row_scale.log())
-        self._evidence: Tensor | None = None
-        self._call_evidence: Tensor | None = None
-        self._pending_calls = 0
-        self._immediate = None  # set by QSTEOptimizer
+        row_scale, coordinate = quantize_weight(weight.detach(), cfg)
+        self._install(cfg, coordinate, row_scale.log())
 
     @classmethod
     def from_state(cls, coordinate: Tensor, log_scale: Tensor,
@@ -102,17 +200,19 @@ class Surface(nn.Module):
             raise ValueError("log_scale must have one entry per row")
         self = cls.__new__(cls)
         nn.Module.__init__(self)
-        self.cfg = coerce_config(cfg)
-        self.rows, self.columns = (int(s) for s in coordinate.shape)
-        self.coordinate = nn.Parameter(coordinate.contiguous(), requires_grad=False)
-        self.packed_sign = nn.Parameter(_on_gpu(kernels.pack_coordinate, self.coordinate.data),
-                                        requires_grad=False)
-        self.log_scale = nn.Parameter(log_scale.detach().float().clone())
-        self._evidence = None
-        self._call_evidence = None
-        self._pending_calls = 0
-        self._immediate = None
+        self._install(coerce_config(cfg), coordinate.contiguous(), log_scale.detach().float().clone())
         return self
+
+    def _install(self, cfg: QSTEConfig, coordinate: Tensor, log_scale: Tensor) -> None:
+        self.cfg = cfg
+        self.rows, self.columns = (int(s) for s in coordinate.shape)
+        # parameters (not buffers) so FSDP/DDP own them; requires_grad=False
+        # leaves the coordinate optimizer as their only writer
+        self.coordinate = nn.Parameter(coordinate, requires_grad=False)
+        self.packed_sign = nn.Parameter(_on_gpu(kernels.pack_coordinate, coordinate),
+                                        requires_grad=False)
+        self.log_scale = nn.Parameter(log_scale)
+        self.ledger = EvidenceLedger(_ACCUM_DTYPE[cfg.evidence_accum_dtype])
 
     # -- forward-side state ------------------------------------------------
 
@@ -133,89 +233,40 @@ class Surface(nn.Module):
     def extra_repr(self) -> str:
         return f"rows={self.rows}, columns={self.columns}"
 
-    # -- evidence bookkeeping (surface.py:104-206) --------------------------
+    # -- evidence (the reference's Surface methods, routed by the ledger) ------
+
+    def route_evidence(self, sink: Sink | None) -> None:
+        """Where complete evidence goes: the optimizer's apply, or None to hold it."""
+
+        self.ledger.sink = sink
 
     def note_forward(self) -> None:
         if torch.is_grad_enabled():
-            self._pending_calls += 1
+            self.ledger.open_uses += 1
 
     @torch.no_grad()
     def reset_tracking(self) -> None:
-        self._call_evidence = None
-        self._pending_calls = 0
+        self.ledger.forget_uses()
 
     @torch.no_grad()
     def consume_evidence(self, evidence: Tensor) -> None:
-        """Accept one use's worth of coordinate evidence (fp32 [rows, columns]).
+        """Accept one use's worth of coordinate evidence (fp32 [rows, columns])."""
 
-        The common single-use case hands it straight to the optimizer inside
-        backward; a tied surface sums its uses first.
-        """
-
-        self._pending_calls = max(0, self._pending_calls - 1)
-        immediate = self._immediate
-        if (self._pending_calls == 0 and self._call_evidence is None
-                and self._evidence is None and immediate is not None):
-            immediate(self, evidence.detach().float())
-            return
-        if (self._pending_calls == 0 and self._call_evidence is None
-                and self._evidence is not None and immediate is None):
-            self._evidence.add_(evidence.detach().to(self._evidence.dtype))
-            return
-
-        accum = _ACCUM_DTYPE[self.cfg.evidence_accum_dtype]
-        compact = evidence.detach().to(accum)
-        if self._call_evidence is None:
-            self._call_evidence = compact.clone()
-        else:
-            self._call_evidence.add_(compact)
-        if self._pending_calls:
-            return
-
-        total = self._call_evidence.float()
-        self._call_evidence = None
-        if immediate is not None:
-            if self._evidence is not None:
-                total.add_(self._evidence.float())
-                self._evidence = None
-            immediate(self, total)
-        elif self._evidence is None:
-            self._evidence = total.to(accum)
-        else:
-            self._evidence.add_(total.to(accum))
+        self.ledger.deliver(self, evidence)
 
     @torch.no_grad()
     def flush_evidence(self, *, keep_buffer: bool = False) -> Tensor | None:
         """Everything accumulated, whether or not the forward count balanced."""
 
-        total = None
-        if self._call_evidence is not None:
-            total = self._call_evidence.float()
-            self._call_evidence = None
-        if self._evidence is not None:
-            part = self._evidence.float()
-            total = part if total is None else total.add_(part)
-            if keep_buffer:
-                self._evidence.zero_()
-            else:
-                self._evidence = None
-        self._pending_calls = 0
-        return total
+        return self.ledger.drain(keep_buffer)
 
     @torch.no_grad()
     def prepare_accumulator(self) -> None:
-        self.reset_tracking()
-        self._evidence = torch.zeros(
-            self.rows, self.columns, device=self.coordinate.device,
-            dtype=_ACCUM_DTYPE[self.cfg.evidence_accum_dtype])
+        self.ledger.fix_buffer((self.rows, self.columns), self.coordinate.device)
 
     @torch.no_grad()
     def scale_evidence_(self, divisor: float) -> None:
-        if divisor == 0:
-            raise ValueError("gradient scale must be nonzero")
-        for buffer in (self._evidence, self._call_evidence):
-            if buffer is not None:
-                buffer.div_(divisor)
+        self.ledger.divide(divisor)
 
     @torch.no_grad()
     def refresh_packed(self) -> None:
@@ -224,6 +275,8 @@ class Surface(nn.Module):
         self.packed_sign.data.copy_(_on_gpu(kernels.pack_coordinate, self.coordinate.data))
 
     def memory(self) -> dict[str, int]:
+        """Bytes this surface holds, by role, against an fp32 matrix."""
+
         return {
             "packed_sign": self.packed_sign.numel(),
             "coordinate": self.coordinate.numel(),

@@ -143,6 +143,11 @@ def _update_cases(fallback) -> dict:
         ("u96x160", 96, 160, 256, 17, 5, 1.0, 1e-3),
         ("u256x512", 256, 512, 256, 1_000_004, 0, 1.0, 3e-2),
         ("u64x200", 64, 200, 256, 2**31 + 11, 9, 2.0, 10.0),
+        # learning rates that are not powers of two: the step size is
+        # reciprocal(rms) * lr there, which one division would not reproduce
+        ("u48x96lr3", 48, 96, 64, 5, 2, 0.3, 1.0),
+        ("u128x256lr7", 128, 256, 256, 23, 70, 0.7, 0.1),
+        ("u40x72lr1", 40, 72, 64, 3_000_010, 11, 0.1, 5.0),
     ]
     for idx, (name, rows, cols, block, seed, step, lr, mag) in enumerate(cases):
         g = torch.Generator().manual_seed(1000 + idx)

@@ -150,8 +150,12 @@ def test_gradient_accumulation_matches_one_large_batch(accum, tol):
         for chunk in data.chunk(microbatches):
             (model(chunk).square().sum() / len(data)).backward()
         surface = qste.surfaces(model)[0]
-        evidence = surface._evidence.float().clone()
-        coords.step()
+        evidence = surface.ledger.held.float().clone()
+        before = surface.coordinate.clone()
+        flips = coords.step()
+        # the step ran on the accumulated evidence, not on a cleared buffer
+        assert flips > 0
+        assert int((surface.coordinate != before).sum()) > 0
         return evidence, surface.coordinate.clone()
 
     one_e, one_c = run(1)
@@ -174,9 +178,11 @@ def test_unscale_divides_the_held_evidence():
     x = torch.randn(16, 64, device=DEV)
     (model(x).sum() * 1024.0).backward()
     surface = qste.surfaces(model)[0]
-    held = surface._evidence.float().clone()
+    held = surface.ledger.held.float().clone()
     coords.unscale_(1024.0)
-    assert torch.allclose(surface._evidence.float(), held / 1024.0, rtol=1e-6, atol=0)
-    assert coords.step() >= 0
+    assert torch.allclose(surface.ledger.held.float(), held / 1024.0, rtol=1e-6, atol=0)
+    before = surface.coordinate.clone()
+    assert coords.step() > 0
+    assert int((surface.coordinate != before).sum()) > 0
     # deferred mode keeps the buffer for the next accumulation, emptied
-    assert surface._evidence is not None and not surface._evidence.any()
+    assert surface.ledger.held is not None and not surface.ledger.held.any()

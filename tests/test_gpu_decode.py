@@ -1,27 +1,23 @@
 """Skinny-M forward (decode, M <= 16 bf16 rows) against the CPU oracle.
 
-Two kernels serve this path: for M <= 2 an fp8 x fp4 MFMA kernel (x split
-into two fp8 limbs with a per-row power-of-two scale, weight bits turned into
-fp4 0 / 0.5 / 1 / 2 by masks), otherwise a bf16 MFMA kernel whose weight
-operand is biased (v0(k mod 4) + 0.5 * bit, the bias removed with two per-row
-sums).  Besides ordinary shapes the tests cover what those schemes could get
-wrong: every M from 1 to 16 (rows of x padded to the 16 MFMA rows, limbs in
-the spare rows), K that ends inside a 512-column chunk, N that ends inside a
-16-row block and inside a workgroup, inputs with many exact zeros (ReLU
-outputs), a row of large values next to rows of tiny ones (the row scale), an
-all-zero row, and the full config-5 shape.
+One kernel serves this path: a bf16 MFMA kernel whose weight operand is
+biased (v0(k mod 4) + 0.5 * bit, the bias removed with two per-row sums).
+Besides ordinary shapes the tests cover what that scheme could get wrong:
+every M from 1 to 16 (rows of x padded to the 16 MFMA rows), K that ends
+inside a 512-column chunk, N that ends inside a 16-row block and inside a
+workgroup, inputs with many exact zeros (ReLU outputs), a row of large values
+next to rows of tiny ones, an all-zero row, and the full config-5 shape.
 
-Bars, against the float64 oracle:
+Bars, against the float64 oracle (the reference's PackedLinear computes in
+fp32 and rounds once to the input dtype, modules.py:114-120):
 * rel-L2 <= 1e-3 against the oracle rounded to bf16 (the forward contract);
-* every element within one bf16 ulp of the oracle plus 2^-12 * sum_k |x[m,k]| *
-  scale[n].  The second term is the accumulation error of the M <= 2 path: its
-  fp8 x fp4 MFMA sums each 128-product group keeping about 16 bits below the
-  group's largest product (measured on the device: at most 3.5e-5 of the
-  group's sum of magnitudes), so outputs that cancel to near zero carry an
-  absolute error on the scale of sum |x|, not of |y|;
-* fewer than 5% of elements differ from the rounded oracle (1-ulp rounding
-  flips: 0.5% at K=1024 and 2.3% at K=8192 on the fp8 x fp4 path, about
-  0.05% on the bf16 MFMA path).
+* every element within one bf16 ulp of the oracle plus 2^-16 * sum_k
+  |x[m,k]| * scale[n]: the fp32 accumulation of the biased operand sums
+  magnitudes up to 4.5 * sum |x| and removes the bias by a subtraction, so
+  its rounding error scales with sum |x| (about 2^-20 of it), not with |y|;
+* fewer than 0.5% of elements differ from the rounded oracle on random data
+  (1-ulp rounding flips of outputs that sit near a bf16 rounding boundary),
+  5% on single special-valued rows (sum |x| large against |y|).
 """
 
 from __future__ import annotations
@@ -56,18 +52,19 @@ def _bf(a: np.ndarray) -> np.ndarray:
     return torch.from_numpy(np.asarray(a, dtype=np.float32)).to(torch.bfloat16).float().numpy()
 
 
-def _check(got: torch.Tensor, want: np.ndarray, x: np.ndarray | None = None, scale: np.ndarray | None = None):
+def _check(got: torch.Tensor, want: np.ndarray, x: np.ndarray | None = None, scale: np.ndarray | None = None,
+           flips: float = 0.005):
     got = got.float().cpu().numpy().astype(np.float64)
     want = np.asarray(want, dtype=np.float64)
     want_r = _bf(want).astype(np.float64)
     denom = np.linalg.norm(want_r)
     err = np.linalg.norm(got - want_r) / (denom if denom > 0 else 1.0)
     assert err <= 1e-3, err
-    assert np.mean(got != want_r) < 0.05, np.mean(got != want_r)
+    assert np.mean(got != want_r) < flips, np.mean(got != want_r)
     if x is not None:
         ulp = np.abs(want_r) * 2.0 ** -7
         mag = np.abs(x).astype(np.float64).sum(axis=1)[:, None] * np.abs(scale).astype(np.float64)[None, :]
-        bound = ulp + 2.0 ** -12 * mag
+        bound = ulp + 2.0 ** -16 * mag
         assert np.all(np.abs(got - want) <= bound), np.max(np.abs(got - want) / bound)
 
 
@@ -116,8 +113,11 @@ def test_decode_special_values():
     x[5, :] = _bf(np.float32(1.5))           # constant row
     got = _run(x, packed, scale, bias, cols)
     want = oracle.linear_fwd(x, packed, scale, bias, cols)
+    # one row at a time: a row whose outputs are small against sum |x| (the
+    # large-valued row) sees more 1-ulp rounding flips than random data, so
+    # the per-row flip bar is 5%; the error bound itself is unchanged
     for r in range(m):
-        _check(got[r:r + 1], want[r:r + 1], x[r:r + 1], scale)
+        _check(got[r:r + 1], want[r:r + 1], x[r:r + 1], scale, flips=0.05)
     assert np.array_equal(got[4].float().cpu().numpy(), _bf(bias))
 
 

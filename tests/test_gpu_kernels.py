@@ -291,25 +291,96 @@ def test_coordinate_update_matches_oracle(rows, cols, block):
         assert flips == oflips
 
 
+@pytest.mark.parametrize("rows,cols,block", [(24, 40, 96), (50, 256, 100), (7, 33, 3), (64, 512, 384)])
+def test_coordinate_update_any_block_size(rows, cols, block):
+    """Momentum blocks that are not powers of two (the specification and the
+    reference's config accept any positive size): the generic kernels index
+    blocks by division, bit-exact against the oracle."""
+
+    print(f"block {block} {rows}x{cols}", flush=True)
+    rng = np.random.default_rng(rows * 7 + block)
+    coord = rng.integers(-127, 128, size=(rows, cols)).astype(np.int8)
+    state = oracle.fresh_state(coord, block)
+    gstate = _to_gpu_state(state)
+    for step in range(3):
+        ev = (rng.standard_normal((rows, cols)) * 0.1).astype(np.float32)
+        kw = dict(beta1=0.9, beta2=0.99, update_clip=2.0, coordinate_lr=0.3, block_size=block, seed=5, step=step)
+        flips = _gpu_step(ev, gstate, **kw)
+        oflips = oracle.coordinate_update(ev, state, **kw)
+        _assert_state_equal(gstate, state, (rows, cols, block, step))
+        assert flips == oflips
+
+
 @pytest.mark.parametrize("clip", [0.05, 1e6])
 def test_coordinate_update_clip_regimes(clip):
     """Both sides of the RMS clip on a shape where the usq pass also computes
-    the momentum as if the clip divisor were 1: with the clip engaged that
-    guess is thrown away and the momentum pass recomputes; with it idle
-    (divisor exactly 1) the guess is the result.  Bit-exact either way."""
+    the momentum as if the clip divisor were 1 (host-known steps >= 64): with
+    the clip engaged that guess is thrown away and the momentum pass
+    recomputes; with it idle (divisor exactly 1) the guess is the result.
+    Steps below 64 take the plain two-pass order.  Bit-exact either way."""
 
     rows, cols, block = 96, 1024, 256
     rng = np.random.default_rng(11)
     coord = rng.integers(-127, 128, size=(rows, cols)).astype(np.int8)
     state = oracle.fresh_state(coord, block)
     gstate = _to_gpu_state(state)
-    for step in range(4):
+    for step in (0, 1, 64, 65, 200):
         ev = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
         kw = dict(beta1=0.9, beta2=0.99, update_clip=clip, coordinate_lr=1.0, block_size=block,
                   seed=17, step=step)
         flips = _gpu_step(ev, gstate, **kw)
         oflips = oracle.coordinate_update(ev, state, **kw)
         _assert_state_equal(gstate, state, (clip, step))
+        assert flips == oflips
+
+
+def _c_step(ev, gstate, rows, cols, kw, step):
+    """The C entry with a caller-held workspace; returns (flips, scalars)."""
+
+    from qste_amd.kernels import _lib
+
+    lib = _lib.load()
+    need = lib.qste_coordinate_update_workspace_bytes(rows, cols, kw["block_size"])
+    at = lib.qste_coordinate_update_scalars_offset(rows, cols, kw["block_size"])
+    assert 0 < at and at + 16 <= need
+    work = torch.empty(need, dtype=torch.uint8, device=DEV)
+    flips = torch.empty((), dtype=torch.int64, device=DEV)
+    g = t(ev)
+    rc = lib.qste_coordinate_update(
+        g.data_ptr(), gstate["coordinate"].data_ptr(), gstate["packed"].data_ptr(),
+        gstate["moment_q"].data_ptr(), gstate["moment_scale"].data_ptr(), gstate["row_v"].data_ptr(),
+        gstate["col_v"].data_ptr(), rows, cols, kw["beta1"], kw["beta2"], kw["update_clip"],
+        kw["coordinate_lr"], kw["block_size"], kw["seed"], step, None, flips.data_ptr(), None,
+        work.data_ptr(), need, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    scalars = work[at:at + 16].view(torch.float32).cpu().numpy()
+    return int(flips.item()), scalars
+
+
+# row path (cols % 256 == 0) and the generic kernels; steps >= 64 let the
+# usq pass compute the momentum speculatively
+@pytest.mark.parametrize("rows,cols,block", [(64, 2048, 256), (37, 45, 64), (200, 200, 128)])
+@pytest.mark.parametrize("lr", [0.3, 0.7, 0.1, 1.0])
+def test_coordinate_update_step_size_matches_spec(rows, cols, block, lr):
+    """The step size the kernel used -- reciprocal(rms(m)) * fp32(lr), as
+    fallback.py:204-206 evaluates ``coordinate_lr / moment_rms`` -- read back
+    from the workspace, equals the oracle's bit for bit, and so do the RMS
+    clip divisor, the momentum RMS and the whole state."""
+
+    print(f"step size {rows}x{cols} block {block} lr {lr}", flush=True)
+    rng = np.random.default_rng(rows + cols + int(lr * 10))
+    coord = rng.integers(-127, 128, size=(rows, cols)).astype(np.int8)
+    state = oracle.fresh_state(coord, block)
+    gstate = _to_gpu_state(state)
+    kw = dict(beta1=0.9, beta2=0.99, update_clip=2.0, coordinate_lr=lr, block_size=block, seed=41)
+    for step in (0, 1, 70):
+        ev = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+        flips, got = _c_step(ev, gstate, rows, cols, kw, step)
+        want = np.zeros(4, dtype=np.float32)
+        oflips = oracle.coordinate_update(ev, state, scalars=want, step=step, **kw)
+        assert got.view(np.uint32).tolist() == want.view(np.uint32).tolist(), (step, got, want)
+        assert want[2] == oracle.step_size(want[3], lr)
+        _assert_state_equal(gstate, state, (rows, cols, lr, step))
         assert flips == oflips
 
 
@@ -336,14 +407,15 @@ def test_coordinate_update_device_step_flips_and_gate():
     assert int(flips.item()) == oflips
 
 
-def test_coordinate_update_rejects_bad_block():
+@pytest.mark.parametrize("block", [0, -64])
+def test_coordinate_update_rejects_bad_block(block):
     z = torch.zeros(4, 8, dtype=torch.int8, device=DEV)
     with pytest.raises(ValueError):
         K().coordinate_update(torch.zeros(4, 8, device=DEV), z, torch.zeros(4, 1, dtype=torch.uint8, device=DEV),
                               z.clone(), torch.zeros(1, dtype=torch.float16, device=DEV),
                               torch.zeros(4, dtype=torch.float16, device=DEV),
                               torch.zeros(8, dtype=torch.float16, device=DEV), beta1=0.9, beta2=0.99,
-                              update_clip=2.0, coordinate_lr=1.0, block_size=48, seed=1, step=0)
+                              update_clip=2.0, coordinate_lr=1.0, block_size=block, seed=1, step=0)
 
 
 # ---------------------------------------------------------------------------

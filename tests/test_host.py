@@ -59,7 +59,7 @@ def test_error_codes_and_workspace_queries_need_no_gpu():
 
     lib = _lib.load()
     assert lib.qste_version() >= 1
-    for code, word in ((-1, b"dtype"), (-2, b"shape"), (-3, b"NULL"), (-4, b"workspace"), (-5, b"power of two")):
+    for code, word in ((-1, b"dtype"), (-2, b"shape"), (-3, b"NULL"), (-4, b"workspace"), (-5, b"block size must be positive")):
         assert word in lib.qste_error_string(code)
     assert lib.qste_coordinate_update_workspace_bytes(4096, 14336, 256) > 0
     assert lib.qste_coordinate_update_workspace_bytes(0, 8, 256) == 0
@@ -81,8 +81,12 @@ def test_error_codes_and_workspace_queries_need_no_gpu():
     assert lib.qste_packed_linear_affine(None, 7, None, None, None, None, 1, 1, 8, None) == -1
     assert lib.qste_packed_transpose(None, 2, None, None, None, -1, 4, 8, None) == -2
     assert lib.qste_pack_affine_rows(None, 0, None, None, None, 4, 0, None) == -2
+    # any positive momentum block size is accepted (48 is not a power of
+    # two); zero or negative is refused
     assert lib.qste_coordinate_update(None, None, None, None, None, None, None, 4, 8, 0.9, 0.99, 2.0, 1.0,
-                                      48, 1, 0, None, None, None, None, 0, None) == -5
+                                      48, 1, 0, None, None, None, None, 0, None) == -3
+    assert lib.qste_coordinate_update(None, None, None, None, None, None, None, 4, 8, 0.9, 0.99, 2.0, 1.0,
+                                      0, 1, 0, None, None, None, None, 0, None) == -5
     assert lib.qste_coordinate_update(None, None, None, None, None, None, None, 4, 8, 0.9, 0.99, 2.0, 1.0,
                                       64, 1, 0, None, None, None, None, 0, None) == -3
 
@@ -401,6 +405,73 @@ def test_optimizer_flush_clamp_and_state_dict(fake):
     assert coords.state_bytes() > 0
 
 
+@pytest.mark.parametrize("accum", [torch.float32, torch.float16])
+def test_ledger_drain_never_returns_the_buffer_it_clears(accum):
+    """A prepared buffer survives a drain with keep_buffer, emptied; what the
+    drain returns is the evidence, in a tensor of its own (an fp32 buffer's
+    .float() is the buffer itself, and clearing it would hand the step zeros)."""
+
+    from qste_amd.surface import EvidenceLedger
+
+    ledger = EvidenceLedger(accum)
+    ledger.fix_buffer((3, 5), torch.device("cpu"))
+    address = ledger.held.data_ptr()
+    seen = []
+    for _ in range(2):
+        e = torch.randn(3, 5)
+        seen.append(e.to(accum).float())
+        ledger.open_uses += 1
+        ledger.deliver(None, e)
+    assert ledger.held.data_ptr() == address  # added in place
+    out = ledger.drain(keep_buffer=True)
+    assert out is not None and out.data_ptr() != address
+    assert torch.allclose(out, (seen[0].to(accum) + seen[1].to(accum)).float())
+    assert out.abs().sum() > 0
+    assert ledger.held.data_ptr() == address and not ledger.held.any()
+    assert ledger.drain(keep_buffer=False).abs().sum() == 0 and ledger.held is None
+
+
+def test_ledger_sums_tied_uses_before_the_sink():
+    from qste_amd.surface import EvidenceLedger
+
+    got = []
+    ledger = EvidenceLedger(torch.float32)
+    ledger.sink = lambda owner, e: got.append((owner, e))
+    parts = [torch.randn(2, 4) for _ in range(3)]
+    ledger.open_uses = 3
+    for i, e in enumerate(parts):
+        ledger.deliver("s", e)
+        assert len(got) == (1 if i == 2 else 0)
+    assert got[0][0] == "s"
+    assert torch.allclose(got[0][1], parts[0] + parts[1] + parts[2])
+    # single use: straight through, no buffer
+    ledger.open_uses = 1
+    ledger.deliver("s", parts[0])
+    assert torch.equal(got[1][1], parts[0]) and ledger.tied is None and ledger.held is None
+
+
+def test_fp32_accumulation_steps_on_the_accumulated_evidence(fake):
+    """prepare_accumulation with fp32 buffers: step() applies the sum of the
+    microbatches' evidence, not a cleared buffer."""
+
+    import qste_amd as qste
+
+    model = _mlp(6)
+    qste.convert(model, include=["0"], config={"evidence_accum_dtype": "fp32"})
+    coords = qste.QSTEOptimizer(model)
+    coords.prepare_accumulation()
+    x = torch.randn(8, 24)
+    for chunk in x.chunk(2):
+        model(chunk).square().sum().backward()
+    assert fake.calls == []
+    coords.step()
+    assert len(fake.calls) == 1
+    applied = fake.calls[0]["evidence"]
+    assert applied.abs().sum() > 0
+    s = qste.surfaces(model)[0]
+    assert s.ledger.held is not None and not s.ledger.held.any()
+
+
 def test_export_packed_gives_the_same_forward(fake):
     import qste_amd as qste
 
@@ -542,7 +613,7 @@ def test_embedding_forward_and_evidence(fake):
     torch.manual_seed(12)
     surface = qste.Surface(torch.randn(40, 16))
     captured = []
-    surface._immediate = lambda _, evidence: captured.append(evidence.clone())
+    surface.route_evidence(lambda _, evidence: captured.append(evidence.clone()))
     ids = torch.randint(0, 40, (3, 5))
     grad = torch.randn(3, 5, 16)
     out = qste.qste_embedding(ids, surface)

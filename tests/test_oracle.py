@@ -317,3 +317,43 @@ def test_planted_mistake_is_caught(golden):
     kwargs["beta1"] = float(np.nextafter(np.float32(0.9), np.float32(1.0)))
     oracle.coordinate_update(g[f"{name}__evidence"], state, **kwargs)
     assert not np.array_equal(state["moment_q"], g[f"{name}__out_moment_q"])
+
+
+def test_step_size_is_torchs_reciprocal_times_lr():
+    """fallback.py:204-206 writes the step size as ``coordinate_lr / moment_rms``
+    with a Python float over a 0-dim fp32 tensor.  Torch evaluates that through
+    ``Tensor.__rtruediv__`` as ``reciprocal() * lr``: two roundings.  The
+    oracle must equal torch's own evaluation bit for bit over learning rates
+    that are and are not powers of two, and one fp32 division (the obvious
+    spelling) must fail the same comparison, so the check discriminates."""
+
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(2024)
+    lrs = [0.3, 0.7, 0.1, 1.0, 2.0, 4.0, 0.25, 1e-3, 3.0, 0.05]
+    lrs += [float(v) for v in rng.uniform(1e-4, 8.0, size=40)]
+    rms = np.exp(rng.uniform(np.log(1e-8), np.log(1e3), size=30)).astype(np.float32)
+    rms = np.concatenate([rms, np.float32([1e-8, 1.0, 0.5, 3.0, 127.0])])
+    pairs = diff_one_division = 0
+    for lr in lrs:
+        for r in rms:
+            want = (lr / torch.tensor(float(r), dtype=torch.float32)).item()
+            got = oracle.step_size(r, lr)
+            assert np.float32(want).view(np.uint32) == got.view(np.uint32), (lr, float(r))
+            one = np.float32(np.float32(lr) / r)
+            diff_one_division += int(one != got)
+            pairs += 1
+    assert pairs >= 1000
+    # the single division disagrees often enough for this test to notice it
+    assert diff_one_division > 0.05 * pairs, diff_one_division
+
+
+def test_step_size_reaches_the_coordinate_step(golden):
+    """The step reports the step size it used; it is ``step_size(rms(m), lr)``."""
+
+    g = golden("coordinate_update")
+    for name in sorted({k.split("__")[0] for k in g}):
+        state, kwargs = _golden_step(g, name)
+        scalars = np.zeros(4, dtype=np.float32)
+        oracle.coordinate_update(g[f"{name}__evidence"], state, scalars=scalars, **kwargs)
+        assert scalars[2] == oracle.step_size(scalars[3], kwargs["coordinate_lr"]), name
+        assert scalars[1] >= 1.0 and scalars[3] >= np.float32(1e-8), name
