@@ -44,6 +44,7 @@ extern "C" {
 #define QSTE_E_WORKSPACE (-4)
 #define QSTE_E_BLOCK (-5)
 #define QSTE_E_ALIGN (-6)
+#define QSTE_E_SCRATCH (-7)
 
 /* Library version; bumps when an entry point's contract changes. */
 int qste_version(void);
@@ -167,6 +168,26 @@ int qste_coordinate_update(const float* evidence, int8_t* coordinate, uint8_t* p
                            const int64_t* step_device, int64_t* flips_out,
                            const uint8_t* update_enabled, void* workspace,
                            size_t workspace_bytes, void* stream);
+
+/* qste_coordinate_update without a caller workspace: it allocates nothing
+ * and takes no workspace argument.  No counterpart in the reference; it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving or training loops, harnesses that forbid
+ * hipMalloc).  Its scratch is a static device array of
+ * qste_coordinate_update_static_limit() bytes (16 MiB) per GPU, held until
+ * the process ends; a surface whose qste_coordinate_update_workspace_bytes()
+ * exceeds it is refused with QSTE_E_SCRATCH (14336 x 4096 at block 256 needs
+ * about 10 MiB).  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other threads) race and must not be
+ * issued.  Results equal qste_coordinate_update's bit for bit. */
+size_t qste_coordinate_update_static_limit(void);
+int qste_coordinate_update_static(const float* evidence, int8_t* coordinate, uint8_t* packed,
+                                  int8_t* moment_q, uint16_t* moment_scale, uint16_t* row_v,
+                                  uint16_t* col_v, int64_t rows, int64_t cols, double beta1,
+                                  double beta2, double update_clip, double coordinate_lr,
+                                  int64_t block_size, int64_t seed, int64_t step,
+                                  const int64_t* step_device, int64_t* flips_out,
+                                  const uint8_t* update_enabled, void* stream);
 
 /* ---- packed activations (src/qste/nn.py) ------------------------------- */
 

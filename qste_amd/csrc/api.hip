@@ -21,6 +21,10 @@ int launch_colsums(const void*, int, const float*, int64_t, int64_t, float*, flo
                    hipStream_t);
 size_t coordinate_update_workspace(int64_t, int64_t, int64_t);
 size_t coordinate_update_scalars_offset(int64_t, int64_t, int64_t);
+size_t coordinate_update_static_limit();
+int launch_coordinate_update_static(const float*, int8_t*, uint8_t*, int8_t*, uint16_t*, uint16_t*, uint16_t*,
+                                    int64_t, int64_t, double, double, double, double, int64_t, int64_t, int64_t,
+                                    const int64_t*, int64_t*, const uint8_t*, hipStream_t);
 int launch_coordinate_update(const float*, int8_t*, uint8_t*, int8_t*, uint16_t*, uint16_t*, uint16_t*,
                              int64_t, int64_t, double, double, double, double, int64_t, int64_t, int64_t,
                              const int64_t*, int64_t*, const uint8_t*, void*, size_t, hipStream_t);
@@ -147,6 +151,8 @@ const char* qste_error_string(int code) {
     case QSTE_E_WORKSPACE: return "qste: workspace missing or smaller than the *_workspace_bytes query";
     case QSTE_E_BLOCK: return "qste: momentum block size must be positive";
     case QSTE_E_ALIGN: return "qste: pointer alignment not supported";
+    case QSTE_E_SCRATCH:
+      return "qste: surface too large for the library's static scratch (qste_coordinate_update_static_limit)";
     default: return hipGetErrorString(static_cast<hipError_t>(code));
   }
 }
@@ -320,6 +326,29 @@ int qste_coordinate_update(const float* evidence, int8_t* coordinate, uint8_t* p
   return launch_coordinate_update(evidence, coordinate, packed, moment_q, moment_scale, row_v, col_v, rows,
                                   cols, beta1, beta2, update_clip, coordinate_lr, block_size, seed, step,
                                   step_device, flips_out, update_enabled, workspace, workspace_bytes, s);
+}
+
+size_t qste_coordinate_update_static_limit(void) { return coordinate_update_static_limit(); }
+
+int qste_coordinate_update_static(const float* evidence, int8_t* coordinate, uint8_t* packed,
+                                  int8_t* moment_q, uint16_t* moment_scale, uint16_t* row_v, uint16_t* col_v,
+                                  int64_t rows, int64_t cols, double beta1, double beta2, double update_clip,
+                                  double coordinate_lr, int64_t block_size, int64_t seed, int64_t step,
+                                  const int64_t* step_device, int64_t* flips_out,
+                                  const uint8_t* update_enabled, void* stream) {
+  if (block_size <= 0) return QSTE_E_BLOCK;
+  if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  hipStream_t s = as_stream(stream);
+  if (rows == 0 || cols == 0) {
+    if (!flips_out) return 0;
+    set_i64_kernel<<<1, 1, 0, s>>>(flips_out, 0);
+    return static_cast<int>(hipGetLastError());
+  }
+  if (!evidence || !coordinate || !packed || !moment_q || !moment_scale || !row_v || !col_v)
+    return QSTE_E_NULL;
+  return launch_coordinate_update_static(evidence, coordinate, packed, moment_q, moment_scale, row_v, col_v,
+                                         rows, cols, beta1, beta2, update_clip, coordinate_lr, block_size, seed,
+                                         step, step_device, flips_out, update_enabled, s);
 }
 
 }  // extern "C"

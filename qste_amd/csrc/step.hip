@@ -41,6 +41,8 @@
 // momentum passes: a wave owns a 1024-column chunk of one row at a time,
 // keeps its column factors in registers, and finds a momentum block's
 // maximum among block_size / 4 consecutive lanes with DPP lane moves.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace qste {
@@ -1273,6 +1275,70 @@ int launch_coordinate_update(const float* g, int8_t* coord, uint8_t* packed, int
   finish_kernel<<<ceil_div(p.blocks, kThreads) < 1024 ? ceil_div(p.blocks, kThreads) : 1024, kThreads, 0,
                   stream>>>(moment_scale, flips_out, p, w);
   return static_cast<int>(hipGetLastError());
+}
+
+// -- the step without a caller workspace ------------------------------------------
+// For callers that cannot allocate (code under graph capture, serving loops,
+// harnesses that forbid hipMalloc): the workspace is a file-scope device
+// array of kStaticScratchBytes, one copy per GPU, that lives until the
+// process ends.  Host code never passes the array's name to a kernel (on the
+// host it is only a stand-in for the symbol); each device's address comes
+// from hipGetSymbolAddress, looked up once per device with that device
+// current and kept.  Every call on a GPU shares that GPU's array, so calls
+// that overlap on one GPU (different streams, or threads) race on it.  No
+// kernel of the step reads a workspace byte it did not write earlier in the
+// same call, so nothing has to be cleared between calls.
+constexpr size_t kStaticScratchBytes = size_t{16} << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex scratch_lock;
+void* scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, or NULL with *rc set.
+void* device_scratch(int* rc) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *rc = static_cast<int>(e);
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    *rc = QSTE_E_SHAPE;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> hold(scratch_lock);
+  if (scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      *rc = e != hipSuccess ? static_cast<int>(e) : static_cast<int>(hipErrorInvalidSymbol);
+      return nullptr;
+    }
+    scratch_ptr[dev] = ptr;
+  }
+  *rc = 0;
+  return scratch_ptr[dev];
+}
+}  // namespace
+
+size_t coordinate_update_static_limit() { return kStaticScratchBytes; }
+
+int launch_coordinate_update_static(const float* g, int8_t* coord, uint8_t* packed, int8_t* moment_q,
+                                    uint16_t* moment_scale, uint16_t* row_v, uint16_t* col_v, int64_t rows,
+                                    int64_t cols, double beta1, double beta2, double update_clip,
+                                    double coordinate_lr, int64_t block_size, int64_t seed, int64_t step_,
+                                    const int64_t* step_device, int64_t* flips_out,
+                                    const uint8_t* update_enabled, hipStream_t stream) {
+  const size_t need = coordinate_update_workspace(rows, cols, block_size);
+  if (need > kStaticScratchBytes) return QSTE_E_SCRATCH;
+  int rc = 0;
+  void* ptr = device_scratch(&rc);
+  if (ptr == nullptr) return rc;
+  return launch_coordinate_update(g, coord, packed, moment_q, moment_scale, row_v, col_v, rows, cols, beta1, beta2,
+                                  update_clip, coordinate_lr, block_size, seed, step_, step_device, flips_out,
+                                  update_enabled, ptr, kStaticScratchBytes, stream);
 }
 
 }  // namespace qste
