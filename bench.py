@@ -51,7 +51,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip per-kernel, step and GEMV timing")
     ap.add_argument("--no-configs", action="store_true", help="skip the config 2 and config 3 step lines")
-    ap.add_argument("--cpu-tokens", type=int, default=256)
+    ap.add_argument("--cpu-tokens", type=int, default=512)
     ap.add_argument("--configs-only", action="store_true",
                     help="only the config 2 and config 3 step lines (for a kernel profile of those workloads)")
     ap.add_argument("--pmc-calibrate", action="store_true",
@@ -119,31 +119,111 @@ class SwiGLU:
         return self.down(F.silu(self.gate(x)) * self.up(x))
 
 
+def cfg1_workload(device, base=0):
+    """Config 1: one QSTE Linear 2048 -> 2048 in fp32 on 256 tokens.
+
+    Seeded on the CPU (torch.Generator, seeds base+0..3) and copied over:
+    x ~ N(0,1) [256, 2048] (s0); coordinates U{-127..127} (s1); row scales
+    |N(0,1)| * 0.02 (s2) held as log_scale = ln(scale); bias 0; target
+    ~ N(0,1) [256, 2048] (s3).  Returns (layer, x, target) on the device."""
+
+    import torch
+
+    import qste_amd as qste
+
+    def gen(k):
+        return torch.Generator().manual_seed(base + k)
+
+    x = torch.randn(256, 2048, generator=gen(0))
+    coord = torch.randint(-127, 128, (2048, 2048), generator=gen(1), dtype=torch.int32).to(torch.int8)
+    scale = torch.randn(2048, generator=gen(2)).abs_().mul_(0.02).clamp_min_(1e-6)
+    target = torch.randn(256, 2048, generator=gen(3))
+    surface = qste.Surface.from_state(coord.to(device), scale.log().to(device))
+    layer = qste.QSTELinear(surface, torch.zeros(2048, device=device))
+    return layer, x.to(device), target.to(device)
+
+
+def cfg1_step_gpu(layer, x, target, coords):
+    """Forward, MSE against the target, backward (the coordinate step runs
+    inside it), then QSTEOptimizer.step; returns the flips."""
+
+    import torch.nn.functional as F
+
+    F.mse_loss(layer(x), target).backward()
+    return coords.step()
+
+
+def cfg1_lines(device, cpu: bool):
+    """Config 1 timed on the GPU and, as the CPU anchor, on the host's cores
+    with the port of the reference's CPU backend (all of config 1, fp32)."""
+
+    import qste_amd as qste
+
+    layer, x, target = cfg1_workload(device)
+    coords = qste.QSTEOptimizer([layer.surface])
+    ms = timed_wall(lambda: cfg1_step_gpu(layer, x, target, coords), 20, warmup=3)
+    flop = 6.0 * 256 * 2048 * 2048
+    out = {"workload": "cfg1 QSTE Linear 2048->2048 fp32, 256 tokens, fwd+MSE+bwd+coordinate step",
+           "gpu_ms_per_step": round(ms, 4), "gpu_tflops": round(flop / ms / 1e9, 3)}
+    if cpu:
+        from oracle import cpu_baseline as cb
+
+        threads = cb.set_threads(cb.default_threads())
+        xs = x.cpu()
+        tg = target.cpu()
+        layer_cpu = cb.Surface(layer.surface.coordinate.cpu().numpy(), layer.scale.detach().cpu().numpy())
+        cb.cfg1_step(xs, tg, layer_cpu, 0)
+        iters, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 10.0 and iters < 2000:
+            cb.cfg1_step(xs, tg, layer_cpu, iters + 1)
+            iters += 1
+        secs = (time.perf_counter() - t0) / iters
+        out.update({"cpu_ms_per_step": round(secs * 1e3, 3), "cpu_tflops": round(flop / secs / 1e12, 4),
+                    "cpu_threads": threads, "cpu_model": cb.cpu_model(), "cpu_iterations": iters,
+                    "cpu_kind": "port of the reference's cpu.cpp (LUT expansion + torch fp32 GEMM, "
+                                "OpenMP encoding and 4-pass step)"})
+    return out
+
+
 def relu_mlp(d=1024, ratio=4, device="cuda"):
-    """Config 2: fc1 d -> ratio*d, ReLU, fc2 back, both QSTE (convert), bf16."""
+    """Config 2: fc1 d -> ratio*d, ReLU, fc2 back, both QSTE, bf16.
+
+    Each layer follows config 1's recipe with its own seeds (layer i: 10i+1
+    coordinates U{-127..127}, 10i+2 row scales |N(0,1)| * 0.02, bias 0),
+    built on the CPU and moved over; the ReLU between them is the packed
+    one-bit ReLU that ``convert`` puts in (it keeps one bit per element for
+    backward)."""
 
     import torch
     import torch.nn as nn
 
     import qste_amd as qste
 
-    torch.manual_seed(0)
-    model = nn.Sequential(nn.Linear(d, ratio * d), nn.ReLU(), nn.Linear(ratio * d, d))
-    return qste.convert(model).to(device=device, dtype=torch.bfloat16)
+    def layer(i, rows, cols):
+        gc = torch.Generator().manual_seed(10 * i + 1)
+        gs = torch.Generator().manual_seed(10 * i + 2)
+        coord = torch.randint(-127, 128, (rows, cols), generator=gc, dtype=torch.int32).to(torch.int8)
+        scale = torch.randn(rows, generator=gs).abs_().mul_(0.02).clamp_min_(1e-6)
+        surface = qste.Surface.from_state(coord.to(device), scale.log().to(device))
+        return qste.QSTELinear(surface, torch.zeros(rows, device=device))
+
+    model = nn.Sequential(layer(0, ratio * d, d), qste.nn.ReLU(), layer(1, d, ratio * d))
+    return model.to(device=device, dtype=torch.bfloat16)
 
 
 class GPT2Small:
     """Config 3: a GPT-2-small-shaped decoder (12 layers, d=768, 12 heads, MLP
     ratio 4, vocab 50257, context 1024, tied embedding), random init, bf16.
     Only the MLPs are converted to QSTE (their tanh-GELU becomes the packed
-    one); attention stays float, its two batched products run in fp32."""
+    one); attention stays float bf16: torch's fused causal attention (flash
+    or memory-efficient kernels only -- the unfused math path is excluded,
+    so a missing fused kernel is an error rather than a silent fallback)."""
 
     def __new__(cls, device="cuda", layers=12, d=768, heads=12, vocab=50257, context=1024):
-        import math
-
         import torch
         import torch.nn as nn
         import torch.nn.functional as F
+        from torch.nn.attention import SDPBackend, sdpa_kernel
 
         import qste_amd as qste
 
@@ -159,11 +239,9 @@ class GPT2Small:
             def attention(self, x):
                 b, s, _ = x.shape
                 q, k, v = self.qkv(x).split(d, dim=-1)
-                q, k, v = (t.reshape(b, s, heads, d // heads).transpose(1, 2).float() for t in (q, k, v))
-                att = torch.matmul(q, k.transpose(-1, -2).contiguous()) * (1.0 / math.sqrt(d // heads))
-                mask = torch.ones(s, s, dtype=torch.bool, device=x.device).triu(1)
-                att = att.masked_fill(mask, float("-inf")).softmax(-1)
-                y = torch.matmul(att, v.contiguous()).to(x.dtype)
+                q, k, v = (t.reshape(b, s, heads, d // heads).transpose(1, 2) for t in (q, k, v))
+                with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                    y = F.scaled_dot_product_attention(q, k, v, is_causal=True)
                 return self.proj(y.transpose(1, 2).reshape(b, s, d))
 
             def forward(self, x):
@@ -434,36 +512,56 @@ def decode_gemv(device, K=8192, N=28672, copies=10):
     return res
 
 
-def cpu_baseline(d, ffn, tokens):
-    import numpy as np
+def cpu_baseline(d, ffn, tokens, full_tokens=16384):
+    """Config 4 on this host's cores with the port of the reference's CPU
+    backend (oracle/cpu_baseline.py): LUT tile expansion + torch's fp32 GEMMs,
+    OpenMP encodings and four-pass coordinate steps.
 
-    import oracle
+    The token-proportional work (the three forwards with their encodings,
+    the SwiGLU, every backward product) is timed on ``tokens`` of the
+    workload's tokens and scaled to all of them; the three coordinate steps
+    (3 x ffn x d elements, the same cost at any token count) are timed in
+    full.  ``value`` is config 4's FLOPs over that estimated step time."""
+
+    import numpy as np
+    import torch
+
     from oracle import cpu_baseline as cb
 
+    threads = cb.set_threads(cb.default_threads())
     rng = np.random.default_rng(0)
-    x = rng.standard_normal((tokens, d), dtype=np.float32)
-    dy = rng.standard_normal((tokens, d), dtype=np.float32)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(tokens, d, generator=g)
+    dy = torch.randn(tokens, d, generator=g)
+    shapes = ((ffn, d), (ffn, d), (d, ffn))
     layers = []
-    for rows, cols in ((ffn, d), (ffn, d), (d, ffn)):
+    for rows, cols in shapes:
         coord = rng.integers(-127, 128, size=(rows, cols), dtype=np.int8)
-        packed = oracle.pack_coordinate(coord)
         scale = (np.abs(rng.standard_normal(rows)) * 0.01).astype(np.float32)
-        layers.append((packed, scale, oracle.fresh_state(coord, 256)))
-    t0 = time.perf_counter()
-    iters = 0
+        layers.append(cb.Surface(coord, scale))
+    cb.swiglu_products(x, dy, layers)  # warm the BLAS and the thread pool
+    iters, t0 = 0, time.perf_counter()
     while True:
-        cb.swiglu_mlp_step(x, layers, dy, step=iters)
+        cb.swiglu_products(x, dy, layers)
         iters += 1
-        if time.perf_counter() - t0 > 10.0 or iters >= 3:
+        if time.perf_counter() - t0 > 8.0 or iters >= 20:
             break
-    secs = (time.perf_counter() - t0) / iters
-    flop = 6.0 * tokens * (2 * ffn * d + d * ffn)
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(flop / secs / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
-            "sample": f"SwiGLU d={d} ffn={ffn} fwd+bwd+coordinate step on {tokens} tokens "
-                      f"(of {16384}), fp32, numpy BLAS + C oracle, {iters} iteration(s), "
-                      f"{secs:.2f} s each"}
+    t_tokens = (time.perf_counter() - t0) / iters
+    evidence = [torch.randn(rows, cols, generator=g).mul_(0.01) for rows, cols in shapes]
+    t_step = 0.0
+    for k, (layer, ev) in enumerate(zip(layers, evidence)):
+        work = ev.clone()  # the step consumes its evidence as scratch
+        t1 = time.perf_counter()
+        layer.step(work, seed=1 + 1_000_003 * k, step=0)
+        t_step += time.perf_counter() - t1
+    secs = t_tokens * (full_tokens / tokens) + t_step
+    flop = 6.0 * full_tokens * (2 * ffn * d + d * ffn)
+    return {"value": round(flop / secs / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "cpu_model": cb.cpu_model(),
+            "sample": f"cfg4 SwiGLU d={d} ffn={ffn}, fp32: token-proportional work timed on {tokens} of "
+                      f"{full_tokens} tokens ({t_tokens * 1e3:.1f} ms per pass, {iters} passes) and scaled "
+                      f"to {full_tokens}; the three coordinate steps timed in full ({t_step * 1e3:.1f} ms, "
+                      f"token-independent); estimated step {secs:.2f} s on {threads} threads"}
 
 
 def main():
@@ -568,6 +666,7 @@ def main():
         line["packed_activations"]["step_ms"] = round((time.perf_counter() - t1) / 3 * 1e3, 3)
         if not args.no_configs:
             line["configs"] = config_steps(device)
+    line["cfg1"] = cfg1_lines(device, cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(d, ffn, args.cpu_tokens)
     print(json.dumps(line), flush=True)

@@ -147,6 +147,36 @@ def test_packed_linear_decode(M):
     assert rel_l2(y.float().cpu().numpy(), bf(want)) <= 1e-3
 
 
+@pytest.mark.parametrize("step", [0, 70])
+def test_full_size_step_matches_the_oracle(step):
+    """Config-4 gate surface (14336 x 4096, the row kernels): two consecutive
+    steps from fresh state, the second at ``step`` (70 lets the usq pass
+    compute the momentum speculatively), bit-exact against the oracle on the
+    same evidence: coordinates, packed signs, momentum, fp16 statistics and
+    flip counts."""
+
+    from qste_amd import kernels
+
+    print(f"full-size step, second step number {step}", flush=True)
+    R, C = 14336, 4096
+    rng = np.random.default_rng(step + 3)
+    coord0 = rng.integers(-127, 128, size=(R, C), dtype=np.int8)
+    state = oracle.fresh_state(coord0, 256)
+    dev = {k: torch.from_numpy(v.copy()).to(DEV) for k, v in state.items()}
+    for k, number in enumerate((0, step + 1)):
+        ev = (rng.standard_normal((R, C), dtype=np.float32) * np.float32(0.01 * (k + 1)))
+        flips = kernels.coordinate_update(
+            torch.from_numpy(ev).to(DEV), dev["coordinate"], dev["packed"], dev["moment_q"],
+            dev["moment_scale"], dev["row_v"], dev["col_v"], beta1=0.9, beta2=0.99, update_clip=2.0,
+            coordinate_lr=0.7, block_size=256, seed=1 + 1_000_003, step=number)
+        oflips = oracle.coordinate_update(ev, state, beta1=0.9, beta2=0.99, update_clip=2.0, coordinate_lr=0.7,
+                                          block_size=256, seed=1 + 1_000_003, step=number)
+        for key, want in state.items():
+            got = dev[key].cpu().numpy()
+            assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), (number, key, int((got != want).sum()))
+        assert flips == oflips and flips > 0
+
+
 def test_full_size_step_properties():
     """Config-4 gate surface (14336 x 4096): integer invariants and reproducibility."""
 
@@ -208,3 +238,56 @@ def test_bf16_parameters_reach_the_kernels_intact():
     model(xr).backward(dy)
     ref_dx = dy.double() @ (sign * model.scale.detach().double()[:, None])
     assert float((xr.grad.double() - ref_dx).norm() / ref_dx.norm()) <= 5e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_weight_path_forward_evidence_and_scale_gradient(dtype):
+    """``.weight`` (QSTEWeightFn, reference functional.py:213-252) for code
+    that reads the dense matrix: forward is exactly sign * scale in the
+    scale's dtype; backward turns dL/dW into the surface's evidence dW * s
+    and the scale gradient row_inner(dW, sign) (times d scale / d log_scale),
+    against the float64 oracle, and the coordinate step applied on that
+    evidence inside backward equals the oracle's bit for bit."""
+
+    import qste_amd as qste
+
+    print(f"weight path {dtype}", flush=True)
+    rows, cols, m = 384, 520, 96
+    g = torch.Generator().manual_seed(31)
+    coord = torch.randint(-127, 128, (rows, cols), generator=g, dtype=torch.int32).to(torch.int8)
+    scale = torch.rand(rows, generator=g) * 0.02 + 0.005
+    surface = qste.Surface.from_state(coord.to(DEV), scale.log().to(DEV))
+    layer = qste.QSTELinear(surface, None).to(dtype=dtype)
+    coords = qste.QSTEOptimizer([surface])
+    seen = []
+    apply = coords._apply
+    surface.route_evidence(lambda s, e: (seen.append(e.detach().clone()), apply(s, e)))
+    x = torch.randn(m, cols, generator=g).to(DEV)
+    dy = torch.randn(m, rows, generator=g).to(DEV)
+
+    packed_before = surface.packed_sign.detach().cpu().numpy().copy()  # the step rewrites it in backward
+    w = layer.weight
+    assert w.dtype == dtype
+    s_eff = layer.scale.detach()
+    sign = torch.where(surface.coordinate >= 0, 1.0, -1.0).to(DEV)
+    assert torch.equal(w.detach().float(), (sign * s_eff.float()[:, None]).to(dtype).float())
+    (x.to(dtype) @ w.t()).float().mul(dy).sum().backward()
+    flips = coords.step()
+    torch.cuda.synchronize()
+
+    dw = (dy.double().t() @ x.to(dtype).double())            # dL/dW in float64
+    s64 = s_eff.double()
+    assert len(seen) == 1
+    want_e = dw * s64[:, None]
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert float((seen[0].double() - want_e).norm() / want_e.norm()) <= tol
+    gs = oracle.row_inner(dw.float().cpu().numpy(), packed_before, cols)
+    want_gs = torch.from_numpy(gs).to(DEV) * s64          # d scale / d log_scale = scale
+    got_gs = surface.log_scale.grad.double()
+    assert float((got_gs - want_gs).norm() / want_gs.norm()) <= tol
+    state = oracle.fresh_state(coord.numpy(), 256)
+    oflips = oracle.coordinate_update(seen[0].cpu().numpy(), state, beta1=0.9, beta2=0.99, update_clip=2.0,
+                                      coordinate_lr=1.0, block_size=256, seed=1, step=0)
+    assert np.array_equal(surface.coordinate.cpu().numpy(), state["coordinate"])
+    assert np.array_equal(surface.packed_sign.cpu().numpy(), state["packed"])
+    assert flips == oflips and flips > 0

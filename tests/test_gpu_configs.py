@@ -1,4 +1,9 @@
-"""The BASELINE configurations 2 and 3 end to end, at their real shapes.
+"""The BASELINE configurations 1, 2 and 3 end to end, at their real shapes.
+
+* config 1 -- one QSTE Linear 2048 -> 2048 in fp32 (256 tokens, MSE against a
+  target, backward, one coordinate step): forward, input gradient, evidence
+  and bias gradient against the float64 oracle (rel-L2 <= 1e-5), the step on
+  the GPU's own evidence bit-exact against the oracle;
 
 * config 2 -- the converted ReLU MLP (1024 -> 4096 -> 1024, bf16, 8192
   tokens): each layer's forward against a float64 product over the same signs
@@ -51,6 +56,61 @@ def _packed_of(coord):
     from qste_amd import kernels
 
     return kernels.pack_coordinate(coord)
+
+
+@pytest.mark.parametrize("base", [0, 100])
+def test_config1_single_linear_fp32(base):
+    """Config 1's workload (2048 -> 2048, 256 tokens, fp32, MSE against a
+    target, backward, one coordinate step from fresh state), with the
+    recipe's seeds 0..3 (offset by ``base``): y, the input gradient and the
+    evidence within rel-L2 1e-5 of the float64 oracle, and the step on the
+    GPU's own evidence bit-exact against the oracle's."""
+
+    import numpy as np
+
+    import oracle
+    import qste_amd as qste
+    from bench import cfg1_workload
+
+    print(f"config 1 base {base}", flush=True)
+    layer, x, target = cfg1_workload(DEV, base)
+    surface = layer.surface
+    coords = qste.QSTEOptimizer([surface])
+    seen = []
+    apply = coords._apply
+    surface.route_evidence(lambda s, e: (seen.append(e.detach().clone()), apply(s, e)))
+    packed = surface.packed_sign.detach().cpu().numpy()
+    coord0 = surface.coordinate.detach().cpu().numpy().copy()
+    scale = layer.scale.detach().cpu().numpy()
+    xr = x.clone().requires_grad_(True)
+    y = layer(xr)
+    loss = F.mse_loss(y, target)
+    loss.backward()
+    flips = coords.step()
+    torch.cuda.synchronize()
+
+    xs = x.cpu().numpy()
+    want_y = oracle.linear_fwd(xs, packed, scale, np.zeros(2048, np.float32), 2048)
+    assert _rel(y.detach().cpu(), torch.from_numpy(want_y)) <= 1e-5
+    dy = (2.0 / y.numel()) * (y.detach() - target)
+    dy_np = dy.cpu().numpy()
+    want_dx = oracle.linear_dgrad(dy_np, packed, 2048, scale)
+    assert _rel(xr.grad.cpu(), torch.from_numpy(want_dx)) <= 1e-5
+    bits, off, xsc = oracle.pack_affine_rows(xs)
+    want_e = oracle.decoded_evidence(dy_np, bits, off, xsc, 2048) * scale.astype(np.float64)[:, None]
+    assert len(seen) == 1
+    assert _rel(seen[0].cpu(), torch.from_numpy(want_e)) <= 1e-5
+    assert _rel(layer.bias.grad.cpu(), torch.from_numpy(dy_np.astype(np.float64).sum(0))) <= 1e-5
+
+    state = oracle.fresh_state(coord0, 256)
+    oflips = oracle.coordinate_update(seen[0].cpu().numpy(), state, beta1=0.9, beta2=0.99, update_clip=2.0,
+                                      coordinate_lr=1.0, block_size=256, seed=1, step=0)
+    assert np.array_equal(surface.coordinate.cpu().numpy(), state["coordinate"])
+    assert np.array_equal(surface.packed_sign.cpu().numpy(), state["packed"])
+    got = coords.state[id(surface)]
+    for k in ("moment_q", "moment_scale", "row_v", "col_v"):
+        assert np.array_equal(got[k].cpu().numpy().view(np.uint8), state[k].view(np.uint8)), k
+    assert flips == oflips and flips > 0
 
 
 def test_config2_relu_mlp():

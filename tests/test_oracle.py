@@ -357,3 +357,26 @@ def test_step_size_reaches_the_coordinate_step(golden):
         oracle.coordinate_update(g[f"{name}__evidence"], state, scalars=scalars, **kwargs)
         assert scalars[2] == oracle.step_size(scalars[3], kwargs["coordinate_lr"]), name
         assert scalars[1] >= 1.0 and scalars[3] >= np.float32(1e-8), name
+
+
+def test_blas_products_equal_the_c_restatement():
+    """The float64 BLAS products used for full-size samples against the C
+    restatement (itself pinned to the reference-written product vectors)."""
+
+    rng = np.random.default_rng(12)
+    rows, cols, m = 70, 203, 33
+    packed = rng.integers(0, 256, size=(rows, (cols + 7) // 8), dtype=np.uint8)
+    x = rng.standard_normal((m, cols)).astype(np.float32)
+    dy = rng.standard_normal((m, rows)).astype(np.float32)
+    scale = (rng.random(rows) + 0.5).astype(np.float32)
+    bias = rng.standard_normal(rows).astype(np.float32)
+    xs = (rng.random(m) + 0.1).astype(np.float32)
+    xbits = rng.integers(0, 256, size=(m, (cols + 7) // 8), dtype=np.uint8)
+    tol = dict(rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(oracle.linear_fwd_f64(x, packed, scale, bias, cols),
+                               oracle.linear_fwd(x, packed, scale, bias, cols), **tol)
+    np.testing.assert_allclose(oracle.linear_dgrad_f64(dy, packed, cols, scale),
+                               oracle.linear_dgrad(dy, packed, cols, scale), **tol)
+    np.testing.assert_allclose(oracle.evidence_f64(dy, xbits, cols, xs),
+                               oracle.evidence(dy, xbits, cols, xs), **tol)
+    np.testing.assert_array_equal(oracle.signs_f64(packed, cols), oracle.unpack_rows(packed, cols))
