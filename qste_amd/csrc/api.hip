@@ -33,6 +33,8 @@ int mfma_linear_forward(const void*, int, const uint8_t*, const float*, const fl
                         int64_t, int64_t, hipStream_t);
 int mfma_linear_dgrad(const void*, int, const uint8_t*, const float*, void*, int64_t, int64_t, int64_t,
                       hipStream_t);
+int mfma_linear_dgrad_t(const void*, int, const uint8_t*, int64_t, const uint16_t*, void*, int64_t, int64_t,
+                        int64_t, hipStream_t);
 int mfma_evidence(const void*, int, const uint8_t*, const float*, float*, int64_t, int64_t, int64_t,
                   const float*, const float*, const uint8_t*, float*, const EvidencePlan*, float*, hipStream_t);
 int64_t mfma_evidence_tiles(int64_t cols);
@@ -262,12 +264,12 @@ int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x, con
     if (mfma_pair_ok(dy, dtype, samples, rows, cols)) {
       const EvidencePlan plan = mfma_evidence_plan(samples, rows, cols, dx != nullptr);
       float* partial = reinterpret_cast<float*>(base + l.partial);
+      uint8_t* w_t = reinterpret_cast<uint8_t*>(base + l.w_t);
+      uint16_t* s16 = reinterpret_cast<uint16_t*>(base + l.s16);
+      const int64_t pb = (cols + 7) / 8;
       if (plan.pair) {
-        uint8_t* w_t = reinterpret_cast<uint8_t*>(base + l.w_t);
         uint8_t* x_t = reinterpret_cast<uint8_t*>(base + l.x_t);
-        uint16_t* s16 = reinterpret_cast<uint16_t*>(base + l.s16);
         uint16_t* xs16 = reinterpret_cast<uint16_t*>(base + l.xs16);
-        const int64_t pb = (cols + 7) / 8;
         if ((rc = launch_transpose_bits(packed_w, w_t, rows, cols, pb, l.w_t_pitch, s))) return rc;
         if ((rc = launch_transpose_bits(packed_x, x_t, samples, cols, pb, l.x_t_pitch, s))) return rc;
         if ((rc = launch_f32_to_16(scale, s16, rows, (rows + 63) / 64 * 64, dtype, s))) return rc;
@@ -277,7 +279,14 @@ int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x, con
         if (rc == 0) return launch_sum_partials(gs_part, mfma_evidence_tiles(cols), rows, grad_scale, s);
         if (rc != 1) return rc;
       } else {
-        if (dx && (rc = dgrad_dispatch(dy, dtype, packed_w, scale, dx, samples, rows, cols, s))) return rc;
+        if (dx) {
+          // dgrad from transposed signs (bits along K, bf16 scales)
+          if ((rc = launch_transpose_bits(packed_w, w_t, rows, cols, pb, l.w_t_pitch, s))) return rc;
+          if ((rc = launch_f32_to_16(scale, s16, rows, (rows + 63) / 64 * 64, dtype, s))) return rc;
+          rc = mfma_linear_dgrad_t(dy, dtype, w_t, l.w_t_pitch, s16, dx, samples, rows, cols, s);
+          if (rc == 1) rc = dgrad_dispatch(dy, dtype, packed_w, scale, dx, samples, rows, cols, s);
+          if (rc) return rc;
+        }
         dgrad_done = true;
         int64_t tiles = 0;
         if ((rc = evidence_dispatch(dy, dtype, packed_x, x_scale, evidence, samples, rows, cols, v, scale,

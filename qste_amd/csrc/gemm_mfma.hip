@@ -386,6 +386,7 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   // (k = 16s .. 16s+15 of the step) uses buffer s & 1
   bf16x8 a[2][MBN], b[2][NBN];
   uint64_t bits[NBN];
+  uint4 kscl[4];  // bits along K with a scale: the step's bf16 scales of this lane's k, per substep
   // A as rows of K: this lane, as a source of the transposed read, names
   // k-row 16s + 8kg + 4h + t and m = 128wm + 32mb + 16(g%2) + 4a .. +3
   // (lane = 16g + 4a... with t = (lane%16)/4, a = lane%4, g = lane/16);
@@ -411,10 +412,17 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   // (a set bit is +1); the expansions invert them, so no arithmetic waits on
   // these reads (LDS reads complete in order: a use right after this read
   // would also wait for every dense-fragment read issued before it)
-  auto load_bits = [&](const uint8_t* Bs) {
+  // (and, with a per-k scale, the step's scales for this lane's k: read
+  // here, once per step, rather than beside each expansion, where a use
+  // would wait for every dense-fragment read issued before it)
+  auto load_bits = [&](const uint8_t* Bs, const uint16_t* Ss) {
     if (BKIND != B_BITS_ALONG_N) {
 #pragma unroll
       for (int nb = 0; nb < NBN; ++nb) bits[nb] = *reinterpret_cast<const uint64_t*>(Bs + 8 * (WNC * wn + 32 * nb + l32));
+    }
+    if (BKIND == B_BITS_ALONG_K_SCALED) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) kscl[q] = *reinterpret_cast<const uint4*>(Ss + 16 * q + 8 * kg);
     }
   };
   // the inverted byte of k-bits of substep s (a set bit is -1)
@@ -424,9 +432,8 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
 #pragma unroll
       for (int nb = 0; nb < NBN; ++nb) dst[nb] = signs_along_k(neg_byte(nb, s), one);
     } else if (BKIND == B_BITS_ALONG_K_SCALED) {
-      const uint4 sc = *reinterpret_cast<const uint4*>(Ss + 16 * s + 8 * kg);
 #pragma unroll
-      for (int nb = 0; nb < NBN; ++nb) dst[nb] = scaled_signs_along_k(neg_byte(nb, s), sc);
+      for (int nb = 0; nb < NBN; ++nb) dst[nb] = scaled_signs_along_k(neg_byte(nb, s), kscl[s]);
     } else {
       const int kk = 16 * s + 8 * kg;
       const uint4 sc = *reinterpret_cast<const uint4*>(Ss + kk);
@@ -452,8 +459,7 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
     if (BKIND == B_BITS_ALONG_K) {
       dst[nb] = signs_along_k(neg_byte(nb, s), one);
     } else if (BKIND == B_BITS_ALONG_K_SCALED) {
-      const uint4 sc = *reinterpret_cast<const uint4*>(Ss + 16 * s + 8 * kg);
-      dst[nb] = scaled_signs_along_k(neg_byte(nb, s), sc);
+      dst[nb] = scaled_signs_along_k(neg_byte(nb, s), kscl[s]);
     } else {
       const int kk = 16 * s + 8 * kg;
       const uint4 sc = *reinterpret_cast<const uint4*>(Ss + kk);
@@ -505,7 +511,7 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
     mfma_row(3, 0);
     __builtin_amdgcn_sched_barrier(0);
     issue(it + 3, N3a, N3b, N3s, 1);
-    load_bits(N1b);
+    load_bits(N1b, N1s);
     load_a(N1a, 0, a[0]);
     mfma_row(3, 1);
     __builtin_amdgcn_sched_barrier(0);
@@ -536,7 +542,7 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   }
   issue(2, A2, B2, S2);
   stage_barrier<BKIND != B_BITS_ALONG_N ? 2 * NL : NL>();  // along K: steps 0, 1 complete; along N: step 0, 1
-  load_bits(B0);
+  load_bits(B0, S0);
   load_a(A0, 0, a[0]);
   expand_b(B0, S0, 0, b[0]);
   int it = 0;
@@ -957,6 +963,33 @@ int mfma_linear_dgrad(const void* dy, int dtype, const uint8_t* packed, const fl
         <<<wide_grid(m, cols), mfma::wide::THREADS, 0, stream>>>(p);
   else
     mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_N, mfma::EPI_PLAIN, QSTE_BF16>
+        <<<wide_grid(m, cols), mfma::wide::THREADS, 0, stream>>>(p);
+  return static_cast<int>(hipGetLastError());
+}
+
+// dgrad from a transposed copy of the signs (w_t [cols][w_t_pitch], bit r of
+// row c = sign of W[r][c], zero past rows) and the bf16 row scales (zero
+// padded to a multiple of 64): the bits run along K, so a lane's 8 k-values
+// are one byte and each expansion is one shift-and-OR per pair, as in the
+// forward.  Measured 6-10% faster than bits along N at config 4's shapes;
+// the results are identical (the same bf16 operand values, the same
+// accumulation order).
+int mfma_linear_dgrad_t(const void* dy, int dtype, const uint8_t* w_t, int64_t w_t_pitch, const uint16_t* scale16,
+                        void* dx, int64_t m, int64_t rows, int64_t cols, hipStream_t stream) {
+  if (!dgrad_ok(dy, dtype, w_t, m, rows, cols) || !fits32(cols * w_t_pitch) || !aligned16(w_t)) return 1;
+  mfma::Params p{};
+  p.a = static_cast<const uint16_t*>(dy);
+  p.bits = w_t;
+  p.kscale16 = scale16;
+  p.out = dx;
+  p.M = m; p.N = cols; p.K = rows;
+  p.lda = rows; p.pb = w_t_pitch;
+  p.a_rows = m; p.bit_rows = cols;
+  if (dtype == QSTE_F16)
+    mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K_SCALED, mfma::EPI_PLAIN, QSTE_F16>
+        <<<wide_grid(m, cols), mfma::wide::THREADS, 0, stream>>>(p);
+  else
+    mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K_SCALED, mfma::EPI_PLAIN, QSTE_BF16>
         <<<wide_grid(m, cols), mfma::wide::THREADS, 0, stream>>>(p);
   return static_cast<int>(hipGetLastError());
 }
