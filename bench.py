@@ -8,7 +8,11 @@ activations, seeded int8 coordinates U{-127..127}, row scales |N(0,1)|*0.01,
 upstream gradient N(0,1).  One step = forward of the three layers (with the
 1-bit activation encoding), backward (input gradient, evidence, scale
 gradient) and the coordinate step of all three surfaces, which runs inside
-backward as in the reference.  ``value`` = 6 * T * sum(R*C) / step time.
+backward as in the reference.  The SwiGLU gate between the layers is
+qste_amd.nn.swiglu, one fused kernel each way whose values and gradients
+equal torch's F.silu(g) * u bit for bit; the same step with torch's silu and
+mul is reported as ``step_torch_gate_ms``.  ``value`` = 6 * T * sum(R*C) /
+step time.
 
 Alongside, measured live with HIP events on the stream the kernels run on:
 each GEMM kind at the gate-layer shape (the dominant kernel is reported as
@@ -105,17 +109,27 @@ def make_layer(rows, cols, seed, device, scale_std=0.01):
 
 
 class SwiGLU:
-    def __init__(self, d, ffn, device):
+    """down(silu(gate(x)) * up(x)) over three binary layers.  ``fused``: the
+    gate is qste_amd.nn.swiglu (one kernel each way, same values and
+    gradients as torch's F.silu(.) * (.), and the down layer's activation
+    encoding made by that kernel); otherwise torch's silu and mul."""
+
+    def __init__(self, d, ffn, device, fused=True):
         import torch.nn as nn
 
         self.gate = make_layer(ffn, d, 11, device)
         self.up = make_layer(ffn, d, 21, device)
         self.down = make_layer(d, ffn, 31, device)
         self.modules = nn.ModuleList([self.gate, self.up, self.down])
+        self.fused = fused
 
     def __call__(self, x):
         import torch.nn.functional as F
 
+        import qste_amd as qste
+
+        if self.fused:
+            return self.down(qste.nn.swiglu(self.gate(x), self.up(x)))
         return self.down(F.silu(self.gate(x)) * self.up(x))
 
 
@@ -656,7 +670,17 @@ def main():
         line["coordinate_step"] = step_bandwidth(ffn, d, device)
         line["decode_gemv"] = decode_gemv(device)
         line["packed_activations"] = packed_activation_bandwidth(T, ffn, device)
-        # the same step with the SiLU retaining its int8 derivative (qste.packed_activations())
+        # the same step with torch's silu and mul for the gate (what a model
+        # written F.silu(gate(x)) * up(x) runs)
+        mlp.fused = False
+        step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        line["step_torch_gate_ms"] = round((time.perf_counter() - t1) / 3 * 1e3, 3)
+        # and with the SiLU retaining its int8 derivative (qste.packed_activations())
         packed_step()
         torch.cuda.synchronize()
         t1 = time.perf_counter()
@@ -664,6 +688,7 @@ def main():
             packed_step()
         torch.cuda.synchronize()
         line["packed_activations"]["step_ms"] = round((time.perf_counter() - t1) / 3 * 1e3, 3)
+        mlp.fused = True
         if not args.no_configs:
             line["configs"] = config_steps(device)
     line["cfg1"] = cfg1_lines(device, cpu=not args.no_cpu_baseline)

@@ -272,6 +272,28 @@ int qste_smooth_backward(const void* grad, int dtype, const void* payload,
                          int unsigned_payload, const float* scale, void* out, int64_t rows,
                          int64_t cols, void* stream);
 
+/* ---- the SwiGLU gate (no counterpart in the reference) ------------------ */
+
+/* out = silu(gate) * up elementwise over [rows, cols] in `dtype`, each step
+ * rounded where torch's F.silu(gate) * up rounds (silu rounded to the dtype,
+ * then the product), so the values equal torch's.  When `packed` is not
+ * NULL, every row of `out` is also given the one-bit affine encoding of
+ * qste_pack_affine_rows (packed uint8 [rows, (cols+7)/8], offset and scale
+ * fp32 [rows]), byte-identical to that entry on the same rows: the saved
+ * activation of a binary layer that reads `out` next.
+ * No counterpart in the reference, which runs torch's silu and mul (a
+ * SwiGLU MLP's gate: down(silu(gate(x)) * up(x))). */
+int qste_swiglu_forward(const void* gate, const void* up, int dtype, void* out, uint8_t* packed,
+                        float* offset, float* scale, int64_t rows, int64_t cols, void* stream);
+
+/* The gradients of out = silu(gate) * up over `count` elements, rounded as
+ * torch's autograd of that expression rounds them: a = dtype(silu(gate)),
+ * grad_up = dtype(grad * a), da = dtype(grad * up),
+ * grad_gate = dtype((da * s) * (1 + gate * (1 - s))), s = sigmoid(gate).
+ * No counterpart in the reference (see qste_swiglu_forward). */
+int qste_swiglu_backward(const void* grad, const void* gate, const void* up, int dtype, void* grad_gate,
+                         void* grad_up, int64_t count, void* stream);
+
 /* ---- binary embedding (src/qste/modules.py:68-100) ---------------------- */
 
 /* out [count, cols] (out_dtype) = sign(packed[ids[n]]) * scale[ids[n]];

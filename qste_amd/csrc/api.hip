@@ -47,6 +47,9 @@ int launch_transpose_bits(const uint8_t*, uint8_t*, int64_t, int64_t, int64_t, i
 int launch_f32_to_16(const float*, uint16_t*, int64_t, int64_t, int, hipStream_t);
 int gemv_linear_forward(const void*, int, const uint8_t*, const float*, const float*, void*, int64_t,
                         int64_t, int64_t, hipStream_t);
+int launch_swiglu_forward(const void*, const void*, int, void*, uint8_t*, float*, float*, int64_t, int64_t,
+                          hipStream_t);
+int launch_swiglu_backward(const void*, const void*, const void*, int, void*, void*, int64_t, hipStream_t);
 }  // namespace qste
 
 using namespace qste;
@@ -335,6 +338,25 @@ int qste_coordinate_update(const float* evidence, int8_t* coordinate, uint8_t* p
   return launch_coordinate_update(evidence, coordinate, packed, moment_q, moment_scale, row_v, col_v, rows,
                                   cols, beta1, beta2, update_clip, coordinate_lr, block_size, seed, step,
                                   step_device, flips_out, update_enabled, workspace, workspace_bytes, s);
+}
+
+int qste_swiglu_forward(const void* gate, const void* up, int dtype, void* out, uint8_t* packed, float* offset,
+                        float* scale, int64_t rows, int64_t cols, void* stream) {
+  if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
+  if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  if (rows * cols == 0) return 0;
+  if (!gate || !up || !out) return QSTE_E_NULL;
+  if (packed && (!offset || !scale)) return QSTE_E_NULL;
+  return launch_swiglu_forward(gate, up, dtype, out, packed, offset, scale, rows, cols, as_stream(stream));
+}
+
+int qste_swiglu_backward(const void* grad, const void* gate, const void* up, int dtype, void* grad_gate,
+                         void* grad_up, int64_t count, void* stream) {
+  if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
+  if (count < 0) return QSTE_E_SHAPE;
+  if (count == 0) return 0;
+  if (!grad || !gate || !up || !grad_gate || !grad_up) return QSTE_E_NULL;
+  return launch_swiglu_backward(grad, gate, up, dtype, grad_gate, grad_up, count, as_stream(stream));
 }
 
 size_t qste_coordinate_update_static_limit(void) { return coordinate_update_static_limit(); }

@@ -7,6 +7,7 @@
 // All three are HBM-bound byte work: one thread owns one packed output byte,
 // so no two threads ever write the same byte and no atomics are needed.
 #include "common.hpp"
+#include "encode.hpp"
 
 namespace qste {
 
@@ -147,10 +148,8 @@ __global__ __launch_bounds__(THREADS) void pack_affine_rows_bf16x8_kernel(
 
 // Rows of bf16 whose 8-value chunks number at most CH * THREADS: a
 // workgroup per row, each thread's chunks t, t + THREADS, ... held in
-// registers (loops unrolled, constant indices) from the first pass to the
-// second, so the row is read once.  Sums of eight values are pairwise in
-// double; sums of bf16 values this long are exact in double, so the result
-// does not depend on the order.
+// registers from the first pass to the second (encode_row_chunks), so the
+// row is read once.
 template <int THREADS, int CH>
 __global__ __launch_bounds__(THREADS) void pack_affine_rows_bf16_reg_kernel(
     const uint16_t* __restrict__ x, uint8_t* __restrict__ packed, float* __restrict__ offset,
@@ -158,7 +157,6 @@ __global__ __launch_bounds__(THREADS) void pack_affine_rows_bf16_reg_kernel(
   __shared__ double red[THREADS / kWave];
   const int64_t row = blockIdx.x;
   const uint4* src = reinterpret_cast<const uint4*>(x + row * cols);
-  uint8_t* dst = packed + row * stride;
   const int t = threadIdx.x;
   uint4 v[CH];
 #pragma unroll
@@ -166,44 +164,7 @@ __global__ __launch_bounds__(THREADS) void pack_affine_rows_bf16_reg_kernel(
     const int64_t q = t + static_cast<int64_t>(k) * THREADS;
     v[k] = q < stride ? src[q] : make_uint4(0, 0, 0, 0);
   }
-  // bf16 value i (0..7) of chunk k
-  auto value = [&](int k, int i) {
-    const uint32_t w = i < 2 ? v[k].x : i < 4 ? v[k].y : i < 6 ? v[k].z : v[k].w;
-    return (i & 1) ? __uint_as_float(w & 0xFFFF0000u) : __uint_as_float(w << 16);
-  };
-  double sum = 0.0;
-#pragma unroll
-  for (int k = 0; k < CH; ++k) {
-    double d[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) d[i] = static_cast<double>(value(k, i));
-    sum += ((d[0] + d[1]) + (d[2] + d[3])) + ((d[4] + d[5]) + (d[6] + d[7]));
-  }
-  sum = block_sum(sum, red);
-  const float n = static_cast<float>(cols);
-  const float mean = static_cast<float>(sum) / n;
-  double dev = 0.0;
-#pragma unroll
-  for (int k = 0; k < CH; ++k) {
-    const int64_t q = t + static_cast<int64_t>(k) * THREADS;
-    uint32_t byte = 0;
-    double d[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float c = value(k, i) - mean;
-      byte |= (c >= 0.0f ? 1u : 0u) << i;
-      d[i] = static_cast<double>(fabsf(c));
-    }
-    if (q < stride) {
-      dst[q] = static_cast<uint8_t>(byte);
-      dev += ((d[0] + d[1]) + (d[2] + d[3])) + ((d[4] + d[5]) + (d[6] + d[7]));
-    }
-  }
-  dev = block_sum(dev, red);
-  if (t == 0) {
-    offset[row] = mean;
-    scale[row] = static_cast<float>(dev) / n;
-  }
+  encode_row_chunks<THREADS, CH>(v, packed + row * stride, offset + row, scale + row, cols, stride, red);
 }
 
 // ---------------------------------------------------------------------------

@@ -1,0 +1,261 @@
+// The SwiGLU gate h = silu(g) * u and its backward, fused.
+//
+// A SwiGLU MLP (down(silu(gate(x)) * up(x))) spends, between its GEMMs, one
+// elementwise pass per torch operator: silu, the product, and in backward
+// two products and silu's backward, each reading and writing a full
+// [tokens, ffn] tensor.  Here the forward is one pass (read g and u, write h)
+// and the backward one pass (read dh, g and u, write dg and du); u and g are
+// what autograd keeps, where torch's chain keeps g, silu(g) and u.
+//
+// Every value is rounded where torch's operator chain rounds it, so the
+// results equal F.silu(g) * u and its autograd gradients in the same dtype:
+//   a  = dtype(g / (1 + exp(-g)))                  (silu, ActivationSiluKernel)
+//   h  = dtype(a * u)                               (mul)
+//   du = dtype(dh * a),  da = dtype(dh * u)         (mul's backward)
+//   dg = dtype((da * s) * (1 + g * (1 - s))),  s = 1 / (1 + exp(-g))
+//                                                   (silu_backward; torch's
+//                                                   build contracts the
+//                                                   inner multiply-add)
+// The arithmetic is fp32 (torch's opmath for bf16/fp16); a bf16 x bf16
+// product is exact in fp32, so only the final rounding matters there.
+//
+// The forward can also encode each row of h as the next layer's saved
+// activation (the one-bit affine encoding, encode.hpp), from the values it
+// already holds, so the down projection's forward need not read h again.
+#include "common.hpp"
+#include "encode.hpp"
+
+namespace qste {
+namespace swiglu {
+
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ float silu_value(float x) { return x / (1.0f + expf(-x)); }
+
+// The two fp32 factors of dg, from the rounded da and the input g
+__device__ __forceinline__ void silu_grad_factors(float da, float x, float& ds, float& inner) {
+  const float s = 1.0f / (1.0f + expf(-x));
+  inner = fmaf(x, 1.0f - s, 1.0f);
+  ds = da * s;
+}
+
+// dg before its rounding to the dtype (fp32, as torch's silu_backward
+// computes it; its vectorized fp16 kernel rounds that fp32 product to fp16)
+__device__ __forceinline__ float silu_grad(float da, float x) {
+  float ds, inner;
+  silu_grad_factors(da, x, ds, inner);
+  return ds * inner;
+}
+
+template <int DT>
+__device__ __forceinline__ float forward_one(float g, float u) {
+  using E = Elem<DT>;
+  const float a = E::round(silu_value(g));
+  return a * u;  // rounded by the caller's store
+}
+
+// Generic elementwise forward: any dtype, any alignment.
+template <int DT>
+__global__ __launch_bounds__(kThreads) void forward_kernel(const typename Elem<DT>::T* __restrict__ g,
+                                                           const typename Elem<DT>::T* __restrict__ u,
+                                                           typename Elem<DT>::T* __restrict__ h, int64_t n) {
+  using E = Elem<DT>;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads)
+    E::store(h, i, forward_one<DT>(E::load(g, i), E::load(u, i)));
+}
+
+// bf16, 8 values per 16-byte access
+__device__ __forceinline__ uint4 forward_chunk(const uint4& gc, const uint4& uc) {
+  uint32_t out[4];
+  const uint32_t gw[4] = {gc.x, gc.y, gc.z, gc.w}, uw[4] = {uc.x, uc.y, uc.z, uc.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float g0 = __uint_as_float(gw[j] << 16), g1 = __uint_as_float(gw[j] & 0xFFFF0000u);
+    const float u0 = __uint_as_float(uw[j] << 16), u1 = __uint_as_float(uw[j] & 0xFFFF0000u);
+    out[j] = f32x2_to_bf16x2(forward_one<QSTE_BF16>(g0, u0), forward_one<QSTE_BF16>(g1, u1));
+  }
+  return make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+__global__ __launch_bounds__(kThreads) void forward_bf16x8_kernel(const uint4* __restrict__ g,
+                                                                  const uint4* __restrict__ u,
+                                                                  uint4* __restrict__ h, int64_t chunks) {
+  for (int64_t q = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; q < chunks;
+       q += static_cast<int64_t>(gridDim.x) * kThreads)
+    h[q] = forward_chunk(g[q], u[q]);
+}
+
+// bf16 rows of `stride` 8-value chunks (stride <= CH * kThreads), a
+// workgroup per row: h is written and its row encoded from the registers.
+template <int CH>
+__global__ __launch_bounds__(kThreads) void forward_encode_kernel(const uint16_t* __restrict__ g,
+                                                                  const uint16_t* __restrict__ u,
+                                                                  uint16_t* __restrict__ h,
+                                                                  uint8_t* __restrict__ packed,
+                                                                  float* __restrict__ offset,
+                                                                  float* __restrict__ scale, int64_t cols,
+                                                                  int64_t stride) {
+  __shared__ double red[kThreads / kWave];
+  const int64_t row = blockIdx.x;
+  const uint4* gr = reinterpret_cast<const uint4*>(g + row * cols);
+  const uint4* ur = reinterpret_cast<const uint4*>(u + row * cols);
+  uint4* hr = reinterpret_cast<uint4*>(h + row * cols);
+  const int t = threadIdx.x;
+  uint4 gv[CH], uv[CH], v[CH];
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int64_t q = t + static_cast<int64_t>(k) * kThreads;
+    gv[k] = q < stride ? gr[q] : make_uint4(0, 0, 0, 0);
+    uv[k] = q < stride ? ur[q] : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int k = 0; k < CH; ++k) {
+    const int64_t q = t + static_cast<int64_t>(k) * kThreads;
+    v[k] = q < stride ? forward_chunk(gv[k], uv[k]) : make_uint4(0, 0, 0, 0);
+    if (q < stride) hr[q] = v[k];
+  }
+  encode_row_chunks<kThreads, CH>(v, packed + row * stride, offset + row, scale + row, cols, stride, red);
+}
+
+template <int DT>
+__device__ __forceinline__ void backward_one(float dh, float g, float u, float& dg, float& du) {
+  using E = Elem<DT>;
+  const float a = E::round(silu_value(g));
+  du = dh * a;
+  const float da = E::round(dh * u);
+  dg = silu_grad(da, g);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void backward_kernel(const typename Elem<DT>::T* __restrict__ dh,
+                                                            const typename Elem<DT>::T* __restrict__ g,
+                                                            const typename Elem<DT>::T* __restrict__ u,
+                                                            typename Elem<DT>::T* __restrict__ dg,
+                                                            typename Elem<DT>::T* __restrict__ du, int64_t n) {
+  using E = Elem<DT>;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    float a, b;
+    backward_one<DT>(E::load(dh, i), E::load(g, i), E::load(u, i), a, b);
+    E::store(dg, i, a);
+    E::store(du, i, b);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void backward_bf16x8_kernel(const uint4* __restrict__ dh,
+                                                                   const uint4* __restrict__ g,
+                                                                   const uint4* __restrict__ u,
+                                                                   uint4* __restrict__ dg,
+                                                                   uint4* __restrict__ du, int64_t chunks) {
+  for (int64_t q = blockIdx.x * static_cast<int64_t>(kThreads) + threadIdx.x; q < chunks;
+       q += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const uint4 hc = dh[q], gc = g[q], uc = u[q];
+    const uint32_t hw[4] = {hc.x, hc.y, hc.z, hc.w}, gw[4] = {gc.x, gc.y, gc.z, gc.w};
+    const uint32_t uw[4] = {uc.x, uc.y, uc.z, uc.w};
+    uint32_t og[4], ou[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float dg0, du0, dg1, du1;
+      backward_one<QSTE_BF16>(__uint_as_float(hw[j] << 16), __uint_as_float(gw[j] << 16),
+                              __uint_as_float(uw[j] << 16), dg0, du0);
+      backward_one<QSTE_BF16>(__uint_as_float(hw[j] & 0xFFFF0000u), __uint_as_float(gw[j] & 0xFFFF0000u),
+                              __uint_as_float(uw[j] & 0xFFFF0000u), dg1, du1);
+      og[j] = f32x2_to_bf16x2(dg0, dg1);
+      ou[j] = f32x2_to_bf16x2(du0, du1);
+    }
+    dg[q] = make_uint4(og[0], og[1], og[2], og[3]);
+    du[q] = make_uint4(ou[0], ou[1], ou[2], ou[3]);
+  }
+}
+
+inline int grid_of(int64_t work) {
+  int64_t b = (work + kThreads - 1) / kThreads;
+  if (b > 8192) b = 8192;  // a grid-stride loop covers the rest
+  return static_cast<int>(b < 1 ? 1 : b);
+}
+
+inline bool aligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace swiglu
+
+int launch_pack_affine_rows(const void*, int, uint8_t*, float*, float*, int64_t, int64_t, hipStream_t);
+
+int launch_swiglu_forward(const void* g, const void* u, int dtype, void* h, uint8_t* packed, float* offset,
+                          float* scale, int64_t rows, int64_t cols, hipStream_t s) {
+  using namespace swiglu;
+  const int64_t n = rows * cols;
+  if (n == 0) return 0;
+  const int64_t stride = cols / 8;
+  const bool vec = dtype == QSTE_BF16 && cols % 8 == 0 && aligned(g) && aligned(u) && aligned(h);
+  if (packed && vec && stride <= 8 * kThreads) {
+    if (stride <= 2 * kThreads)
+      forward_encode_kernel<2><<<rows, kThreads, 0, s>>>(static_cast<const uint16_t*>(g),
+                                                         static_cast<const uint16_t*>(u), static_cast<uint16_t*>(h),
+                                                         packed, offset, scale, cols, stride);
+    else
+      forward_encode_kernel<8><<<rows, kThreads, 0, s>>>(static_cast<const uint16_t*>(g),
+                                                         static_cast<const uint16_t*>(u), static_cast<uint16_t*>(h),
+                                                         packed, offset, scale, cols, stride);
+    return static_cast<int>(hipGetLastError());
+  }
+  if (vec) {
+    forward_bf16x8_kernel<<<grid_of(n / 8), kThreads, 0, s>>>(static_cast<const uint4*>(g),
+                                                               static_cast<const uint4*>(u), static_cast<uint4*>(h),
+                                                               n / 8);
+  } else {
+    switch (dtype) {
+      case QSTE_F32:
+        forward_kernel<QSTE_F32><<<grid_of(n), kThreads, 0, s>>>(static_cast<const float*>(g),
+                                                                 static_cast<const float*>(u),
+                                                                 static_cast<float*>(h), n);
+        break;
+      case QSTE_F16:
+        forward_kernel<QSTE_F16><<<grid_of(n), kThreads, 0, s>>>(static_cast<const uint16_t*>(g),
+                                                                 static_cast<const uint16_t*>(u),
+                                                                 static_cast<uint16_t*>(h), n);
+        break;
+      default:
+        forward_kernel<QSTE_BF16><<<grid_of(n), kThreads, 0, s>>>(static_cast<const uint16_t*>(g),
+                                                                  static_cast<const uint16_t*>(u),
+                                                                  static_cast<uint16_t*>(h), n);
+        break;
+    }
+  }
+  int rc = static_cast<int>(hipGetLastError());
+  if (rc || !packed) return rc;
+  // rows too wide (or not bf16) for the fused encoding: encode h as written
+  return launch_pack_affine_rows(h, dtype, packed, offset, scale, rows, cols, s);
+}
+
+int launch_swiglu_backward(const void* dh, const void* g, const void* u, int dtype, void* dg, void* du, int64_t n,
+                           hipStream_t s) {
+  using namespace swiglu;
+  if (n == 0) return 0;
+  if (dtype == QSTE_BF16 && n % 8 == 0 && aligned(dh) && aligned(g) && aligned(u) && aligned(dg) && aligned(du)) {
+    backward_bf16x8_kernel<<<grid_of(n / 8), kThreads, 0, s>>>(
+        static_cast<const uint4*>(dh), static_cast<const uint4*>(g), static_cast<const uint4*>(u),
+        static_cast<uint4*>(dg), static_cast<uint4*>(du), n / 8);
+    return static_cast<int>(hipGetLastError());
+  }
+  switch (dtype) {
+    case QSTE_F32:
+      backward_kernel<QSTE_F32><<<grid_of(n), kThreads, 0, s>>>(
+          static_cast<const float*>(dh), static_cast<const float*>(g), static_cast<const float*>(u),
+          static_cast<float*>(dg), static_cast<float*>(du), n);
+      break;
+    case QSTE_F16:
+      backward_kernel<QSTE_F16><<<grid_of(n), kThreads, 0, s>>>(
+          static_cast<const uint16_t*>(dh), static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u),
+          static_cast<uint16_t*>(dg), static_cast<uint16_t*>(du), n);
+      break;
+    default:
+      backward_kernel<QSTE_BF16><<<grid_of(n), kThreads, 0, s>>>(
+          static_cast<const uint16_t*>(dh), static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u),
+          static_cast<uint16_t*>(dg), static_cast<uint16_t*>(du), n);
+      break;
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
+}  // namespace qste

@@ -64,6 +64,16 @@ def forget_encodings() -> None:
     _last_encoding = None
 
 
+def remember_encoding(value: Tensor, payload: Tensor, aux: Tensor) -> None:
+    """Offer ``value``'s encoding (over its last dimension) to the next binary
+    layer that reads ``value``, as if that layer had encoded it itself."""
+
+    global _last_encoding
+    columns = int(value.shape[-1])
+    key = (value._version, value.data_ptr(), tuple(value.shape), value.dtype, columns)
+    _last_encoding = (weakref.ref(value), key, payload, aux)
+
+
 class QSTELinearFn(Function):
     @staticmethod
     def forward(ctx, inputs, packed, scale, bias, surface: Surface):
@@ -128,6 +138,41 @@ class QSTEWeightFn(Function):
         evidence = grad_weight.mul_(scale.detach().float().unsqueeze(1))
         surface.consume_evidence(evidence)
         return None, grad_scale.to(scale.dtype), None
+
+
+class SwiGLUFn(Function):
+    """``silu(gate) * up`` in one kernel each way, rounded as torch's
+    ``F.silu(gate) * up`` and its autograd round, keeping ``gate`` and ``up``
+    for backward.  With ``encode`` the forward also encodes the output's rows
+    for the binary layer that reads it next (a SwiGLU MLP's down
+    projection), which then does not read the output again to encode it."""
+
+    @staticmethod
+    def forward(ctx, gate, up, encode: bool):
+        out, encoding = kernels.swiglu_forward(gate, up, encode=encode)
+        ctx.save_for_backward(gate, up)
+        if encoding is not None:
+            packed, offset, scale = encoding
+            remember_encoding(out, packed, torch.stack((offset, scale)))
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        gate, up = ctx.saved_tensors
+        grad_gate, grad_up = kernels.swiglu_backward(grad_output.contiguous(), gate, up)
+        return grad_gate, grad_up, None
+
+
+def swiglu(gate: Tensor, up: Tensor) -> Tensor:
+    """The SwiGLU gate ``F.silu(gate) * up`` (same values and gradients), fused.
+
+    No counterpart in the reference; a SwiGLU MLP written
+    ``down(swiglu(gate(x), up(x)))`` computes what
+    ``down(F.silu(gate(x)) * up(x))`` computes, with two elementwise passes
+    instead of five and the down projection's activation encoding produced
+    with its input."""
+
+    return SwiGLUFn.apply(gate, up, torch.is_grad_enabled())
 
 
 def qste_weight(surface: Surface) -> Tensor:

@@ -43,6 +43,8 @@ __all__ = [
     "packed_row_inner",
     "packed_transpose",
     "status",
+    "swiglu_backward",
+    "swiglu_forward",
     "unpack_rows",
 ]
 
@@ -572,6 +574,52 @@ def smooth_backward(grad: Tensor, payload: Tensor, scale: Tensor) -> Tensor:
         _ptr(scale_f32), _ptr(out), rows, cols, _stream(device))
     _lib.check(code, "smooth_backward")
     return out
+
+
+# ---------------------------------------------------------------------------
+# the SwiGLU gate (no counterpart in the reference)
+# ---------------------------------------------------------------------------
+
+
+def swiglu_forward(gate: Tensor, up: Tensor, *, encode: bool = False):
+    """``silu(gate) * up`` with torch's roundings, in one pass.
+
+    Returns ``(out, encoding)``; with ``encode`` the encoding is
+    ``(packed, offset, scale)`` of ``out``'s rows as ``pack_affine_rows``
+    gives them (last dimension = row), else None.
+    """
+
+    device = _require_gpu(gate, up)
+    if gate.shape != up.shape or gate.dtype != up.dtype:
+        raise ValueError("gate and up must have the same shape and dtype")
+    g, u = _aligned(gate), _aligned(up)
+    cols = int(g.shape[-1]) if g.dim() else 1
+    rows = g.numel() // cols if cols else 0
+    out = torch.empty_like(g)
+    packed = offset = scale = None
+    if encode:
+        packed = torch.empty(rows, _packed_width(cols), dtype=torch.uint8, device=device)
+        offset = torch.empty(rows, dtype=torch.float32, device=device)
+        scale = torch.empty(rows, dtype=torch.float32, device=device)
+    code = _lib.load().qste_swiglu_forward(
+        _ptr(g), _ptr(u), _dtype_code(g), _ptr(out), _ptr(packed), _ptr(offset), _ptr(scale), rows, cols,
+        _stream(device))
+    _lib.check(code, "swiglu_forward")
+    return out, ((packed, offset, scale) if encode else None)
+
+
+def swiglu_backward(grad: Tensor, gate: Tensor, up: Tensor) -> tuple[Tensor, Tensor]:
+    """``(grad_gate, grad_up)`` of ``silu(gate) * up`` with torch's roundings."""
+
+    device = _require_gpu(grad, gate, up)
+    if not (grad.shape == gate.shape == up.shape) or not (grad.dtype == gate.dtype == up.dtype):
+        raise ValueError("grad, gate and up must have the same shape and dtype")
+    dh, g, u = _aligned(grad), _aligned(gate), _aligned(up)
+    dg, du = torch.empty_like(g), torch.empty_like(g)
+    code = _lib.load().qste_swiglu_backward(
+        _ptr(dh), _ptr(g), _ptr(u), _dtype_code(g), _ptr(dg), _ptr(du), g.numel(), _stream(device))
+    _lib.check(code, "swiglu_backward")
+    return dg, du
 
 
 # ---------------------------------------------------------------------------

@@ -58,6 +58,8 @@ SIGNATURES = {
     "qste_smooth_activation": (_int, [_vp, _int, _int, _flt, _vp, _int, _vp, _vp, _vp, _i64, _i64,
                                       _vp]),
     "qste_smooth_backward": (_int, [_vp, _int, _vp, _int, _vp, _vp, _i64, _i64, _vp]),
+    "qste_swiglu_forward": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "qste_swiglu_backward": (_int, [_vp, _vp, _vp, _int, _vp, _vp, _i64, _vp]),
     "qste_packed_embedding": (_int, [_vp, _i64, _vp, _vp, _vp, _int, _i64, _i64, _vp]),
     "qste_embedding_backward_workspace_bytes": (_sz, [_i64, _i64]),
     "qste_embedding_backward": (_int, [_vp, _i64, _vp, _int, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _sz,

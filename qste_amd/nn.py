@@ -25,6 +25,7 @@ from torch import Tensor
 from torch.autograd import Function
 
 from . import kernels
+from .functional import swiglu
 
 # The originals, bound before ``packed_activations`` can patch them: the
 # wrappers call these for values the kernels do not produce, and a patched
@@ -735,7 +736,7 @@ def packed_activations():
 __all__ = [
     "CELU", "Dropout", "ELU", "EXACT_REPLACEMENTS", "GELU", "Hardsigmoid", "Hardswish", "Hardtanh",
     "LeakyReLU", "Mish", "REPLACEMENTS", "ReLU", "ReLU6", "SELU", "SMOOTH_REPLACEMENTS", "SiLU",
-    "Sigmoid", "Softplus", "Tanh", "celu", "dropout", "elementwise", "elu", "gelu", "hardsigmoid",
+    "Sigmoid", "Softplus", "Tanh", "celu", "dropout", "elementwise", "elu", "gelu", "hardsigmoid", "swiglu",
     "hardswish", "hardtanh", "leaky_relu", "mish", "packed", "packed_activations", "relu",
     "relu6", "relu_square", "replace", "selu", "sigmoid", "silu", "softplus", "tanh",
 ]

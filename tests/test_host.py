@@ -202,6 +202,26 @@ class OracleKernels:
         return torch.from_numpy(out).to(grad.dtype)
 
 
+    # the SwiGLU gate: torch's own chain on the CPU, encoding by the oracle
+    def swiglu_forward(self, gate, up, *, encode=False):
+        import torch.nn.functional as F
+
+        out = F.silu(gate) * up
+        if not encode:
+            return out, None
+        self.swiglu_encodes = getattr(self, "swiglu_encodes", 0) + 1
+        b, o, s = oracle.pack_affine_rows(out.float().reshape(-1, out.shape[-1]).numpy())
+        return out, (torch.from_numpy(b), torch.from_numpy(o), torch.from_numpy(s))
+
+    def swiglu_backward(self, grad, gate, up):
+        g = gate.detach().requires_grad_(True)
+        u = up.detach().requires_grad_(True)
+        import torch.nn.functional as F
+
+        with torch.enable_grad():
+            (F.silu(g) * u).backward(grad)
+        return g.grad, u.grad
+
     # binary embedding (oracle/embedding.py)
     def packed_embedding(self, ids, packed, scale, columns):
         out = oe.lookup(ids.numpy(), packed.numpy(), scale.detach().float().numpy(), columns)
@@ -213,7 +233,8 @@ class OracleKernels:
 
 
 ACTIVATION_OPS = ("pack_bits", "unpack_bits", "masked_backward", "masked_activation",
-                  "smooth_activation", "smooth_backward", "packed_embedding", "embedding_backward")
+                  "smooth_activation", "smooth_backward", "packed_embedding", "embedding_backward",
+                  "swiglu_forward", "swiglu_backward")
 
 
 @pytest.fixture
@@ -670,3 +691,42 @@ def test_layers_reading_one_input_share_its_encoding(fake, monkeypatch):
     x.add_(1.0)
     model["up"](x)
     assert calls == [(5, 8), (5, 8)]
+
+
+def test_swiglu_hands_its_encoding_to_the_down_layer(fake, monkeypatch):
+    """down(swiglu(gate(x), up(x))): x is encoded once (gate and up share
+    it), h is encoded by the gate kernel and the down layer takes that
+    encoding instead of encoding h again; the result and the gradients equal
+    the torch gate's."""
+
+    import qste_amd as qste
+    from qste_amd import kernels
+
+    calls = []
+    real = kernels.pack_affine_rows
+    monkeypatch.setattr(kernels, "pack_affine_rows", lambda v: (calls.append(tuple(v.shape)), real(v))[1])
+
+    def layer(rows, cols, seed):
+        g = torch.Generator().manual_seed(seed)
+        coord = torch.randint(-127, 128, (rows, cols), generator=g, dtype=torch.int32).to(torch.int8)
+        return qste.QSTELinear(qste.Surface.from_state(coord, torch.full((rows,), -3.0)), None)
+
+    gate, up, down = layer(48, 16, 1), layer(48, 16, 2), layer(16, 48, 3)
+    x = torch.randn(10, 16)
+
+    def run(fused):
+        calls.clear()
+        xr = x.clone().requires_grad_(True)
+        a, b = gate(xr), up(xr)
+        h = qste.nn.swiglu(a, b) if fused else torch.nn.functional.silu(a) * b
+        y = down(h)
+        y.square().sum().backward()
+        return y.detach(), xr.grad, list(calls)
+
+    y0, g0, c0 = run(False)
+    y1, g1, c1 = run(True)
+    assert c0 == [(10, 16), (10, 48)]      # x once (shared), then h
+    assert c1 == [(10, 16)]                 # h's encoding came from the gate kernel
+    assert fake.swiglu_encodes == 1
+    assert torch.allclose(y0, y1, rtol=1e-6, atol=1e-6)
+    assert torch.allclose(g0, g1, rtol=1e-5, atol=1e-6)
