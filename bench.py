@@ -59,7 +59,8 @@ def parse():
     ap.add_argument("--configs-only", action="store_true",
                     help="only the config 2 and config 3 step lines (for a kernel profile of those workloads)")
     ap.add_argument("--pmc-calibrate", action="store_true",
-                    help="one launch of each GEMM kind at the gate-layer shape plus a plain device copy of "
+                    help="one launch of each GEMM kind at the gate-layer shape, one coordinate step there "
+                         "(fresh, then steady), one decode GEMV at M = 1, 4, 16, and a plain device copy of "
                          "COPY_BYTES, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
     return ap.parse_args()
 
@@ -93,7 +94,26 @@ def pmc_calibrate(T, d, ffn, device):
     dst.copy_(src)
     torch.cuda.synchronize()
     kernels_t, _ = gemm_kernels(T, d, ffn, device, iters=1)
-    print(json.dumps({"copy_bytes": COPY_BYTES, "gemm_shape": [T, ffn, d], "kernels": kernels_t}), flush=True)
+    # one coordinate step at the gate shape, fresh then steady (in that
+    # order: their dispatches are told apart by position in the trace)
+    for steady in (False, True):
+        fn, _, _ = step_state(ffn, d, device, steady)
+        fn()
+        torch.cuda.synchronize()
+    # one decode launch at each M, each on a weight copy of its own
+    from qste_amd import kernels
+
+    K, N = 8192, 28672
+    gen = torch.Generator(device=device).manual_seed(1)
+    for M in (1, 4, 16):
+        w = torch.randint(0, 256, (N, K // 8), generator=gen, device=device, dtype=torch.int32).to(torch.uint8)
+        s = torch.randn(N, generator=gen, device=device).abs_().mul_(0.02)
+        x = torch.randn(M, K, generator=gen, device=device).to(torch.bfloat16)
+        torch.cuda.synchronize()
+        kernels.packed_linear_affine(x, w, s, None, K)
+        torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "gemm_shape": [T, ffn, d], "kernels": kernels_t,
+                      "step_shape": [ffn, d], "decode_shape": [N, K]}), flush=True)
 
 
 def make_layer(rows, cols, seed, device, scale_std=0.01):
@@ -434,7 +454,15 @@ def vendor_dense(T, d, ffn, device, iters=5):
     return out
 
 
-def step_bandwidth(rows, cols, device):
+def step_state(rows, cols, device, steady: bool):
+    """A surface's coordinate-step operands at the gate shape.
+
+    fresh: zero second moments and momentum, as at step 0 (the clip engages,
+    so every pass runs).  steady: the state a long run settles into -- second
+    moments at the evidence's mean square, int8 momentum with block scales of
+    a unit-RMS update -- stepped at step 100, where the normalized update's
+    RMS is about 1 and the clip (2.0) stays idle."""
+
     import torch
 
     from qste_amd import kernels
@@ -444,18 +472,56 @@ def step_bandwidth(rows, cols, device):
     coord = torch.randint(-127, 128, (rows, cols), generator=g, device=device, dtype=torch.int32).to(torch.int8)
     packed = kernels.pack_coordinate(coord)
     blocks = (rows * cols + 255) // 256
-    mq = torch.zeros_like(coord)
-    ms_ = torch.full((blocks,), 1 / 127, dtype=torch.float16, device=device)
-    rv = torch.zeros(rows, dtype=torch.float16, device=device)
-    cv = torch.zeros(cols, dtype=torch.float16, device=device)
+    if steady:
+        mq = torch.randint(-127, 128, (rows, cols), generator=g, device=device, dtype=torch.int32).to(torch.int8)
+        ms_ = torch.full((blocks,), 3.0 / 127, dtype=torch.float16, device=device)
+        rv = torch.full((rows,), 1e-4, dtype=torch.float16, device=device)
+        cv = torch.full((cols,), 1e-4, dtype=torch.float16, device=device)
+    else:
+        mq = torch.zeros_like(coord)
+        ms_ = torch.full((blocks,), 1 / 127, dtype=torch.float16, device=device)
+        rv = torch.zeros(rows, dtype=torch.float16, device=device)
+        cv = torch.zeros(cols, dtype=torch.float16, device=device)
     flips = torch.empty((), dtype=torch.int64, device=device)
-    fn = lambda: kernels.coordinate_update(  # noqa: E731
-        ev, coord, packed, mq, ms_, rv, cv, beta1=0.9, beta2=0.99, update_clip=2.0,
-        coordinate_lr=1.0, block_size=256, seed=1, step=0, flips=flips)
-    ms = timed_events(fn, 5)
-    nbytes = rows * cols * (4 + 2 + 2) + rows * ((cols + 7) // 8) + 4 * blocks + 4 * (rows + cols)
-    return {"rows": rows, "cols": cols, "ms": round(ms, 4), "algorithmic_bytes": nbytes,
-            "gbps": round(nbytes / ms / 1e6, 1), "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / HBM_PEAK, 4)}
+    step = 100 if steady else 0
+
+    def fn():
+        kernels.coordinate_update(ev, coord, packed, mq, ms_, rv, cv, beta1=0.9, beta2=0.99, update_clip=2.0,
+                                  coordinate_lr=1.0, block_size=256, seed=1, step=step, flips=flips)
+
+    def divisor():
+        """One more step through the C entry with a workspace of our own, whose
+        scalars block (sqrt mean row statistic, clip divisor, step size,
+        momentum RMS) is read back: the clip divisor it ran with."""
+
+        lib = kernels._lib.load()
+        need = lib.qste_coordinate_update_workspace_bytes(rows, cols, 256)
+        at = lib.qste_coordinate_update_scalars_offset(rows, cols, 256)
+        work = torch.empty(need, dtype=torch.uint8, device=device)
+        rc = lib.qste_coordinate_update(
+            ev.data_ptr(), coord.data_ptr(), packed.data_ptr(), mq.data_ptr(), ms_.data_ptr(), rv.data_ptr(),
+            cv.data_ptr(), rows, cols, 0.9, 0.99, 2.0, 1.0, 256, 1, step, None, flips.data_ptr(), None,
+            work.data_ptr(), need, torch.cuda.current_stream(device).cuda_stream)
+        kernels._lib.check(rc, "coordinate_update")
+        return float(work[at:at + 16].view(torch.float32)[1].item())
+
+    return fn, blocks, divisor
+
+
+def step_bandwidth(rows, cols, device):
+    """Coordinate step of one rows x cols surface, fresh and steady, each with
+    the clip divisor it ran with (1.0: the clip is idle)."""
+
+    out = {}
+    for kind in ("fresh", "steady"):
+        fn, blocks, divisor = step_state(rows, cols, device, kind == "steady")
+        ms = timed_events(fn, 5)
+        nbytes = rows * cols * (4 + 2 + 2) + rows * ((cols + 7) // 8) + 4 * blocks + 4 * (rows + cols)
+        out[kind] = {"rows": rows, "cols": cols, "ms": round(ms, 4), "algorithmic_bytes": nbytes,
+                     "gbps": round(nbytes / ms / 1e6, 1),
+                     "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / HBM_PEAK, 4),
+                     "clip_divisor": divisor()}
+    return out
 
 
 def packed_activation_bandwidth(T, ffn, device):

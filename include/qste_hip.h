@@ -139,6 +139,20 @@ int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x,
                          int64_t samples, int64_t rows, int64_t cols, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* qste_linear_backward with the offset correction's column sums brought by
+ * the caller: offset_dot fp32 [rows] = sum_t dy[t, r] * x_offset[t], which
+ * the entry then uses instead of reading dy for it (when grad_bias is
+ * requested dy is read for the bias sums anyway, and offset_dot is ignored).
+ * Same outputs as qste_linear_backward when offset_dot holds what that entry
+ * would sum (qste_swiglu_backward_sums produces it so).  Replaces
+ * QSTELinearFn.backward (src/qste/functional.py:173-194), as that entry does;
+ * the reference has no split of its column sums. */
+int qste_linear_backward_offset_dot(const void* dy, int dtype, const uint8_t* packed_x, const float* x_offset,
+                                    const float* x_scale, const uint8_t* packed_w, const float* scale, void* dx,
+                                    float* evidence, float* grad_scale, float* grad_bias, const float* offset_dot,
+                                    int64_t samples, int64_t rows, int64_t cols, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+
 /* One fused QSTE coordinate step on one surface
  * (qste.kernels.coordinate_update, loader.py:329-368; spec
  * fallback.py:158-242): factored second moment, global RMS clip, block
@@ -293,6 +307,39 @@ int qste_swiglu_forward(const void* gate, const void* up, int dtype, void* out, 
  * No counterpart in the reference (see qste_swiglu_forward). */
 int qste_swiglu_backward(const void* grad, const void* gate, const void* up, int dtype, void* grad_gate,
                          void* grad_up, int64_t count, void* stream);
+
+/* qste_swiglu_backward over [rows, cols] that also sums its outputs for the
+ * two binary layers that produced gate and up:
+ *   sums[c]        = sum_t grad_gate[t, c] * offset_gate[t]
+ *   sums[cols + c] = sum_t grad_up[t, c] * offset_up[t]
+ * (fp32, offsets fp32 [rows]: those layers' saved input offsets), each
+ * summed in the order qste_linear_backward sums its dy, so the sums are what
+ * that entry would compute from grad_gate and grad_up, bit for bit: the
+ * offset_dot of qste_linear_backward_offset_dot.  grad_gate and grad_up are
+ * those of qste_swiglu_backward.  Needs
+ * qste_swiglu_backward_sums_workspace_bytes(rows, cols) bytes of workspace.
+ * No counterpart in the reference (see qste_swiglu_forward). */
+size_t qste_swiglu_backward_sums_workspace_bytes(int64_t rows, int64_t cols);
+int qste_swiglu_backward_sums(const void* grad, const void* gate, const void* up, int dtype, void* grad_gate,
+                              void* grad_up, const float* offset_gate, const float* offset_up, float* sums,
+                              int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- the learned row scale (src/qste/surface.py:84-85) ------------------- */
+
+/* scale = clamp(exp(log_scale), lo, hi) over n rows, and exp_value = the
+ * exp before the clamp (what the backward reads), rounded as torch's
+ * log_scale.exp().clamp(lo, hi) rounds (lo and hi as fp32; a NaN stays NaN).
+ * Replaces the Surface.scale property's two torch operators
+ * (src/qste/surface.py:84-85). */
+int qste_row_scale(const float* log_scale, float* scale, float* exp_value, int64_t n, float lo, float hi,
+                   void* stream);
+
+/* grad_log_scale = (lo <= exp_value <= hi ? grad : 0) * exp_value: torch's
+ * autograd of exp().clamp(lo, hi) (clamp_backward, then exp's backward by
+ * its result), bit for bit.  Replaces that autograd chain of
+ * src/qste/surface.py:84-85. */
+int qste_row_scale_backward(const float* exp_value, const float* grad, float* grad_log_scale, int64_t n, float lo,
+                            float hi, void* stream);
 
 /* ---- binary embedding (src/qste/modules.py:68-100) ---------------------- */
 

@@ -50,6 +50,11 @@ int gemv_linear_forward(const void*, int, const uint8_t*, const float*, const fl
 int launch_swiglu_forward(const void*, const void*, int, void*, uint8_t*, float*, float*, int64_t, int64_t,
                           hipStream_t);
 int launch_swiglu_backward(const void*, const void*, const void*, int, void*, void*, int64_t, hipStream_t);
+int launch_row_scale(const float*, float*, float*, int64_t, float, float, hipStream_t);
+size_t swiglu_backward_sums_workspace(int64_t, int64_t);
+int launch_swiglu_backward_sums(const void*, const void*, const void*, int, void*, void*, const float*, const float*,
+                                int64_t, int64_t, float*, float*, hipStream_t);
+int launch_row_scale_backward(const float*, const float*, float*, int64_t, float, float, hipStream_t);
 }  // namespace qste
 
 using namespace qste;
@@ -238,10 +243,14 @@ size_t qste_linear_backward_workspace_bytes(int64_t samples, int64_t rows, int64
   return backward_layout(samples, rows, cols).total;
 }
 
-int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x, const float* x_offset,
+namespace {
+
+// offset_dot: sum_t dy[t, r] * x_offset[t] when the caller has it (then dy
+// is not read for it), or NULL
+int linear_backward_impl(const void* dy, int dtype, const uint8_t* packed_x, const float* x_offset,
                          const float* x_scale, const uint8_t* packed_w, const float* scale, void* dx,
-                         float* evidence, float* grad_scale, float* grad_bias, int64_t samples,
-                         int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes,
+                         float* evidence, float* grad_scale, float* grad_bias, const float* offset_dot,
+                         int64_t samples, int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes,
                          void* stream) {
   if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
   if (samples < 0 || rows <= 0 || cols <= 0) return QSTE_E_SHAPE;
@@ -257,9 +266,14 @@ int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x, con
   float* gs_part = reinterpret_cast<float*>(base + l.gs_part);
   int rc;
   if (samples > 0) {
-    if ((rc = launch_colsums(dy, dtype, x_offset, samples, rows, v_part, grad_bias ? db_part : nullptr, v,
-                             grad_bias, s)))
+    // the offset correction's column sums, unless the caller brings them
+    // (with a bias gradient to form, dy is read for both anyway)
+    if (offset_dot && !grad_bias) {
+      v = const_cast<float*>(offset_dot);  // only read from here on
+    } else if ((rc = launch_colsums(dy, dtype, x_offset, samples, rows, v_part, grad_bias ? db_part : nullptr, v,
+                                    grad_bias, s))) {
       return rc;
+    }
     // MFMA path: the plan runs evidence and dgrad in one launch (from
     // transposed copies of the signs and bf16 copies of the scales) or as
     // two, and splits evidence tiles over K where that shortens the work
@@ -311,6 +325,47 @@ int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x, con
   return launch_sum_partials(gs_part, tiles, rows, grad_scale, s);
 }
 
+}  // namespace
+
+int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x, const float* x_offset,
+                         const float* x_scale, const uint8_t* packed_w, const float* scale, void* dx,
+                         float* evidence, float* grad_scale, float* grad_bias, int64_t samples,
+                         int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+  return linear_backward_impl(dy, dtype, packed_x, x_offset, x_scale, packed_w, scale, dx, evidence, grad_scale,
+                              grad_bias, nullptr, samples, rows, cols, workspace, workspace_bytes, stream);
+}
+
+int qste_linear_backward_offset_dot(const void* dy, int dtype, const uint8_t* packed_x, const float* x_offset,
+                                    const float* x_scale, const uint8_t* packed_w, const float* scale, void* dx,
+                                    float* evidence, float* grad_scale, float* grad_bias, const float* offset_dot,
+                                    int64_t samples, int64_t rows, int64_t cols, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  if (!offset_dot) return QSTE_E_NULL;
+  return linear_backward_impl(dy, dtype, packed_x, x_offset, x_scale, packed_w, scale, dx, evidence, grad_scale,
+                              grad_bias, offset_dot, samples, rows, cols, workspace, workspace_bytes, stream);
+}
+
+size_t qste_swiglu_backward_sums_workspace_bytes(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return swiglu_backward_sums_workspace(rows, cols);
+}
+
+int qste_swiglu_backward_sums(const void* grad, const void* gate, const void* up, int dtype, void* grad_gate,
+                              void* grad_up, const float* offset_gate, const float* offset_up, float* sums,
+                              int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
+  if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  if (cols == 0) return 0;
+  if (!sums) return QSTE_E_NULL;
+  hipStream_t s = as_stream(stream);
+  if (rows == 0) return fill_zero(sums, 2 * cols, s);
+  if (!grad || !gate || !up || !grad_gate || !grad_up || !offset_gate || !offset_up) return QSTE_E_NULL;
+  if (!workspace || workspace_bytes < swiglu_backward_sums_workspace(rows, cols)) return QSTE_E_WORKSPACE;
+  return launch_swiglu_backward_sums(grad, gate, up, dtype, grad_gate, grad_up, offset_gate, offset_up, rows, cols,
+                                     sums, static_cast<float*>(workspace), s);
+}
+
 size_t qste_coordinate_update_workspace_bytes(int64_t rows, int64_t cols, int64_t block_size) {
   return coordinate_update_workspace(rows, cols, block_size);
 }
@@ -357,6 +412,22 @@ int qste_swiglu_backward(const void* grad, const void* gate, const void* up, int
   if (count == 0) return 0;
   if (!grad || !gate || !up || !grad_gate || !grad_up) return QSTE_E_NULL;
   return launch_swiglu_backward(grad, gate, up, dtype, grad_gate, grad_up, count, as_stream(stream));
+}
+
+int qste_row_scale(const float* log_scale, float* scale, float* exp_value, int64_t n, float lo, float hi,
+                   void* stream) {
+  if (n < 0) return QSTE_E_SHAPE;
+  if (n == 0) return 0;
+  if (!log_scale || !scale || !exp_value) return QSTE_E_NULL;
+  return launch_row_scale(log_scale, scale, exp_value, n, lo, hi, as_stream(stream));
+}
+
+int qste_row_scale_backward(const float* exp_value, const float* grad, float* grad_log_scale, int64_t n, float lo,
+                            float hi, void* stream) {
+  if (n < 0) return QSTE_E_SHAPE;
+  if (n == 0) return 0;
+  if (!exp_value || !grad || !grad_log_scale) return QSTE_E_NULL;
+  return launch_row_scale_backward(exp_value, grad, grad_log_scale, n, lo, hi, as_stream(stream));
 }
 
 size_t qste_coordinate_update_static_limit(void) { return coordinate_update_static_limit(); }

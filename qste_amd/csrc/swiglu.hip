@@ -169,6 +169,119 @@ __global__ __launch_bounds__(kThreads) void backward_bf16x8_kernel(const uint4* 
   }
 }
 
+// Backward plus the column sums the two binary layers before the gate need.
+// In a SwiGLU MLP the gate and up projections that produced g and u read one
+// input; each layer's backward forms v[c] = sum_t dY[t, c] * offset[t], the
+// offset correction of its evidence (functional.py:139-144), by reading its
+// dY again.  This pass writes dg and du and sums them as it goes, with the
+// chunking and order of colsum_partial_x8_kernel (reduce.hip): chunks of
+// kSumChunk samples, kSumWaves waves per chunk each summing a run of
+// consecutive samples with fmaf in sample order, the waves' sums added in
+// wave order, and the chunk partials [chunk][2][cols] summed in chunk order
+// by sum_partials_kernel.  The sums therefore equal, bit for bit, what the
+// layers' backward computes from dg and du.
+// Lane l of a workgroup owns columns 8 (64 b + l) .. + 7; needs cols % 8 == 0
+// and 16-byte aligned operands.
+constexpr int kSumChunk = 256;
+constexpr int kSumWaves = 4;
+constexpr int kSumThreads = kSumWaves * 64;
+
+template <int DT>
+__device__ __forceinline__ void backward_x8(const uint4& hc, const uint4& gc, const uint4& uc, uint4& og,
+                                            uint4& ou, float (&fg)[8], float (&fu)[8]) {
+  using E = Elem<DT>;
+  const uint16_t* h = reinterpret_cast<const uint16_t*>(&hc);
+  const uint16_t* g = reinterpret_cast<const uint16_t*>(&gc);
+  const uint16_t* u = reinterpret_cast<const uint16_t*>(&uc);
+  uint16_t* rg = reinterpret_cast<uint16_t*>(&og);
+  uint16_t* ru = reinterpret_cast<uint16_t*>(&ou);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float a, b;
+    backward_one<DT>(E::load(h, i), E::load(g, i), E::load(u, i), a, b);
+    E::store(rg, i, a);
+    E::store(ru, i, b);
+    fg[i] = E::load(rg, i);  // the stored (rounded) values are what is summed
+    fu[i] = E::load(ru, i);
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kSumThreads) void backward_sums_kernel(
+    const uint16_t* __restrict__ dh, const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
+    uint16_t* __restrict__ dg, uint16_t* __restrict__ du, const float* __restrict__ off_g,
+    const float* __restrict__ off_u, int64_t samples, int64_t cols, float* __restrict__ part) {
+  constexpr int UNROLL = 4;
+  constexpr int kPad = 17;
+  __shared__ float red[kSumWaves * 64 * kPad];
+  const int lane = threadIdx.x % 64;
+  const int wave = threadIdx.x / 64;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * 512;
+  const int64_t c = base + lane * 8;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kSumChunk;
+  const int64_t c1 = c0 + kSumChunk < samples ? c0 + kSumChunk : samples;
+  constexpr int kPer = kSumChunk / kSumWaves;
+  const int64_t t0 = c0 + wave * kPer < c1 ? c0 + wave * kPer : c1;
+  const int64_t t1 = t0 + kPer < c1 ? t0 + kPer : c1;
+  float vg[8], vu[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) vg[i] = vu[i] = 0.0f;
+  auto one = [&](const uint4& hc, const uint4& gc, const uint4& uc, int64_t t, float og_, float ou_) {
+    uint4 rg, ru;
+    float fg[8], fu[8];
+    backward_x8<DT>(hc, gc, uc, rg, ru, fg, fu);
+    *reinterpret_cast<uint4*>(dg + t * cols + c) = rg;
+    *reinterpret_cast<uint4*>(du + t * cols + c) = ru;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      vg[i] = fmaf(fg[i], og_, vg[i]);
+      vu[i] = fmaf(fu[i], ou_, vu[i]);
+    }
+  };
+  if (c < cols) {
+    int64_t t = t0;
+    for (; t + UNROLL <= t1; t += UNROLL) {
+      uint4 hq[UNROLL], gq[UNROLL], uq[UNROLL];
+      float og[UNROLL], ou[UNROLL];
+#pragma unroll
+      for (int k = 0; k < UNROLL; ++k) {
+        const int64_t at = (t + k) * cols + c;
+        hq[k] = *reinterpret_cast<const uint4*>(dh + at);
+        gq[k] = *reinterpret_cast<const uint4*>(g + at);
+        uq[k] = *reinterpret_cast<const uint4*>(u + at);
+        og[k] = off_g[t + k];
+        ou[k] = off_u[t + k];
+      }
+#pragma unroll
+      for (int k = 0; k < UNROLL; ++k) one(hq[k], gq[k], uq[k], t + k, og[k], ou[k]);
+    }
+    for (; t < t1; ++t) {
+      const int64_t at = t * cols + c;
+      one(*reinterpret_cast<const uint4*>(dh + at), *reinterpret_cast<const uint4*>(g + at),
+          *reinterpret_cast<const uint4*>(u + at), t, off_g[t], off_u[t]);
+    }
+  }
+  float* mine = red + (wave * 64 + lane) * kPad;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    mine[i] = vg[i];
+    mine[8 + i] = vu[i];
+  }
+  __syncthreads();
+  // 1024 results per workgroup (512 columns of the gate sums, then of the up
+  // sums), the waves added in order 0..kSumWaves-1
+  for (int j = threadIdx.x; j < 2 * 512; j += kSumThreads) {
+    const int which = j / 512;
+    const int cc = j % 512;
+    const int64_t col = base + cc;
+    const int slot = (cc / 8) * kPad + which * 8 + cc % 8;
+    float sum = red[slot];
+#pragma unroll
+    for (int w = 1; w < kSumWaves; ++w) sum += red[w * 64 * kPad + slot];
+    if (col < cols) part[(static_cast<int64_t>(blockIdx.y) * 2 + which) * cols + col] = sum;
+  }
+}
+
 inline int grid_of(int64_t work) {
   int64_t b = (work + kThreads - 1) / kThreads;
   if (b > 8192) b = 8192;  // a grid-stride loop covers the rest
@@ -256,6 +369,46 @@ int launch_swiglu_backward(const void* dh, const void* g, const void* u, int dty
       break;
   }
   return static_cast<int>(hipGetLastError());
+}
+
+int launch_colsums(const void*, int, const float*, int64_t, int64_t, float*, float*, float*, float*, hipStream_t);
+int launch_sum_partials(const float*, int64_t, int64_t, float*, hipStream_t);
+
+size_t swiglu_backward_sums_workspace(int64_t rows, int64_t cols) {
+  const int64_t chunks = (rows + swiglu::kSumChunk - 1) / swiglu::kSumChunk;
+  return static_cast<size_t>(chunks * 2 * cols) * sizeof(float);
+}
+
+// sums [2][cols]: sum_t dg[t, c] * off_g[t], then sum_t du[t, c] * off_u[t];
+// part: swiglu_backward_sums_workspace(rows, cols) bytes.
+int launch_swiglu_backward_sums(const void* dh, const void* g, const void* u, int dtype, void* dg, void* du,
+                                const float* off_g, const float* off_u, int64_t rows, int64_t cols, float* sums,
+                                float* part, hipStream_t s) {
+  using namespace swiglu;
+  if (rows * cols == 0) return 0;
+  const int64_t chunks = (rows + kSumChunk - 1) / kSumChunk;
+  const bool x8 = (dtype == QSTE_BF16 || dtype == QSTE_F16) && cols % 8 == 0 && aligned(dh) && aligned(g) &&
+                  aligned(u) && aligned(dg) && aligned(du);
+  if (x8) {
+    const dim3 grid(static_cast<unsigned>((cols + 511) / 512), static_cast<unsigned>(chunks));
+    if (dtype == QSTE_BF16)
+      backward_sums_kernel<QSTE_BF16><<<grid, kSumThreads, 0, s>>>(
+          static_cast<const uint16_t*>(dh), static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u),
+          static_cast<uint16_t*>(dg), static_cast<uint16_t*>(du), off_g, off_u, rows, cols, part);
+    else
+      backward_sums_kernel<QSTE_F16><<<grid, kSumThreads, 0, s>>>(
+          static_cast<const uint16_t*>(dh), static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u),
+          static_cast<uint16_t*>(dg), static_cast<uint16_t*>(du), off_g, off_u, rows, cols, part);
+    const int rc = static_cast<int>(hipGetLastError());
+    if (rc) return rc;
+    return launch_sum_partials(part, chunks, 2 * cols, sums, s);
+  }
+  // any other dtype or layout: the plain pass, then the layers' own column
+  // sums over what it wrote
+  int rc = launch_swiglu_backward(dh, g, u, dtype, dg, du, rows * cols, s);
+  if (rc) return rc;
+  if ((rc = launch_colsums(dg, dtype, off_g, rows, cols, part, nullptr, sums, nullptr, s))) return rc;
+  return launch_colsums(du, dtype, off_u, rows, cols, part, nullptr, sums + cols, nullptr, s);
 }
 
 }  // namespace qste

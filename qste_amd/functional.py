@@ -37,7 +37,7 @@ def encode_activation(flat: Tensor) -> tuple[Tensor, Tensor]:
     """``(bits, aux)`` with ``aux = stack(offset, scale)`` fp32 [2, samples]."""
 
     packed, offset, scale = kernels.pack_affine_rows(flat)
-    return packed, torch.stack((offset, scale))
+    return packed, kernels.stacked_pair(offset, scale)
 
 
 # Layers that read the same input in one forward (a SwiGLU's gate and up
@@ -74,6 +74,36 @@ def remember_encoding(value: Tensor, payload: Tensor, aux: Tensor) -> None:
     _last_encoding = (weakref.ref(value), key, payload, aux)
 
 
+# A binary layer's output carries, as an attribute, the encoding aux of the
+# input it was computed from: a SwiGLU gate that reads two such outputs sums
+# its gradients against those inputs' offsets while it writes them
+# (swiglu_backward_sums), and offers each sum to the layer whose output it
+# was.  An offer names the gradient tensor it belongs to (held, with its
+# version) and the aux it was summed against; a layer takes it only when
+# autograd hands it exactly that gradient, unchanged, and it saved that aux.
+_AUX_ATTR = "_qste_input_aux"
+_offers: dict[int, tuple] = {}
+
+
+def _offer_offset_dot(grad: Tensor, aux: Tensor, offset_dot: Tensor) -> None:
+    _offers[grad.data_ptr()] = (grad, grad._version, aux, offset_dot)
+
+
+def _take_offset_dot(grad2: Tensor, aux: Tensor) -> Tensor | None:
+    offer = _offers.pop(grad2.data_ptr(), None)
+    if offer is None:
+        return None
+    grad, version, offered_aux, offset_dot = offer
+    same = (offered_aux is aux and grad._version == version and grad.numel() == grad2.numel()
+            and grad.dtype == grad2.dtype and grad.is_contiguous() and grad2.is_contiguous()
+            and grad.untyped_storage().data_ptr() == grad2.untyped_storage().data_ptr())
+    return offset_dot if same else None
+
+
+def forget_offers() -> None:
+    _offers.clear()
+
+
 class QSTELinearFn(Function):
     @staticmethod
     def forward(ctx, inputs, packed, scale, bias, surface: Surface):
@@ -87,18 +117,22 @@ class QSTELinearFn(Function):
         ctx.input_shape = inputs.shape
         ctx.input_dtype = inputs.dtype
         ctx.bias_dtype = None if bias is None else bias.dtype
-        return output.to(inputs.dtype)
+        output = output.to(inputs.dtype)
+        setattr(output, _AUX_ATTR, aux)
+        return output
 
     @staticmethod
     def backward(ctx, grad_output):
         forget_encodings()
         payload, aux, packed, scale = ctx.saved_tensors
         grad2 = grad_output.reshape(-1, grad_output.shape[-1])
+        offset_dot = _take_offset_dot(grad2, aux)
         # the input-gradient product only when autograd wants that gradient
         # (the reference always forms it, functional.py:180-183)
         grad_inputs, evidence, grad_scale, grad_bias = kernels.linear_backward(
             grad2, payload, aux[0], aux[1], packed, scale.detach(), ctx.columns,
-            need_bias=ctx.bias_dtype is not None, need_input=ctx.needs_input_grad[0])
+            need_bias=ctx.bias_dtype is not None, need_input=ctx.needs_input_grad[0],
+            offset_dot=offset_dot)
         ctx.surface.consume_evidence(evidence)
         if grad_inputs is not None:
             grad_inputs = grad_inputs.reshape(ctx.input_shape).to(ctx.input_dtype)
@@ -149,17 +183,37 @@ class SwiGLUFn(Function):
 
     @staticmethod
     def forward(ctx, gate, up, encode: bool):
+        forget_offers()
         out, encoding = kernels.swiglu_forward(gate, up, encode=encode)
         ctx.save_for_backward(gate, up)
         if encoding is not None:
             packed, offset, scale = encoding
-            remember_encoding(out, packed, torch.stack((offset, scale)))
+            remember_encoding(out, packed, kernels.stacked_pair(offset, scale))
+        # the encodings of the inputs of the binary layers that produced gate
+        # and up (one [2, tokens] aux each), when both did
+        ctx.auxes = None
+        aux_g, aux_u = getattr(gate, _AUX_ATTR, None), getattr(up, _AUX_ATTR, None)
+        tokens = gate.numel() // gate.shape[-1] if gate.dim() and gate.shape[-1] else 0
+        if (aux_g is not None and aux_u is not None and tokens and aux_g.shape == (2, tokens)
+                and aux_u.shape == (2, tokens)):
+            ctx.auxes = (aux_g, aux_u)
         return out
 
     @staticmethod
     def backward(ctx, grad_output):
+        forget_offers()
         gate, up = ctx.saved_tensors
-        grad_gate, grad_up = kernels.swiglu_backward(grad_output.contiguous(), gate, up)
+        if ctx.auxes is None:
+            grad_gate, grad_up = kernels.swiglu_backward(grad_output.contiguous(), gate, up)
+            return grad_gate, grad_up, None
+        # the gradients and, for the two layers' backward, their offset sums
+        aux_g, aux_u = ctx.auxes
+        cols = gate.shape[-1]
+        grad_gate, grad_up, sums = kernels.swiglu_backward_sums(
+            grad_output.reshape(-1, cols), gate.reshape(-1, cols), up.reshape(-1, cols), aux_g[0], aux_u[0])
+        grad_gate, grad_up = grad_gate.view(gate.shape), grad_up.view(up.shape)
+        _offer_offset_dot(grad_gate, aux_g, sums[0])
+        _offer_offset_dot(grad_up, aux_u, sums[1])
         return grad_gate, grad_up, None
 
 

@@ -200,7 +200,8 @@ def unpack_rows(packed: Tensor, columns: int, *, dtype: torch.dtype | None = Non
 def pack_affine_rows(values: Tensor) -> tuple[Tensor, Tensor, Tensor]:
     """(bits, offset, scale) of each row: x ~ offset + scale * sign(x - offset).
 
-    fallback.py:77-88. Arithmetic in fp32 on the dtype's values.
+    fallback.py:77-88. Arithmetic in fp32 on the dtype's values.  offset and
+    scale are rows 0 and 1 of one fp32 [2, rows] tensor (``stacked_pair``).
     """
 
     device = _require_gpu(values)
@@ -211,13 +212,27 @@ def pack_affine_rows(values: Tensor) -> tuple[Tensor, Tensor, Tensor]:
     if cols == 0:
         raise ValueError("pack_affine_rows needs at least one column")
     packed = torch.empty(rows, _packed_width(cols), dtype=torch.uint8, device=device)
-    offset = torch.empty(rows, dtype=torch.float32, device=device)
-    scale = torch.empty(rows, dtype=torch.float32, device=device)
+    # rows 0 and 1 of one [2, rows] tensor: the layout a saved encoding keeps
+    offset, scale = torch.empty(2, rows, dtype=torch.float32, device=device).unbind(0)
     code = _lib.load().qste_pack_affine_rows(
         _ptr(values), _dtype_code(values), _ptr(packed), _ptr(offset), _ptr(scale), rows, cols,
         _stream(device))
     _lib.check(code, "pack_affine_rows")
     return packed, offset, scale
+
+
+def stacked_pair(offset: Tensor, scale: Tensor) -> Tensor:
+    """``torch.stack((offset, scale))``, without a copy when the two are rows
+    0 and 1 of one [2, n] tensor (as ``pack_affine_rows`` returns them)."""
+
+    base = offset._base
+    n = offset.numel()
+    if (base is not None and scale._base is base and base.dim() == 2 and base.shape[0] == 2
+            and base.shape[1] == n and base.is_contiguous() and offset.dtype == scale.dtype == base.dtype
+            and offset.data_ptr() == base.data_ptr()
+            and scale.data_ptr() == base.data_ptr() + n * base.element_size()):
+        return base
+    return torch.stack((offset, scale))
 
 
 def packed_linear_affine(inputs: Tensor, packed: Tensor, scale: Tensor, bias: Tensor | None,
@@ -308,7 +323,7 @@ def packed_row_inner(matrix: Tensor, packed: Tensor, columns: int) -> Tensor:
 
 def linear_backward(grad: Tensor, packed_x: Tensor, x_offset: Tensor, x_scale: Tensor,
                     packed_w: Tensor, scale: Tensor, columns: int, *, need_bias: bool,
-                    need_input: bool = True):
+                    need_input: bool = True, offset_dot: Tensor | None = None):
     """All of ``QSTELinearFn.backward``'s products in one call (functional.py:173-194).
 
     Returns ``(grad_input [samples, columns] in grad's dtype or None,
@@ -316,6 +331,9 @@ def linear_backward(grad: Tensor, packed_x: Tensor, x_offset: Tensor, x_scale: T
     grad_scale fp32 [rows], grad_bias fp32 [rows] or None)``.  With
     ``need_input=False`` the input-gradient product is not computed (autograd
     asks for no gradient of the layer's input) and grad_input is None.
+    ``offset_dot`` (fp32 [rows], ``sum_t grad[t, r] * x_offset[t]`` summed as
+    this call sums it, e.g. by ``swiglu_backward_sums``) spares the call that
+    pass over ``grad``; it is ignored when a bias gradient is formed.
     """
 
     device = _require_gpu(grad, packed_x, x_offset, x_scale, packed_w, scale)
@@ -333,10 +351,20 @@ def linear_backward(grad: Tensor, packed_x: Tensor, x_offset: Tensor, x_scale: T
     x_offset_f32 = _f32(x_offset)  # held until the launch is queued
     x_scale_f32 = _f32(x_scale)  # held until the launch is queued
     scale_f32 = _f32(scale)  # held until the launch is queued
-    code = lib.qste_linear_backward(
-        _ptr(grad), _dtype_code(grad), _ptr(packed_x), _ptr(x_offset_f32), _ptr(x_scale_f32),
-        _ptr(packed_w), _ptr(scale_f32), _ptr(dx), _ptr(evidence), _ptr(grad_scale),
-        _ptr(grad_bias), samples, rows, int(columns), _ptr(work), work.numel(), _stream(device))
+    if offset_dot is not None:
+        if offset_dot.dtype != torch.float32 or offset_dot.numel() != rows or offset_dot.device != device:
+            raise ValueError("offset_dot must be fp32 [rows] on the layer's device")
+        offset_dot = offset_dot.contiguous()
+        code = lib.qste_linear_backward_offset_dot(
+            _ptr(grad), _dtype_code(grad), _ptr(packed_x), _ptr(x_offset_f32), _ptr(x_scale_f32),
+            _ptr(packed_w), _ptr(scale_f32), _ptr(dx), _ptr(evidence), _ptr(grad_scale),
+            _ptr(grad_bias), _ptr(offset_dot), samples, rows, int(columns), _ptr(work), work.numel(),
+            _stream(device))
+    else:
+        code = lib.qste_linear_backward(
+            _ptr(grad), _dtype_code(grad), _ptr(packed_x), _ptr(x_offset_f32), _ptr(x_scale_f32),
+            _ptr(packed_w), _ptr(scale_f32), _ptr(dx), _ptr(evidence), _ptr(grad_scale),
+            _ptr(grad_bias), samples, rows, int(columns), _ptr(work), work.numel(), _stream(device))
     _lib.check(code, "linear_backward")
     return dx, evidence, grad_scale, grad_bias
 
@@ -599,8 +627,7 @@ def swiglu_forward(gate: Tensor, up: Tensor, *, encode: bool = False):
     packed = offset = scale = None
     if encode:
         packed = torch.empty(rows, _packed_width(cols), dtype=torch.uint8, device=device)
-        offset = torch.empty(rows, dtype=torch.float32, device=device)
-        scale = torch.empty(rows, dtype=torch.float32, device=device)
+        offset, scale = torch.empty(2, rows, dtype=torch.float32, device=device).unbind(0)
     code = _lib.load().qste_swiglu_forward(
         _ptr(g), _ptr(u), _dtype_code(g), _ptr(out), _ptr(packed), _ptr(offset), _ptr(scale), rows, cols,
         _stream(device))
@@ -620,6 +647,65 @@ def swiglu_backward(grad: Tensor, gate: Tensor, up: Tensor) -> tuple[Tensor, Ten
         _ptr(dh), _ptr(g), _ptr(u), _dtype_code(g), _ptr(dg), _ptr(du), g.numel(), _stream(device))
     _lib.check(code, "swiglu_backward")
     return dg, du
+
+
+def swiglu_backward_sums(grad: Tensor, gate: Tensor, up: Tensor, offset_gate: Tensor,
+                         offset_up: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """``swiglu_backward`` of [rows, cols] operands plus ``sums`` fp32 [2, cols]:
+    ``sum_t grad_gate[t] * offset_gate[t]`` and ``sum_t grad_up[t] * offset_up[t]``,
+    each what ``linear_backward`` would sum from that gradient and offset
+    (its ``offset_dot``)."""
+
+    device = _require_gpu(grad, gate, up, offset_gate, offset_up)
+    if not (grad.shape == gate.shape == up.shape) or not (grad.dtype == gate.dtype == up.dtype):
+        raise ValueError("grad, gate and up must have the same shape and dtype")
+    if grad.dim() != 2:
+        raise ValueError("swiglu_backward_sums expects rank-2 operands")
+    rows, cols = grad.shape
+    offs = []
+    for name, o in (("offset_gate", offset_gate), ("offset_up", offset_up)):
+        if o.dtype != torch.float32 or o.numel() != rows:
+            raise ValueError(f"{name} must be fp32 [rows]")
+        offs.append(o.contiguous())
+    dh, g, u = _aligned(grad), _aligned(gate), _aligned(up)
+    dg, du = torch.empty_like(g), torch.empty_like(g)
+    sums = torch.empty(2, cols, dtype=torch.float32, device=device)
+    lib = _lib.load()
+    work = _workspace(lib.qste_swiglu_backward_sums_workspace_bytes(rows, cols), device)
+    code = lib.qste_swiglu_backward_sums(
+        _ptr(dh), _ptr(g), _ptr(u), _dtype_code(g), _ptr(dg), _ptr(du), _ptr(offs[0]), _ptr(offs[1]),
+        _ptr(sums), rows, cols, _ptr(work), work.numel(), _stream(device))
+    _lib.check(code, "swiglu_backward_sums")
+    return dg, du, sums
+
+
+def row_scale(log_scale: Tensor, lo: float, hi: float) -> tuple[Tensor, Tensor]:
+    """``(clamp(exp(log_scale), lo, hi), exp(log_scale))`` fp32, one launch
+    (surface.py:84-85), rounded as torch's ``exp().clamp()``."""
+
+    device = _require_gpu(log_scale)
+    if log_scale.dtype != torch.float32:
+        raise ValueError("row_scale takes fp32 log-scales")
+    ls = log_scale.detach().contiguous()
+    scale, e = torch.empty_like(ls), torch.empty_like(ls)
+    code = _lib.load().qste_row_scale(_ptr(ls), _ptr(scale), _ptr(e), ls.numel(), float(lo), float(hi),
+                                      _stream(device))
+    _lib.check(code, "row_scale")
+    return scale, e
+
+
+def row_scale_backward(exp_value: Tensor, grad: Tensor, lo: float, hi: float) -> Tensor:
+    """Gradient of ``row_scale`` at log_scale: ``(lo <= e <= hi ? grad : 0) * e``."""
+
+    device = _require_gpu(exp_value, grad)
+    if exp_value.dtype != torch.float32 or grad.dtype != torch.float32 or grad.shape != exp_value.shape:
+        raise ValueError("row_scale_backward takes fp32 operands of one shape")
+    e, g = exp_value.contiguous(), grad.contiguous()
+    out = torch.empty_like(e)
+    code = _lib.load().qste_row_scale_backward(_ptr(e), _ptr(g), _ptr(out), e.numel(), float(lo), float(hi),
+                                               _stream(device))
+    _lib.check(code, "row_scale_backward")
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -30,6 +30,7 @@ from typing import Callable, Optional
 import torch
 import torch.nn as nn
 from torch import Tensor
+from torch.autograd import Function
 
 from . import kernels
 from .config import QSTEConfig, coerce_config
@@ -55,6 +56,33 @@ def _on_gpu(fn, tensor: Tensor, *args, **kwargs) -> Tensor:
             f"(called with a tensor on {tensor.device})"
         )
     return fn(tensor.to("cuda"), *args, **kwargs).to(tensor.device)
+
+
+class RowScaleFn(Function):
+    """``clamp(exp(log_scale), lo, hi)`` with torch's values and gradient, one
+    HIP launch each way (surface.py:84-85) instead of torch's two forward and
+    six backward kernels.  Saves exp's result, as torch's exp does."""
+
+    @staticmethod
+    def forward(ctx, log_scale, lo: float, hi: float):
+        scale, e = kernels.row_scale(log_scale, lo, hi)
+        ctx.save_for_backward(e)
+        ctx.bounds = (lo, hi)
+        return scale
+
+    @staticmethod
+    def backward(ctx, grad):
+        (e,) = ctx.saved_tensors
+        return kernels.row_scale_backward(e, grad.float(), *ctx.bounds), None, None
+
+
+def row_scale(log_scale: Tensor, lo: float, hi: float) -> Tensor:
+    """The learned row scale of surface.py:84-85; fp32 GPU log-scales take the
+    fused kernels, anything else torch's operators."""
+
+    if log_scale.device.type == "cuda" and log_scale.dtype == torch.float32:
+        return RowScaleFn.apply(log_scale, float(lo), float(hi))
+    return log_scale.exp().clamp(lo, hi)
 
 
 # Bytes of fp32 temporaries the initial quantization may hold at once; a
@@ -182,8 +210,8 @@ class Surface(nn.Module):
         if weight.ndim != 2:
             raise ValueError("a QSTE surface must wrap a rank-2 weight")
         cfg = coerce_config(cfg)
-        row_scale, coordinate = quantize_weight(weight.detach(), cfg)
-        self._install(cfg, coordinate, row_scale.log())
+        initial_scale, coordinate = quantize_weight(weight.detach(), cfg)
+        self._install(cfg, coordinate, initial_scale.log())
 
     @classmethod
     def from_state(cls, coordinate: Tensor, log_scale: Tensor,
@@ -218,7 +246,7 @@ class Surface(nn.Module):
 
     @property
     def scale(self) -> Tensor:
-        return self.log_scale.exp().clamp(self.cfg.scale_min, self.cfg.scale_max)
+        return row_scale(self.log_scale, self.cfg.scale_min, self.cfg.scale_max)
 
     @property
     def sign(self) -> Tensor:

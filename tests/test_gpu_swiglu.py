@@ -118,10 +118,16 @@ def test_swiglu_mlp_matches_the_torch_gate():
 
     import bench
     import qste_amd as qste
-    from qste_amd import functional
+    from qste_amd import functional, kernels
 
     T, d, ffn = 512, 1024, 3584
     dev = torch.device(DEV)
+    real_backward = kernels.linear_backward
+    handed = []
+
+    def spy(*args, **kw):
+        handed.append(kw.get("offset_dot") is not None)
+        return real_backward(*args, **kw)
 
     def run(fused):
         mlp = bench.SwiGLU(d, ffn, dev)
@@ -141,7 +147,16 @@ def test_swiglu_mlp_matches_the_torch_gate():
         return (y.detach(), x.grad, [s.coordinate.clone() for s in qste.surfaces(mlp.modules)],
                 [s.packed_sign.clone() for s in qste.surfaces(mlp.modules)], flips)
 
-    a, b = run(False), run(True)
+    kernels.linear_backward = spy
+    try:
+        a = run(False)
+        assert handed == [False, False, False]
+        handed.clear()
+        b = run(True)
+        # down summed its own dy; gate and up took the gate kernel's sums
+        assert sorted(handed) == [False, True, True]
+    finally:
+        kernels.linear_backward = real_backward
     assert torch.equal(a[0], b[0])
     assert torch.equal(a[1], b[1])
     for ca, cb in zip(a[2], b[2]):
@@ -149,3 +164,78 @@ def test_swiglu_mlp_matches_the_torch_gate():
     for pa, pb in zip(a[3], b[3]):
         assert torch.equal(pa, pb)
     assert a[4] == b[4] and a[4] > 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("rows,cols", [(512, 3584), (300, 1000), (77, 14336), (1, 8), (257, 520), (9, 1001)])
+def test_backward_sums_equal_the_layer_backward_sums(rows, cols, dtype):
+    """swiglu_backward_sums: the same gradients as swiglu_backward, and sums
+    that make linear_backward's outputs bit-identical to what it computes
+    from those gradients itself (its own column sums), on both layers."""
+
+    from qste_amd import kernels
+
+    print(f"swiglu sums {rows}x{cols} {dtype}", flush=True)
+    gate, up, grad = _inputs((rows, cols), dtype, rows + cols)
+    g = torch.Generator(device=DEV).manual_seed(rows * 7 + cols)
+    off_g = torch.randn(rows, generator=g, device=DEV)
+    off_u = off_g if rows % 2 else torch.randn(rows, generator=g, device=DEV)
+    dg0, du0 = kernels.swiglu_backward(grad, gate, up)
+    dg, du, sums = kernels.swiglu_backward_sums(grad, gate, up, off_g, off_u)
+    assert torch.equal(_bits(dg), _bits(dg0)) and torch.equal(_bits(du), _bits(du0))
+    # within fp32 summation error of the float64 sums
+    for got, dy, off in ((sums[0], dg, off_g), (sums[1], du, off_u)):
+        want = dy.double().t() @ off.double()
+        # a sequential fp32 sum of n terms errs by at most about n ulps of the
+        # sum of magnitudes
+        bound = (rows + 8) * 2.0**-24 * (dy.double().abs().t() @ off.double().abs()) + 1e-30
+        assert bool(((got.double() - want).abs() <= bound).all())
+    # a layer that reads dg (rows of the batch, cols = the layer's rows)
+    columns = 256
+    x = torch.randn(rows, columns, generator=g, device=DEV).to(dtype)
+    packed_x, x_off, x_scale = kernels.pack_affine_rows(x)
+    coord = torch.randint(-127, 128, (cols, columns), generator=g, device=DEV, dtype=torch.int32).to(torch.int8)
+    packed_w = kernels.pack_coordinate(coord)
+    scale = torch.rand(cols, generator=g, device=DEV) * 0.02
+    dg2, _, sums2 = kernels.swiglu_backward_sums(grad, gate, up, x_off, x_off)
+    ref = kernels.linear_backward(dg2, packed_x, x_off, x_scale, packed_w, scale, columns, need_bias=False)
+    got = kernels.linear_backward(dg2, packed_x, x_off, x_scale, packed_w, scale, columns, need_bias=False,
+                                  offset_dot=sums2[0])
+    torch.cuda.synchronize()
+    assert ref[3] is None and got[3] is None
+    for a, b in zip(ref[:3], got[:3]):
+        assert torch.equal(a.view(torch.int16) if a.element_size() == 2 else a.view(torch.int32),
+                           b.view(torch.int16) if b.element_size() == 2 else b.view(torch.int32))
+
+
+def test_row_scale_equals_torch():
+    """clamp(exp(log_scale)) and its gradient, bit for bit against torch's
+    operators, over finite values across the whole exp range, the clamp
+    bounds themselves, infinities and NaN."""
+
+    import math
+
+    from qste_amd.surface import row_scale
+
+    lo, hi = 1e-6, 4.0
+    g = torch.Generator(device=DEV).manual_seed(3)
+    wide = torch.empty(1 << 20, device=DEV).uniform_(-110.0, 100.0, generator=g)
+    near = torch.randn(1 << 16, device=DEV, generator=g) * 3 - 4
+    special = torch.tensor([0.0, -0.0, math.log(lo), math.log(hi), float(torch.tensor(lo).log()),
+                            float(torch.tensor(hi).log()), float("inf"), float("-inf"), float("nan"),
+                            88.7, 88.8, -103.0, -87.3], device=DEV)
+    ls = torch.cat((wide, near, special))
+    grad = torch.randn(ls.numel(), device=DEV, generator=g)
+    grad[-5:] = float("inf")
+    a = ls.clone().requires_grad_(True)
+    ref = a.exp().clamp(lo, hi)
+    ref.backward(grad)
+    b = ls.clone().requires_grad_(True)
+    got = row_scale(b, lo, hi)
+    got.backward(grad)
+    torch.cuda.synchronize()
+    # NaN payloads are not compared: NaN positions, then the rest bitwise
+    for x, y in ((got.detach(), ref.detach()), (b.grad, a.grad)):
+        assert torch.equal(torch.isnan(x), torch.isnan(y))
+        keep = ~torch.isnan(y)
+        assert torch.equal(x[keep].view(torch.int32), y[keep].view(torch.int32))

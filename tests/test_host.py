@@ -135,10 +135,16 @@ class OracleKernels:
         return torch.from_numpy(oracle.row_inner(matrix.float().numpy(), packed.numpy(), columns)).float()
 
     def linear_backward(self, grad, packed_x, x_offset, x_scale, packed_w, scale, columns, *, need_bias,
-                        need_input=True):
+                        need_input=True, offset_dot=None):
         g = grad.float().numpy()
         s = scale.detach().float().numpy()
         self.backward_calls.append(need_input)
+        self.offset_dots = getattr(self, "offset_dots", []) + [offset_dot is not None]
+        if offset_dot is not None:
+            # what was offered must be this gradient summed against this
+            # layer's own saved offsets
+            want = g.astype(np.float64).T @ x_offset.numpy().astype(np.float64)
+            assert np.allclose(offset_dot.numpy(), want, rtol=1e-5, atol=1e-6)
         dx = oracle.linear_dgrad(g, packed_w.numpy(), columns, s)
         e0 = oracle.decoded_evidence(g, packed_x.numpy(), x_offset.numpy(), x_scale.numpy(), columns)
         gs = oracle.row_inner(e0.astype(np.float32), packed_w.numpy(), columns)
@@ -222,6 +228,12 @@ class OracleKernels:
             (F.silu(g) * u).backward(grad)
         return g.grad, u.grad
 
+    def swiglu_backward_sums(self, grad, gate, up, offset_gate, offset_up):
+        dg, du = self.swiglu_backward(grad, gate, up)
+        sums = torch.stack((dg.double().t() @ offset_gate.double(), du.double().t() @ offset_up.double()))
+        self.swiglu_sums = getattr(self, "swiglu_sums", 0) + 1
+        return dg, du, sums.float()
+
     # binary embedding (oracle/embedding.py)
     def packed_embedding(self, ids, packed, scale, columns):
         out = oe.lookup(ids.numpy(), packed.numpy(), scale.detach().float().numpy(), columns)
@@ -234,7 +246,7 @@ class OracleKernels:
 
 ACTIVATION_OPS = ("pack_bits", "unpack_bits", "masked_backward", "masked_activation",
                   "smooth_activation", "smooth_backward", "packed_embedding", "embedding_backward",
-                  "swiglu_forward", "swiglu_backward")
+                  "swiglu_forward", "swiglu_backward", "swiglu_backward_sums")
 
 
 @pytest.fixture
@@ -724,9 +736,15 @@ def test_swiglu_hands_its_encoding_to_the_down_layer(fake, monkeypatch):
         return y.detach(), xr.grad, list(calls)
 
     y0, g0, c0 = run(False)
+    assert fake.offset_dots == [False, False, False]
+    fake.offset_dots = []
     y1, g1, c1 = run(True)
     assert c0 == [(10, 16), (10, 48)]      # x once (shared), then h
     assert c1 == [(10, 16)]                 # h's encoding came from the gate kernel
     assert fake.swiglu_encodes == 1
+    # the gate's backward summed dg and du for the gate and up layers, which
+    # took those sums (checked against their own offsets); down summed its own
+    assert fake.swiglu_sums == 1
+    assert sorted(fake.offset_dots) == [False, True, True]
     assert torch.allclose(y0, y1, rtol=1e-6, atol=1e-6)
     assert torch.allclose(g0, g1, rtol=1e-5, atol=1e-6)
