@@ -566,8 +566,9 @@ def decode_gemv(device, K=8192, N=28672, copies=10):
     scales = [torch.randn(N, generator=g, device=device).abs_().mul_(0.02) for _ in range(copies)]
     res = {}
     reps = 5
-    for M in (1, 4, 16):
-        x = torch.randn(M, K, generator=g, device=device).to(torch.bfloat16)
+    for name, M, dtype in (("M1", 1, torch.bfloat16), ("M4", 4, torch.bfloat16), ("M16", 16, torch.bfloat16),
+                           ("fp16_M1", 1, torch.float16), ("fp16_M16", 16, torch.float16)):
+        x = torch.randn(M, K, generator=g, device=device).to(dtype)
 
         def sweep():
             for i in range(copies):
@@ -584,7 +585,7 @@ def decode_gemv(device, K=8192, N=28672, copies=10):
                 sweep()
         ms = timed_events(graph.replay, 4) / (reps * copies)
         nbytes = N * pb + 4 * N + 2 * M * K + 2 * M * N
-        res[f"M{M}"] = {"us": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
+        res[name] = {"us": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
                         "gbps": round(nbytes / ms / 1e6, 1),
                         "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / HBM_PEAK, 4),
                         "timing": f"graph replay of {reps * copies} launches over {copies} weight copies"}

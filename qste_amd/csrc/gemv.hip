@@ -46,6 +46,7 @@ namespace qste {
 namespace gemv {
 
 typedef short bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -75,8 +76,45 @@ __device__ __forceinline__ uint32_t vreg() {
   return v;
 }
 
-// bf16 pairs of the bases v0 = 4, 2, 1, 0.5 (bit 4, 5, 6, 7 clear)
-constexpr uint32_t kBase[4] = {0x40804080u, 0x40004000u, 0x3F803F80u, 0x3F003F00u};
+// Per activation dtype: the 16-bit pairs of the bases v0 = 4, 2, 1, 0.5,
+// the position of slot a' = 0's bit in each half-word (bf16: bits 4..7,
+// fp16: bits 7..10 -- the top three mantissa bits and the exponent LSB in
+// both, which add exactly 0.5 to bases 4, 2, 1, 0.5, whose bit there is
+// clear), the pair of ones, and the MFMA.
+template <int DT>
+struct Dec;
+
+template <>
+struct Dec<QSTE_BF16> {
+  static constexpr uint32_t base[4] = {0x40804080u, 0x40004000u, 0x3F803F80u, 0x3F003F00u};
+  static constexpr int pos = 4;
+  static constexpr uint32_t ones = 0x3F803F80u;
+  static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t store(float v) { return f32_to_bf16(v); }
+};
+
+template <>
+struct Dec<QSTE_F16> {
+  static constexpr uint32_t base[4] = {0x44004400u, 0x40004000u, 0x3C003C00u, 0x38003800u};
+  static constexpr int pos = 7;
+  static constexpr uint32_t ones = 0x3C003C00u;
+  static __device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  }
+  static __device__ __forceinline__ uint16_t store(float v) { return f32_to_f16(v); }
+};
+
+// Copy u (0..3) of a weight dword: the column 4u + a' (low half) and
+// 16 + 4u + a' (high half) bits moved to position pos + a' of each half.
+template <int POS>
+__device__ __forceinline__ uint32_t weight_copy(uint32_t w, int u) {
+  const int shift = POS - 4 * u;  // compile-time after unrolling
+  return shift >= 0 ? w << shift : w >> -shift;
+}
 
 // Workgroup barrier that waits only for this wave's LDS operations.
 // (__syncthreads() also waits for every outstanding global load, which here
@@ -88,10 +126,6 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-__device__ __forceinline__ f32x4 mma(u32x4 a, u32x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
-                                                 c, 0, 0, 0);
-}
 
 typedef __attribute__((address_space(3))) void lds_t;
 constexpr int XP = 1024 + 16;  // LDS bytes per staged x row: conflict-free 16-byte reads across 16 rows
@@ -105,7 +139,7 @@ struct Smem {
 
 // NBW weight blocks of 16 rows per workgroup; x rows staged MP (>= M, a
 // power of two) at a time.
-template <int NBW, int MP>
+template <int DT, int NBW, int MP>
 __global__ __launch_bounds__(THREADS, 1) void decode_kernel(const uint16_t* __restrict__ x,
                                                             const uint8_t* __restrict__ bits,
                                                             const float* __restrict__ scale,
@@ -128,12 +162,13 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(const uint16_t* __re
 #pragma unroll
   for (int b = 0; b < NBW; ++b) boff[b] = static_cast<uint32_t>((n0 + 16 * b + l16) * pb + 16 * q);
 
+  using T = Dec<DT>;
   uint32_t base[4];
-  base[0] = vreg<kBase[0]>(); base[1] = vreg<kBase[1]>();
-  base[2] = vreg<kBase[2]>(); base[3] = vreg<kBase[3]>();
+  base[0] = vreg<T::base[0]>(); base[1] = vreg<T::base[1]>();
+  base[2] = vreg<T::base[2]>(); base[3] = vreg<T::base[3]>();
   // B of the C/S product (the same for every MFMA): column 0 the bases,
   // column 1 ones, the rest zero
-  const uint32_t cs_one = l16 == 1 ? 0x3F803F80u : 0u;
+  const uint32_t cs_one = l16 == 1 ? T::ones : 0u;
   u32x4 cf;
   cf.x = l16 == 0 ? base[0] : cs_one;
   cf.y = l16 == 0 ? base[1] : cs_one;
@@ -206,13 +241,14 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(const uint16_t* __re
       const uint32_t w = Bd[j];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const uint32_t wu = u == 0 ? w << 4 : w >> (4 * (u - 1));
+        const uint32_t wu = weight_copy<T::pos>(w, u);
+        constexpr uint32_t m0 = 0x00010001u << T::pos;
         u32x4 bf;
-        bf.x = (wu & 0x00100010u) | base[0];
-        bf.y = (wu & 0x00200020u) | base[1];
-        bf.z = (wu & 0x00400040u) | base[2];
-        bf.w = (wu & 0x00800080u) | base[3];
-        acc[b] = mma(af[4 * j + u], bf, acc[b]);
+        bf.x = (wu & m0) | base[0];
+        bf.y = (wu & (m0 << 1)) | base[1];
+        bf.z = (wu & (m0 << 2)) | base[2];
+        bf.w = (wu & (m0 << 3)) | base[3];
+        acc[b] = T::mma(af[4 * j + u], bf, acc[b]);
       }
     }
   };
@@ -253,7 +289,7 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(const uint16_t* __re
       block(af, Bs[i], i < NBW ? i : i - NBW);
       if (i == NBW - 1 || i == STEPS - 1) {
 #pragma unroll
-        for (int f = 0; f < 16; ++f) acc_cs = mma(af[f], cf, acc_cs);
+        for (int f = 0; f < 16; ++f) acc_cs = T::mma(af[f], cf, acc_cs);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -295,30 +331,45 @@ __global__ __launch_bounds__(THREADS, 1) void decode_kernel(const uint16_t* __re
           float r = 4.0f * v[j] - dsum[m];
           r = r * sc;
           r = r + bi;
-          y[static_cast<int64_t>(m) * N + n] = f32_to_bf16(r);
+          y[static_cast<int64_t>(m) * N + n] = T::store(r);
         }
       }
     }
   }
 }
 
-template <int NBW, int MP>
+template <int DT, int NBW, int MP>
 void launch(const void* x, const uint8_t* packed, const float* scale, const float* bias, void* y, int64_t m,
             int64_t rows, int64_t cols, hipStream_t stream) {
   const int grid = static_cast<int>((rows + 16 * NBW - 1) / (16 * NBW));
-  decode_kernel<NBW, MP><<<grid, THREADS, 0, stream>>>(static_cast<const uint16_t*>(x), packed, scale, bias,
+  decode_kernel<DT, NBW, MP><<<grid, THREADS, 0, stream>>>(static_cast<const uint16_t*>(x), packed, scale, bias,
                                                         static_cast<uint16_t*>(y), static_cast<int>(m), rows,
                                                         cols);
 }
 
-template <int NBW>
+template <int DT, int NBW>
 void launch_m(const void* x, const uint8_t* packed, const float* scale, const float* bias, void* y, int64_t m,
               int64_t rows, int64_t cols, hipStream_t stream) {
-  if (m <= 1) launch<NBW, 1>(x, packed, scale, bias, y, m, rows, cols, stream);
-  else if (m <= 2) launch<NBW, 2>(x, packed, scale, bias, y, m, rows, cols, stream);
-  else if (m <= 4) launch<NBW, 4>(x, packed, scale, bias, y, m, rows, cols, stream);
-  else if (m <= 8) launch<NBW, 8>(x, packed, scale, bias, y, m, rows, cols, stream);
-  else launch<NBW, 16>(x, packed, scale, bias, y, m, rows, cols, stream);
+  if (m <= 1) launch<DT, NBW, 1>(x, packed, scale, bias, y, m, rows, cols, stream);
+  else if (m <= 2) launch<DT, NBW, 2>(x, packed, scale, bias, y, m, rows, cols, stream);
+  else if (m <= 4) launch<DT, NBW, 4>(x, packed, scale, bias, y, m, rows, cols, stream);
+  else if (m <= 8) launch<DT, NBW, 8>(x, packed, scale, bias, y, m, rows, cols, stream);
+  else launch<DT, NBW, 16>(x, packed, scale, bias, y, m, rows, cols, stream);
+}
+
+template <int DT>
+void launch_dt(int64_t nbw, const void* x, const uint8_t* packed, const float* scale, const float* bias, void* y,
+               int64_t m, int64_t rows, int64_t cols, hipStream_t stream) {
+  switch (nbw) {
+    case 1: launch_m<DT, 1>(x, packed, scale, bias, y, m, rows, cols, stream); break;
+    case 2: launch_m<DT, 2>(x, packed, scale, bias, y, m, rows, cols, stream); break;
+    case 3: launch_m<DT, 3>(x, packed, scale, bias, y, m, rows, cols, stream); break;
+    case 4: launch_m<DT, 4>(x, packed, scale, bias, y, m, rows, cols, stream); break;
+    case 5: launch_m<DT, 5>(x, packed, scale, bias, y, m, rows, cols, stream); break;
+    case 6: launch_m<DT, 6>(x, packed, scale, bias, y, m, rows, cols, stream); break;
+    case 7: launch_m<DT, 7>(x, packed, scale, bias, y, m, rows, cols, stream); break;
+    default: launch_m<DT, 8>(x, packed, scale, bias, y, m, rows, cols, stream); break;
+  }
 }
 
 }  // namespace gemv
@@ -327,7 +378,7 @@ void launch_m(const void* x, const uint8_t* packed, const float* scale, const fl
 int gemv_linear_forward(const void* x, int dtype, const uint8_t* packed, const float* scale,
                         const float* bias, void* y, int64_t m, int64_t rows, int64_t cols,
                         hipStream_t stream) {
-  if (dtype != QSTE_BF16 || m < 1 || m > 16 || rows < 1 || cols < 128 || cols % 128 != 0 ||
+  if ((dtype != QSTE_BF16 && dtype != QSTE_F16) || m < 1 || m > 16 || rows < 1 || cols < 128 || cols % 128 != 0 ||
       (reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(packed) & 15))
     return 1;
   // 32-bit buffer offsets, with room for the padded last block and the
@@ -338,16 +389,10 @@ int gemv_linear_forward(const void* x, int dtype, const uint8_t* packed, const f
   int64_t nbw = (rows + 16 * 256 - 1) / (16 * 256);
   if (nbw < 1) nbw = 1;
   if (nbw > 8) nbw = 8;
-  switch (nbw) {
-    case 1: gemv::launch_m<1>(x, packed, scale, bias, y, m, rows, cols, stream); break;
-    case 2: gemv::launch_m<2>(x, packed, scale, bias, y, m, rows, cols, stream); break;
-    case 3: gemv::launch_m<3>(x, packed, scale, bias, y, m, rows, cols, stream); break;
-    case 4: gemv::launch_m<4>(x, packed, scale, bias, y, m, rows, cols, stream); break;
-    case 5: gemv::launch_m<5>(x, packed, scale, bias, y, m, rows, cols, stream); break;
-    case 6: gemv::launch_m<6>(x, packed, scale, bias, y, m, rows, cols, stream); break;
-    case 7: gemv::launch_m<7>(x, packed, scale, bias, y, m, rows, cols, stream); break;
-    default: gemv::launch_m<8>(x, packed, scale, bias, y, m, rows, cols, stream); break;
-  }
+  if (dtype == QSTE_F16)
+    gemv::launch_dt<QSTE_F16>(nbw, x, packed, scale, bias, y, m, rows, cols, stream);
+  else
+    gemv::launch_dt<QSTE_BF16>(nbw, x, packed, scale, bias, y, m, rows, cols, stream);
   return static_cast<int>(hipGetLastError());
 }
 
