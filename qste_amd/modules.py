@@ -20,7 +20,12 @@ from .surface import Surface
 
 
 class QSTELinear(nn.Module):
-    """``y = (x @ sign^T) * scale + bias`` with a binary forward matrix."""
+    """Training-time binary linear layer over one ``Surface``.
+
+    Its output is the input times the packed +-1 matrix (transposed), each
+    output column scaled by the surface's learned row scale, plus an optional
+    bias; autograd routes the coordinate evidence to the surface
+    (modules.py:21-66)."""
 
     def __init__(self, surface: Surface, bias: Tensor | None = None):
         super().__init__()
