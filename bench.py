@@ -430,6 +430,43 @@ def gemm_kernels(T, d, ffn, device, iters=5):
     return out, flop
 
 
+def fp32_products(device, T=8192, rows=4096, cols=4096, iters=5):
+    """The three products on fp32 operands (bf16 limbs on the MFMA path),
+    against torch's fp32 matmul of the dense expanded signs: the reference's
+    own route for fp32 inputs (cuda.py:1531-1597)."""
+
+    import torch
+
+    from qste_amd import kernels
+
+    g = torch.Generator(device=device).manual_seed(9)
+    x = torch.randn(T, cols, generator=g, device=device)
+    dy = torch.randn(T, rows, generator=g, device=device)
+    layer = make_layer(rows, cols, 13, device)
+    packed = layer.surface.packed_sign.data
+    scale = layer.scale.detach().float()
+    xbits, off, xs = kernels.pack_affine_rows(x)
+    flop = 2.0 * T * rows * cols
+    out = {"shape": [T, rows, cols]}
+    runs = {
+        "forward": lambda: kernels.packed_linear_affine(x, packed, scale, None, cols),
+        "dgrad": lambda: kernels.packed_transpose(dy, packed, cols, row_scale=scale),
+        "evidence": lambda: kernels.evidence_from_packed(dy, xbits, cols, row_scale=xs),
+    }
+    for name, fn in runs.items():
+        ms = timed_events(fn, iters)
+        out[name] = {"ms": round(ms, 4), "tflops": round(flop / ms / 1e9, 2)}
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        w = kernels.unpack_rows(packed, cols, dtype=torch.float32)
+        ms = timed_events(lambda: torch.mm(x, w.t()), iters)
+        out["torch_fp32_mm"] = {"ms": round(ms, 4), "tflops": round(flop / ms / 1e9, 2)}
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev
+    return out
+
+
 def vendor_dense(T, d, ffn, device, iters=5):
     """torch.matmul (hipBLASLt) on dense bf16 operands of each product's shape,
     as the products store them: the practical GEMM rate of this box, for
@@ -734,6 +771,7 @@ def main():
                             "launches": launches[dominant]}
         line["kernels"] = kernels_t
         line["vendor_dense_bf16_gemm"] = vendor_dense(T, d, ffn, device)
+        line["fp32_products"] = fp32_products(device)
         line["coordinate_step"] = step_bandwidth(ffn, d, device)
         line["decode_gemv"] = decode_gemv(device)
         line["packed_activations"] = packed_activation_bandwidth(T, ffn, device)

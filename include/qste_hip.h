@@ -82,6 +82,21 @@ int qste_packed_linear_affine(const void* x, int dtype, const uint8_t* packed,
                               const float* scale, const float* bias, void* y, int64_t m,
                               int64_t rows, int64_t cols, void* stream);
 
+/* qste_packed_linear_affine with a workspace of
+ * qste_packed_linear_affine_workspace_bytes(m, rows, cols, dtype) bytes
+ * (0: none is used).  fp32 x then runs on the bf16 MFMA path: x splits
+ * exactly into three bf16 limbs (hi + mid + lo) along K, the signs repeat
+ * for each, every product is exact and the sums are the MFMA's fp32
+ * accumulators -- an fp32 product, where the plain entry runs fp32 SIMT
+ * code.  Other dtypes and shapes behave as the plain entry.  Replaces
+ * qste.kernels.packed_linear_affine (loader.py:292-297) for fp32 inputs,
+ * whose reference route is torch's fp32 mm on expanded signs
+ * (cuda.py:1531-1597). */
+size_t qste_packed_linear_affine_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int dtype);
+int qste_packed_linear_affine_ws(const void* x, int dtype, const uint8_t* packed, const float* scale,
+                                 const float* bias, void* y, int64_t m, int64_t rows, int64_t cols, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
 /* dx [m, cols] = dy [m, rows] @ (row_scale (*) sign), output in dy's dtype.
  * row_scale (fp32 [rows], may be NULL) is folded into the expanded operand
  * and rounded to dy's dtype there, as the reference GPU path does
@@ -91,6 +106,16 @@ int qste_packed_linear_affine(const void* x, int dtype, const uint8_t* packed,
 int qste_packed_transpose(const void* dy, int dtype, const uint8_t* packed,
                           const float* row_scale, void* dx, int64_t m, int64_t rows,
                           int64_t cols, void* stream);
+
+/* qste_packed_transpose with a workspace of
+ * qste_packed_transpose_workspace_bytes(m, rows, cols, dtype) bytes: fp32 dy
+ * times the row scale (one fp32 rounding) runs through bf16 limbs on the
+ * MFMA path as above.  Replaces qste.kernels.packed_transpose
+ * (loader.py:299-304) for fp32 inputs. */
+size_t qste_packed_transpose_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int dtype);
+int qste_packed_transpose_ws(const void* dy, int dtype, const uint8_t* packed, const float* row_scale, void* dx,
+                             int64_t m, int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes,
+                             void* stream);
 
 /* evidence fp32 [rows, cols] = dy[samples, rows]^T @ (row_scale (*) sign_x),
  * sign_x from packed_x uint8 [samples, (cols+7)/8]; row_scale (fp32
@@ -102,6 +127,10 @@ int qste_packed_transpose(const void* dy, int dtype, const uint8_t* packed,
  * Replaces qste.kernels.evidence_from_packed (loader.py:306-313;
  * fallback.py:126-138). */
 size_t qste_evidence_from_packed_workspace_bytes(int64_t samples, int64_t rows, int64_t cols);
+/* The workspace for a given dtype: for fp32 dy, room for its bf16 limbs
+ * (dy times the sample scale, one fp32 rounding, then split as above),
+ * which qste_evidence_from_packed then uses for the MFMA path. */
+size_t qste_evidence_from_packed_workspace_bytes_dtype(int64_t samples, int64_t rows, int64_t cols, int dtype);
 int qste_evidence_from_packed(const void* dy, int dtype, const uint8_t* packed_x,
                               const float* row_scale, float* evidence, int64_t samples,
                               int64_t rows, int64_t cols, void* workspace,
@@ -132,6 +161,11 @@ int qste_packed_row_inner(const float* matrix, const uint8_t* packed, float* out
  * No counterpart as a single call in the reference: it fuses five of its
  * calls (cuda.py:1568-1688, functional.py:143, 193). */
 size_t qste_linear_backward_workspace_bytes(int64_t samples, int64_t rows, int64_t cols);
+/* The workspace for a given dtype: for fp32 dy it includes room for the
+ * bf16 limbs of dX's and the evidence's dense operands, with which
+ * qste_linear_backward runs both products on the MFMA path; given only
+ * qste_linear_backward_workspace_bytes() it runs them in fp32 SIMT code. */
+size_t qste_linear_backward_workspace_bytes_dtype(int64_t samples, int64_t rows, int64_t cols, int dtype);
 int qste_linear_backward(const void* dy, int dtype, const uint8_t* packed_x,
                          const float* x_offset, const float* x_scale,
                          const uint8_t* packed_w, const float* scale, void* dx,

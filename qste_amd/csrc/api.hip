@@ -55,6 +55,17 @@ size_t swiglu_backward_sums_workspace(int64_t, int64_t);
 int launch_swiglu_backward_sums(const void*, const void*, const void*, int, void*, void*, const float*, const float*,
                                 int64_t, int64_t, float*, float*, hipStream_t);
 int launch_row_scale_backward(const float*, const float*, float*, int64_t, float, float, hipStream_t);
+// fp32 products through bf16 limbs (gemm_mfma.hip): 0 bytes / return 1 when
+// the shape is not for them
+size_t f32_forward_workspace(int64_t, int64_t, int64_t);
+int mfma_f32_forward(const float*, const uint8_t*, const float*, const float*, float*, int64_t, int64_t, int64_t,
+                     void*, size_t, hipStream_t);
+size_t f32_dgrad_workspace(int64_t, int64_t, int64_t);
+int mfma_f32_dgrad(const float*, const uint8_t*, const float*, float*, int64_t, int64_t, int64_t, void*, size_t,
+                   hipStream_t);
+size_t f32_evidence_workspace(int64_t, int64_t, int64_t);
+int mfma_f32_evidence(const float*, const uint8_t*, const float*, float*, int64_t, int64_t, int64_t, const float*,
+                      const float*, const uint8_t*, float*, void*, size_t, hipStream_t);
 }  // namespace qste
 
 using namespace qste;
@@ -66,12 +77,14 @@ inline bool dtype_ok(int d) { return d == QSTE_F32 || d == QSTE_F16 || d == QSTE
 inline size_t align_up(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
 
 struct BackwardLayout {
-  size_t v_part, db_part, v, gs_part, w_t, x_t, s16, xs16, partial, total;
+  size_t v_part, db_part, v, gs_part, w_t, x_t, s16, xs16, partial, limbs, limb_bytes, total;
   int64_t chunks, tiles;
   int64_t w_t_pitch, x_t_pitch;  // bytes per row of the transposed sign copies
 };
 
-BackwardLayout backward_layout(int64_t samples, int64_t rows, int64_t cols) {
+// with_limbs: room for fp32 dy's bf16 limbs (the dX and evidence products
+// take turns in it)
+BackwardLayout backward_layout(int64_t samples, int64_t rows, int64_t cols, bool with_limbs = false) {
   BackwardLayout l{};
   l.chunks = colsum_chunks(samples);
   int64_t tiles = simt_evidence_tiles(cols);
@@ -97,6 +110,12 @@ BackwardLayout backward_layout(int64_t samples, int64_t rows, int64_t cols) {
   const int64_t alone = mfma_evidence_plan(samples, rows, cols, false).partial_bytes;
   if (alone > partial) partial = alone;
   l.partial = at; at += align_up(static_cast<size_t>(partial));
+  l.limb_bytes = 0;
+  if (with_limbs) {
+    const size_t d = f32_dgrad_workspace(samples, rows, cols), e = f32_evidence_workspace(samples, rows, cols);
+    l.limb_bytes = d > e ? d : e;
+  }
+  l.limbs = at; at += align_up(l.limb_bytes);
   l.total = at;
   return l;
 }
@@ -200,6 +219,44 @@ int qste_packed_linear_affine(const void* x, int dtype, const uint8_t* packed, c
   return forward_dispatch(x, dtype, packed, scale, bias, y, m, rows, cols, as_stream(stream));
 }
 
+size_t qste_packed_linear_affine_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int dtype) {
+  return dtype == QSTE_F32 ? f32_forward_workspace(m, rows, cols) : 0;
+}
+
+int qste_packed_linear_affine_ws(const void* x, int dtype, const uint8_t* packed, const float* scale,
+                                 const float* bias, void* y, int64_t m, int64_t rows, int64_t cols, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
+  if (m < 0 || rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  if (m * rows == 0) return 0;
+  if (!y || !scale || (cols > 0 && (!x || !packed))) return QSTE_E_NULL;
+  if (dtype == QSTE_F32 && cols > 0) {
+    const int rc = mfma_f32_forward(static_cast<const float*>(x), packed, scale, bias, static_cast<float*>(y), m,
+                                    rows, cols, workspace, workspace_bytes, as_stream(stream));
+    if (rc != 1) return rc;
+  }
+  return forward_dispatch(x, dtype, packed, scale, bias, y, m, rows, cols, as_stream(stream));
+}
+
+size_t qste_packed_transpose_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int dtype) {
+  return dtype == QSTE_F32 ? f32_dgrad_workspace(m, rows, cols) : 0;
+}
+
+int qste_packed_transpose_ws(const void* dy, int dtype, const uint8_t* packed, const float* row_scale, void* dx,
+                             int64_t m, int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
+  if (m < 0 || rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  if (m * cols == 0) return 0;
+  if (!dx || (rows > 0 && (!dy || !packed))) return QSTE_E_NULL;
+  if (dtype == QSTE_F32 && rows > 0 && row_scale) {
+    const int rc = mfma_f32_dgrad(static_cast<const float*>(dy), packed, row_scale, static_cast<float*>(dx), m, rows,
+                                  cols, workspace, workspace_bytes, as_stream(stream));
+    if (rc != 1) return rc;
+  }
+  return dgrad_dispatch(dy, dtype, packed, row_scale, dx, m, rows, cols, as_stream(stream));
+}
+
 int qste_packed_transpose(const void* dy, int dtype, const uint8_t* packed, const float* row_scale,
                           void* dx, int64_t m, int64_t rows, int64_t cols, void* stream) {
   if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
@@ -214,6 +271,11 @@ size_t qste_evidence_from_packed_workspace_bytes(int64_t samples, int64_t rows, 
   return static_cast<size_t>(mfma_evidence_plan(samples, rows, cols, false).partial_bytes);
 }
 
+size_t qste_evidence_from_packed_workspace_bytes_dtype(int64_t samples, int64_t rows, int64_t cols, int dtype) {
+  if (dtype == QSTE_F32) return f32_evidence_workspace(samples, rows, cols);
+  return qste_evidence_from_packed_workspace_bytes(samples, rows, cols);
+}
+
 int qste_evidence_from_packed(const void* dy, int dtype, const uint8_t* packed_x, const float* row_scale,
                               float* evidence, int64_t samples, int64_t rows, int64_t cols, void* workspace,
                               size_t workspace_bytes, void* stream) {
@@ -221,6 +283,13 @@ int qste_evidence_from_packed(const void* dy, int dtype, const uint8_t* packed_x
   if (samples < 0 || rows < 0 || cols < 0) return QSTE_E_SHAPE;
   if (rows * cols == 0) return 0;
   if (!evidence || (samples > 0 && (!dy || !packed_x))) return QSTE_E_NULL;
+  if (dtype == QSTE_F32 && samples > 0 && workspace) {
+    const int rc = mfma_f32_evidence(static_cast<const float*>(dy), packed_x, row_scale, evidence, samples, rows, cols,
+                                     nullptr, nullptr, nullptr, nullptr, workspace, workspace_bytes,
+                                     as_stream(stream));
+    if (rc != 1) return rc;
+    workspace = nullptr;  // what remains for fp32 is the unsplit SIMT kernel
+  }
   // without a workspace the evidence runs unsplit
   EvidencePlan plan = mfma_evidence_plan(samples, rows, cols, false);
   if (!workspace) plan.splits = 1;
@@ -243,6 +312,11 @@ size_t qste_linear_backward_workspace_bytes(int64_t samples, int64_t rows, int64
   return backward_layout(samples, rows, cols).total;
 }
 
+size_t qste_linear_backward_workspace_bytes_dtype(int64_t samples, int64_t rows, int64_t cols, int dtype) {
+  if (samples < 0 || rows < 0 || cols < 0) return 0;
+  return backward_layout(samples, rows, cols, dtype == QSTE_F32).total;
+}
+
 namespace {
 
 // offset_dot: sum_t dy[t, r] * x_offset[t] when the caller has it (then dy
@@ -256,7 +330,11 @@ int linear_backward_impl(const void* dy, int dtype, const uint8_t* packed_x, con
   if (samples < 0 || rows <= 0 || cols <= 0) return QSTE_E_SHAPE;
   if (!evidence || !grad_scale || !scale || !packed_w) return QSTE_E_NULL;
   if (samples > 0 && (!dy || !packed_x || !x_offset || !x_scale)) return QSTE_E_NULL;
-  const BackwardLayout l = backward_layout(samples, rows, cols);
+  // fp32 takes its products through bf16 limbs when the workspace has room
+  // for them (qste_linear_backward_workspace_bytes_dtype), the SIMT kernels
+  // otherwise
+  BackwardLayout l = backward_layout(samples, rows, cols, dtype == QSTE_F32);
+  if (workspace_bytes < l.total) l = backward_layout(samples, rows, cols);
   if (!workspace || workspace_bytes < l.total) return QSTE_E_WORKSPACE;
   hipStream_t s = as_stream(stream);
   char* base = static_cast<char*>(workspace);
@@ -311,6 +389,21 @@ int linear_backward_impl(const void* dy, int dtype, const uint8_t* packed_x, con
           return rc;
         return launch_sum_partials(gs_part, tiles, rows, grad_scale, s);
       }
+    }
+    if (dtype == QSTE_F32 && l.limb_bytes > 0) {
+      // the dX and evidence products take turns in the limbs' space
+      void* lw = base + l.limbs;
+      if (dx) {
+        rc = mfma_f32_dgrad(static_cast<const float*>(dy), packed_w, scale, static_cast<float*>(dx), samples, rows,
+                            cols, lw, l.limb_bytes, s);
+        if (rc == 1) rc = dgrad_dispatch(dy, dtype, packed_w, scale, dx, samples, rows, cols, s);
+        if (rc) return rc;
+      }
+      dgrad_done = true;
+      rc = mfma_f32_evidence(static_cast<const float*>(dy), packed_x, x_scale, evidence, samples, rows, cols, v,
+                             scale, packed_w, gs_part, lw, l.limb_bytes, s);
+      if (rc == 0) return launch_sum_partials(gs_part, mfma_evidence_tiles(cols), rows, grad_scale, s);
+      if (rc != 1) return rc;
     }
     if (dx && !dgrad_done && (rc = dgrad_dispatch(dy, dtype, packed_w, scale, dx, samples, rows, cols, s)))
       return rc;

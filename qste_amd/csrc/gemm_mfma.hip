@@ -42,8 +42,10 @@ enum { A_ROWS_M = 0, A_ROWS_K = 1 };        // A[m][k] stored with k (or m) cont
 // a per-k bf16 scale, both brought in by direct loads.
 enum { B_BITS_ALONG_K = 0, B_BITS_ALONG_N = 1, B_BITS_ALONG_K_SCALED = 2 };
 // EPI_PARTIAL: the bare fp32 accumulators of one K range of a split-K
-// evidence, finished by evidence_combine_kernel
-enum { EPI_FORWARD = 0, EPI_PLAIN = 1, EPI_EVIDENCE = 2, EPI_PARTIAL = 3 };
+// evidence, finished by evidence_combine_kernel.  EPI_FORWARD_F32: the
+// forward's scale and bias, stored as fp32 (the fp32 products, whose dense
+// operand arrives as three bf16 limbs along K).
+enum { EPI_FORWARD = 0, EPI_PLAIN = 1, EPI_EVIDENCE = 2, EPI_PARTIAL = 3, EPI_FORWARD_F32 = 4 };
 
 struct Params {
   const uint16_t* a;     // bf16 dense operand (x or dy)
@@ -570,6 +572,33 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
         const int lrow = WMR * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
 #pragma unroll
         for (int nb = 0; nb < NBN; ++nb) part[lrow * BN + WNC * wn + 32 * nb + l32] = acc[mb][nb][r];
+      }
+    return;
+  }
+
+  if (EPI == EPI_FORWARD_F32) {
+    // y = acc * scale[n] + bias[n] in fp32, stored as computed (32 lanes x 4
+    // bytes per row per store)
+    float* y = static_cast<float*>(p.out);
+    float sc[NBN], bi[NBN];
+#pragma unroll
+    for (int nb = 0; nb < NBN; ++nb) {
+      const int64_t col = n0 + WNC * wn + 32 * nb + l32;
+      sc[nb] = (col < p.N && p.n_scale) ? p.n_scale[col] : 1.0f;
+      bi[nb] = (col < p.N && p.n_bias) ? p.n_bias[col] : 0.0f;
+    }
+#pragma unroll
+    for (int mb = 0; mb < MBN; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + WMR * wm + 32 * mb + 8 * (r >> 2) + 4 * kg + (r & 3);
+#pragma unroll
+        for (int nb = 0; nb < NBN; ++nb) {
+          const int64_t col = n0 + WNC * wn + 32 * nb + l32;
+          float v = acc[mb][nb][r] * sc[nb];
+          v = v + bi[nb];
+          if (row < p.M && col < p.N) y[row * p.N + col] = v;
+        }
       }
     return;
   }
@@ -1189,6 +1218,174 @@ int mfma_backward_pair(const void* dy, int dtype, const uint8_t* x_t, int64_t x_
   int rc = static_cast<int>(hipGetLastError());
   if (rc || !split) return rc;
   return launch_combine(sp, m_add, scale, packed_w, ev, gs_partial, rows, cols, stream);
+}
+
+// ---------------------------------------------------------------------------
+// fp32 products on the bf16 MFMA path.  An fp32 value v splits exactly into
+// three bf16 limbs: hi = bf16(v), mid = bf16(v - hi), lo = bf16(v - hi - mid)
+// (each difference is exact in fp32; v - hi has at most 16 significant
+// bits and v - hi - mid at most 8, so lo holds it exactly; only values whose
+// last limb falls below bf16's subnormals lose it).  A limb times +-1 is
+// exact, so a product over K becomes the same bf16 MFMA product over 3K --
+// the dense operand's three limbs along K against the signs repeated three
+// times -- with every product exact and the sums in the MFMA's fp32
+// accumulators.  Per-k scales (the row scale of dX, the sample scale of
+// the evidence) are multiplied into the fp32 operand first, one fp32
+// rounding each, where the reference's fp32 GEMM rounds the product inside
+// its fused multiply-add.
+// ---------------------------------------------------------------------------
+
+namespace limbs {
+
+// out[plane * p + r * ld + c] for the three limbs p of x[r, c] (times
+// row_mul[r] or col_mul[c] when given)
+__global__ __launch_bounds__(256) void split_kernel(const float* __restrict__ x, int64_t rows, int64_t cols,
+                                                    const float* __restrict__ row_mul,
+                                                    const float* __restrict__ col_mul, uint16_t* __restrict__ out,
+                                                    int64_t ld, int64_t plane) {
+  const int64_t n = rows * cols;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / cols, c = i - r * cols;
+    float v = x[i];
+    if (row_mul) v = v * row_mul[r];
+    if (col_mul) v = v * col_mul[c];
+    const uint16_t hi = f32_to_bf16(v);
+    const float r1 = v - bf16_to_f32(hi);
+    const uint16_t mid = f32_to_bf16(r1);
+    const float r2 = r1 - bf16_to_f32(mid);
+    const uint16_t lo = f32_to_bf16(r2);
+    uint16_t* o = out + r * ld + c;
+    o[0] = hi;
+    o[plane] = mid;
+    o[2 * plane] = lo;
+  }
+}
+
+// out[plane * p + r * out_ld + j] = in[r * in_ld + j] for p = 0, 1, 2 and
+// j < bytes (the packed signs repeated for each limb); in may be plane 0 of
+// out itself, which is then left as it is
+__global__ __launch_bounds__(256) void repeat_kernel(const uint8_t* in, int64_t rows, int64_t bytes, int64_t in_ld,
+                                                     uint8_t* out, int64_t out_ld, int64_t plane) {
+  const int64_t n = rows * bytes;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / bytes, j = i - r * bytes;
+    const uint8_t v = in[r * in_ld + j];
+    uint8_t* o = out + r * out_ld + j;
+    if (o != in + r * in_ld + j) o[0] = v;
+    o[plane] = v;
+    o[2 * plane] = v;
+  }
+}
+
+inline int grid_for(int64_t n) {
+  const int64_t b = (n + 255) / 256;
+  return static_cast<int>(b > 16384 ? 16384 : (b < 1 ? 1 : b));
+}
+
+inline size_t up256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+}  // namespace limbs
+
+int launch_transpose_bits(const uint8_t*, uint8_t*, int64_t, int64_t, int64_t, int64_t, hipStream_t);
+
+// Whether a product of these sizes takes the limbs (enough rows of output to
+// fill 256-row tiles; below that the fp32 SIMT kernels are as fast)
+static bool f32_limbs_worth(int64_t m) { return m >= 128; }
+
+size_t f32_forward_workspace(int64_t m, int64_t rows, int64_t cols) {
+  if (m <= 0 || rows <= 0 || cols <= 0 || cols % 64 != 0 || !f32_limbs_worth(m)) return 0;
+  return limbs::up256(static_cast<size_t>(m) * 3 * cols * 2) + limbs::up256(static_cast<size_t>(rows) * 3 * cols / 8);
+}
+
+// y [m, rows] fp32 = (x @ sign^T) * scale + bias through the limbs.  Returns
+// 1 when the call is not for this path (shape, or too little workspace).
+int mfma_f32_forward(const float* x, const uint8_t* packed, const float* scale, const float* bias, float* y,
+                     int64_t m, int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes,
+                     hipStream_t stream) {
+  const size_t need = f32_forward_workspace(m, rows, cols);
+  if (need == 0 || !workspace || workspace_bytes < need) return 1;
+  const int64_t k3 = 3 * cols, kb = cols / 8;
+  if (!fits32(m * k3 * 2) || !fits32(rows * k3 / 8)) return 1;
+  uint16_t* a = static_cast<uint16_t*>(workspace);
+  uint8_t* b = static_cast<uint8_t*>(workspace) + limbs::up256(static_cast<size_t>(m) * k3 * 2);
+  limbs::split_kernel<<<limbs::grid_for(m * cols), 256, 0, stream>>>(x, m, cols, nullptr, nullptr, a, k3, cols);
+  limbs::repeat_kernel<<<limbs::grid_for(rows * kb), 256, 0, stream>>>(packed, rows, kb, kb, b, 3 * kb, kb);
+  mfma::Params p{};
+  p.a = a;
+  p.bits = b;
+  p.out = y;
+  p.M = m; p.N = rows; p.K = k3;
+  p.lda = k3; p.pb = 3 * kb;
+  p.a_rows = m; p.bit_rows = rows;
+  p.n_scale = scale; p.n_bias = bias;
+  mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD_F32, QSTE_BF16>
+      <<<wide_grid(m, rows), mfma::wide::THREADS, 0, stream>>>(p);
+  return static_cast<int>(hipGetLastError());
+}
+
+size_t f32_dgrad_workspace(int64_t m, int64_t rows, int64_t cols) {
+  if (m <= 0 || rows <= 0 || cols <= 0 || rows % 64 != 0 || !f32_limbs_worth(m)) return 0;
+  return limbs::up256(static_cast<size_t>(m) * 3 * rows * 2) + limbs::up256(static_cast<size_t>(cols) * 3 * rows / 8);
+}
+
+// dx [m, cols] fp32 = dy @ (row_scale * sign) through the limbs: dy scaled
+// by the row scale along K, the signs transposed (bits along K).
+int mfma_f32_dgrad(const float* dy, const uint8_t* packed, const float* row_scale, float* dx, int64_t m,
+                   int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const size_t need = f32_dgrad_workspace(m, rows, cols);
+  if (need == 0 || !workspace || workspace_bytes < need) return 1;
+  const int64_t k3 = 3 * rows, kb = rows / 8;
+  if (!fits32(m * k3 * 2) || !fits32(cols * k3 / 8)) return 1;
+  uint16_t* a = static_cast<uint16_t*>(workspace);
+  uint8_t* b = static_cast<uint8_t*>(workspace) + limbs::up256(static_cast<size_t>(m) * k3 * 2);
+  limbs::split_kernel<<<limbs::grid_for(m * rows), 256, 0, stream>>>(dy, m, rows, nullptr, row_scale, a, k3, rows);
+  // the transposed signs into plane 0 of each row of b (its pitch 3 * kb is
+  // a multiple of 8 as rows % 64 == 0), then repeated into planes 1 and 2
+  int rc = launch_transpose_bits(packed, b, rows, cols, (cols + 7) / 8, 3 * kb, stream);
+  if (rc) return rc;
+  limbs::repeat_kernel<<<limbs::grid_for(cols * kb), 256, 0, stream>>>(b, cols, kb, 3 * kb, b, 3 * kb, kb);
+  mfma::Params p{};
+  p.a = a;
+  p.bits = b;
+  p.out = dx;
+  p.M = m; p.N = cols; p.K = k3;
+  p.lda = k3; p.pb = 3 * kb;
+  p.a_rows = m; p.bit_rows = cols;
+  mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD_F32, QSTE_BF16>
+      <<<wide_grid(m, cols), mfma::wide::THREADS, 0, stream>>>(p);
+  return static_cast<int>(hipGetLastError());
+}
+
+size_t f32_evidence_workspace(int64_t samples, int64_t rows, int64_t cols) {
+  if (samples <= 0 || rows <= 0 || cols <= 0 || rows % 64 != 0 || cols % 64 != 0 || !f32_limbs_worth(rows))
+    return 0;
+  return limbs::up256(static_cast<size_t>(3 * samples) * rows * 2) +
+         limbs::up256(static_cast<size_t>(3 * samples) * (cols / 8));
+}
+
+// The evidence of fp32 dy through the limbs: dy scaled by the sample scale,
+// its limbs stacked along the samples (rows of K), the sample signs repeated
+// the same way, and the fused evidence epilogue (offset correction, row
+// scale, scale-gradient partials in mfma_evidence_tiles(cols) slots).
+int mfma_f32_evidence(const float* dy, const uint8_t* packed_x, const float* x_scale, float* ev, int64_t samples,
+                      int64_t rows, int64_t cols, const float* m_add, const float* m_scale, const uint8_t* w_bits,
+                      float* gs_partial, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const size_t need = f32_evidence_workspace(samples, rows, cols);
+  if (need == 0 || !workspace || workspace_bytes < need) return 1;
+  const int64_t k3 = 3 * samples, cb = cols / 8;
+  if (!fits32(k3 * rows * 2) || !fits32(k3 * cb)) return 1;
+  uint16_t* a = static_cast<uint16_t*>(workspace);
+  uint8_t* b = static_cast<uint8_t*>(workspace) + limbs::up256(static_cast<size_t>(k3) * rows * 2);
+  limbs::split_kernel<<<limbs::grid_for(samples * rows), 256, 0, stream>>>(dy, samples, rows, x_scale, nullptr, a,
+                                                                          rows, samples * rows);
+  limbs::repeat_kernel<<<limbs::grid_for(samples * cb), 256, 0, stream>>>(packed_x, samples, cb, cb, b, cb,
+                                                                         samples * cb);
+  mfma::Params p = evidence_params(a, b, nullptr, ev, k3, rows, cols, m_add, m_scale, w_bits, gs_partial);
+  mfma::wide::wide_kernel<mfma::A_ROWS_K, mfma::B_BITS_ALONG_N, mfma::EPI_EVIDENCE, QSTE_BF16>
+      <<<wide_grid(rows, cols), mfma::wide::THREADS, 0, stream>>>(p);
+  return static_cast<int>(hipGetLastError());
 }
 
 }  // namespace qste

@@ -252,9 +252,18 @@ def packed_linear_affine(inputs: Tensor, packed: Tensor, scale: Tensor, bias: Te
     out = torch.empty(flat.shape[0], rows, dtype=inputs.dtype, device=device)
     scale_f32 = _f32(scale)  # held until the launch is queued
     bias_f32 = _f32(bias)  # held until the launch is queued
-    code = _lib.load().qste_packed_linear_affine(
-        _ptr(flat), _dtype_code(flat), _ptr(packed), _ptr(scale_f32), _ptr(bias_f32),
-        _ptr(out), flat.shape[0], rows, int(columns), _stream(device))
+    lib = _lib.load()
+    # fp32 runs its product through bf16 limbs on the MFMA path, in a workspace
+    nbytes = lib.qste_packed_linear_affine_workspace_bytes(flat.shape[0], rows, int(columns), _dtype_code(flat))
+    if nbytes:
+        work = _workspace(nbytes, device)
+        code = lib.qste_packed_linear_affine_ws(
+            _ptr(flat), _dtype_code(flat), _ptr(packed), _ptr(scale_f32), _ptr(bias_f32),
+            _ptr(out), flat.shape[0], rows, int(columns), _ptr(work), work.numel(), _stream(device))
+    else:
+        code = lib.qste_packed_linear_affine(
+            _ptr(flat), _dtype_code(flat), _ptr(packed), _ptr(scale_f32), _ptr(bias_f32),
+            _ptr(out), flat.shape[0], rows, int(columns), _stream(device))
     _lib.check(code, "packed_linear_affine")
     return out.view(*inputs.shape[:-1], rows)
 
@@ -273,9 +282,18 @@ def packed_transpose(inputs: Tensor, packed: Tensor, columns: int,
     flat = inputs.reshape(-1, rows).contiguous()
     out = torch.empty(flat.shape[0], int(columns), dtype=inputs.dtype, device=device)
     row_scale_f32 = _f32(row_scale)  # held until the launch is queued
-    code = _lib.load().qste_packed_transpose(
-        _ptr(flat), _dtype_code(flat), _ptr(packed), _ptr(row_scale_f32), _ptr(out),
-        flat.shape[0], rows, int(columns), _stream(device))
+    lib = _lib.load()
+    nbytes = (lib.qste_packed_transpose_workspace_bytes(flat.shape[0], rows, int(columns), _dtype_code(flat))
+              if row_scale_f32 is not None else 0)
+    if nbytes:
+        work = _workspace(nbytes, device)
+        code = lib.qste_packed_transpose_ws(
+            _ptr(flat), _dtype_code(flat), _ptr(packed), _ptr(row_scale_f32), _ptr(out),
+            flat.shape[0], rows, int(columns), _ptr(work), work.numel(), _stream(device))
+    else:
+        code = lib.qste_packed_transpose(
+            _ptr(flat), _dtype_code(flat), _ptr(packed), _ptr(row_scale_f32), _ptr(out),
+            flat.shape[0], rows, int(columns), _stream(device))
     _lib.check(code, "packed_transpose")
     return out.view(*inputs.shape[:-1], int(columns))
 
@@ -297,7 +315,7 @@ def evidence_from_packed(grad: Tensor, packed: Tensor, columns: int,
     out = torch.empty(rows, int(columns), dtype=torch.float32, device=device)
     row_scale_f32 = _f32(row_scale)  # held until the launch is queued
     lib = _lib.load()
-    nbytes = lib.qste_evidence_from_packed_workspace_bytes(samples, rows, int(columns))
+    nbytes = lib.qste_evidence_from_packed_workspace_bytes_dtype(samples, rows, int(columns), _dtype_code(grad))
     work = _workspace(nbytes, device) if nbytes else None
     code = lib.qste_evidence_from_packed(
         _ptr(grad), _dtype_code(grad), _ptr(packed), _ptr(row_scale_f32), _ptr(out), samples,
@@ -346,7 +364,7 @@ def linear_backward(grad: Tensor, packed_x: Tensor, x_offset: Tensor, x_scale: T
     evidence = torch.empty(rows, int(columns), dtype=torch.float32, device=device)
     grad_scale = torch.empty(rows, dtype=torch.float32, device=device)
     grad_bias = torch.empty(rows, dtype=torch.float32, device=device) if need_bias else None
-    nbytes = lib.qste_linear_backward_workspace_bytes(samples, rows, int(columns))
+    nbytes = lib.qste_linear_backward_workspace_bytes_dtype(samples, rows, int(columns), _dtype_code(grad))
     work = _workspace(nbytes, device)
     x_offset_f32 = _f32(x_offset)  # held until the launch is queued
     x_scale_f32 = _f32(x_scale)  # held until the launch is queued

@@ -40,6 +40,12 @@ SIGNATURES = {
     "qste_evidence_from_packed": (_int, [_vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
     "qste_packed_row_inner": (_int, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "qste_linear_backward_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "qste_linear_backward_workspace_bytes_dtype": (_sz, [_i64, _i64, _i64, _int]),
+    "qste_evidence_from_packed_workspace_bytes_dtype": (_sz, [_i64, _i64, _i64, _int]),
+    "qste_packed_linear_affine_workspace_bytes": (_sz, [_i64, _i64, _i64, _int]),
+    "qste_packed_linear_affine_ws": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "qste_packed_transpose_workspace_bytes": (_sz, [_i64, _i64, _i64, _int]),
+    "qste_packed_transpose_ws": (_int, [_vp, _int, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
     "qste_linear_backward": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                     _i64, _i64, _i64, _vp, _sz, _vp]),
     "qste_linear_backward_offset_dot": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
