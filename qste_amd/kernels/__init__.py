@@ -733,7 +733,9 @@ def row_scale_backward(exp_value: Tensor, grad: Tensor, lo: float, hi: float) ->
 
 def _check_ids(ids: Tensor, rows: int) -> Tensor:
     flat = ids.reshape(-1).to(torch.int64).contiguous()
-    if flat.numel() and (int(flat.min()) < 0 or int(flat.max()) >= rows):
+    if flat.numel():
+        lo, hi = torch.stack(torch.aminmax(flat)).tolist()  # one reduction, one copy to the host
+    if flat.numel() and (lo < 0 or hi >= rows):
         raise IndexError(f"embedding id out of range for {rows} rows")
     return flat
 

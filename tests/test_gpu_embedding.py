@@ -59,7 +59,10 @@ def test_lookup_matches_oracle(K, rows, cols):
 
 
 @pytest.mark.parametrize("rows,cols,count,vocab_used", [(40, 16, 15, 40), (300, 64, 500, 20),
-                                                        (1000, 771, 64, 1000), (5, 8, 0, 5)])
+                                                        (1000, 771, 64, 1000), (5, 8, 0, 5),
+                                                        # three 8-bit sort passes, a ragged last block,
+                                                        # many tokens per id (order within an id matters)
+                                                        (70000, 64, 20001, 300), (70000, 32, 5000, 70000)])
 def test_backward_matches_oracle(K, rows, cols, count, vocab_used):
     print(f"backward {rows}x{cols} count={count}", flush=True)
     packed, scale = _table(rows, cols, 7)
