@@ -186,9 +186,49 @@ constexpr int kSumChunk = 256;
 constexpr int kSumWaves = 4;
 constexpr int kSumThreads = kSumWaves * 64;
 
+// bf16 gates with magnitude in [2^-12, 2^4) -- nearly every gate a layer
+// produces -- take sigmoid(g) and the rounded silu(g) from LDS tables that
+// the workgroup fills first with the arithmetic above (one entry per bf16
+// value in that range), so the exponential and the two correctly rounded
+// divisions are paid once per table entry, not once per element.  Other
+// gates (tiny, huge, zero, inf, NaN) compute them.  A table entry is the
+// value the computation gives for that input, so the results are the same
+// bits either way.
+constexpr uint32_t kTabExpLo = 127 - 12;  // biased exponent of 2^-12
+constexpr int kTabExps = 16;
+constexpr uint32_t kTabHalf = kTabExps * 128;  // entries per sign (7 mantissa bits)
+constexpr int kTabEntries = 2 * kTabHalf;
+static_assert(kTabHalf == 1u << 11, "sign bit -> table half");
+
+// bf16 bits of table entry j
+__device__ __forceinline__ uint32_t tab_bits(uint32_t j) {
+  return ((j & kTabHalf) << 4) | ((kTabExpLo << 7) + (j & (kTabHalf - 1)));
+}
+
+__device__ __forceinline__ void fill_silu_table(float* tab_s, uint16_t* tab_a, int tid, int threads) {
+  for (int j = tid; j < kTabEntries; j += threads) {
+    const float x = __uint_as_float(tab_bits(static_cast<uint32_t>(j)) << 16);
+    tab_a[j] = f32_to_bf16(silu_value(x));
+    tab_s[j] = 1.0f / (1.0f + expf(-x));
+  }
+}
+
+// backward_one with a = the rounded silu(g) and s = sigmoid(g) given
+template <int DT>
+__device__ __forceinline__ void backward_given(float dh, float g, float u, float a, float s, float& dg,
+                                               float& du) {
+  using E = Elem<DT>;
+  du = dh * a;
+  const float da = E::round(dh * u);
+  const float inner = fmaf(g, 1.0f - s, 1.0f);
+  const float ds = da * s;
+  dg = ds * inner;
+}
+
 template <int DT>
 __device__ __forceinline__ void backward_x8(const uint4& hc, const uint4& gc, const uint4& uc, uint4& og,
-                                            uint4& ou, float (&fg)[8], float (&fu)[8]) {
+                                            uint4& ou, float (&fg)[8], float (&fu)[8], const float* tab_s,
+                                            const uint16_t* tab_a) {
   using E = Elem<DT>;
   const uint16_t* h = reinterpret_cast<const uint16_t*>(&hc);
   const uint16_t* g = reinterpret_cast<const uint16_t*>(&gc);
@@ -198,7 +238,19 @@ __device__ __forceinline__ void backward_x8(const uint4& hc, const uint4& gc, co
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     float a, b;
-    backward_one<DT>(E::load(h, i), E::load(g, i), E::load(u, i), a, b);
+    if constexpr (DT == QSTE_BF16) {
+      const uint32_t bits = g[i];
+      const uint32_t off = (bits & 0x7FFFu) - (kTabExpLo << 7);  // wraps above the range when below it
+      if (off < kTabHalf) {
+        const uint32_t idx = off | ((bits >> 15) << 11);
+        backward_given<DT>(E::load(h, i), E::load(g, i), E::load(u, i), bf16_to_f32(tab_a[idx]), tab_s[idx], a,
+                           b);
+      } else {
+        backward_one<DT>(E::load(h, i), E::load(g, i), E::load(u, i), a, b);
+      }
+    } else {
+      backward_one<DT>(E::load(h, i), E::load(g, i), E::load(u, i), a, b);
+    }
     E::store(rg, i, a);
     E::store(ru, i, b);
     fg[i] = E::load(rg, i);  // the stored (rounded) values are what is summed
@@ -213,7 +265,17 @@ __global__ __launch_bounds__(kSumThreads) void backward_sums_kernel(
     const float* __restrict__ off_u, int64_t samples, int64_t cols, float* __restrict__ part) {
   constexpr int UNROLL = 4;
   constexpr int kPad = 17;
-  __shared__ float red[kSumWaves * 64 * kPad];
+  constexpr int kRed = kSumWaves * 64 * kPad;
+  constexpr int kTab = DT == QSTE_BF16 ? kTabEntries + kTabEntries / 2 : 0;  // floats: s, then a as bf16
+  // the tables while the samples are summed, then the waves' partial sums
+  __shared__ float lds[kRed > kTab ? kRed : kTab];
+  float* red = lds;
+  float* tab_s = lds;
+  uint16_t* tab_a = reinterpret_cast<uint16_t*>(lds + kTabEntries);
+  if constexpr (DT == QSTE_BF16) {
+    fill_silu_table(tab_s, tab_a, threadIdx.x, kSumThreads);
+    __syncthreads();
+  }
   const int lane = threadIdx.x % 64;
   const int wave = threadIdx.x / 64;
   const int64_t base = static_cast<int64_t>(blockIdx.x) * 512;
@@ -229,7 +291,7 @@ __global__ __launch_bounds__(kSumThreads) void backward_sums_kernel(
   auto one = [&](const uint4& hc, const uint4& gc, const uint4& uc, int64_t t, float og_, float ou_) {
     uint4 rg, ru;
     float fg[8], fu[8];
-    backward_x8<DT>(hc, gc, uc, rg, ru, fg, fu);
+    backward_x8<DT>(hc, gc, uc, rg, ru, fg, fu, tab_s, tab_a);
     *reinterpret_cast<uint4*>(dg + t * cols + c) = rg;
     *reinterpret_cast<uint4*>(du + t * cols + c) = ru;
 #pragma unroll
@@ -261,6 +323,7 @@ __global__ __launch_bounds__(kSumThreads) void backward_sums_kernel(
           *reinterpret_cast<const uint4*>(u + at), t, off_g[t], off_u[t]);
     }
   }
+  __syncthreads();  // every wave is done with the tables
   float* mine = red + (wave * 64 + lane) * kPad;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {

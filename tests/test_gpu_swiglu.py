@@ -208,6 +208,42 @@ def test_backward_sums_equal_the_layer_backward_sums(rows, cols, dtype):
                            b.view(torch.int16) if b.element_size() == 2 else b.view(torch.int32))
 
 
+def _same_or_both_nan(a, b):
+    """bf16 tensors equal bit for bit, except that any NaN matches any NaN."""
+
+    nan = torch.isnan(a.float()) & torch.isnan(b.float())
+    return bool(((_bits(a) == _bits(b)) | nan).all())
+
+
+def test_backward_sums_every_bf16_gate():
+    """Every one of the 65536 bf16 gate values (in and out of the range the
+    kernel's sigmoid/silu tables hold: zeros, subnormals, tiny and huge
+    magnitudes, infinities, NaNs), with random gradients and up values:
+    dg and du bit for bit against torch's autograd chain and the plain
+    kernel, and the sums against the float64 bound."""
+
+    from qste_amd import kernels
+
+    every = torch.arange(-32768, 32768, dtype=torch.int32, device=DEV).to(torch.int16)
+    gate = every.view(torch.bfloat16).reshape(256, 256)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    up = torch.randn(256, 256, generator=g, device=DEV).bfloat16()
+    grad = torch.randn(256, 256, generator=g, device=DEV).bfloat16()
+    off = torch.randn(256, generator=g, device=DEV)
+    g1, u1 = gate.clone().requires_grad_(True), up.clone().requires_grad_(True)
+    (F.silu(g1) * u1).backward(grad)
+    dg0, du0 = kernels.swiglu_backward(grad, gate, up)
+    dg, du, sums = kernels.swiglu_backward_sums(grad, gate, up, off, off)
+    torch.cuda.synchronize()
+    assert _same_or_both_nan(dg, g1.grad) and _same_or_both_nan(du, u1.grad)
+    assert _same_or_both_nan(dg, dg0) and _same_or_both_nan(du, du0)
+    finite = torch.isfinite(dg.float()).all(0) & torch.isfinite(du.float()).all(0)
+    for got, dy in ((sums[0], dg), (sums[1], du)):
+        want = dy.double().t() @ off.double()
+        bound = 264 * 2.0**-24 * (dy.double().abs().t() @ off.double().abs()) + 1e-30
+        assert bool(((got.double() - want).abs() <= bound)[finite].all())
+
+
 def test_row_scale_equals_torch():
     """clamp(exp(log_scale)) and its gradient, bit for bit against torch's
     operators, over finite values across the whole exp range, the clamp
