@@ -194,64 +194,76 @@ __device__ __forceinline__ uint64_t transpose_8x8(uint64_t x) {
   return x;
 }
 
-// A workgroup transposes a 64-row x 512-column tile through LDS: the 64
-// input rows are read as 64-byte segments, each thread transposes two 8 x 8
-// blocks (one column byte, 16 rows), and each output column's 8 bytes (the
-// tile's 64 rows) leave as one 8-byte store.  out_pitch must be a multiple
-// of 8.
-constexpr int kTrRows = 64, kTrColBytes = 64;  // tile: 64 rows x 512 columns
+// A workgroup transposes a 512-row x 512-column tile through LDS: the input
+// rows arrive as 16-byte loads, each thread transposes 16 8 x 8 blocks of
+// one column byte (eight row blocks at a time, so each of its 8 columns
+// gathers 64 rows into one 8-byte LDS word), and every output column leaves
+// as 64 contiguous bytes (eight 8-byte stores by consecutive lanes).
+// out_pitch must be a multiple of 8.
+constexpr int kTrRows = 512, kTrColBytes = 64;  // tile: 512 rows x 512 columns
+constexpr int kTrPad = 4;                       // bytes of padding per staged input row
 __global__ __launch_bounds__(256) void transpose_bits_kernel(const uint8_t* __restrict__ in,
                                                              uint8_t* __restrict__ out, int64_t rows,
                                                              int64_t cols, int64_t in_pitch,
                                                              int64_t out_pitch) {
-  __shared__ uint8_t tile[kTrRows][kTrColBytes + 4];
-  __shared__ uint64_t otile[8 * kTrColBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t tile[kTrRows][kTrColBytes + kTrPad];
+  __shared__ uint64_t otile[8 * kTrColBytes][kTrRows / 64];  // [column][64-row group]
   const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kTrRows;
   const int64_t cb0 = static_cast<int64_t>(blockIdx.x) * kTrColBytes;
   const int tid = threadIdx.x;
-  {
-    // 64 rows x 64 bytes, 16 bytes per thread
-    const int row = tid >> 2, part = tid & 3;
+  const bool vec = (in_pitch & 15) == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0;
+  // 512 rows x 64 bytes: load i of thread t is row (t >> 2) + 64 i, bytes
+  // 16 (t & 3) .. + 15
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = (tid >> 2) + 64 * i, part = tid & 3;
     const int64_t r = r0 + row;
-    const bool dwords = (in_pitch & 3) == 0 && (reinterpret_cast<uintptr_t>(in) & 3) == 0;
+    const int64_t cb = cb0 + 16 * part;
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    if (r < rows) {
+      if (vec && cb + 16 <= in_pitch) {
+        const uint4 q = *reinterpret_cast<const uint4*>(in + r * in_pitch + cb);
+        w[0] = q.x, w[1] = q.y, w[2] = q.z, w[3] = q.w;
+      } else {
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const int64_t cb = cb0 + 16 * part + 4 * d;
-      uint32_t w = 0;
-      if (r < rows) {
-        if (dwords && cb + 4 <= in_pitch) {
-          w = *reinterpret_cast<const uint32_t*>(in + r * in_pitch + cb);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (cb + i < in_pitch) w |= static_cast<uint32_t>(in[r * in_pitch + cb + i]) << (8 * i);
-        }
+        for (int k = 0; k < 16; ++k)
+          if (cb + k < in_pitch) w[k >> 2] |= static_cast<uint32_t>(in[r * in_pitch + cb + k]) << (8 * (k & 3));
       }
-      *reinterpret_cast<uint32_t*>(&tile[row][16 * part + 4 * d]) = w;
     }
+#pragma unroll
+    for (int d = 0; d < 4; ++d) *reinterpret_cast<uint32_t*>(&tile[row][16 * part + 4 * d]) = w[d];
   }
   __syncthreads();
   {
-    // column byte cbl, row blocks 2 rbp and 2 rbp + 1
-    const int cbl = tid & 63, rbp = tid >> 6;
+    // column byte cbl; 64-row groups 2 rg and 2 rg + 1
+    const int cbl = tid & 63, rg = tid >> 6;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int rb = 2 * rbp + h;
-      uint64_t x = 0;
+      const int g = 2 * rg + h;
+      uint64_t col[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) x |= static_cast<uint64_t>(tile[8 * rb + i][cbl]) << (8 * i);
-      x = transpose_8x8(x);
+      for (int b = 0; b < 8; ++b) {
+        const int rb = 8 * g + b;  // row block: rows 8 rb .. 8 rb + 7
+        uint64_t x = 0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        reinterpret_cast<uint8_t*>(&otile[8 * cbl + j])[rb] = static_cast<uint8_t>(x >> (8 * j));
+        for (int i = 0; i < 8; ++i) x |= static_cast<uint64_t>(tile[8 * rb + i][cbl]) << (8 * i);
+        x = transpose_8x8(x);  // byte j: column 8 cbl + j over the block's 8 rows
+#pragma unroll
+        for (int j = 0; j < 8; ++j) col[j] |= ((x >> (8 * j)) & 0xFFull) << (8 * b);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) otile[8 * cbl + j][g] = col[j];
     }
   }
   __syncthreads();
+  // 512 columns x 64 bytes: store i of thread t is column (t >> 3) + 32 i,
+  // bytes 8 (t & 7) .. + 7 of its 64
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int cl = 2 * tid + k;
+  for (int i = 0; i < 16; ++i) {
+    const int cl = (tid >> 3) + 32 * i, piece = tid & 7;
     const int64_t c = 8 * cb0 + cl;
-    if (c < cols) *reinterpret_cast<uint64_t*>(out + c * out_pitch + r0 / 8) = otile[cl];
+    const int64_t ob = r0 / 8 + 8 * piece;
+    if (c < cols && ob < out_pitch) *reinterpret_cast<uint64_t*>(out + c * out_pitch + ob) = otile[cl][piece];
   }
 }
 
