@@ -372,15 +372,18 @@ def timed_wall(fn, iters, warmup=2):
     return (time.perf_counter() - t0) / iters * 1e3
 
 
-def timed_events(fn, iters, stream=None):
-    """Average milliseconds of ``fn`` over ``iters`` calls, by HIP events."""
+def timed_events(fn, iters, stream=None, warm=3):
+    """Average milliseconds of ``fn`` over ``iters`` calls, by HIP events,
+    after ``warm`` untimed calls (the first launches after the GPU idled
+    while inputs were built run up to 20% slower, at lower clocks)."""
 
     import torch
 
     stream = stream or torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
-    fn()
+    for _ in range(max(1, warm)):
+        fn()
     torch.cuda.synchronize()
     start.record(stream)
     for _ in range(iters):
