@@ -54,6 +54,27 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_lib.SIGNATURES)
 
 
+def test_library_allocates_and_clears_no_device_memory():
+    """Scratch comes from caller workspaces (or the static scratch array), and
+    nothing is cleared with a memset: the built library imports no HIP
+    allocation, free or memset routine."""
+
+    import shutil
+    import subprocess
+
+    from qste_amd.kernels import _lib
+
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    lib = _lib.load()
+    out = subprocess.run([nm, "-D", "--undefined-only", lib._name], capture_output=True, text=True, check=True)
+    imported = {line.split()[-1].split("@")[0] for line in out.stdout.splitlines() if line.strip()}
+    assert "hipLaunchKernel" in imported or any(n.startswith("__hip") for n in imported)
+    banned = {n for n in imported if re.match(r"hip(Ext)?(Malloc|Free|Memset|HostMalloc|HostFree|MallocAsync)", n)}
+    assert not banned, sorted(banned)
+
+
 def test_error_codes_and_workspace_queries_need_no_gpu():
     from qste_amd.kernels import _lib
 
