@@ -65,8 +65,9 @@ __global__ void colsum_partial_kernel(const typename Elem<DT>::T* __restrict__ d
   if (db_part) db_part[blockIdx.y * rows + r] = db;
 }
 
-// bf16 / f16 with rows % 8 == 0: each lane reduces 8 adjacent columns (one
-// 16-byte load per sample), so a wave covers 512 columns.  The chunk's
+// rows a multiple of the 16-byte vector (8 bf16 / f16 or 4 fp32 columns):
+// each lane reduces one vector of adjacent columns (one 16-byte load per
+// sample), so a wave covers 512 (or 256) columns.  The chunk's
 // kColChunk samples are split over the workgroup's kColWaves waves (a
 // contiguous quarter each, UNROLL loads in flight), and the waves' sums are
 // added in wave order through LDS: a fixed order, so the result does not
@@ -77,25 +78,27 @@ constexpr int kColThreads = kColWaves * kWave;
 
 template <int DT>
 __global__ __launch_bounds__(kColThreads) void colsum_partial_x8_kernel(
-    const uint16_t* __restrict__ dy, const float* __restrict__ offset, int64_t samples, int64_t rows,
+    const typename Elem<DT>::T* __restrict__ dy, const float* __restrict__ offset, int64_t samples, int64_t rows,
     float* __restrict__ v_part, float* __restrict__ db_part) {
+  using T = typename Elem<DT>::T;
+  constexpr int NV = 16 / sizeof(T);  // columns per lane
   constexpr int UNROLL = 8;
-  constexpr int kPad = 17;  // 16 sums per lane, padded against bank conflicts
+  constexpr int kPad = 2 * NV + 1;  // 2 NV sums per lane, padded against bank conflicts
   __shared__ float red[kColWaves * kWave * kPad];
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kWave * 8);
-  const int64_t r = base + lane * 8;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kWave * NV);
+  const int64_t r = base + lane * NV;
   const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kColChunk;
   const int64_t c1 = c0 + kColChunk < samples ? c0 + kColChunk : samples;
   constexpr int kPer = kColChunk / kColWaves;
   const int64_t t0 = c0 + wave * kPer < c1 ? c0 + wave * kPer : c1;
   const int64_t t1 = t0 + kPer < c1 ? t0 + kPer : c1;
-  float v[8], db[8];
+  float v[NV], db[NV];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = db[i] = 0.0f;
+  for (int i = 0; i < NV; ++i) v[i] = db[i] = 0.0f;
   if (r < rows) {
-    const uint16_t* col = dy + r;
+    const T* col = dy + r;
     int64_t t = t0;
     for (; t + UNROLL <= t1; t += UNROLL) {
       uint4 q[UNROLL];
@@ -107,9 +110,9 @@ __global__ __launch_bounds__(kColThreads) void colsum_partial_x8_kernel(
       }
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) {
-        const uint16_t* e = reinterpret_cast<const uint16_t*>(&q[u]);
+        const T* e = reinterpret_cast<const T*>(&q[u]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NV; ++i) {
           const float g = Elem<DT>::load(e, i);
           v[i] = fmaf(g, o[u], v[i]);
           db[i] += g;
@@ -119,9 +122,9 @@ __global__ __launch_bounds__(kColThreads) void colsum_partial_x8_kernel(
     for (; t < t1; ++t) {
       const uint4 q = *reinterpret_cast<const uint4*>(col + t * rows);
       const float o = offset[t];
-      const uint16_t* e = reinterpret_cast<const uint16_t*>(&q);
+      const T* e = reinterpret_cast<const T*>(&q);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < NV; ++i) {
         const float g = Elem<DT>::load(e, i);
         v[i] = fmaf(g, o, v[i]);
         db[i] += g;
@@ -130,20 +133,21 @@ __global__ __launch_bounds__(kColThreads) void colsum_partial_x8_kernel(
   }
   float* mine = red + (wave * kWave + lane) * kPad;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < NV; ++i) {
     mine[i] = v[i];
-    mine[8 + i] = db[i];
+    mine[NV + i] = db[i];
   }
   __syncthreads();
-  // 1024 results per workgroup (512 columns of v, then of db), consecutive
-  // threads on consecutive columns; waves summed in order 0..kColWaves-1.
+  // 2 * 64 NV results per workgroup (its columns of v, then of db),
+  // consecutive threads on consecutive columns; waves summed in order
+  // 0..kColWaves-1.
   const int64_t part = static_cast<int64_t>(blockIdx.y) * rows;
 #pragma unroll
-  for (int j = threadIdx.x; j < 2 * kWave * 8; j += kColThreads) {
-    const int which = j / (kWave * 8);
-    const int c = j % (kWave * 8);
+  for (int j = threadIdx.x; j < 2 * kWave * NV; j += kColThreads) {
+    const int which = j / (kWave * NV);
+    const int c = j % (kWave * NV);
     const int64_t rc = base + c;
-    const int slot = (c / 8) * kPad + which * 8 + c % 8;
+    const int slot = (c / NV) * kPad + which * NV + c % NV;
     float s = red[slot];
 #pragma unroll
     for (int w = 1; w < kColWaves; ++w) s += red[w * kWave * kPad + slot];
@@ -176,16 +180,20 @@ int launch_colsums(const void* dy, int dtype, const float* offset, int64_t sampl
                    hipStream_t stream) {
   if (rows == 0) return 0;
   const int chunks = colsum_chunks(samples);
-  const bool x8 = (dtype == QSTE_BF16 || dtype == QSTE_F16) && rows % 8 == 0 &&
+  const int nv = dtype == QSTE_F32 ? 4 : 8;  // columns per 16-byte vector
+  const bool x8 = (dtype == QSTE_BF16 || dtype == QSTE_F16 || dtype == QSTE_F32) && rows % nv == 0 &&
                   (reinterpret_cast<uintptr_t>(dy) & 15) == 0;
   if (chunks > 0 && x8) {
-    dim3 grid(ceil_div(rows, kWave * 8), chunks);
+    dim3 grid(ceil_div(rows, kWave * nv), chunks);
     if (dtype == QSTE_BF16)
       colsum_partial_x8_kernel<QSTE_BF16><<<grid, kColThreads, 0, stream>>>(
           static_cast<const uint16_t*>(dy), offset, samples, rows, v_part, db_part);
-    else
+    else if (dtype == QSTE_F16)
       colsum_partial_x8_kernel<QSTE_F16><<<grid, kColThreads, 0, stream>>>(
           static_cast<const uint16_t*>(dy), offset, samples, rows, v_part, db_part);
+    else
+      colsum_partial_x8_kernel<QSTE_F32><<<grid, kColThreads, 0, stream>>>(
+          static_cast<const float*>(dy), offset, samples, rows, v_part, db_part);
     int rc = static_cast<int>(hipGetLastError());
     if (rc) return rc;
   } else if (chunks > 0) {
