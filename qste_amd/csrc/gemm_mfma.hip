@@ -890,6 +890,57 @@ __global__ __launch_bounds__(THREADS) void evidence_combine_kernel(Split sp, con
   for (int o = 8; o >= 1; o >>= 1) signed_e0 += __shfl_xor(signed_e0, o, kWave);
   if (gs_partial && lane % 16 == 0) gs_partial[(static_cast<int64_t>(tn) * WAVES_N + lane / 16) * M + row] = signed_e0;
 }
+// Split-K forward for products with few output tiles and a long K chain
+// (fp32 limbs at small M): workgroup w covers tile w % tiles over K range
+// w / tiles (ks_steps K steps) and stores its bare accumulators in slab w of
+// `partial` (BM x BN fp32 each) for forward_combine_kernel.
+template <int DT>
+__global__ __launch_bounds__(THREADS, 1) void forward_split_kernel(Params p, int tiles, int ks_steps,
+                                                                   float* partial) {
+  using SZ = StageSizes<A_ROWS_M, B_BITS_ALONG_K>;
+  QSTE_WIDE_STAGES(SZ::a, SZ::b, SZ::s)
+  const int w = static_cast<int>(blockIdx.x), i = w % tiles, j = w / tiles;
+  const int64_t k0 = static_cast<int64_t>(j) * ks_steps * BK;
+  Params q = p;
+  q.a = p.a + k0;          // columns k0 .. of every dense row (lda unchanged)
+  q.bits = p.bits + k0 / 8;  // bits k0 .. of every packed row (pb unchanged)
+  q.K = p.K - k0 < static_cast<int64_t>(ks_steps) * BK ? p.K - k0 : static_cast<int64_t>(ks_steps) * BK;
+  q.out = partial + static_cast<int64_t>(w) * (BM * BN);
+  wide_tile<A_ROWS_M, B_BITS_ALONG_K, EPI_PARTIAL, DT>(q, i, A0, A1, A2, A3, B0, B1, B2, B3, Sc);
+}
+
+// y = (the K ranges' accumulators summed in range order) * scale[n] +
+// bias[n], fp32, as EPI_FORWARD_F32 finishes an unsplit tile.  Workgroup
+// (x, i): rows 4x .. 4x + 3 of tile i, a wave per row, 4 columns per lane.
+__global__ __launch_bounds__(THREADS) void forward_combine_kernel(const float* __restrict__ partial, int tiles,
+                                                                  int splits, const float* __restrict__ n_scale,
+                                                                  const float* __restrict__ n_bias,
+                                                                  float* __restrict__ y, int64_t M, int64_t N) {
+  const int tiles_m = static_cast<int>((M + BM - 1) / BM), tiles_n = static_cast<int>((N + BN - 1) / BN);
+  const int i = static_cast<int>(blockIdx.y);
+  int tm, tn;
+  tile_of<2>(i, tiles_m, tiles_n, tm, tn);  // the forward's mapping
+  const int lrow = static_cast<int>(blockIdx.x) * (THREADS / kWave) + static_cast<int>(threadIdx.x) / kWave;
+  const int lcol = 4 * (static_cast<int>(threadIdx.x) % kWave);
+  const int64_t row = static_cast<int64_t>(tm) * BM + lrow;
+  if (row >= M) return;  // the whole wave
+  const float* src = partial + static_cast<int64_t>(i) * (BM * BN) + lrow * BN + lcol;
+  float4 acc = *reinterpret_cast<const float4*>(src);
+  for (int j = 1; j < splits; ++j) {
+    const float4 v = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(j) * tiles * (BM * BN));
+    acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+  }
+  const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int64_t col = static_cast<int64_t>(tn) * BN + lcol + q;
+    if (col < N) {
+      float v = a[q] * (n_scale ? n_scale[col] : 1.0f);
+      v = v + (n_bias ? n_bias[col] : 0.0f);
+      y[row * N + col] = v;
+    }
+  }
+}
 #undef QSTE_WIDE_STAGES
 }  // namespace wide
 }  // namespace mfma
@@ -1294,9 +1345,34 @@ int launch_transpose_bits(const uint8_t*, uint8_t*, int64_t, int64_t, int64_t, i
 // fill 256-row tiles; below that the fp32 SIMT kernels are as fast)
 static bool f32_limbs_worth(int64_t m) { return m >= 128; }
 
+// K ranges of the fp32 forward over 3 * cols limbs: a product with fewer
+// output tiles than half the device's 256 CUs and a long K chain is cut into
+// up to 16 ranges of at least 4 K steps (one round of workgroups), else 1.
+struct F32Split {
+  int splits, ks_steps;
+};
+static F32Split f32_forward_split(int64_t m, int64_t rows, int64_t cols) {
+  const int tiles = wide_grid(m, rows);
+  const int nk = static_cast<int>(3 * cols / mfma::wide::BK);
+  int s = 1;
+  if (tiles > 0 && 2 * tiles <= 256 && nk >= 16) {
+    s = 16;
+    if (s > 256 / tiles) s = 256 / tiles;
+    if (s > nk / 4) s = nk / 4;
+  }
+  if (s < 2) return {1, nk};
+  const int ks = (nk + s - 1) / s;
+  return {(nk + ks - 1) / ks, ks};
+}
+
 size_t f32_forward_workspace(int64_t m, int64_t rows, int64_t cols) {
   if (m <= 0 || rows <= 0 || cols <= 0 || cols % 64 != 0 || !f32_limbs_worth(m)) return 0;
-  return limbs::up256(static_cast<size_t>(m) * 3 * cols * 2) + limbs::up256(static_cast<size_t>(rows) * 3 * cols / 8);
+  const F32Split sp = f32_forward_split(m, rows, cols);
+  const size_t partial = sp.splits > 1 ? static_cast<size_t>(sp.splits) * wide_grid(m, rows) *
+                                             mfma::wide::BM * mfma::wide::BN * sizeof(float)
+                                       : 0;
+  return limbs::up256(static_cast<size_t>(m) * 3 * cols * 2) + limbs::up256(static_cast<size_t>(rows) * 3 * cols / 8) +
+         partial;
 }
 
 // y [m, rows] fp32 = (x @ sign^T) * scale + bias through the limbs.  Returns
@@ -1320,8 +1396,21 @@ int mfma_f32_forward(const float* x, const uint8_t* packed, const float* scale, 
   p.lda = k3; p.pb = 3 * kb;
   p.a_rows = m; p.bit_rows = rows;
   p.n_scale = scale; p.n_bias = bias;
+  const F32Split sp = f32_forward_split(m, rows, cols);
+  const int tiles = wide_grid(m, rows);
+  if (sp.splits > 1) {
+    float* partial = reinterpret_cast<float*>(b + limbs::up256(static_cast<size_t>(rows) * k3 / 8));
+    mfma::wide::forward_split_kernel<QSTE_BF16>
+        <<<tiles * sp.splits, mfma::wide::THREADS, 0, stream>>>(p, tiles, sp.ks_steps, partial);
+    int rc = static_cast<int>(hipGetLastError());
+    if (rc) return rc;
+    const dim3 grid(mfma::wide::BM / (mfma::wide::THREADS / kWave), static_cast<unsigned>(tiles));
+    mfma::wide::forward_combine_kernel<<<grid, mfma::wide::THREADS, 0, stream>>>(partial, tiles, sp.splits, scale,
+                                                                               bias, y, m, rows);
+    return static_cast<int>(hipGetLastError());
+  }
   mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD_F32, QSTE_BF16>
-      <<<wide_grid(m, rows), mfma::wide::THREADS, 0, stream>>>(p);
+      <<<tiles, mfma::wide::THREADS, 0, stream>>>(p);
   return static_cast<int>(hipGetLastError());
 }
 
