@@ -73,7 +73,15 @@ def _require_gpu(*tensors: Tensor) -> torch.device:
     return device
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device: torch.device) -> int:
+    """The device's current HIP stream as an address (torch's current-stream
+    query without building a Stream object where torch offers it)."""
+
+    if _RAW_STREAM is not None and device.index is not None:
+        return _RAW_STREAM(device.index)
     return torch.cuda.current_stream(device).cuda_stream
 
 
