@@ -88,9 +88,13 @@ int qste_packed_linear_affine(const void* x, int dtype, const uint8_t* packed,
  * exactly into three bf16 limbs (hi + mid + lo) along K, the signs repeat
  * for each, every product is exact and the sums are the MFMA's fp32
  * accumulators -- an fp32 product, where the plain entry runs fp32 SIMT
- * code.  Other dtypes and shapes behave as the plain entry.  Replaces
- * qste.kernels.packed_linear_affine (loader.py:292-297) for fp32 inputs,
- * whose reference route is torch's fp32 mm on expanded signs
+ * code.  Where a product has few output tiles against its K (fp32 at small
+ * m; bf16 / fp16 with 16 < m and at most a round of 256-row tiles), K is
+ * cut into ranges whose fp32 accumulators the workspace holds, summed in
+ * range order before the scale, bias and one rounding.  Other dtypes and
+ * shapes behave as the plain entry.  Replaces
+ * qste.kernels.packed_linear_affine (loader.py:292-297); the reference's
+ * route for fp32 inputs is torch's fp32 mm on expanded signs
  * (cuda.py:1531-1597). */
 size_t qste_packed_linear_affine_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int dtype);
 int qste_packed_linear_affine_ws(const void* x, int dtype, const uint8_t* packed, const float* scale,

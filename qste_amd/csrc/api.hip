@@ -58,6 +58,9 @@ int launch_row_scale_backward(const float*, const float*, float*, int64_t, float
 // fp32 products through bf16 limbs (gemm_mfma.hip): 0 bytes / return 1 when
 // the shape is not for them
 size_t f32_forward_workspace(int64_t, int64_t, int64_t);
+size_t mfma_forward_split_workspace(int64_t, int64_t, int64_t, int);
+int mfma_linear_forward_split(const void*, int, const uint8_t*, const float*, const float*, void*, int64_t, int64_t,
+                              int64_t, void*, size_t, hipStream_t);
 int mfma_f32_forward(const float*, const uint8_t*, const float*, const float*, float*, int64_t, int64_t, int64_t,
                      void*, size_t, hipStream_t);
 size_t f32_dgrad_workspace(int64_t, int64_t, int64_t);
@@ -220,7 +223,7 @@ int qste_packed_linear_affine(const void* x, int dtype, const uint8_t* packed, c
 }
 
 size_t qste_packed_linear_affine_workspace_bytes(int64_t m, int64_t rows, int64_t cols, int dtype) {
-  return dtype == QSTE_F32 ? f32_forward_workspace(m, rows, cols) : 0;
+  return dtype == QSTE_F32 ? f32_forward_workspace(m, rows, cols) : mfma_forward_split_workspace(m, rows, cols, dtype);
 }
 
 int qste_packed_linear_affine_ws(const void* x, int dtype, const uint8_t* packed, const float* scale,
@@ -233,6 +236,10 @@ int qste_packed_linear_affine_ws(const void* x, int dtype, const uint8_t* packed
   if (dtype == QSTE_F32 && cols > 0) {
     const int rc = mfma_f32_forward(static_cast<const float*>(x), packed, scale, bias, static_cast<float*>(y), m,
                                     rows, cols, workspace, workspace_bytes, as_stream(stream));
+    if (rc != 1) return rc;
+  } else if (cols > 0) {
+    const int rc = mfma_linear_forward_split(x, dtype, packed, scale, bias, y, m, rows, cols, workspace,
+                                             workspace_bytes, as_stream(stream));
     if (rc != 1) return rc;
   }
   return forward_dispatch(x, dtype, packed, scale, bias, y, m, rows, cols, as_stream(stream));

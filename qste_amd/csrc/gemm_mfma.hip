@@ -910,12 +910,14 @@ __global__ __launch_bounds__(THREADS, 1) void forward_split_kernel(Params p, int
 }
 
 // y = (the K ranges' accumulators summed in range order) * scale[n] +
-// bias[n], fp32, as EPI_FORWARD_F32 finishes an unsplit tile.  Workgroup
-// (x, i): rows 4x .. 4x + 3 of tile i, a wave per row, 4 columns per lane.
+// bias[n], as the forward epilogues finish an unsplit tile: stored as fp32
+// (OUT = QSTE_F32) or rounded once to bf16 / fp16.  Workgroup (x, i): rows
+// 4x .. 4x + 3 of tile i, a wave per row, 4 columns per lane.
+template <int OUT>
 __global__ __launch_bounds__(THREADS) void forward_combine_kernel(const float* __restrict__ partial, int tiles,
                                                                   int splits, const float* __restrict__ n_scale,
                                                                   const float* __restrict__ n_bias,
-                                                                  float* __restrict__ y, int64_t M, int64_t N) {
+                                                                  void* __restrict__ out, int64_t M, int64_t N) {
   const int tiles_m = static_cast<int>((M + BM - 1) / BM), tiles_n = static_cast<int>((N + BN - 1) / BN);
   const int i = static_cast<int>(blockIdx.y);
   int tm, tn;
@@ -937,7 +939,10 @@ __global__ __launch_bounds__(THREADS) void forward_combine_kernel(const float* _
     if (col < N) {
       float v = a[q] * (n_scale ? n_scale[col] : 1.0f);
       v = v + (n_bias ? n_bias[col] : 0.0f);
-      y[row * N + col] = v;
+      if constexpr (OUT == QSTE_F32)
+        static_cast<float*>(out)[row * N + col] = v;
+      else
+        static_cast<uint16_t*>(out)[row * N + col] = round16<OUT>(v);
     }
   }
 }
@@ -1031,6 +1036,71 @@ int mfma_linear_forward(const void* x, int dtype, const uint8_t* packed, const f
   else
     mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD, QSTE_BF16>
         <<<wide_grid(m, rows), mfma::wide::THREADS, 0, stream>>>(p);
+  return static_cast<int>(hipGetLastError());
+}
+
+// K ranges of a forward with `tiles` output tiles and nk K steps: a product
+// with fewer tiles than half the device's 256 CUs and a long K chain is cut
+// into up to 16 ranges of at least 4 K steps (one round of workgroups),
+// else 1.
+struct SplitK {
+  int splits, ks_steps;
+};
+static SplitK forward_split_plan(int tiles, int nk) {
+  int s = 1;
+  if (tiles > 0 && 2 * tiles <= 256 && nk >= 16) {
+    s = 16;
+    if (s > 256 / tiles) s = 256 / tiles;
+    if (s > nk / 4) s = nk / 4;
+  }
+  if (s < 2) return {1, nk};
+  const int ks = (nk + s - 1) / s;
+  return {(nk + ks - 1) / ks, ks};
+}
+// The 16-bit forward with few output tiles (M past the decode GEMV's 16, a
+// round of 256-row tiles or less) over a long K: K ranges as for the fp32
+// limbs, their accumulators in a caller workspace, then scale, bias and one
+// rounding.  Workspace bytes, 0 where no split pays.
+size_t mfma_forward_split_workspace(int64_t m, int64_t rows, int64_t cols, int dtype) {
+  if (!mfma_dtype(dtype) || m <= 16 || rows <= 0 || cols <= 0 || cols % 64 != 0) return 0;
+  const int tiles = wide_grid(m, rows);
+  const SplitK sp = forward_split_plan(tiles, static_cast<int>(cols / mfma::wide::BK));
+  return sp.splits > 1 ? static_cast<size_t>(sp.splits) * tiles * mfma::wide::BM * mfma::wide::BN * sizeof(float)
+                       : 0;
+}
+
+// Returns 1 when the call is not for this path (shape, or too little workspace).
+int mfma_linear_forward_split(const void* x, int dtype, const uint8_t* packed, const float* scale,
+                              const float* bias, void* y, int64_t m, int64_t rows, int64_t cols, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream) {
+  const size_t need = mfma_forward_split_workspace(m, rows, cols, dtype);
+  if (need == 0 || !workspace || workspace_bytes < need || !forward_ok(x, dtype, packed, m, rows, cols) ||
+      !aligned16(workspace))
+    return 1;
+  mfma::Params p{};
+  p.a = static_cast<const uint16_t*>(x);
+  p.bits = packed;
+  p.M = m; p.N = rows; p.K = cols;
+  p.lda = cols; p.pb = cols / 8;
+  p.a_rows = m; p.bit_rows = rows;
+  const int tiles = wide_grid(m, rows);
+  const SplitK sp = forward_split_plan(tiles, static_cast<int>(cols / mfma::wide::BK));
+  float* partial = static_cast<float*>(workspace);
+  if (dtype == QSTE_F16)
+    mfma::wide::forward_split_kernel<QSTE_F16>
+        <<<tiles * sp.splits, mfma::wide::THREADS, 0, stream>>>(p, tiles, sp.ks_steps, partial);
+  else
+    mfma::wide::forward_split_kernel<QSTE_BF16>
+        <<<tiles * sp.splits, mfma::wide::THREADS, 0, stream>>>(p, tiles, sp.ks_steps, partial);
+  int rc = static_cast<int>(hipGetLastError());
+  if (rc) return rc;
+  const dim3 grid(mfma::wide::BM / (mfma::wide::THREADS / kWave), static_cast<unsigned>(tiles));
+  if (dtype == QSTE_F16)
+    mfma::wide::forward_combine_kernel<QSTE_F16>
+        <<<grid, mfma::wide::THREADS, 0, stream>>>(partial, tiles, sp.splits, scale, bias, y, m, rows);
+  else
+    mfma::wide::forward_combine_kernel<QSTE_BF16>
+        <<<grid, mfma::wide::THREADS, 0, stream>>>(partial, tiles, sp.splits, scale, bias, y, m, rows);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -1345,29 +1415,13 @@ int launch_transpose_bits(const uint8_t*, uint8_t*, int64_t, int64_t, int64_t, i
 // fill 256-row tiles; below that the fp32 SIMT kernels are as fast)
 static bool f32_limbs_worth(int64_t m) { return m >= 128; }
 
-// K ranges of the fp32 forward over 3 * cols limbs: a product with fewer
-// output tiles than half the device's 256 CUs and a long K chain is cut into
-// up to 16 ranges of at least 4 K steps (one round of workgroups), else 1.
-struct F32Split {
-  int splits, ks_steps;
-};
-static F32Split f32_forward_split(int64_t m, int64_t rows, int64_t cols) {
-  const int tiles = wide_grid(m, rows);
-  const int nk = static_cast<int>(3 * cols / mfma::wide::BK);
-  int s = 1;
-  if (tiles > 0 && 2 * tiles <= 256 && nk >= 16) {
-    s = 16;
-    if (s > 256 / tiles) s = 256 / tiles;
-    if (s > nk / 4) s = nk / 4;
-  }
-  if (s < 2) return {1, nk};
-  const int ks = (nk + s - 1) / s;
-  return {(nk + ks - 1) / ks, ks};
+static SplitK f32_forward_split(int64_t m, int64_t rows, int64_t cols) {
+  return forward_split_plan(wide_grid(m, rows), static_cast<int>(3 * cols / mfma::wide::BK));
 }
 
 size_t f32_forward_workspace(int64_t m, int64_t rows, int64_t cols) {
   if (m <= 0 || rows <= 0 || cols <= 0 || cols % 64 != 0 || !f32_limbs_worth(m)) return 0;
-  const F32Split sp = f32_forward_split(m, rows, cols);
+  const SplitK sp = f32_forward_split(m, rows, cols);
   const size_t partial = sp.splits > 1 ? static_cast<size_t>(sp.splits) * wide_grid(m, rows) *
                                              mfma::wide::BM * mfma::wide::BN * sizeof(float)
                                        : 0;
@@ -1396,7 +1450,7 @@ int mfma_f32_forward(const float* x, const uint8_t* packed, const float* scale, 
   p.lda = k3; p.pb = 3 * kb;
   p.a_rows = m; p.bit_rows = rows;
   p.n_scale = scale; p.n_bias = bias;
-  const F32Split sp = f32_forward_split(m, rows, cols);
+  const SplitK sp = f32_forward_split(m, rows, cols);
   const int tiles = wide_grid(m, rows);
   if (sp.splits > 1) {
     float* partial = reinterpret_cast<float*>(b + limbs::up256(static_cast<size_t>(rows) * k3 / 8));
@@ -1405,8 +1459,8 @@ int mfma_f32_forward(const float* x, const uint8_t* packed, const float* scale, 
     int rc = static_cast<int>(hipGetLastError());
     if (rc) return rc;
     const dim3 grid(mfma::wide::BM / (mfma::wide::THREADS / kWave), static_cast<unsigned>(tiles));
-    mfma::wide::forward_combine_kernel<<<grid, mfma::wide::THREADS, 0, stream>>>(partial, tiles, sp.splits, scale,
-                                                                               bias, y, m, rows);
+    mfma::wide::forward_combine_kernel<QSTE_F32>
+        <<<grid, mfma::wide::THREADS, 0, stream>>>(partial, tiles, sp.splits, scale, bias, y, m, rows);
     return static_cast<int>(hipGetLastError());
   }
   mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD_F32, QSTE_BF16>

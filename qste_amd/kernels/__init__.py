@@ -261,7 +261,8 @@ def packed_linear_affine(inputs: Tensor, packed: Tensor, scale: Tensor, bias: Te
     scale_f32 = _f32(scale)  # held until the launch is queued
     bias_f32 = _f32(bias)  # held until the launch is queued
     lib = _lib.load()
-    # fp32 runs its product through bf16 limbs on the MFMA path, in a workspace
+    # fp32 runs its product through bf16 limbs on the MFMA path, in a
+    # workspace; products with few output tiles split K there
     nbytes = lib.qste_packed_linear_affine_workspace_bytes(flat.shape[0], rows, int(columns), _dtype_code(flat))
     if nbytes:
         work = _workspace(nbytes, device)

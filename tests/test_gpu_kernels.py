@@ -426,6 +426,34 @@ MFMA_SHAPES = [(576, 320, 300), (1024, 2048, 1000), (128, 64, 17), (256, 512, 2)
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("rows,cols,m", [(4096, 4096, 64), (1000, 8192, 17), (2048, 2048, 256), (640, 4096, 100)])
+def test_split_k_forward(rows, cols, m, dt):
+    """16 < m with few output tiles over a long K: the forward cuts K into
+    ranges (the workspace query says so), and agrees with the oracle and,
+    up to rare one-ulp roundings from the other fp32 summation order, with
+    the unsplit kernel the plain entry runs."""
+
+    print(f"split-K forward {rows}x{cols} m={m} {dt}", flush=True)
+    lib = K()._lib.load()
+    code = {"bf16": 2, "f16": 1}[dt]
+    assert lib.qste_packed_linear_affine_workspace_bytes(m, rows, cols, code) > 0
+    packed, x, scale, bias, _ = _problem(rows, cols, m, dt, rows + cols + 7 * m)
+    tx, tp, ts, tb = t(x, DT[dt]), t(packed), t(scale), t(bias)
+    y = K().packed_linear_affine(tx, tp, ts, tb, cols)
+    plain = torch.empty_like(y)
+    rc = lib.qste_packed_linear_affine(tx.data_ptr(), code, tp.data_ptr(), ts.data_ptr(), tb.data_ptr(),
+                                       plain.data_ptr(), m, rows, cols, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    got, ref = f32(y), f32(plain)
+    want_r = round_out(oracle.linear_fwd(x, packed, scale, bias, cols), dt)
+    assert rel_l2(got, want_r) <= 1e-3
+    assert np.mean(got != want_r) < 0.01
+    assert np.mean(got != ref) < 0.01
+    ulp = np.abs(ref) * (2.0 ** -7 if dt == "bf16" else 2.0 ** -10)
+    assert np.all(np.abs(got - ref) <= ulp + 1e-6)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("rows,cols,m", MFMA_SHAPES)
 def test_mfma_products_ragged(rows, cols, m, dt):
     print(f"mfma {rows}x{cols} m={m} {dt}", flush=True)
