@@ -365,19 +365,21 @@ int qste_swiglu_backward_sums(const void* grad, const void* gate, const void* up
 /* ---- the learned row scale (src/qste/surface.py:84-85) ------------------- */
 
 /* scale = clamp(exp(log_scale), lo, hi) over n rows, and exp_value = the
- * exp before the clamp (what the backward reads), rounded as torch's
- * log_scale.exp().clamp(lo, hi) rounds (lo and hi as fp32; a NaN stays NaN).
+ * exp before the clamp (what the backward reads), all three in `dtype`
+ * (fp32, fp16 or bf16, the log-scale parameter's), rounded as torch's
+ * log_scale.exp().clamp(lo, hi) rounds on a tensor of that dtype (exp on
+ * the fp32 value, rounded once; lo and hi as fp32; a NaN stays NaN).
  * Replaces the Surface.scale property's two torch operators
  * (src/qste/surface.py:84-85). */
-int qste_row_scale(const float* log_scale, float* scale, float* exp_value, int64_t n, float lo, float hi,
+int qste_row_scale(const void* log_scale, int dtype, void* scale, void* exp_value, int64_t n, float lo, float hi,
                    void* stream);
 
-/* grad_log_scale = (lo <= exp_value <= hi ? grad : 0) * exp_value: torch's
- * autograd of exp().clamp(lo, hi) (clamp_backward, then exp's backward by
- * its result), bit for bit.  Replaces that autograd chain of
- * src/qste/surface.py:84-85. */
-int qste_row_scale_backward(const float* exp_value, const float* grad, float* grad_log_scale, int64_t n, float lo,
-                            float hi, void* stream);
+/* grad_log_scale = (lo <= exp_value <= hi ? grad : 0) * exp_value, all in
+ * `dtype` (the bounds rounded to it for the comparisons): torch's autograd of exp().clamp(lo, hi) (clamp_backward, then
+ * exp's backward by its result), bit for bit.  Replaces that autograd chain
+ * of src/qste/surface.py:84-85. */
+int qste_row_scale_backward(const void* exp_value, const void* grad, int dtype, void* grad_log_scale, int64_t n,
+                            float lo, float hi, void* stream);
 
 /* ---- binary embedding (src/qste/modules.py:68-100) ---------------------- */
 

@@ -50,11 +50,11 @@ int gemv_linear_forward(const void*, int, const uint8_t*, const float*, const fl
 int launch_swiglu_forward(const void*, const void*, int, void*, uint8_t*, float*, float*, int64_t, int64_t,
                           hipStream_t);
 int launch_swiglu_backward(const void*, const void*, const void*, int, void*, void*, int64_t, hipStream_t);
-int launch_row_scale(const float*, float*, float*, int64_t, float, float, hipStream_t);
+int launch_row_scale(const void*, int, void*, void*, int64_t, float, float, hipStream_t);
 size_t swiglu_backward_sums_workspace(int64_t, int64_t);
 int launch_swiglu_backward_sums(const void*, const void*, const void*, int, void*, void*, const float*, const float*,
                                 int64_t, int64_t, float*, float*, hipStream_t);
-int launch_row_scale_backward(const float*, const float*, float*, int64_t, float, float, hipStream_t);
+int launch_row_scale_backward(const void*, const void*, int, void*, int64_t, float, float, hipStream_t);
 // fp32 products through bf16 limbs (gemm_mfma.hip): 0 bytes / return 1 when
 // the shape is not for them
 size_t f32_forward_workspace(int64_t, int64_t, int64_t);
@@ -514,20 +514,22 @@ int qste_swiglu_backward(const void* grad, const void* gate, const void* up, int
   return launch_swiglu_backward(grad, gate, up, dtype, grad_gate, grad_up, count, as_stream(stream));
 }
 
-int qste_row_scale(const float* log_scale, float* scale, float* exp_value, int64_t n, float lo, float hi,
+int qste_row_scale(const void* log_scale, int dtype, void* scale, void* exp_value, int64_t n, float lo, float hi,
                    void* stream) {
+  if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
   if (n < 0) return QSTE_E_SHAPE;
   if (n == 0) return 0;
   if (!log_scale || !scale || !exp_value) return QSTE_E_NULL;
-  return launch_row_scale(log_scale, scale, exp_value, n, lo, hi, as_stream(stream));
+  return launch_row_scale(log_scale, dtype, scale, exp_value, n, lo, hi, as_stream(stream));
 }
 
-int qste_row_scale_backward(const float* exp_value, const float* grad, float* grad_log_scale, int64_t n, float lo,
-                            float hi, void* stream) {
+int qste_row_scale_backward(const void* exp_value, const void* grad, int dtype, void* grad_log_scale, int64_t n,
+                            float lo, float hi, void* stream) {
+  if (!dtype_ok(dtype)) return QSTE_E_DTYPE;
   if (n < 0) return QSTE_E_SHAPE;
   if (n == 0) return 0;
   if (!exp_value || !grad || !grad_log_scale) return QSTE_E_NULL;
-  return launch_row_scale_backward(exp_value, grad, grad_log_scale, n, lo, hi, as_stream(stream));
+  return launch_row_scale_backward(exp_value, grad, dtype, grad_log_scale, n, lo, hi, as_stream(stream));
 }
 
 size_t qste_coordinate_update_static_limit(void) { return coordinate_update_static_limit(); }

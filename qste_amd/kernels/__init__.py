@@ -707,30 +707,30 @@ def swiglu_backward_sums(grad: Tensor, gate: Tensor, up: Tensor, offset_gate: Te
 
 
 def row_scale(log_scale: Tensor, lo: float, hi: float) -> tuple[Tensor, Tensor]:
-    """``(clamp(exp(log_scale), lo, hi), exp(log_scale))`` fp32, one launch
-    (surface.py:84-85), rounded as torch's ``exp().clamp()``."""
+    """``(clamp(exp(log_scale), lo, hi), exp(log_scale))`` in log_scale's
+    dtype (fp32, fp16 or bf16), one launch (surface.py:84-85), rounded as
+    torch's ``exp().clamp()`` on that dtype."""
 
     device = _require_gpu(log_scale)
-    if log_scale.dtype != torch.float32:
-        raise ValueError("row_scale takes fp32 log-scales")
     ls = log_scale.detach().contiguous()
     scale, e = torch.empty_like(ls), torch.empty_like(ls)
-    code = _lib.load().qste_row_scale(_ptr(ls), _ptr(scale), _ptr(e), ls.numel(), float(lo), float(hi),
-                                      _stream(device))
+    code = _lib.load().qste_row_scale(_ptr(ls), _dtype_code(ls), _ptr(scale), _ptr(e), ls.numel(), float(lo),
+                                      float(hi), _stream(device))
     _lib.check(code, "row_scale")
     return scale, e
 
 
 def row_scale_backward(exp_value: Tensor, grad: Tensor, lo: float, hi: float) -> Tensor:
-    """Gradient of ``row_scale`` at log_scale: ``(lo <= e <= hi ? grad : 0) * e``."""
+    """Gradient of ``row_scale`` at log_scale: ``(lo <= e <= hi ? grad : 0) * e``,
+    in e's dtype (grad is taken in that dtype)."""
 
     device = _require_gpu(exp_value, grad)
-    if exp_value.dtype != torch.float32 or grad.dtype != torch.float32 or grad.shape != exp_value.shape:
-        raise ValueError("row_scale_backward takes fp32 operands of one shape")
-    e, g = exp_value.contiguous(), grad.contiguous()
+    if grad.shape != exp_value.shape:
+        raise ValueError("row_scale_backward takes operands of one shape")
+    e, g = exp_value.contiguous(), grad.to(exp_value.dtype).contiguous()
     out = torch.empty_like(e)
-    code = _lib.load().qste_row_scale_backward(_ptr(e), _ptr(g), _ptr(out), e.numel(), float(lo), float(hi),
-                                               _stream(device))
+    code = _lib.load().qste_row_scale_backward(_ptr(e), _ptr(g), _dtype_code(e), _ptr(out), e.numel(), float(lo),
+                                               float(hi), _stream(device))
     _lib.check(code, "row_scale_backward")
     return out
 

@@ -73,14 +73,17 @@ class RowScaleFn(Function):
     @staticmethod
     def backward(ctx, grad):
         (e,) = ctx.saved_tensors
-        return kernels.row_scale_backward(e, grad.float(), *ctx.bounds), None, None
+        return kernels.row_scale_backward(e, grad, *ctx.bounds), None, None
+
+
+_ROW_SCALE_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
 
 
 def row_scale(log_scale: Tensor, lo: float, hi: float) -> Tensor:
-    """The learned row scale of surface.py:84-85; fp32 GPU log-scales take the
-    fused kernels, anything else torch's operators."""
+    """The learned row scale of surface.py:84-85; GPU log-scales (fp32, fp16,
+    bf16) take the fused kernels, anything else torch's operators."""
 
-    if log_scale.device.type == "cuda" and log_scale.dtype == torch.float32:
+    if log_scale.device.type == "cuda" and log_scale.dtype in _ROW_SCALE_DTYPES:
         return RowScaleFn.apply(log_scale, float(lo), float(hi))
     return log_scale.exp().clamp(lo, hi)
 

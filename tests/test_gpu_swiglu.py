@@ -275,3 +275,32 @@ def test_row_scale_equals_torch():
         assert torch.equal(torch.isnan(x), torch.isnan(y))
         keep = ~torch.isnan(y)
         assert torch.equal(x[keep].view(torch.int32), y[keep].view(torch.int32))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bounds", [(1e-6, 4.0), (1e-5, 10.0), (0.003, 0.3)])
+def test_row_scale_16bit_every_value(dtype, bounds):
+    """A bf16 / fp16 log-scale (a model moved to that dtype): every one of the
+    65536 values of the dtype, with random gradients (and infinite ones),
+    bit for bit against torch's exp().clamp() and its autograd on a tensor
+    of that dtype, for bounds that are and are not representable in it."""
+
+    from qste_amd.surface import row_scale
+
+    lo, hi = bounds
+    ls = torch.arange(-32768, 32768, dtype=torch.int32, device=DEV).to(torch.int16).view(dtype)
+    g = torch.Generator(device=DEV).manual_seed(11)
+    grad = torch.randn(ls.numel(), device=DEV, generator=g).to(dtype)
+    grad[::4096] = float("inf")
+    a = ls.clone().requires_grad_(True)
+    ref = a.exp().clamp(lo, hi)
+    ref.backward(grad)
+    b = ls.clone().requires_grad_(True)
+    got = row_scale(b, lo, hi)
+    got.backward(grad)
+    torch.cuda.synchronize()
+    assert got.dtype == dtype and b.grad.dtype == dtype
+    for x, y in ((got.detach(), ref.detach()), (b.grad, a.grad)):
+        assert torch.equal(torch.isnan(x), torch.isnan(y))
+        keep = ~torch.isnan(y)
+        assert torch.equal(x[keep].view(torch.int16), y[keep].view(torch.int16)), int((x != y)[keep].sum())
