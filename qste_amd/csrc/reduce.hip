@@ -28,13 +28,22 @@ __global__ __launch_bounds__(kRowThreads) void row_inner_kernel(const float* __r
 }
 
 // Sum of `parts` partial vectors [parts][n] into out[n], in order of p (the
-// loads are issued eight at a time; the additions stay sequential).
+// loads are issued 32 at a time, so a few rounds of memory latency cover
+// the usual 16-64 parts; the additions stay sequential).
 __global__ void sum_partials_kernel(const float* __restrict__ partial, int64_t parts, int64_t n,
                                     float* __restrict__ out) {
+  constexpr int kBatch = 32;
   const int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
   if (i >= n) return;
   float s = 0.0f;
   int64_t p = 0;
+  for (; p + kBatch <= parts; p += kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) v[u] = partial[(p + u) * n + i];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) s += v[u];
+  }
   for (; p + 8 <= parts; p += 8) {
     float v[8];
 #pragma unroll
@@ -168,7 +177,8 @@ int launch_row_inner(const float* mat, const uint8_t* packed, float* out, int64_
 int launch_sum_partials(const float* partial, int64_t parts, int64_t n, float* out,
                         hipStream_t stream) {
   if (n == 0) return 0;
-  sum_partials_kernel<<<ceil_div(n, 256), 256, 0, stream>>>(partial, parts, n, out);
+  // one wave per workgroup: a few thousand outputs still spread over most CUs
+  sum_partials_kernel<<<ceil_div(n, kWave), kWave, 0, stream>>>(partial, parts, n, out);
   return static_cast<int>(hipGetLastError());
 }
 
