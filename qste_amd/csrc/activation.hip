@@ -36,8 +36,20 @@ constexpr int kThreads = 256;
 template <int DT>
 struct Chunk;
 
+// fetch / unpack split a whole chunk's load from its conversion, so a
+// caller can issue several loads before the first conversion waits on one.
 template <>
 struct Chunk<QSTE_F32> {
+  struct Raw {
+    float4 a, b;
+  };
+  __device__ __forceinline__ static Raw fetch(const float* p) {
+    return {reinterpret_cast<const float4*>(p)[0], reinterpret_cast<const float4*>(p)[1]};
+  }
+  __device__ __forceinline__ static void unpack(const Raw& r, float v[8]) {
+    v[0] = r.a.x; v[1] = r.a.y; v[2] = r.a.z; v[3] = r.a.w;
+    v[4] = r.b.x; v[5] = r.b.y; v[6] = r.b.z; v[7] = r.b.w;
+  }
   __device__ __forceinline__ static void load(const float* p, int n, bool vec, float v[8]) {
     if (vec && n == 8) {
       const float4 a = reinterpret_cast<const float4*>(p)[0];
@@ -64,6 +76,18 @@ struct Chunk<QSTE_F32> {
 template <int DT>
 struct Chunk16 {
   using E = Elem<DT>;
+  using Raw = uint4;
+  __device__ __forceinline__ static Raw fetch(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ static void unpack(const Raw& q, float v[8]) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint16_t lo = static_cast<uint16_t>(w[j] & 0xFFFFu);
+      const uint16_t hi = static_cast<uint16_t>(w[j] >> 16);
+      v[2 * j] = E::load(&lo, 0);
+      v[2 * j + 1] = E::load(&hi, 0);
+    }
+  }
   __device__ __forceinline__ static void load(const uint16_t* p, int n, bool vec, float v[8]) {
     if (vec && n == 8) {
       const uint4 q = *reinterpret_cast<const uint4*>(p);
@@ -420,24 +444,77 @@ __device__ __forceinline__ float derivative_any(int kind, float x, float y, floa
 }
 
 // Maximum over a row's G threads (G = 64: within the wave; otherwise G is the
-// whole workgroup).
+// whole workgroup) of |d| as bit patterns: for non-negative floats the bit
+// order is the numeric order and every NaN lies above +inf, so the maximum
+// keeps a NaN as the reference's amax does.
 template <int G>
-__device__ __forceinline__ float group_max(float v, float* red) {
-  v = wave_max(v);
+__device__ __forceinline__ uint32_t group_max_bits(uint32_t v, float* red) {
+#pragma unroll
+  for (int offset = kWave / 2; offset > 0; offset >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(v, offset, kWave)));
   if (G == kWave) return v;
+  uint32_t* r = reinterpret_cast<uint32_t*>(red);
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   __syncthreads();
-  if (lane == 0) red[wave] = v;
+  if (lane == 0) r[wave] = v;
   __syncthreads();
-  float m = red[0];
+  uint32_t m = r[0];
 #pragma unroll
-  for (int w = 1; w < G / kWave; ++w) m = fmaxf(m, red[w]);
+  for (int w = 1; w < G / kWave; ++w) m = max(m, r[w]);
   return m;
 }
 
-// fmaxf drops a NaN; the reference's amax keeps it.
-__device__ __forceinline__ float nan_max(float m, float v) { return (v != v || m != m) ? __builtin_nanf("") : fmaxf(m, v); }
+__device__ __forceinline__ uint32_t abs_bits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
+
+// v_cvt_i32_f32: NaN converts to 0 and values beyond the int32 range saturate
+// (the quantizer's NaN -> 0 rule in one instruction).
+__device__ __forceinline__ int32_t cvt_i32_nan0(float v) {
+  int32_t r;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
+
+// bf16 SiLU table entry: .x the derivative's bits, .y the value's bf16 bits.
+using SmoothEntry = uint2;
+
+// The entry of any bf16 input (the table holds those of tab16_index's range).
+template <int KIND>
+__device__ __forceinline__ SmoothEntry smooth_entry(uint32_t h, float a) {
+  float v, d;
+  value_and_derivative<KIND, QSTE_BF16>(__uint_as_float(h << 16), a, v, d);
+  return make_uint2(__float_as_uint(d), f32_to_bf16(v));
+}
+
+// One whole bf16 chunk through the table: derivatives into d, the values'
+// bf16 bits packed two to a word into ybits.  Every lane looks up all eight
+// entries (inputs outside the tabulated range read entry 0) before the first
+// use, and only lanes holding such an input recompute those elements.
+template <int KIND>
+__device__ __forceinline__ void table_chunk(const uint4& raw, const SmoothEntry* tab, float a, float d[8],
+                                            uint32_t ybits[4]) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  uint32_t idx[8], miss = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t h = (j & 1) ? (w[j / 2] >> 16) : (w[j / 2] & 0xFFFFu);
+    uint32_t i;
+    const bool in = tab16_index(h, i);
+    idx[j] = in ? i : 0u;
+    miss |= (in ? 0u : 1u) << j;
+  }
+  SmoothEntry e[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) e[j] = tab[idx[j]];
+  if (miss) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (miss & (1u << j)) e[j] = smooth_entry<KIND>((j & 1) ? (w[j / 2] >> 16) : (w[j / 2] & 0xFFFFu), a);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) d[j] = __uint_as_float(e[j].x);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ybits[j] = e[2 * j].y | (e[2 * j + 1].y << 16);
+}
 
 // One row per group of G threads: G = 64 is a wave (BLOCK / 64 rows per
 // workgroup), G = BLOCK a whole workgroup.  Thread t owns the 8-element
@@ -450,21 +527,41 @@ __device__ __forceinline__ float nan_max(float m, float v) { return (v != v || m
 // mode: 0 -- compute y = f(x), store it (when y != NULL), derive from it
 //       1 -- y holds the forward output already (computed elsewhere); read it
 //       2 -- `provided` holds the fp32 derivative (x, y unused)
+// tab (bf16 SiLU in mode 0 with whole chunks, may be NULL): value and
+// derivative of the tabulated bf16 inputs (tab16_index), filled by the caller.
 template <int DT, int G, int CH, int KIND, int BLOCK>
 __device__ __forceinline__ void smooth_row(const typename Elem<DT>::T* __restrict__ x,
                                            typename Elem<DT>::T* __restrict__ y,
-                                           const float* __restrict__ provided, int mode, int kind, float a,
+                                           const float* __restrict__ provided, int run_mode, int kind, float a,
                                            void* __restrict__ payload, float* __restrict__ scale,
-                                           int64_t rows, int64_t cols, float* red) {
+                                           int64_t rows, int64_t cols, float* red, int64_t block,
+                                           const SmoothEntry* tab = nullptr) {
   using E = Elem<DT>;
   const bool kUsq = (KIND == kDynamic ? kind : KIND) == QSTE_ACT_RELU_SQUARE;
+  // the specialised kinds run in one mode only (smooth_dispatch)
+  const int mode = KIND == QSTE_ACT_SILU || KIND == QSTE_ACT_GELU
+                       ? 0
+                       : (KIND == QSTE_ACT_GELU_TANH || KIND == QSTE_ACT_HARDSWISH ? 1 : run_mode);
   constexpr int kRowsPerBlock = BLOCK / G;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + threadIdx.x / G;
+  const int64_t row = block * kRowsPerBlock + threadIdx.x / G;
   const int t = threadIdx.x % G;
   const bool live = row < rows;
   const int64_t nch = (cols + 7) / 8;
   const bool whole = (cols & 7) == 0;
   const int64_t base = (live ? row : 0) * cols;
+
+  // mode 0: v holds the input chunk q on entry and its derivatives on exit
+  auto from_input = [&](int64_t q, float v[8], bool write_y) __attribute__((always_inline)) {
+    const int n = static_cast<int>(cols - q * 8 < 8 ? cols - q * 8 : 8);
+    float yv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float d;
+      value_and_derivative_any<KIND, DT>(kind, v[j], a, yv[j], d);
+      v[j] = j < n ? d : 0.0f;
+    }
+    if (write_y && y != nullptr) Chunk<DT>::store(y + base + q * 8, n, whole, yv);
+  };
 
   auto derive = [&](int64_t q, float d[8], bool write_y) __attribute__((always_inline)) {
     const int n = static_cast<int>(cols - q * 8 < 8 ? cols - q * 8 : 8);
@@ -476,46 +573,44 @@ __device__ __forceinline__ void smooth_row(const typename Elem<DT>::T* __restric
     }
     float xv[8], yv[8];
     Chunk<DT>::load(x + base + q * 8, n, whole, xv);
-    if (mode == 1) {
-      const bool reads_y = KIND == kDynamic ? derivative_reads_y(kind) : derivative_reads_y(KIND);
-      if (reads_y) {
-        Chunk<DT>::load(y + base + q * 8, n, whole, yv);
-      } else {
+    if (mode == 0) {
+      from_input(q, xv, write_y);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) yv[j] = 0.0f;
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float v = derivative_any<KIND, DT>(kind, xv[j], yv[j], a);
-        d[j] = j < n ? v : 0.0f;
-      }
+      for (int j = 0; j < 8; ++j) d[j] = xv[j];
+      return;
+    }
+    const bool reads_y = KIND == kDynamic ? derivative_reads_y(kind) : derivative_reads_y(KIND);
+    if (reads_y) {
+      Chunk<DT>::load(y + base + q * 8, n, whole, yv);
     } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        value_and_derivative_any<KIND, DT>(kind, xv[j], a, yv[j], d[j]);
-        d[j] = j < n ? d[j] : 0.0f;
-      }
-      if (write_y && y != nullptr) Chunk<DT>::store(y + base + q * 8, n, whole, yv);
+      for (int j = 0; j < 8; ++j) yv[j] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = derivative_any<KIND, DT>(kind, xv[j], yv[j], a);
+      d[j] = j < n ? v : 0.0f;
     }
   };
 
   // d / s through r = RN(1 / s): the row scale lies in [1e-8 / 255, amax / 127]
-  // and |d / s| <= 255, so no step leaves the normal range (a NaN or infinite
-  // scale gives a NaN quotient, stored as 0, as the division would)
+  // and |d / s| <= 255, so no step leaves the normal range.  A NaN or
+  // infinite scale, or an infinite d, gives a NaN or zero quotient here where
+  // the division gives NaN or zero, and both store 0.
   auto quantize = [&](int64_t q, const float d[8], float s, float r) __attribute__((always_inline)) {
     const int n = static_cast<int>(cols - q * 8 < 8 ? cols - q * 8 : 8);
     uint32_t lo = 0, hi = 0;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
+      const float q0 = d[j] * r;
+      const float quot = fmaf(fmaf(-q0, s, d[j]), r, q0);
       uint32_t byte;
       if (kUsq) {
-        float v = rintf(E::round(div_by(d[j], s, r)));
-        v = v != v ? 0.0f : fminf(fmaxf(v, 0.0f), 255.0f);
-        byte = static_cast<uint32_t>(v);
+        const int32_t v = cvt_i32_nan0(rintf(E::round(quot)));
+        byte = static_cast<uint32_t>(min(max(v, 0), 255));
       } else {
-        float v = rintf(div_by(d[j], s, r));
-        v = v != v ? 0.0f : fminf(fmaxf(v, -127.0f), 127.0f);
-        byte = static_cast<uint32_t>(static_cast<int32_t>(v)) & 0xFFu;
+        const int32_t v = cvt_i32_nan0(rintf(quot));
+        byte = static_cast<uint32_t>(min(max(v, -127), 127)) & 0xFFu;
       }
       if (j < 4) lo |= byte << (8 * j);
       else hi |= byte << (8 * (j - 4));
@@ -529,15 +624,49 @@ __device__ __forceinline__ void smooth_row(const typename Elem<DT>::T* __restric
   };
 
   float cache[CH > 0 ? CH : 1][8];
-  float amax = 0.0f;
+  uint32_t amax = 0;
   if constexpr (CH > 0) {
+    if (mode == 0 && whole && nch > 0) {
+      // every chunk's load is issued before the first conversion, branch-free
+      // (chunks past the row, and dead rows, read chunk 0 of their row or of
+      // row 0 and are not used)
+      typename Chunk<DT>::Raw raw[CH];
 #pragma unroll
-    for (int k = 0; k < CH; ++k) {
-      const int64_t q = t + static_cast<int64_t>(k) * G;
-      if (live && q < nch) {
-        derive(q, cache[k], true);
+      for (int k = 0; k < CH; ++k) {
+        const int64_t q = t + static_cast<int64_t>(k) * G;
+        raw[k] = Chunk<DT>::fetch(x + base + (q < nch ? q : 0) * 8);
+      }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) amax = nan_max(amax, fabsf(cache[k][j]));
+      for (int k = 0; k < CH; ++k) {
+        const int64_t q = t + static_cast<int64_t>(k) * G;
+        if (live && q < nch) {
+          bool done = false;
+          if constexpr (KIND == QSTE_ACT_SILU && DT == QSTE_BF16) {
+            if (tab != nullptr) {
+              uint32_t ybits[4];
+              table_chunk<KIND>(raw[k], tab, a, cache[k], ybits);
+              if (y != nullptr)
+                *reinterpret_cast<uint4*>(y + base + q * 8) = make_uint4(ybits[0], ybits[1], ybits[2], ybits[3]);
+              done = true;
+            }
+          }
+          if (!done) {
+            Chunk<DT>::unpack(raw[k], cache[k]);
+            from_input(q, cache[k], true);
+          }
+#pragma unroll
+          for (int j = 0; j < 8; ++j) amax = max(amax, abs_bits(cache[k][j]));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < CH; ++k) {
+        const int64_t q = t + static_cast<int64_t>(k) * G;
+        if (live && q < nch) {
+          derive(q, cache[k], true);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) amax = max(amax, abs_bits(cache[k][j]));
+        }
       }
     }
   } else if (live) {
@@ -545,24 +674,23 @@ __device__ __forceinline__ void smooth_row(const typename Elem<DT>::T* __restric
       float d[8];
       derive(q, d, true);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) amax = nan_max(amax, fabsf(d[j]));
+      for (int j = 0; j < 8; ++j) amax = max(amax, abs_bits(d[j]));
     }
   }
-  // the reference's amax keeps a NaN: carry it through the reduction as the
-  // largest key, then tell NaN from an infinite derivative
-  float key = amax != amax ? __builtin_inff() : amax;
-  key = group_max<G>(key, red);
-  float nan_flag = (amax != amax) ? 1.0f : 0.0f;
-  if (key == __builtin_inff()) nan_flag = group_max<G>(nan_flag, red);
+  amax = group_max_bits<G>(amax, red);
   if (!live) return;
   float s;
-  if (kUsq) {
-    // relu(x)^2: maximum, clamp and division in the dtype (nn.py:316-318)
-    s = E::round(E::round(fmaxf(key, 1e-8f)) / 255.0f);
+  if (amax > 0x7F800000u) {
+    s = __builtin_nanf("");
   } else {
-    s = fmaxf(key, 1e-8f) / 127.0f;
+    const float key = __uint_as_float(amax);
+    if (kUsq) {
+      // relu(x)^2: maximum, clamp and division in the dtype (nn.py:316-318)
+      s = E::round(E::round(fmaxf(key, 1e-8f)) / 255.0f);
+    } else {
+      s = fmaxf(key, 1e-8f) / 127.0f;
+    }
   }
-  if (nan_flag > 0.0f) s = __builtin_nanf("");
   const float r = 1.0f / s;
   if constexpr (CH > 0) {
 #pragma unroll
@@ -580,13 +708,32 @@ __device__ __forceinline__ void smooth_row(const typename Elem<DT>::T* __restric
   if (t == 0) scale[row] = s;
 }
 
+// bf16 SiLU takes its value and derivative from an LDS table (4096 entries of
+// 8 bytes, tab16_index's range) that each workgroup fills once and then walks
+// row blocks, so the exponential and divisions are paid per table entry, not
+// per element.
+template <int DT, int KIND>
+constexpr bool kSmoothTable = KIND == QSTE_ACT_SILU && DT == QSTE_BF16;
+
 template <int DT, int G, int CH, int KIND, int BLOCK>
 __global__ __launch_bounds__(BLOCK) void smooth_rows_kernel(
     const typename Elem<DT>::T* __restrict__ x, typename Elem<DT>::T* __restrict__ y,
     const float* __restrict__ provided, int mode, SmoothParams p, void* __restrict__ payload,
-    float* __restrict__ scale, int64_t rows, int64_t cols) {
+    float* __restrict__ scale, int64_t rows, int64_t cols, int64_t blocks) {
   __shared__ float red[BLOCK / kWave];
-  smooth_row<DT, G, CH, KIND, BLOCK>(x, y, provided, mode, p.kind, p.a, payload, scale, rows, cols, red);
+  if constexpr (kSmoothTable<DT, KIND>) {
+    __shared__ SmoothEntry tab[kTab16Entries];
+    for (int j = threadIdx.x; j < kTab16Entries; j += BLOCK)
+      tab[j] = smooth_entry<KIND>(tab16_bits(static_cast<uint32_t>(j)), p.a);
+    __syncthreads();
+    // every thread walks the same blocks, so the reductions' barriers match
+    for (int64_t b = blockIdx.x; b < blocks; b += gridDim.x)
+      smooth_row<DT, G, CH, KIND, BLOCK>(x, y, provided, mode, p.kind, p.a, payload, scale, rows, cols, red, b,
+                                         mode == 0 ? tab : nullptr);
+  } else {
+    smooth_row<DT, G, CH, KIND, BLOCK>(x, y, provided, mode, p.kind, p.a, payload, scale, rows, cols, red,
+                                       blockIdx.x);
+  }
 }
 
 // grad * (payload * scale), each product rounded to the dtype
@@ -666,8 +813,11 @@ int smooth_launch(const void* x, void* y, const float* provided, int mode, Smoot
   using T = typename Elem<DT>::T;
   constexpr int kRows = BLOCK / G;
   const int64_t blocks = (rows + kRows - 1) / kRows;
-  smooth_rows_kernel<DT, G, CH, KIND, BLOCK><<<static_cast<unsigned>(blocks), BLOCK, 0, s>>>(
-      static_cast<const T*>(x), static_cast<T*>(y), provided, mode, p, payload, scale, rows, cols);
+  // the tabulated kind: a few workgroups per CU, each filling its table once
+  const int64_t grid = kSmoothTable<DT, KIND> ? (blocks < 8192 / (BLOCK / kWave) ? blocks : 8192 / (BLOCK / kWave))
+                                              : blocks;
+  smooth_rows_kernel<DT, G, CH, KIND, BLOCK><<<static_cast<unsigned>(grid), BLOCK, 0, s>>>(
+      static_cast<const T*>(x), static_cast<T*>(y), provided, mode, p, payload, scale, rows, cols, blocks);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -780,7 +930,7 @@ int qste_smooth_activation(const void* x, int dtype, int kind, float param, void
   if (kind < QSTE_ACT_GELU || kind > QSTE_ACT_PROVIDED) return QSTE_E_SHAPE;
   if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
   if (rows == 0) return 0;
-  if (!payload || !scale) return QSTE_E_NULL;
+  if (!scale || (!payload && cols > 0)) return QSTE_E_NULL;
   int mode = 0;
   if (kind == QSTE_ACT_PROVIDED) {
     if (!derivative && cols > 0) return QSTE_E_NULL;

@@ -90,6 +90,32 @@ struct Elem<QSTE_BF16> {
 };
 
 // ---------------------------------------------------------------------------
+// Lookup tables over bf16 inputs.  A function of one bf16 value can be
+// tabulated: entry j (0 .. kTab16Entries - 1) holds it for the bf16 value
+// with bits tab16_bits(j), the values whose magnitude lies in [2^-12, 2^4)
+// (both signs; nearly every activation or gate a layer produces).  A
+// workgroup fills its table with the same code it would run per element,
+// so a looked-up result is the same bits as the computed one.
+// ---------------------------------------------------------------------------
+
+constexpr uint32_t kTab16ExpLo = 127 - 12;        // biased exponent of 2^-12
+constexpr uint32_t kTab16Half = 16 * 128;         // 16 exponents x 7 mantissa bits, per sign
+constexpr int kTab16Entries = 2 * kTab16Half;
+static_assert(kTab16Half == 1u << 11, "sign bit -> table half");
+
+__device__ __forceinline__ uint32_t tab16_bits(uint32_t j) {
+  return ((j & kTab16Half) << 4) | ((kTab16ExpLo << 7) + (j & (kTab16Half - 1)));
+}
+
+// The entry of bf16 bits `bits`, or false outside the tabulated range
+// (zeros, subnormals, tiny or huge magnitudes, infinities, NaN).
+__device__ __forceinline__ bool tab16_index(uint32_t bits, uint32_t& idx) {
+  const uint32_t off = (bits & 0x7FFFu) - (kTab16ExpLo << 7);  // wraps above the range when below it
+  idx = off | ((bits >> 15) << 11);
+  return off < kTab16Half;
+}
+
+// ---------------------------------------------------------------------------
 // Packed signs: bit j of byte b is column 8b + j; set means +1.
 // ---------------------------------------------------------------------------
 
@@ -174,11 +200,14 @@ __device__ __forceinline__ T block_sum(T v, T* scratch) {
 // x - q0 d is exact under FMA and RN(q0 + r (x - q0 d)) is the correctly
 // rounded quotient (Markstein's correction step).  Three operations instead
 // of a full IEEE division per element.  Valid while no step overflows or
-// underflows (callers keep d and x in the normal range).
+// underflows (callers keep d and x in the normal range).  An infinite x or
+// d, or a zero d, makes the residual NaN (inf - inf, 0 * inf) while q0 is
+// already the IEEE quotient (+-inf, +-0, or NaN for inf / inf and 0 / 0), so
+// q0 is returned then.
 __device__ __forceinline__ float div_by(float x, float d, float r) {
   const float q0 = x * r;
   const float e = fmaf(-q0, d, x);
-  return fmaf(e, r, q0);
+  return e == e ? fmaf(e, r, q0) : q0;
 }
 
 inline int ceil_div(int64_t a, int64_t b) { return static_cast<int>((a + b - 1) / b); }

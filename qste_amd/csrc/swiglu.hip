@@ -186,28 +186,14 @@ constexpr int kSumChunk = 256;
 constexpr int kSumWaves = 4;
 constexpr int kSumThreads = kSumWaves * 64;
 
-// bf16 gates with magnitude in [2^-12, 2^4) -- nearly every gate a layer
-// produces -- take sigmoid(g) and the rounded silu(g) from LDS tables that
-// the workgroup fills first with the arithmetic above (one entry per bf16
-// value in that range), so the exponential and the two correctly rounded
-// divisions are paid once per table entry, not once per element.  Other
-// gates (tiny, huge, zero, inf, NaN) compute them.  A table entry is the
-// value the computation gives for that input, so the results are the same
-// bits either way.
-constexpr uint32_t kTabExpLo = 127 - 12;  // biased exponent of 2^-12
-constexpr int kTabExps = 16;
-constexpr uint32_t kTabHalf = kTabExps * 128;  // entries per sign (7 mantissa bits)
-constexpr int kTabEntries = 2 * kTabHalf;
-static_assert(kTabHalf == 1u << 11, "sign bit -> table half");
-
-// bf16 bits of table entry j
-__device__ __forceinline__ uint32_t tab_bits(uint32_t j) {
-  return ((j & kTabHalf) << 4) | ((kTabExpLo << 7) + (j & (kTabHalf - 1)));
-}
-
+// bf16 gates in the tabulated range (tab16_index) take sigmoid(g) and the
+// rounded silu(g) from LDS tables that the workgroup fills first with the
+// arithmetic above, so the exponential and the two correctly rounded
+// divisions are paid once per table entry, not once per element; other
+// gates compute them.
 __device__ __forceinline__ void fill_silu_table(float* tab_s, uint16_t* tab_a, int tid, int threads) {
-  for (int j = tid; j < kTabEntries; j += threads) {
-    const float x = __uint_as_float(tab_bits(static_cast<uint32_t>(j)) << 16);
+  for (int j = tid; j < kTab16Entries; j += threads) {
+    const float x = __uint_as_float(tab16_bits(static_cast<uint32_t>(j)) << 16);
     tab_a[j] = f32_to_bf16(silu_value(x));
     tab_s[j] = 1.0f / (1.0f + expf(-x));
   }
@@ -239,10 +225,8 @@ __device__ __forceinline__ void backward_x8(const uint4& hc, const uint4& gc, co
   for (int i = 0; i < 8; ++i) {
     float a, b;
     if constexpr (DT == QSTE_BF16) {
-      const uint32_t bits = g[i];
-      const uint32_t off = (bits & 0x7FFFu) - (kTabExpLo << 7);  // wraps above the range when below it
-      if (off < kTabHalf) {
-        const uint32_t idx = off | ((bits >> 15) << 11);
+      uint32_t idx;
+      if (tab16_index(g[i], idx)) {
         backward_given<DT>(E::load(h, i), E::load(g, i), E::load(u, i), bf16_to_f32(tab_a[idx]), tab_s[idx], a,
                            b);
       } else {
@@ -266,12 +250,12 @@ __global__ __launch_bounds__(kSumThreads) void backward_sums_kernel(
   constexpr int UNROLL = 4;
   constexpr int kPad = 17;
   constexpr int kRed = kSumWaves * 64 * kPad;
-  constexpr int kTab = DT == QSTE_BF16 ? kTabEntries + kTabEntries / 2 : 0;  // floats: s, then a as bf16
+  constexpr int kTab = DT == QSTE_BF16 ? kTab16Entries + kTab16Entries / 2 : 0;  // floats: s, then a as bf16
   // the tables while the samples are summed, then the waves' partial sums
   __shared__ float lds[kRed > kTab ? kRed : kTab];
   float* red = lds;
   float* tab_s = lds;
-  uint16_t* tab_a = reinterpret_cast<uint16_t*>(lds + kTabEntries);
+  uint16_t* tab_a = reinterpret_cast<uint16_t*>(lds + kTab16Entries);
   if constexpr (DT == QSTE_BF16) {
     fill_silu_table(tab_s, tab_a, threadIdx.x, kSumThreads);
     __syncthreads();

@@ -204,6 +204,47 @@ def test_relu_square_and_provided_derivative(K, dtype):
     assert np.array_equal(p.cpu().numpy(), rp) and np.array_equal(s.cpu().numpy(), rs)
 
 
+def test_silu_every_bf16_input(K):
+    """bf16 SiLU on every bit pattern, one element per row so the row scale is
+    |d| / 127 and shows the derivative exactly: the value equals torch's, the
+    payload and scale equal those derived from torch's value (the kernel's
+    per-element formula), and the derivative is within a few fp32 ulps (1e-6
+    absolute where 1 + x * (1 - sigmoid(x)) cancels) of
+    sigmoid(x) * (1 + x * (1 - sigmoid(x))) computed by torch in fp32."""
+
+    bits = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16)
+    x = bits.view(torch.bfloat16).reshape(-1, 1).to(DEV)
+    for shape in ((65536, 1), (16, 4096), (8, 8192)):
+        print(f"silu every bf16 {shape}", flush=True)
+        xs = x.reshape(shape)
+        y, payload, scale = K.smooth_activation(xs, "silu")
+        ref = F.silu(xs)
+        assert torch.equal(torch.isnan(y), torch.isnan(ref))
+        assert torch.equal(y[~torch.isnan(y)], ref[~torch.isnan(ref)])
+        _, p1, s1 = K.smooth_activation(xs, "silu", output=ref)
+        assert torch.equal(payload, p1)
+        assert torch.equal(torch.isnan(scale), torch.isnan(s1))
+        assert torch.equal(scale[~torch.isnan(scale)], s1[~torch.isnan(s1)])
+    xf = x.float().reshape(-1)
+    sg = torch.sigmoid(xf)
+    d = sg * (1 + xf * (1 - sg))
+    _, payload, scale = K.smooth_activation(x, "silu")
+    got = scale * payload.reshape(-1).float().sign()
+    ok = torch.isfinite(d) & (d.abs() > 1e-8)
+    assert torch.allclose(got[ok] * 127, d[ok], rtol=2e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_smooth_activation_empty_rows_and_columns(K, dtype):
+    for shape in ((3, 0), (0, 8), (0, 0)):
+        print(f"smooth empty {shape} {dtype}", flush=True)
+        x = torch.zeros(shape, dtype=dtype, device=DEV)
+        y, payload, scale = K.smooth_activation(x, "silu")
+        assert y.shape == shape and payload.shape == shape and scale.shape == (shape[0],)
+        if shape[0]:
+            assert torch.equal(scale, torch.full((shape[0],), 1e-8 / 127, device=DEV))
+
+
 def test_smooth_activation_at_the_mlp_shape(K):
     """cfg4's SiLU input [16384, 14336] bf16, checked through properties."""
 
