@@ -348,7 +348,7 @@ def config_steps(device):
         coords.step()
         adam.zero_grad(set_to_none=True)
 
-    ms = timed_wall(step3, 5)
+    ms = timed_wall(step3, 10, warmup=3)
     tokens = 8 * 1023
     mlp_flop = 6.0 * tokens * 12 * (2 * 3072 * 768)
     out["cfg3_gpt2_small"] = {"ms_per_step": round(ms, 3), "tokens_per_s": round(tokens / ms * 1e3, 1),
