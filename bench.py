@@ -353,7 +353,7 @@ def config_steps(device):
     mlp_flop = 6.0 * tokens * 12 * (2 * 3072 * 768)
     out["cfg3_gpt2_small"] = {"ms_per_step": round(ms, 3), "tokens_per_s": round(tokens / ms * 1e3, 1),
                               "mlp_fwd_bwd_flop": mlp_flop, "batch": 8, "seq": 1024,
-                              "note": "whole training step; MLPs QSTE with packed tanh-GELU, attention float"}
+                              "note": "whole training step; MLPs QSTE with packed tanh-GELU, attention and head bf16 (SDPA flash/efficient)"}
     return out
 
 
