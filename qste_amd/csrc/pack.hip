@@ -194,28 +194,32 @@ __device__ __forceinline__ uint64_t transpose_8x8(uint64_t x) {
   return x;
 }
 
-// A workgroup transposes a 512-row x 512-column tile through LDS: the input
-// rows arrive as 16-byte loads, each thread transposes 16 8 x 8 blocks of
-// one column byte (eight row blocks at a time, so each of its 8 columns
-// gathers 64 rows into one 8-byte LDS word), and every output column leaves
-// as 64 contiguous bytes (eight 8-byte stores by consecutive lanes).
-// out_pitch must be a multiple of 8.
-constexpr int kTrRows = 512, kTrColBytes = 64;  // tile: 512 rows x 512 columns
-constexpr int kTrPad = 4;                       // bytes of padding per staged input row
+// A workgroup transposes an RT-row x 512-column tile (RT = 512 or 128)
+// through LDS: the input rows arrive as 16-byte loads, a thread transposes
+// the 8 x 8 blocks of one column byte over 64-row groups (eight row blocks
+// at a time, so each of its 8 columns gathers 64 rows into one 8-byte LDS
+// word), and every output column leaves as RT / 8 contiguous bytes (8-byte
+// stores by consecutive lanes).  The 128-row tile gives small matrices four
+// times the workgroups.  out_pitch must be a multiple of 8.
+constexpr int kTrColBytes = 64;  // tile columns: 512
+constexpr int kTrPad = 4;        // bytes of padding per staged input row
+template <int RT>
 __global__ __launch_bounds__(256) void transpose_bits_kernel(const uint8_t* __restrict__ in,
                                                              uint8_t* __restrict__ out, int64_t rows,
                                                              int64_t cols, int64_t in_pitch,
                                                              int64_t out_pitch) {
-  __shared__ __attribute__((aligned(16))) uint8_t tile[kTrRows][kTrColBytes + kTrPad];
-  __shared__ uint64_t otile[8 * kTrColBytes][kTrRows / 64];  // [column][64-row group]
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kTrRows;
+  constexpr int kGroups = RT / 64;                     // 64-row groups per tile
+  constexpr int kPerThread = kGroups > 4 ? kGroups / 4 : 1;
+  __shared__ __attribute__((aligned(16))) uint8_t tile[RT][kTrColBytes + kTrPad];
+  __shared__ uint64_t otile[8 * kTrColBytes][kGroups];  // [column][64-row group]
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * RT;
   const int64_t cb0 = static_cast<int64_t>(blockIdx.x) * kTrColBytes;
   const int tid = threadIdx.x;
   const bool vec = (in_pitch & 15) == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0;
-  // 512 rows x 64 bytes: load i of thread t is row (t >> 2) + 64 i, bytes
+  // RT rows x 64 bytes: load i of thread t is row (t >> 2) + 64 i, bytes
   // 16 (t & 3) .. + 15
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kGroups; ++i) {
     const int row = (tid >> 2) + 64 * i, part = tid & 3;
     const int64_t r = r0 + row;
     const int64_t cb = cb0 + 16 * part;
@@ -234,12 +238,12 @@ __global__ __launch_bounds__(256) void transpose_bits_kernel(const uint8_t* __re
     for (int d = 0; d < 4; ++d) *reinterpret_cast<uint32_t*>(&tile[row][16 * part + 4 * d]) = w[d];
   }
   __syncthreads();
-  {
-    // column byte cbl; 64-row groups 2 rg and 2 rg + 1
+  if (kGroups >= 4 || (tid >> 6) < kGroups) {
+    // column byte cbl; 64-row groups kPerThread rg .. + kPerThread - 1
     const int cbl = tid & 63, rg = tid >> 6;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int g = 2 * rg + h;
+    for (int h = 0; h < kPerThread; ++h) {
+      const int g = kPerThread * rg + h;
       uint64_t col[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
@@ -256,11 +260,11 @@ __global__ __launch_bounds__(256) void transpose_bits_kernel(const uint8_t* __re
     }
   }
   __syncthreads();
-  // 512 columns x 64 bytes: store i of thread t is column (t >> 3) + 32 i,
-  // bytes 8 (t & 7) .. + 7 of its 64
+  // 512 columns x RT / 8 bytes: store i of thread t is column
+  // t / kGroups + (256 / kGroups) i, bytes 8 (t % kGroups) .. + 7
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int cl = (tid >> 3) + 32 * i, piece = tid & 7;
+  for (int i = 0; i < 2 * kGroups; ++i) {
+    const int cl = tid / kGroups + (256 / kGroups) * i, piece = tid % kGroups;
     const int64_t c = 8 * cb0 + cl;
     const int64_t ob = r0 / 8 + 8 * piece;
     if (c < cols && ob < out_pitch) *reinterpret_cast<uint64_t*>(out + c * out_pitch + ob) = otile[cl][piece];
@@ -279,9 +283,16 @@ int launch_transpose_bits(const uint8_t* in, uint8_t* out, int64_t rows, int64_t
   if (rows == 0 || cols == 0 || out_pitch == 0) return 0;
   if (out_pitch % 8 != 0 || (reinterpret_cast<uintptr_t>(out) & 7)) return QSTE_E_ALIGN;
   // row tiles cover every output byte (out_pitch * 8 rows, the padding
-  // included, which reads as zero)
-  dim3 grid(ceil_div(in_pitch, kTrColBytes), ceil_div(out_pitch * 8, kTrRows));
-  transpose_bits_kernel<<<grid, 256, 0, stream>>>(in, out, rows, cols, in_pitch, out_pitch);
+  // included, which reads as zero); 128-row tiles where 512-row ones would
+  // leave CUs idle
+  const int col_tiles = ceil_div(in_pitch, kTrColBytes);
+  if (static_cast<int64_t>(col_tiles) * ceil_div(out_pitch * 8, 512) >= 1024) {
+    transpose_bits_kernel<512><<<dim3(col_tiles, ceil_div(out_pitch * 8, 512)), 256, 0, stream>>>(
+        in, out, rows, cols, in_pitch, out_pitch);
+  } else {
+    transpose_bits_kernel<128><<<dim3(col_tiles, ceil_div(out_pitch * 8, 128)), 256, 0, stream>>>(
+        in, out, rows, cols, in_pitch, out_pitch);
+  }
   return static_cast<int>(hipGetLastError());
 }
 
