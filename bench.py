@@ -329,11 +329,12 @@ def config_steps(device):
         model(x).backward(dy)
         coords.step()
 
-    ms = timed_wall(step2, 10)
+    ms = timed_median(step2, 15)
     flop = 6.0 * 8192 * (2 * 4096 * 1024)
     out["cfg2_relu_mlp"] = {"ms_per_step": round(ms, 3), "tflops": round(flop / ms / 1e9, 2),
                             "frac_of_mfma_peak": round(flop / (ms * 1e-3) / MFMA_BF16_PEAK, 4),
-                            "tokens": 8192, "d": 1024, "ffn": 4096}
+                            "tokens": 8192, "d": 1024, "ffn": 4096,
+                            "timing": "median of 15 steps, each host-clocked and synchronized"}
     del model, coords, x, dy
     # config 3: GPT-2 small, batch 8 x 1024 random ids, AdamW + QSTEOptimizer
     model = GPT2Small(device=device)
@@ -348,11 +349,12 @@ def config_steps(device):
         coords.step()
         adam.zero_grad(set_to_none=True)
 
-    ms = timed_wall(step3, 10, warmup=3)
+    ms = timed_median(step3, 10, warmup=3)
     tokens = 8 * 1023
     mlp_flop = 6.0 * tokens * 12 * (2 * 3072 * 768)
     out["cfg3_gpt2_small"] = {"ms_per_step": round(ms, 3), "tokens_per_s": round(tokens / ms * 1e3, 1),
                               "mlp_fwd_bwd_flop": mlp_flop, "batch": 8, "seq": 1024,
+                              "timing": "median of 10 steps, each host-clocked and synchronized",
                               "note": "whole training step; MLPs QSTE with packed tanh-GELU, attention and head bf16 (SDPA flash/efficient)"}
     return out
 
@@ -370,6 +372,28 @@ def timed_wall(fn, iters, warmup=2):
         fn()
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) / iters * 1e3
+
+
+def timed_median(fn, iters, warmup=2):
+    """Median milliseconds of ``fn`` over ``iters`` calls, each timed by the
+    host clock between synchronizations (steps that end in a host read of
+    the flip count synchronize anyway; the median keeps a host stall in one
+    step out of a host-bound config's figure)."""
+
+    import statistics
+
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(iters):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(times)
 
 
 def timed_events(fn, iters, stream=None, warm=3):
