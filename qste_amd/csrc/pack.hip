@@ -194,56 +194,53 @@ __device__ __forceinline__ uint64_t transpose_8x8(uint64_t x) {
   return x;
 }
 
-// A workgroup transposes an RT-row x 512-column tile (RT = 512 or 128)
-// through LDS: the input rows arrive as 16-byte loads, a thread transposes
-// the 8 x 8 blocks of one column byte over 64-row groups (eight row blocks
-// at a time, so each of its 8 columns gathers 64 rows into one 8-byte LDS
-// word), and every output column leaves as RT / 8 contiguous bytes (8-byte
-// stores by consecutive lanes).  The 128-row tile gives small matrices four
-// times the workgroups.  out_pitch must be a multiple of 8.
-constexpr int kTrColBytes = 64;  // tile columns: 512
-constexpr int kTrPad = 4;        // bytes of padding per staged input row
-template <int RT>
+// A workgroup transposes 128-row x 512-column tiles through LDS (walking
+// row tiles by gridDim.y): the input rows arrive as 16-byte loads, a thread
+// transposes the 8 x 8 blocks of one column byte over a 64-row group (eight
+// row blocks at a time, so each of its 8 columns gathers 64 rows into one
+// 8-byte LDS word), and every output column leaves as 16 contiguous bytes
+// (8-byte stores by consecutive lanes).  Tiles of 128 rows give a
+// 3072 x 768 sign matrix 48 workgroups (12 with 512-row tiles: 6.0 instead
+// of 11.8 us).  out_pitch must be a multiple of 8.
+constexpr int kTrRows = 128, kTrColBytes = 64;  // tile: 128 rows x 512 columns
+constexpr int kTrGroups = kTrRows / 64;          // 64-row groups per tile
+constexpr int kTrPad = 4;                        // bytes of padding per staged input row
 __global__ __launch_bounds__(256) void transpose_bits_kernel(const uint8_t* __restrict__ in,
                                                              uint8_t* __restrict__ out, int64_t rows,
                                                              int64_t cols, int64_t in_pitch,
-                                                             int64_t out_pitch) {
-  constexpr int kGroups = RT / 64;                     // 64-row groups per tile
-  constexpr int kPerThread = kGroups > 4 ? kGroups / 4 : 1;
-  __shared__ __attribute__((aligned(16))) uint8_t tile[RT][kTrColBytes + kTrPad];
-  __shared__ uint64_t otile[8 * kTrColBytes][kGroups];  // [column][64-row group]
-  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * RT;
+                                                             int64_t out_pitch, int64_t row_tiles) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[kTrRows][kTrColBytes + kTrPad];
+  __shared__ uint64_t otile[8 * kTrColBytes][kTrGroups];  // [column][64-row group]
   const int64_t cb0 = static_cast<int64_t>(blockIdx.x) * kTrColBytes;
   const int tid = threadIdx.x;
   const bool vec = (in_pitch & 15) == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0;
-  // RT rows x 64 bytes: load i of thread t is row (t >> 2) + 64 i, bytes
-  // 16 (t & 3) .. + 15
+  for (int64_t ty = blockIdx.y; ty < row_tiles; ty += gridDim.y) {
+    const int64_t r0 = ty * kTrRows;
+    // 128 rows x 64 bytes: load i of thread t is row (t >> 2) + 64 i, bytes
+    // 16 (t & 3) .. + 15
 #pragma unroll
-  for (int i = 0; i < kGroups; ++i) {
-    const int row = (tid >> 2) + 64 * i, part = tid & 3;
-    const int64_t r = r0 + row;
-    const int64_t cb = cb0 + 16 * part;
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
-    if (r < rows) {
-      if (vec && cb + 16 <= in_pitch) {
-        const uint4 q = *reinterpret_cast<const uint4*>(in + r * in_pitch + cb);
-        w[0] = q.x, w[1] = q.y, w[2] = q.z, w[3] = q.w;
-      } else {
+    for (int i = 0; i < kTrGroups; ++i) {
+      const int row = (tid >> 2) + 64 * i, part = tid & 3;
+      const int64_t r = r0 + row;
+      const int64_t cb = cb0 + 16 * part;
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+      if (r < rows) {
+        if (vec && cb + 16 <= in_pitch) {
+          const uint4 q = *reinterpret_cast<const uint4*>(in + r * in_pitch + cb);
+          w[0] = q.x, w[1] = q.y, w[2] = q.z, w[3] = q.w;
+        } else {
 #pragma unroll
-        for (int k = 0; k < 16; ++k)
-          if (cb + k < in_pitch) w[k >> 2] |= static_cast<uint32_t>(in[r * in_pitch + cb + k]) << (8 * (k & 3));
+          for (int k = 0; k < 16; ++k)
+            if (cb + k < in_pitch) w[k >> 2] |= static_cast<uint32_t>(in[r * in_pitch + cb + k]) << (8 * (k & 3));
+        }
       }
+#pragma unroll
+      for (int d = 0; d < 4; ++d) *reinterpret_cast<uint32_t*>(&tile[row][16 * part + 4 * d]) = w[d];
     }
-#pragma unroll
-    for (int d = 0; d < 4; ++d) *reinterpret_cast<uint32_t*>(&tile[row][16 * part + 4 * d]) = w[d];
-  }
-  __syncthreads();
-  if (kGroups >= 4 || (tid >> 6) < kGroups) {
-    // column byte cbl; 64-row groups kPerThread rg .. + kPerThread - 1
-    const int cbl = tid & 63, rg = tid >> 6;
-#pragma unroll
-    for (int h = 0; h < kPerThread; ++h) {
-      const int g = kPerThread * rg + h;
+    __syncthreads();
+    if ((tid >> 6) < kTrGroups) {
+      // column byte cbl of 64-row group g
+      const int cbl = tid & 63, g = tid >> 6;
       uint64_t col[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
       for (int b = 0; b < 8; ++b) {
@@ -258,16 +255,17 @@ __global__ __launch_bounds__(256) void transpose_bits_kernel(const uint8_t* __re
 #pragma unroll
       for (int j = 0; j < 8; ++j) otile[8 * cbl + j][g] = col[j];
     }
-  }
-  __syncthreads();
-  // 512 columns x RT / 8 bytes: store i of thread t is column
-  // t / kGroups + (256 / kGroups) i, bytes 8 (t % kGroups) .. + 7
+    __syncthreads();
+    // 512 columns x 16 bytes: store i of thread t is column t / 2 + 128 i,
+    // bytes 8 (t % 2) .. + 7
 #pragma unroll
-  for (int i = 0; i < 2 * kGroups; ++i) {
-    const int cl = tid / kGroups + (256 / kGroups) * i, piece = tid % kGroups;
-    const int64_t c = 8 * cb0 + cl;
-    const int64_t ob = r0 / 8 + 8 * piece;
-    if (c < cols && ob < out_pitch) *reinterpret_cast<uint64_t*>(out + c * out_pitch + ob) = otile[cl][piece];
+    for (int i = 0; i < 2 * kTrGroups; ++i) {
+      const int cl = tid / kTrGroups + (256 / kTrGroups) * i, piece = tid % kTrGroups;
+      const int64_t c = 8 * cb0 + cl;
+      const int64_t ob = r0 / 8 + 8 * piece;
+      if (c < cols && ob < out_pitch) *reinterpret_cast<uint64_t*>(out + c * out_pitch + ob) = otile[cl][piece];
+    }
+    __syncthreads();  // the next row tile reuses tile and otile
   }
 }
 
@@ -283,16 +281,10 @@ int launch_transpose_bits(const uint8_t* in, uint8_t* out, int64_t rows, int64_t
   if (rows == 0 || cols == 0 || out_pitch == 0) return 0;
   if (out_pitch % 8 != 0 || (reinterpret_cast<uintptr_t>(out) & 7)) return QSTE_E_ALIGN;
   // row tiles cover every output byte (out_pitch * 8 rows, the padding
-  // included, which reads as zero); 128-row tiles where 512-row ones would
-  // leave CUs idle
-  const int col_tiles = ceil_div(in_pitch, kTrColBytes);
-  if (static_cast<int64_t>(col_tiles) * ceil_div(out_pitch * 8, 512) >= 1024) {
-    transpose_bits_kernel<512><<<dim3(col_tiles, ceil_div(out_pitch * 8, 512)), 256, 0, stream>>>(
-        in, out, rows, cols, in_pitch, out_pitch);
-  } else {
-    transpose_bits_kernel<128><<<dim3(col_tiles, ceil_div(out_pitch * 8, 128)), 256, 0, stream>>>(
-        in, out, rows, cols, in_pitch, out_pitch);
-  }
+  // included, which reads as zero)
+  const int64_t row_tiles = (out_pitch * 8 + kTrRows - 1) / kTrRows;
+  const dim3 grid(ceil_div(in_pitch, kTrColBytes), static_cast<unsigned>(row_tiles < 65535 ? row_tiles : 65535));
+  transpose_bits_kernel<<<grid, 256, 0, stream>>>(in, out, rows, cols, in_pitch, out_pitch, row_tiles);
   return static_cast<int>(hipGetLastError());
 }
 
