@@ -281,7 +281,8 @@ int launch_transpose_bits(const uint8_t* in, uint8_t* out, int64_t rows, int64_t
   if (rows == 0 || cols == 0 || out_pitch == 0) return 0;
   if (out_pitch % 8 != 0 || (reinterpret_cast<uintptr_t>(out) & 7)) return QSTE_E_ALIGN;
   // row tiles cover every output byte (out_pitch * 8 rows, the padding
-  // included, which reads as zero)
+  // included, which reads as zero); beyond the grid's 65535 rows of
+  // workgroups each walks several tiles
   const int64_t row_tiles = (out_pitch * 8 + kTrRows - 1) / kTrRows;
   const dim3 grid(ceil_div(in_pitch, kTrColBytes), static_cast<unsigned>(row_tiles < 65535 ? row_tiles : 65535));
   transpose_bits_kernel<<<grid, 256, 0, stream>>>(in, out, rows, cols, in_pitch, out_pitch, row_tiles);
