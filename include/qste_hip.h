@@ -212,6 +212,13 @@ size_t qste_coordinate_update_workspace_bytes(int64_t rows, int64_t cols, int64_
  * fp32(coordinate_lr), fallback.py:204-206) and rms(m).  Tests compare them
  * with the specification's.  No counterpart in the reference. */
 size_t qste_coordinate_update_scalars_offset(int64_t rows, int64_t cols, int64_t block_size);
+/* Diagnostics of the step above: 1 when a surface of this shape and block
+ * size takes the one-launch step on the current device (every pass in one
+ * kernel with grid barriers: columns a multiple of 2048, block_size a power
+ * of two in 8..256, at most 256 rows per compute unit's strip), 0 when it
+ * takes the multi-launch path (vector-aligned operands are needed too).
+ * Both give the same results bit for bit.  No counterpart in the reference. */
+int qste_coordinate_update_one_launch(int64_t rows, int64_t cols, int64_t block_size);
 int qste_coordinate_update(const float* evidence, int8_t* coordinate, uint8_t* packed,
                            int8_t* moment_q, uint16_t* moment_scale, uint16_t* row_v,
                            uint16_t* col_v, int64_t rows, int64_t cols, double beta1,

@@ -22,6 +22,7 @@ int launch_colsums(const void*, int, const float*, int64_t, int64_t, float*, flo
 size_t coordinate_update_workspace(int64_t, int64_t, int64_t);
 size_t coordinate_update_scalars_offset(int64_t, int64_t, int64_t);
 size_t coordinate_update_static_limit();
+int coordinate_update_one_launch(int64_t, int64_t, int64_t);
 int launch_coordinate_update_static(const float*, int8_t*, uint8_t*, int8_t*, uint16_t*, uint16_t*, uint16_t*,
                                     int64_t, int64_t, double, double, double, double, int64_t, int64_t, int64_t,
                                     const int64_t*, int64_t*, const uint8_t*, hipStream_t);
@@ -472,6 +473,10 @@ size_t qste_coordinate_update_workspace_bytes(int64_t rows, int64_t cols, int64_
 
 size_t qste_coordinate_update_scalars_offset(int64_t rows, int64_t cols, int64_t block_size) {
   return coordinate_update_scalars_offset(rows, cols, block_size);
+}
+
+int qste_coordinate_update_one_launch(int64_t rows, int64_t cols, int64_t block_size) {
+  return coordinate_update_one_launch(rows, cols, block_size);
 }
 
 int qste_coordinate_update(const float* evidence, int8_t* coordinate, uint8_t* packed, int8_t* moment_q,

@@ -42,6 +42,7 @@
 // keeps its column factors in registers, and finds a momentum block's
 // maximum among block_size / 4 consecutive lanes with DPP lane moves.
 #include <mutex>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -164,6 +165,17 @@ __device__ __forceinline__ float group_max_last(float v, int n) {
   if (n >= 16) v = fmaxf(v, dpp_f32<kShr8>(v));
   if (n >= 32) v = fmaxf(v, dpp_f32<kBcast15, 0xA>(v));
   if (n >= 64) v = fmaxf(v, dpp_f32<kBcast31, 0xC>(v));
+  return v;
+}
+
+template <int N>
+__device__ __forceinline__ float group_max_last_n(float v) {
+  if (N >= 2) v = fmaxf(v, dpp_f32<kShr1>(v));
+  if (N >= 4) v = fmaxf(v, dpp_f32<kShr2>(v));
+  if (N >= 8) v = fmaxf(v, dpp_f32<kShr4>(v));
+  if (N >= 16) v = fmaxf(v, dpp_f32<kShr8>(v));
+  if (N >= 32) v = fmaxf(v, dpp_f32<kBcast15, 0xA>(v));
+  if (N >= 64) v = fmaxf(v, dpp_f32<kBcast31, 0xC>(v));
   return v;
 }
 
@@ -1094,6 +1106,570 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(uint16_t* __restrict__
   }
 }
 
+// -- one-launch step --------------------------------------------------------------
+// Shapes with cols % 2048 == 0, a power-of-two block_size in 8..256 and at
+// most kMaxRows rows per workgroup run the whole step as one launch of one
+// workgroup per compute unit, every workgroup resident at once, with grid
+// barriers between the passes.  Workgroup b owns a strip: rows [r0, r1) of
+// one 2048-column group; wave w of it owns the strip's columns
+// 2048 cg + 256 w .. + 255, four consecutive columns per lane.  The first
+// kRegRows rows of a wave's strip stay in registers and the next lds_rows in
+// LDS from the statistics pass on, so the later passes read only the rest of
+// the evidence again (most of which the Infinity Cache still holds).
+//
+//   A  row partials (per wave, combined over the waves in order) and column
+//      partials (per lane over the strip's rows in order)
+//   -- barrier --
+//      column sums (each workgroup a slice of the columns) -> col_v, column
+//      factors; row statistics of the strip's rows -> row_v (by the first
+//      column group's workgroup), clamped-row partial
+//   -- barrier --
+//   B  sqrt of the mean row statistic, row factors; sum of U^2 (and, with
+//      spec, the momentum at divisor 1: new block scales, sum of m^2)
+//   -- barrier --
+//   C  clip divisor; unless spec held it to 1: the momentum, new block
+//      scales, sum of m^2
+//   -- barrier --
+//   D  step size; stochastic rounding, requantization, packing, flips; the
+//      new block scales into moment_scale
+//      the last workgroup to finish sums the flips.
+//
+// Every value that crosses workgroups (partials, factors) is written with
+// agent-scope atomic stores and read with agent-scope atomic loads, which are
+// coherent across the XCDs' L2 caches, and every thread waits for its stores
+// to complete before its workgroup arrives at a barrier; the evidence, read
+// only, and values a workgroup passes to itself take ordinary loads and
+// stores.  A barrier that waits longer than kSpinLimit polls (seconds) sets
+// the error word and lets the workgroup go on, so every launch ends; the
+// flip count is then -1.  The arithmetic is the multi-launch path's,
+// element by element; reductions are in double and in a fixed order, so a
+// call is deterministic.
+namespace fused {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;  // 8
+constexpr int kTile = 256 * kWaves;       // columns per workgroup
+constexpr int kMaxRows = 128;             // rows per workgroup
+constexpr int kPerCU = 2;                 // workgroups per compute unit (4 waves per SIMD)
+constexpr int kBatch = 4;                 // rows of a wave's strip loaded together (two batches in flight)
+constexpr int kLdsTotal = 160 * 1024 / kPerCU;  // LDS per workgroup (gfx950: 160 KiB per compute unit)
+constexpr uint32_t kSpinLimit = 1u << 21;  // polls of about 1 us
+constexpr int kSyncWords = 64 * 11;       // [0] barrier total, [64 (1 + g)] group g, [576] flips (64 bits), [640] error
+constexpr int kSyncFlips = 64 * 9, kSyncError = 64 * 10;
+constexpr uint32_t kDead = 0x80000000u;   // lane offset past every strip: the load returns 0, reads nothing
+
+struct FWork {
+  unsigned* sync;       // kSyncWords, zeroed by sync_clear_kernel
+  double* colpart;      // [nwg][kTile]
+  double* rowpart;      // [cgs][rows]
+  float* col_factor;    // [cols]
+  double* clamp_part;   // [wpc]
+  double* usq_part;     // [nwg]
+  double* msq_part;     // [nwg]
+  uint16_t* s_new;      // [blocks]
+  float* s_rcp;         // [blocks]
+  float* scalars;       // [4]
+  int wpc;              // workgroups per column group
+  int cgs;              // column groups
+  int lds_rows;         // rows of a wave's strip held in LDS
+};
+
+__device__ __forceinline__ void st_agent(double* p, double v) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(int64_t* p, int64_t v) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), static_cast<uint64_t>(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ double ld_agent(const double* p) {
+  return __builtin_bit_cast(double, __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ int64_t ld_agent(const int64_t* p) {
+  return static_cast<int64_t>(
+      __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<const uint32_t*>(p), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ unsigned add_agent(unsigned* p, unsigned v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned ld_agent(const unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Every load and store this thread issued has completed.
+__device__ __forceinline__ void drain() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Grid barrier number `gen` (1, 2, ...) of this launch.  Workgroups arrive
+// at one of eight group counters (b % 8); the last of a group adds one to
+// the total, which every workgroup then polls.
+__device__ __forceinline__ void grid_barrier(unsigned* sync, unsigned gen) {
+  drain();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned g = blockIdx.x & 7u;
+    const unsigned gsize = (gridDim.x - g + 7u) >> 3;
+    const unsigned groups = gridDim.x < 8u ? gridDim.x : 8u;
+    if (add_agent(sync + 64 * (1 + g), 1u) + 1u == gen * gsize) add_agent(sync, 1u);
+    uint32_t spins = 0;
+    while (ld_agent(sync) < gen * groups) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++spins > kSpinLimit) {
+        add_agent(sync + kSyncError, 1u);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+__global__ void sync_clear_kernel(unsigned* sync) {
+  for (int i = threadIdx.x; i < kSyncWords; i += blockDim.x) sync[i] = 0u;
+}
+
+typedef __attribute__((address_space(3))) void lds_t;
+
+// Buffer resource over `bytes` bytes at `base` (loads past the end read 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t strip_rsrc(const void* base, int64_t bytes) {
+  const uint32_t n = bytes > 0xFFFFFFFFll ? 0xFFFFFFFFu : static_cast<uint32_t>(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(n), 0x00020000);
+}
+
+// What a pass reads of one row of a wave's strip.
+enum : int { kNeedE = 1, kNeedQ = 2, kNeedFinal = 4 };
+
+struct RowIn {
+  float4 v;          // evidence (rows in memory; LDS rows are read when used)
+  uint32_t q4, c4;   // int8 momentum, int8 coordinates
+  uint32_t old;      // packed byte holding this lane's four signs
+  uint32_t s16;      // new fp16 block scale
+  float s_old, rdec;
+};
+
+__global__ __launch_bounds__(kThreads, kPerCU) void fused_step_kernel(const float* __restrict__ g, int8_t* __restrict__ coord,
+                                                              uint8_t* __restrict__ packed,
+                                                              int8_t* __restrict__ moment_q,
+                                                              uint16_t* __restrict__ moment_scale,
+                                                              uint16_t* __restrict__ row_v,
+                                                              uint16_t* __restrict__ col_v, Params p, FWork w,
+                                                              int64_t* __restrict__ flips_out) {
+  extern __shared__ __align__(16) unsigned char dyn[];
+  __shared__ double red[kMaxRows * kWaves];  // row partials per wave; later the column-sum slots
+  __shared__ float rowf[kMaxRows];           // new row statistic, then the row factor
+  __shared__ float rowv_prev[kMaxRows];      // row_v before this step
+  __shared__ double bred[kWaves];
+  __shared__ int64_t ired[kWaves];
+  float4* stage = reinterpret_cast<float4*>(dyn);
+
+  const bool on = enabled(p);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = blockIdx.x;
+  const int cg = b / w.wpc, part = b - cg * w.wpc;
+  const int64_t r0 = p.rows * part / w.wpc;
+  const int nrows = static_cast<int>(p.rows * (part + 1) / w.wpc - r0);
+  const int nL = nrows < w.lds_rows ? nrows : w.lds_rows;  // strip rows 0 .. nL-1 stay in LDS
+  const int64_t cols = p.cols;
+  const int64_t col = static_cast<int64_t>(cg) * kTile + 256 * wave + 4 * lane;
+  const int64_t flat0 = r0 * cols + col;  // flat index of this lane's first element of the strip
+  const uint32_t row_bytes = static_cast<uint32_t>(cols * 4);
+  const __amdgpu_buffer_rsrc_t strip = strip_rsrc(g + r0 * cols, static_cast<int64_t>(nrows) * cols * 4);
+  const uint32_t voff = static_cast<uint32_t>(col * 4);
+  float4* st = stage + wave * kWave + lane;  // LDS row j of this lane: st[j * kThreads]
+  const int nb = (nrows + kBatch - 1) / kBatch;
+
+  for (int t = threadIdx.x; t < nrows; t += kThreads) rowv_prev[t] = f16_to_f32(row_v[r0 + t]);
+
+  // Strip row at position `pos` of a pass's walk: forward, or backward so
+  // that a pass starts on the rows the previous one read last.
+  auto row_at = [&](int pos, bool fwd) { return __builtin_amdgcn_readfirstlane(fwd ? pos : nrows - 1 - pos); };
+  // Per-row operands through buffer instructions: a wave-uniform byte
+  // offset per row (scalar), the lane's column offset (vector).  The block
+  // scales of row i start at block (r0 + i) * cols >> shift (cols is a
+  // multiple of 256 and block_size divides 256, so rows hold whole blocks).
+  const int bshift = p.block_shift;
+  const int64_t blk0 = (r0 * cols) >> bshift;                 // first block of the strip
+  const int64_t nblk = (static_cast<int64_t>(nrows) * cols) >> bshift;
+  const uint32_t row_blocks = static_cast<uint32_t>(cols >> bshift);
+  const __amdgpu_buffer_rsrc_t rq = strip_rsrc(moment_q + r0 * cols, static_cast<int64_t>(nrows) * cols);
+  const __amdgpu_buffer_rsrc_t rc8 = strip_rsrc(coord + r0 * cols, static_cast<int64_t>(nrows) * cols);
+  const __amdgpu_buffer_rsrc_t rpk = strip_rsrc(packed + (r0 * cols >> 3), static_cast<int64_t>(nrows) * cols / 8);
+  const __amdgpu_buffer_rsrc_t rso = strip_rsrc(moment_scale + blk0, nblk * 2);
+  const __amdgpu_buffer_rsrc_t rsn = strip_rsrc(w.s_new + blk0, nblk * 2);
+  const __amdgpu_buffer_rsrc_t rsr = strip_rsrc(w.s_rcp + blk0, nblk * 4);
+  const uint32_t vq = static_cast<uint32_t>(col);             // byte offset of the lane's 4 int8 values
+  const uint32_t vpk = static_cast<uint32_t>(col >> 3);       // its packed byte
+  const uint32_t vblk = static_cast<uint32_t>(col >> bshift); // its block within the row
+  // Loads of strip row i (i < 0: nothing; evidence only for rows in memory).
+  auto load = [&](auto need_tag, int i, RowIn& in) {
+    constexpr int NEED = decltype(need_tag)::value;
+    const bool live = i >= 0;
+    const uint32_t ic = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(live ? i : 0));
+    if (NEED & kNeedE) {
+      // LDS rows and positions past the strip read nothing: a lane offset
+      // past the buffer's end returns zeros without a memory access
+      const bool mem = live && static_cast<int>(ic) >= nL;
+      in.v = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(strip, mem ? voff : kDead, ic * row_bytes, 0));
+    }
+    const uint32_t rowb = ic * static_cast<uint32_t>(cols);  // byte offset of the row's int8 values
+    const uint32_t rblk = ic * row_blocks;                    // the row's first block
+    if (NEED & (kNeedQ | kNeedFinal)) {
+      in.q4 = __builtin_amdgcn_raw_buffer_load_b32(rq, vq, rowb, 0);
+      in.s_old = f16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(rso, 2 * vblk, 2 * rblk, 0));
+    }
+    if (NEED & kNeedFinal) {
+      in.c4 = __builtin_amdgcn_raw_buffer_load_b32(rc8, vq, rowb, 0);
+      in.old = __builtin_amdgcn_raw_buffer_load_b8(rpk, vpk, rowb >> 3, 0);
+      in.s16 = __builtin_amdgcn_raw_buffer_load_b16(rsn, 2 * vblk, 2 * rblk, 0);
+      in.rdec = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsr, 4 * vblk, 4 * rblk, 0));
+    }
+  };
+  // One pass over the strip: two batches of kBatch rows in flight, the
+  // evidence of LDS rows read from LDS when used.
+  auto sweep = [&](auto need_tag, bool fwd, auto&& op) {
+    RowIn cur[kBatch], nxt[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) load(need_tag, u < nrows ? row_at(u, fwd) : -1, cur[u]);
+    for (int k = 0; k < nb; ++k) {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int pos = (k + 1) * kBatch + u;
+        load(need_tag, pos < nrows ? row_at(pos, fwd) : -1, nxt[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int pos = k * kBatch + u;
+        if (pos < nrows) {
+          const int i = row_at(pos, fwd);
+          if (i < nL) cur[u].v = st[i * kThreads];
+          op(i, cur[u]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) cur[u] = nxt[u];
+    }
+  };
+  using E_ = std::integral_constant<int, kNeedE>;
+  using EQ_ = std::integral_constant<int, kNeedE | kNeedQ>;
+  using EF_ = std::integral_constant<int, kNeedE | kNeedFinal>;
+
+  // ---- A: statistics -----------------------------------------------------------
+  double c0 = 0.0, c1 = 0.0, c2 = 0.0, c3 = 0.0;
+  auto stats = [&](int i, const RowIn& in) {
+    const float4 v = in.v;
+    const double d0 = square_eps(v.x), d1 = square_eps(v.y), d2 = square_eps(v.z), d3 = square_eps(v.w);
+    c0 += d0; c1 += d1; c2 += d2; c3 += d3;
+    const double rp = wave_total((d0 + d1) + (d2 + d3));
+    if (lane == 0) red[i * kWaves + wave] = rp;
+  };
+  // the LDS rows by direct loads (no registers), all in flight together;
+  // lane l of a wave lands at the wave's row base + 16 l
+  for (int j = 0; j < nL; ++j)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(strip, (lds_t*)(stage + j * kThreads + wave * kWave), 16, voff,
+                                             static_cast<int>(static_cast<uint32_t>(j) * row_bytes), 0, 0);
+  // rows in memory first (the walk skips the LDS rows), then the LDS rows
+  {
+    const int nm = nrows - nL, nbm = (nm + kBatch - 1) / kBatch;
+    RowIn cur[kBatch], nxt[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) load(E_{}, u < nm ? nL + u : -1, cur[u]);
+    for (int k = 0; k < nbm; ++k) {
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int pos = (k + 1) * kBatch + u;
+        load(E_{}, pos < nm ? nL + pos : -1, nxt[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (k * kBatch + u < nm) stats(nL + k * kBatch + u, cur[u]);
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) cur[u] = nxt[u];
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct loads have landed in LDS
+  for (int j = 0; j < nL; ++j) {
+    RowIn in;
+    in.v = st[j * kThreads];
+    stats(j, in);
+  }
+  {
+    double* cp = w.colpart + (static_cast<int64_t>(cg) * w.wpc + part) * kTile + 256 * wave + 4 * lane;
+    st_agent(cp + 0, c0);
+    st_agent(cp + 1, c1);
+    st_agent(cp + 2, c2);
+    st_agent(cp + 3, c3);
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < nrows; t += kThreads) {
+    const double* rr = red + t * kWaves;
+    const double s = ((rr[0] + rr[1]) + (rr[2] + rr[3])) + ((rr[4] + rr[5]) + (rr[6] + rr[7]));
+    st_agent(w.rowpart + static_cast<int64_t>(cg) * p.rows + r0 + t, s);
+  }
+  grid_barrier(w.sync, 1);
+
+  // ---- column and row statistics --------------------------------------------------
+  {
+    // workgroup b sums columns [b cpw, (b + 1) cpw): thread (cl, sub) the
+    // partials sub, sub + nsub, ... of column cl, then the nsub sums in order
+    const int cpw = static_cast<int>((cols + gridDim.x - 1) / gridDim.x);
+    const int nsub = kThreads / cpw;
+    const int cl = threadIdx.x % cpw, sub = threadIdx.x / cpw;
+    const int64_t c = static_cast<int64_t>(b) * cpw + cl;
+    double s = 0.0;
+    if (sub < nsub && c < cols) {
+      const int ccg = static_cast<int>(c / kTile);
+      const double* src = w.colpart + static_cast<int64_t>(ccg) * w.wpc * kTile + (c - static_cast<int64_t>(ccg) * kTile);
+      for (int k0 = sub; k0 < w.wpc; k0 += 8 * nsub) {
+        double v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int k = k0 + u * nsub;
+          v[u] = k < w.wpc ? ld_agent(src + static_cast<int64_t>(k) * kTile) : 0.0;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+      }
+    }
+    __syncthreads();  // every row partial in red was read before the barrier
+    if (sub < nsub) red[sub * cpw + cl] = s;
+    __syncthreads();
+    if (threadIdx.x < cpw && c < cols) {
+      double t = 0.0;
+      for (int k = 0; k < nsub; ++k) t += red[k * cpw + threadIdx.x];
+      const float mean = static_cast<float>(t) / static_cast<float>(p.rows);
+      const float nc = fmaf(mean, p.a2, f16_to_f32(col_v[c]) * p.b2);
+      if (on) col_v[c] = f32_to_f16(nc);
+      st_agent(w.col_factor + c, 1.0f / sqrtf(fmaxf(nc, 1e-10f)));
+    }
+  }
+  {
+    double acc = 0.0;
+    for (int t = threadIdx.x; t < nrows; t += kThreads) {
+      double v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        v[k] = k < w.cgs ? ld_agent(w.rowpart + static_cast<int64_t>(k) * p.rows + r0 + t) : 0.0;
+      double s = 0.0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s += v[k];
+      const float mean = static_cast<float>(s) / static_cast<float>(cols);
+      const float nr = fmaf(mean, p.a2, rowv_prev[t] * p.b2);
+      if (cg == 0 && on) row_v[r0 + t] = f32_to_f16(nr);
+      rowf[t] = nr;
+      acc += static_cast<double>(fmaxf(nr, 1e-10f));
+    }
+    acc = block_sum(acc, bred);
+    if (cg == 0 && threadIdx.x == 0) st_agent(w.clamp_part + part, acc);
+  }
+  grid_barrier(w.sync, 2);
+
+  // ---- B: factors, sum of U^2 ------------------------------------------------------
+  {
+    double a = 0.0;
+    for (int k = threadIdx.x; k < w.wpc; k += kThreads) a += ld_agent(w.clamp_part + k);
+    a = block_sum(a, bred);
+    const float sqrt_mean = sqrtf(static_cast<float>(a) / static_cast<float>(p.rows));
+    if (b == 0 && threadIdx.x == 0) w.scalars[0] = sqrt_mean;
+    for (int t = threadIdx.x; t < nrows; t += kThreads) rowf[t] = row_factor_of(sqrt_mean, rowf[t]);
+  }
+  float cf[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) cf[e] = ld_agent(w.col_factor + col + e);
+  __syncthreads();
+
+  const int gsize = static_cast<int>(p.block_size >> 2);  // lanes per momentum block
+  double usq = 0.0, msq = 0.0;
+  // U of one row; with MOM the momentum (DIV: U / divisor), block scales,
+  // m^2.  GS: lanes per momentum block when known at compile time (64 for
+  // the default block of 256), 0 for the run-time gsize.
+  auto row_op = [&](auto usq_on, auto mom_on, auto div_on, auto gs_tag, int i, const RowIn& in, float divisor,
+                    float rdiv) {
+    constexpr bool USQ = decltype(usq_on)::value, MOM = decltype(mom_on)::value, DIV = decltype(div_on)::value;
+    constexpr int GS = decltype(gs_tag)::value;
+    const float rf = rowf[i];
+    const float4 v = in.v;
+    const float u[4] = {normalized(v.x, rf, cf[0]), normalized(v.y, rf, cf[1]), normalized(v.z, rf, cf[2]),
+                        normalized(v.w, rf, cf[3])};
+    if (USQ) {
+      const float s0 = u[0] * u[0], s1 = u[1] * u[1], s2 = u[2] * u[2], s3 = u[3] * u[3];
+      usq += (static_cast<double>(s0) + static_cast<double>(s1)) + (static_cast<double>(s2) + static_cast<double>(s3));
+    }
+    if (MOM) {
+      float amax = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float ue = DIV ? div_by(u[e], divisor, rdiv) : u[e];
+        const float prev = static_cast<float>(static_cast<int8_t>(in.q4 >> (8 * e)));
+        const float m = moment_of(ue, prev, in.s_old, p);
+        amax = fmaxf(amax, fabsf(m));
+        const float sq = m * m;
+        msq += static_cast<double>(sq);
+      }
+      const int gs = GS ? GS : gsize;
+      amax = GS ? group_max_last_n<GS>(amax) : group_max_last(amax, gsize);
+      if ((lane & (gs - 1)) == gs - 1) {
+        const uint32_t ic = static_cast<uint32_t>(i);
+        const uint16_t s16 = f32_to_f16(fmaxf(amax, 1e-6f) / 127.0f);
+        __builtin_amdgcn_raw_buffer_store_b16(s16, rsn, 2 * vblk, 2 * ic * row_blocks, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, 1.0f / fmaxf(f16_to_f32(s16), 1e-12f)),
+                                              rsr, 4 * vblk, 4 * ic * row_blocks, 0);
+      }
+    }
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  using G64_ = std::integral_constant<int, 64>;
+  using G0_ = std::integral_constant<int, 0>;
+  const bool spec = p.spec, g64 = gsize == 64;
+  if (spec && g64)
+    sweep(EQ_{}, false, [&](int i, const RowIn& in) { row_op(T_{}, T_{}, F_{}, G64_{}, i, in, 1.0f, 1.0f); });
+  else if (spec)
+    sweep(EQ_{}, false, [&](int i, const RowIn& in) { row_op(T_{}, T_{}, F_{}, G0_{}, i, in, 1.0f, 1.0f); });
+  else
+    sweep(E_{}, false, [&](int i, const RowIn& in) { row_op(T_{}, F_{}, F_{}, G0_{}, i, in, 1.0f, 1.0f); });
+  usq = block_sum(usq, bred);
+  if (threadIdx.x == 0) st_agent(w.usq_part + b, usq);
+  if (spec) {
+    msq = block_sum(msq, bred);
+    if (threadIdx.x == 0) st_agent(w.msq_part + b, msq);
+  }
+  grid_barrier(w.sync, 3);
+
+  // ---- C: clip divisor, momentum -----------------------------------------------------
+  float divisor;
+  {
+    double a = 0.0;
+    for (int k = threadIdx.x; k < static_cast<int>(gridDim.x); k += kThreads) a += ld_agent(w.usq_part + k);
+    a = block_sum(a, bred);
+    float rms = sqrtf(static_cast<float>(a) / static_cast<float>(p.count));
+    rms = fmaxf(rms, 1e-8f);
+    const float ratio = rms / p.clip;
+    divisor = ratio > 1.0f ? ratio : 1.0f;
+    if (b == 0 && threadIdx.x == 0) w.scalars[1] = divisor;
+  }
+  const float rdiv = 1.0f / divisor;
+  bool fwd_d = true;  // the final pass walks against the pass before it
+  if (!(spec && divisor == 1.0f)) {
+    msq = 0.0;
+    if (g64)
+      sweep(EQ_{}, true, [&](int i, const RowIn& in) { row_op(F_{}, T_{}, T_{}, G64_{}, i, in, divisor, rdiv); });
+    else
+      sweep(EQ_{}, true, [&](int i, const RowIn& in) { row_op(F_{}, T_{}, T_{}, G0_{}, i, in, divisor, rdiv); });
+    msq = block_sum(msq, bred);
+    if (threadIdx.x == 0) st_agent(w.msq_part + b, msq);
+    grid_barrier(w.sync, 4);
+    fwd_d = false;
+  }
+
+  // ---- D: rounding, requantization, packing --------------------------------------------
+  float step_size;
+  {
+    double a = 0.0;
+    for (int k = threadIdx.x; k < static_cast<int>(gridDim.x); k += kThreads) a += ld_agent(w.msq_part + k);
+    a = block_sum(a, bred);
+    const float padded = static_cast<float>(p.blocks * p.block_size);
+    float mrms = sqrtf(static_cast<float>(a) / padded);
+    mrms = fmaxf(mrms, 1e-8f);
+    step_size = step_size_of(mrms, p.lr);
+    if (b == 0 && threadIdx.x == 0) {
+      w.scalars[2] = step_size;
+      w.scalars[3] = mrms;
+    }
+  }
+  const int64_t step = p.step_device ? *p.step_device : p.step;
+  const uint32_t combined = p.seed_part ^ step_hash(step);
+  const int shift_nib = 4 * (lane & 1);
+  int64_t flips = 0;
+  auto final_row = [&](auto div1_tag, int i, const RowIn& in) {
+    constexpr bool DIV1 = decltype(div1_tag)::value;
+    const float rf = rowf[i];
+    const int64_t i0 = flat0 + static_cast<int64_t>(i) * cols;  // flat index of the lane's first element
+    const uint32_t head = scramble_head(static_cast<uint32_t>(i0) ^ combined);
+    const float decode = fmaxf(f16_to_f32(static_cast<uint16_t>(in.s16)), 1e-12f);
+    // A finite block scale bounds every |m| of its block, so the quotient
+    // m / decode needs no guard for infinite operands (a NaN m stays NaN
+    // either way); a row with an infinite scale takes the guarded division.
+    const bool finite = __builtin_amdgcn_ballot_w64(!(decode < INFINITY)) == 0;
+    const float gv[4] = {in.v.x, in.v.y, in.v.z, in.v.w};
+    uint32_t cn = 0, qn = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float u2 = normalized(gv[e], rf, cf[e]);
+      if (!DIV1) u2 = div_by(u2, divisor, rdiv);
+      const float prev = static_cast<float>(static_cast<int8_t>(in.q4 >> (8 * e)));
+      const float cval = static_cast<float>(static_cast<int8_t>(in.c4 >> (8 * e)));
+      const float m = moment_of(u2, prev, in.s_old, p);
+      const float delta = m * step_size;
+      const float target = cval - delta;
+      const float lower = floorf(target);
+      const float uu = static_cast<float>(scramble_tail(head ^ static_cast<uint32_t>(e))) * (1.0f / 4294967296.0f);
+      const float frac = target - lower;
+      float rounded = lower + (uu < frac ? 1.0f : 0.0f);
+      rounded = fminf(127.0f, fmaxf(-127.0f, rounded));
+      float x;
+      if (finite) {
+        const float q0 = m * in.rdec;
+        x = fmaf(fmaf(-q0, decode, m), in.rdec, q0);
+      } else {
+        x = div_by(m, decode, in.rdec);
+      }
+      // clamp(rint(x)) == rint(clamp(x)) for integer bounds; adding 1.5 * 2^23
+      // rounds to the nearest integer, ties to even, into the low byte
+      const float q = fminf(127.0f, fmaxf(-127.0f, x)) + 12582912.0f;
+      cn |= static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(rounded))) << (8 * e);
+      qn |= (__float_as_uint(q) & 0xFFu) << (8 * e);
+    }
+    // sign bits: a coordinate >= 0 has bit 7 of its byte clear; the
+    // multiply gathers bits 7, 15, 23, 31 into bits 28..31
+    const uint32_t nib = ((~cn & 0x80808080u) * 0x00204081u) >> 28;
+    // the other half of the packed byte comes from the neighbouring lane
+    const uint32_t other = static_cast<uint32_t>(__shfl_xor(static_cast<int>(nib), 1));
+    if (on) {
+      const uint32_t rowb = static_cast<uint32_t>(i) * static_cast<uint32_t>(cols);
+      __builtin_amdgcn_raw_buffer_store_b32(cn, rc8, vq, rowb, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(qn, rq, vq, rowb, 0);
+      if ((lane & 1) == 0)
+        __builtin_amdgcn_raw_buffer_store_b8(static_cast<uint8_t>(nib | (other << 4)), rpk, vpk, rowb >> 3, 0);
+      // the block's new scale into place: every lane of the block read the
+      // old one before this row's arithmetic
+      if ((lane & (gsize - 1)) == gsize - 1)
+        __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(in.s16), rso, 2 * vblk,
+                                              2 * static_cast<uint32_t>(i) * row_blocks, 0);
+    }
+    flips += __popc(((in.old >> shift_nib) ^ nib) & 0xFu);
+  };
+  if (divisor == 1.0f)
+    sweep(EF_{}, fwd_d, [&](int i, const RowIn& in) { final_row(T_{}, i, in); });
+  else
+    sweep(EF_{}, fwd_d, [&](int i, const RowIn& in) { final_row(F_{}, i, in); });
+  // flip total: one 64-bit atomic per workgroup adds its flips (shifted
+  // by 10 bits) and one arrival; the workgroup that completes the arrivals
+  // holds the total.  Integer sums, so the result does not depend on order.
+  flips = block_sum(flips, ired);
+  if (threadIdx.x == 0) {
+    const uint64_t mine = (static_cast<uint64_t>(on ? flips : 0) << 10) | 1u;
+    const uint64_t now = __hip_atomic_fetch_add(reinterpret_cast<uint64_t*>(w.sync + kSyncFlips), mine,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + mine;
+    if ((now & 1023u) == gridDim.x && flips_out)
+      *flips_out = ld_agent(w.sync + kSyncError) ? int64_t{-1} : static_cast<int64_t>(now >> 10);
+  }
+}
+
+}  // namespace fused
+
 // -- plan ------------------------------------------------------------------------
 constexpr int kSegments = 13;
 
@@ -1126,9 +1702,12 @@ static Layout layout(int64_t rows, int64_t cols, int64_t block_size, Work* w) {
       sizeof(int64_t) * kFinalGroups,
       sizeof(float) * static_cast<size_t>(blocks),
   };
+  // the scalars block first: both step paths keep it at offset 0
   Layout l{};
   size_t at = 0;
-  for (int i = 0; i < kSegments; ++i) {
+  constexpr int order[kSegments] = {9, 0, 1, 2, 3, 4, 5, 6, 7, 8, 10, 11, 12};
+  for (int k = 0; k < kSegments; ++k) {
+    const int i = order[k];
     l.off[i] = at;
     at += align_up(sizes[i]);
   }
@@ -1140,7 +1719,101 @@ static Layout layout(int64_t rows, int64_t cols, int64_t block_size, Work* w) {
   return l;
 }
 
+// Layout of the one-launch step's workspace; cgs / wpc from fused_plan.
+struct FusedLayout {
+  size_t scalars, sync, colpart, rowpart, col_factor, clamp, usq, msq, s_new, s_rcp, total;
+};
+
+static FusedLayout fused_layout(int64_t rows, int64_t cols, int64_t block_size, int cgs, int wpc) {
+  const int64_t nwg = static_cast<int64_t>(cgs) * wpc;
+  const int64_t blocks = (rows * cols + block_size - 1) / block_size;
+  FusedLayout l{};
+  size_t at = 0;
+  auto seg = [&](size_t& off, size_t bytes) {
+    off = at;
+    at += align_up(bytes);
+  };
+  seg(l.scalars, sizeof(float) * 4);
+  seg(l.sync, sizeof(unsigned) * fused::kSyncWords);
+  seg(l.colpart, sizeof(double) * static_cast<size_t>(nwg * fused::kTile));
+  seg(l.rowpart, sizeof(double) * static_cast<size_t>(cgs * rows));
+  seg(l.col_factor, sizeof(float) * static_cast<size_t>(cols));
+  seg(l.clamp, sizeof(double) * static_cast<size_t>(wpc));
+  seg(l.usq, sizeof(double) * static_cast<size_t>(nwg));
+  seg(l.msq, sizeof(double) * static_cast<size_t>(nwg));
+  seg(l.s_new, sizeof(uint16_t) * static_cast<size_t>(blocks));
+  seg(l.s_rcp, sizeof(float) * static_cast<size_t>(blocks));
+  l.total = at;
+  return l;
+}
+
 }  // namespace step
+
+// The one-launch step's grid for a shape on the current device: cgs column
+// groups of 2048 columns, wpc workgroups (strips of rows) each, one
+// workgroup per compute unit, lds_rows rows of each wave's strip in LDS.
+// False when the shape takes the multi-launch path: columns not a multiple
+// of 2048 (or more than 8 groups), block_size not a power of two in 8..256,
+// more than kMaxRows rows per strip, or a device that cannot hold the grid.
+struct FusedPlan {
+  int cgs, wpc, lds_rows;
+  size_t lds_bytes;
+};
+
+static bool fused_plan(int64_t rows, int64_t cols, int64_t block_size, FusedPlan* fp) {
+  using namespace step::fused;
+  if (rows <= 0 || cols <= 0 || cols % kTile != 0 || cols / kTile > 8) return false;
+  if (block_size < 8 || block_size > 256 || (block_size & (block_size - 1)) != 0) return false;
+  struct Dev {
+    int cus = -1;  // workgroups of the step resident at once (kPerCU per compute unit)
+    size_t static_lds = 0;
+  };
+  static Dev cache[64];
+  static std::mutex lock;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  Dev d;
+  {
+    std::lock_guard<std::mutex> hold(lock);
+    if (cache[dev].cus < 0) {
+      Dev n;
+      n.cus = 0;
+      hipFuncAttributes attr{};
+      int cus = 0;
+      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+          hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(fused_step_kernel)) == hipSuccess) {
+        const size_t dyn = static_cast<size_t>(kLdsTotal) - attr.sharedSizeBytes;
+        int per_cu = 0;
+        if (attr.sharedSizeBytes < static_cast<size_t>(kLdsTotal) &&
+            hipFuncSetAttribute(reinterpret_cast<const void*>(fused_step_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(dyn)) == hipSuccess &&
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_step_kernel, kThreads, dyn) == hipSuccess &&
+            per_cu >= kPerCU) {
+          n.cus = cus * kPerCU;
+          n.static_lds = attr.sharedSizeBytes;
+        }
+      }
+      (void)hipGetLastError();
+      cache[dev] = n;
+    }
+    d = cache[dev];
+  }
+  if (d.cus <= 0) return false;
+  const int cgs = static_cast<int>(cols / kTile);
+  int64_t wpc = d.cus / cgs;
+  if (wpc > rows) wpc = rows;
+  if (wpc < 4) return false;  // a workgroup sums at most 512 columns after the first barrier
+  if ((rows + wpc - 1) / wpc > kMaxRows || cgs * wpc > 1023) return false;
+  if ((cols + cgs * wpc - 1) / (cgs * wpc) > kThreads) return false;
+  const int64_t max_rows = (rows + wpc - 1) / wpc;
+  int lds_rows = static_cast<int>((static_cast<size_t>(kLdsTotal) - d.static_lds) / (kThreads * 16));
+  if (lds_rows > max_rows) lds_rows = static_cast<int>(max_rows);
+  fp->cgs = cgs;
+  fp->wpc = static_cast<int>(wpc);
+  fp->lds_rows = lds_rows;
+  fp->lds_bytes = static_cast<size_t>(lds_rows) * kThreads * 16;
+  return true;
+}
 
 // Workgroups of final_row_kernel resident at once on the current device
 // (compute units x workgroups per unit at its register use), cached per
@@ -1162,12 +1835,21 @@ static int64_t resident_final_groups() {
 
 size_t coordinate_update_workspace(int64_t rows, int64_t cols, int64_t block_size) {
   if (rows <= 0 || cols <= 0 || block_size <= 0) return 0;
-  return step::layout(rows, cols, block_size, nullptr).total;
+  size_t need = step::layout(rows, cols, block_size, nullptr).total;
+  FusedPlan fp;
+  if (fused_plan(rows, cols, block_size, &fp)) {
+    const size_t f = step::fused_layout(rows, cols, block_size, fp.cgs, fp.wpc).total;
+    if (f > need) need = f;
+  }
+  return need;
 }
 
-size_t coordinate_update_scalars_offset(int64_t rows, int64_t cols, int64_t block_size) {
-  if (rows <= 0 || cols <= 0 || block_size <= 0) return 0;
-  return step::layout(rows, cols, block_size, nullptr).off[9];
+// Both paths keep the scalars block at the start of the workspace.
+size_t coordinate_update_scalars_offset(int64_t, int64_t, int64_t) { return 0; }
+
+int coordinate_update_one_launch(int64_t rows, int64_t cols, int64_t block_size) {
+  FusedPlan fp;
+  return fused_plan(rows, cols, block_size, &fp) ? 1 : 0;
 }
 
 int launch_coordinate_update(const float* g, int8_t* coord, uint8_t* packed, int8_t* moment_q,
@@ -1226,6 +1908,33 @@ int launch_coordinate_update(const float* g, int8_t* coord, uint8_t* packed, int
   // falls towards 1), not in the first tens of steps from a fresh state
   p.spec = p.vec && cols % 256 == 0 && block_size >= 4 && block_size <= 256 &&
            (reinterpret_cast<uintptr_t>(moment_q) & 3) == 0 && step_device == nullptr && step_ >= 64;
+
+  FusedPlan fp;
+  if (p.vec && (reinterpret_cast<uintptr_t>(coord) & 3) == 0 && (reinterpret_cast<uintptr_t>(moment_q) & 3) == 0 &&
+      fused_plan(rows, cols, block_size, &fp)) {
+    const FusedLayout fl = fused_layout(rows, cols, block_size, fp.cgs, fp.wpc);
+    if (workspace_bytes < fl.total) return QSTE_E_WORKSPACE;
+    fused::FWork fw{};
+    fw.sync = reinterpret_cast<unsigned*>(base + fl.sync);
+    fw.colpart = reinterpret_cast<double*>(base + fl.colpart);
+    fw.rowpart = reinterpret_cast<double*>(base + fl.rowpart);
+    fw.col_factor = reinterpret_cast<float*>(base + fl.col_factor);
+    fw.clamp_part = reinterpret_cast<double*>(base + fl.clamp);
+    fw.usq_part = reinterpret_cast<double*>(base + fl.usq);
+    fw.msq_part = reinterpret_cast<double*>(base + fl.msq);
+    fw.s_new = reinterpret_cast<uint16_t*>(base + fl.s_new);
+    fw.s_rcp = reinterpret_cast<float*>(base + fl.s_rcp);
+    fw.scalars = reinterpret_cast<float*>(base + fl.scalars);
+    fw.wpc = fp.wpc;
+    fw.cgs = fp.cgs;
+    fw.lds_rows = fp.lds_rows;
+    fused::sync_clear_kernel<<<1, 256, 0, stream>>>(fw.sync);
+    int rc0 = static_cast<int>(hipGetLastError());
+    if (rc0) return rc0;
+    fused::fused_step_kernel<<<fp.cgs * fp.wpc, fused::kThreads, fp.lds_bytes, stream>>>(
+        g, coord, packed, moment_q, moment_scale, row_v, col_v, p, fw, flips_out);
+    return static_cast<int>(hipGetLastError());
+  }
 
   // row path: whole 256-column slots, momentum blocks inside one slot, and
   // at least one usq workgroup per chunk

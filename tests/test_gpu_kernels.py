@@ -291,6 +291,33 @@ def test_coordinate_update_matches_oracle(rows, cols, block):
         assert flips == oflips
 
 
+# the one-launch step: strips whose rows sit in registers, in LDS and in
+# memory; every power-of-two block size; strips of unequal height; fresh
+# steps, speculative steps with the clip idle and with it engaged (the guess
+# thrown away)
+ONE_LAUNCH = [(64, 2048, 256), (512, 4096, 8), (3000, 2048, 16), (1111, 4096, 32), (700, 6144, 64),
+              (9000, 4096, 128), (4096, 14336, 256)]
+
+
+@pytest.mark.parametrize("rows,cols,block", ONE_LAUNCH)
+def test_coordinate_update_one_launch_matches_oracle(rows, cols, block):
+    from qste_amd.kernels import _lib
+
+    assert _lib.load().qste_coordinate_update_one_launch(rows, cols, block) == 1
+    print(f"one launch {rows}x{cols} block {block}", flush=True)
+    rng = np.random.default_rng(rows + cols + block)
+    coord = rng.integers(-127, 128, size=(rows, cols)).astype(np.int8)
+    state = oracle.fresh_state(coord, block)
+    gstate = _to_gpu_state(state)
+    for step, clip in ((0, 2.0), (1, 2.0), (64, 1e6), (65, 0.05)):
+        ev = (rng.standard_normal((rows, cols)) * 0.1).astype(np.float32)
+        kw = dict(beta1=0.9, beta2=0.99, update_clip=clip, coordinate_lr=0.7, block_size=block, seed=3, step=step)
+        flips = _gpu_step(ev, gstate, **kw)
+        oflips = oracle.coordinate_update(ev, state, **kw)
+        _assert_state_equal(gstate, state, (rows, cols, block, step))
+        assert flips == oflips
+
+
 @pytest.mark.parametrize("rows,cols,block", [(24, 40, 96), (50, 256, 100), (7, 33, 3), (64, 512, 384)])
 def test_coordinate_update_any_block_size(rows, cols, block):
     """Momentum blocks that are not powers of two (the specification and the
@@ -342,7 +369,7 @@ def _c_step(ev, gstate, rows, cols, kw, step):
     lib = _lib.load()
     need = lib.qste_coordinate_update_workspace_bytes(rows, cols, kw["block_size"])
     at = lib.qste_coordinate_update_scalars_offset(rows, cols, kw["block_size"])
-    assert 0 < at and at + 16 <= need
+    assert 0 <= at and at + 16 <= need
     work = torch.empty(need, dtype=torch.uint8, device=DEV)
     flips = torch.empty((), dtype=torch.int64, device=DEV)
     g = t(ev)
