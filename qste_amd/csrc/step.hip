@@ -1108,14 +1108,17 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(uint16_t* __restrict__
 
 // -- one-launch step --------------------------------------------------------------
 // Shapes with cols % 2048 == 0, a power-of-two block_size in 8..256 and at
-// most kMaxRows rows per workgroup run the whole step as one launch of one
-// workgroup per compute unit, every workgroup resident at once, with grid
-// barriers between the passes.  Workgroup b owns a strip: rows [r0, r1) of
-// one 2048-column group; wave w of it owns the strip's columns
+// most kMaxRows rows per workgroup run the whole step as one launch of
+// kPerCU workgroups per compute unit, every workgroup resident at once, with
+// grid barriers between the passes.  Workgroup b owns a strip: rows [r0, r1)
+// of one 2048-column group; wave w of it owns the strip's columns
 // 2048 cg + 256 w .. + 255, four consecutive columns per lane.  The first
-// kRegRows rows of a wave's strip stay in registers and the next lds_rows in
-// LDS from the statistics pass on, so the later passes read only the rest of
-// the evidence again (most of which the Infinity Cache still holds).
+// lds_rows rows of the strip stay in LDS from the statistics pass on; every
+// pass streams the other rows through buffer loads, two batches of kBatch
+// rows in flight per wave (registers go to loads in flight rather than to
+// holding evidence: with fewer loads in flight the passes wait on memory
+// latency), and walks them against the previous pass's direction so that it
+// starts on the rows the Infinity Cache received last.
 //
 //   A  row partials (per wave, combined over the waves in order) and column
 //      partials (per lane over the strip's rows in order)
@@ -1131,8 +1134,9 @@ __global__ __launch_bounds__(kThreads) void finish_kernel(uint16_t* __restrict__
 //      scales, sum of m^2
 //   -- barrier --
 //   D  step size; stochastic rounding, requantization, packing, flips; the
-//      new block scales into moment_scale
-//      the last workgroup to finish sums the flips.
+//      new block scales into moment_scale; one 64-bit atomic per workgroup
+//      adds its flips and its arrival, and the last to arrive writes the
+//      total.
 //
 // Every value that crosses workgroups (partials, factors) is written with
 // agent-scope atomic stores and read with agent-scope atomic loads, which are
