@@ -55,7 +55,6 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip per-kernel, step and GEMV timing")
     ap.add_argument("--no-configs", action="store_true", help="skip the config 2 and config 3 step lines")
-    ap.add_argument("--cpu-tokens", type=int, default=512)
     ap.add_argument("--configs-only", action="store_true",
                     help="only the config 2 and config 3 step lines (for a kernel profile of those workloads)")
     ap.add_argument("--pmc-calibrate", action="store_true",
@@ -308,6 +307,49 @@ class GPT2Small:
         return model.to(device=device, dtype=torch.bfloat16)
 
 
+def in_step_times(step, T, d, ffn, steps=3):
+    """Per-call time of the layers' forward and backward products inside the
+    training step: HIP events recorded on the current stream around every
+    ``packed_linear_affine`` and ``linear_backward`` call of ``steps`` steps
+    (events do not synchronize, so the step runs as it does untimed)."""
+
+    import torch
+
+    from qste_amd import kernels
+
+    records = []
+    originals = (kernels.packed_linear_affine, kernels.linear_backward)
+
+    def wrap(kind, fn):
+        def timed(*args, **kwargs):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            out = fn(*args, **kwargs)
+            b.record()
+            records.append((kind, args[0].shape[-1], a, b))
+            return out
+        return timed
+
+    kernels.packed_linear_affine = wrap("forward", originals[0])
+    kernels.linear_backward = wrap("backward_call", originals[1])
+    try:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    finally:
+        kernels.packed_linear_affine, kernels.linear_backward = originals
+    flop = 2.0 * T * ffn * d  # one product at any of the three shapes
+    out = {}
+    for kind, products in (("forward", 1), ("backward_call", 2)):
+        times = [a.elapsed_time(b) for k, _, a, b in records if k == kind]
+        if not times:
+            continue
+        ms = sum(times) / len(times)
+        out[kind] = {"ms": round(ms, 4), "calls": len(times), "tflops": round(products * flop / ms / 1e9, 2),
+                     "frac_of_mfma_peak": round(products * flop / (ms * 1e-3) / MFMA_BF16_PEAK, 4)}
+    return out
+
+
 def config_steps(device):
     """Configs 2 and 3 (fwd+bwd+step), reported beside the headline."""
 
@@ -329,12 +371,13 @@ def config_steps(device):
         model(x).backward(dy)
         coords.step()
 
-    ms = timed_median(step2, 15)
+    ms, mean, worst = timed_median(step2, 15)
     flop = 6.0 * 8192 * (2 * 4096 * 1024)
-    out["cfg2_relu_mlp"] = {"ms_per_step": round(ms, 3), "tflops": round(flop / ms / 1e9, 2),
+    out["cfg2_relu_mlp"] = {"ms_per_step": round(ms, 3), "mean_ms": round(mean, 3), "max_ms": round(worst, 3),
+                            "tflops": round(flop / ms / 1e9, 2),
                             "frac_of_mfma_peak": round(flop / (ms * 1e-3) / MFMA_BF16_PEAK, 4),
                             "tokens": 8192, "d": 1024, "ffn": 4096,
-                            "timing": "median of 15 steps, each host-clocked and synchronized"}
+                            "timing": "median (mean, max) of 15 steps, each host-clocked and synchronized"}
     del model, coords, x, dy
     # config 3: GPT-2 small, batch 8 x 1024 random ids, AdamW + QSTEOptimizer
     model = GPT2Small(device=device)
@@ -349,12 +392,13 @@ def config_steps(device):
         coords.step()
         adam.zero_grad(set_to_none=True)
 
-    ms = timed_median(step3, 10, warmup=3)
+    ms, mean, worst = timed_median(step3, 10, warmup=3)
     tokens = 8 * 1023
     mlp_flop = 6.0 * tokens * 12 * (2 * 3072 * 768)
-    out["cfg3_gpt2_small"] = {"ms_per_step": round(ms, 3), "tokens_per_s": round(tokens / ms * 1e3, 1),
+    out["cfg3_gpt2_small"] = {"ms_per_step": round(ms, 3), "mean_ms": round(mean, 3), "max_ms": round(worst, 3),
+                              "tokens_per_s": round(tokens / ms * 1e3, 1),
                               "mlp_fwd_bwd_flop": mlp_flop, "batch": 8, "seq": 1024,
-                              "timing": "median of 10 steps, each host-clocked and synchronized",
+                              "timing": "median (mean, max) of 10 steps, each host-clocked and synchronized",
                               "note": "whole training step; MLPs QSTE with packed tanh-GELU, attention and head bf16 (SDPA flash/efficient)"}
     return out
 
@@ -378,7 +422,8 @@ def timed_median(fn, iters, warmup=2):
     """Median milliseconds of ``fn`` over ``iters`` calls, each timed by the
     host clock between synchronizations (steps that end in a host read of
     the flip count synchronize anyway; the median keeps a host stall in one
-    step out of a host-bound config's figure)."""
+    step out of a host-bound config's figure), with the mean and maximum of
+    the same per-step times."""
 
     import statistics
 
@@ -393,7 +438,7 @@ def timed_median(fn, iters, warmup=2):
         fn()
         torch.cuda.synchronize()
         times.append((time.perf_counter() - t0) * 1e3)
-    return statistics.median(times)
+    return statistics.median(times), statistics.mean(times), max(times)
 
 
 def timed_events(fn, iters, stream=None, warm=3):
@@ -656,19 +701,136 @@ def decode_gemv(device, K=8192, N=28672, copies=10):
                         "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / HBM_PEAK, 4),
                         "timing": f"graph replay of {reps * copies} launches over {copies} weight copies"}
         del graph
+    # the floor: a plain streaming read of the same weight copies, replayed
+    # from a graph the same way (every kernel that reads these bytes once,
+    # launch included, takes at least this long)
+    def reads():
+        for i in range(copies):
+            kernels.stream_read(weights[i])
+
+    reads()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            reads()
+    ms = timed_events(graph.replay, 4) / (reps * copies)
+    nbytes = N * pb
+    res["read_floor"] = {"us": round(ms * 1e3, 2), "bytes": nbytes, "gbps": round(nbytes / ms / 1e6, 1),
+                         "timing": f"graph replay of {reps * copies} qste_stream_read launches over the "
+                                   f"{copies} weight copies"}
+    del graph
+    # back-to-back empty launches in the same harness: the fixed cost per launch
+    empty = torch.empty(16, dtype=torch.uint8, device=device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps * copies):
+            kernels.stream_read(empty, groups=1)
+    ms = timed_events(graph.replay, 4) / (reps * copies)
+    res["launch_floor_us"] = round(ms * 1e3, 2)
+    del graph
     return res
 
 
-def cpu_baseline(d, ffn, tokens, full_tokens=16384):
+def device_report(device, T, d, ffn):
+    """What the runtime reports (compute units, maximum clocks), the shader
+    clock one wave measures at idle, and the clock rocm-smi reads while the
+    evidence product runs back to back (the chip is power-limited under the
+    GEMMs, so their clock is below the maximum)."""
+
+    import subprocess
+    import threading
+
+    import torch
+
+    from qste_amd import kernels
+
+    info = kernels.device_info(device)
+    out = {"arch": getattr(torch.cuda.get_device_properties(device), "gcnArchName", "?").split(":")[0],
+           "cus": info["cus"], "max_sclk_mhz": info["max_sclk_mhz"], "mclk_mhz": info["mclk_mhz"],
+           "lds_per_cu": info["lds_per_cu"], "sclk_idle_probe_mhz": round(kernels.measured_sclk_mhz(device), 1)}
+    smi = "/opt/rocm/bin/rocm-smi"
+    if not os.path.exists(smi):
+        out["sclk_under_gemm_mhz"] = None
+        return out
+    g = torch.Generator(device=device).manual_seed(11)
+    dy = torch.randn(T, ffn, generator=g, device=device).to(torch.bfloat16)
+    xs = torch.randn(T, d, generator=g, device=device).to(torch.bfloat16)
+    packed_x, _, x_scale = kernels.pack_affine_rows(xs)
+    samples = []
+    stop = threading.Event()
+
+    def sample():
+        while not stop.is_set():
+            try:
+                res = subprocess.run([smi, "--showclocks", "--json"], capture_output=True, text=True, timeout=10)
+                data = json.loads(res.stdout)
+                for card in data.values():
+                    for key, val in card.items():
+                        if "sclk" in key.lower() and "mhz" in str(val).lower():
+                            samples.append(float(str(val).strip("()Mhz ").split("Mhz")[0].strip("(")))
+            except Exception:
+                return
+
+    # the evidence product (the dominant GEMM kind) back to back for ~2 s
+    run = lambda: kernels.evidence_from_packed(dy, packed_x, d, row_scale=x_scale)  # noqa: E731
+    run()
+    torch.cuda.synchronize()
+    th = threading.Thread(target=sample, daemon=True)
+    t0 = time.perf_counter()
+    th.start()
+    launches = 0
+    while time.perf_counter() - t0 < 2.0:
+        for _ in range(50):
+            run()
+        launches += 50
+        torch.cuda.synchronize()
+    stop.set()
+    th.join(timeout=15)
+    busy = sorted(samples)
+    out["sclk_under_gemm_mhz"] = {"samples": len(busy), "min": busy[0] if busy else None,
+                                  "median": busy[len(busy) // 2] if busy else None,
+                                  "max": busy[-1] if busy else None,
+                                  "load": f"{launches} evidence products at {ffn} x {d} x {T} tokens, sampled by "
+                                          "rocm-smi --showclocks"}
+    return out
+
+
+def memory_bandwidth(device, pair_bytes=256 << 20, pairs=3):
+    """Measured HBM rates with buffers rotated over more than the 256 MB
+    Infinity Cache: a device copy (torch copy_, read + write bytes) and a
+    plain streaming read (qste_stream_read)."""
+
+    import torch
+
+    from qste_amd import kernels
+
+    src = [torch.empty(pair_bytes, dtype=torch.uint8, device=device).fill_(i + 1) for i in range(pairs)]
+    dst = [torch.empty(pair_bytes, dtype=torch.uint8, device=device) for _ in range(pairs)]
+    reps = 4
+
+    def copy_all():
+        for i in range(pairs):
+            dst[i].copy_(src[i])
+
+    ms = timed_events(copy_all, reps) / pairs
+    read_ms = timed_events(lambda: [kernels.stream_read(t) for t in src + dst], reps) / (2 * pairs)
+    return {"copy": {"gbps": round(2 * pair_bytes / ms / 1e6, 1), "bytes_per_copy": pair_bytes,
+                     "rotation": f"{pairs} pairs of {pair_bytes >> 20} MiB"},
+            "read": {"gbps": round(pair_bytes / read_ms / 1e6, 1), "bytes_per_read": pair_bytes,
+                     "rotation": f"{2 * pairs} buffers of {pair_bytes >> 20} MiB"}}
+
+
+def cpu_baseline(d, ffn, tokens=16384, warm_tokens=512):
     """Config 4 on this host's cores with the port of the reference's CPU
     backend (oracle/cpu_baseline.py): LUT tile expansion + torch's fp32 GEMMs,
     OpenMP encodings and four-pass coordinate steps.
 
-    The token-proportional work (the three forwards with their encodings,
-    the SwiGLU, every backward product) is timed on ``tokens`` of the
-    workload's tokens and scaled to all of them; the three coordinate steps
-    (3 x ffn x d elements, the same cost at any token count) are timed in
-    full.  ``value`` is config 4's FLOPs over that estimated step time."""
+    One whole training step at the full token count: the three forwards with
+    their encodings, the SwiGLU, every backward product (each layer's input
+    gradient included) and the three coordinate steps on the evidence that
+    backward produced, after one warm-up pass of the products on
+    ``warm_tokens`` tokens.  ``value`` is config 4's FLOPs over that time."""
 
     import numpy as np
     import torch
@@ -678,37 +840,30 @@ def cpu_baseline(d, ffn, tokens, full_tokens=16384):
     threads = cb.set_threads(cb.default_threads())
     rng = np.random.default_rng(0)
     g = torch.Generator().manual_seed(0)
-    x = torch.randn(tokens, d, generator=g)
-    dy = torch.randn(tokens, d, generator=g)
     shapes = ((ffn, d), (ffn, d), (d, ffn))
     layers = []
     for rows, cols in shapes:
         coord = rng.integers(-127, 128, size=(rows, cols), dtype=np.int8)
         scale = (np.abs(rng.standard_normal(rows)) * 0.01).astype(np.float32)
         layers.append(cb.Surface(coord, scale))
-    cb.swiglu_products(x, dy, layers)  # warm the BLAS and the thread pool
-    iters, t0 = 0, time.perf_counter()
-    while True:
-        cb.swiglu_products(x, dy, layers)
-        iters += 1
-        if time.perf_counter() - t0 > 8.0 or iters >= 20:
-            break
-    t_tokens = (time.perf_counter() - t0) / iters
-    evidence = [torch.randn(rows, cols, generator=g).mul_(0.01) for rows, cols in shapes]
-    t_step = 0.0
+    cb.swiglu_products(torch.randn(warm_tokens, d, generator=g), torch.randn(warm_tokens, d, generator=g),
+                       layers)  # warm the BLAS and the thread pool
+    x = torch.randn(tokens, d, generator=g)
+    dy = torch.randn(tokens, d, generator=g)
+    t0 = time.perf_counter()
+    evidence = cb.swiglu_products(x, dy, layers)
+    t_products = time.perf_counter() - t0
+    t1 = time.perf_counter()
     for k, (layer, ev) in enumerate(zip(layers, evidence)):
-        work = ev.clone()  # the step consumes its evidence as scratch
-        t1 = time.perf_counter()
-        layer.step(work, seed=1 + 1_000_003 * k, step=0)
-        t_step += time.perf_counter() - t1
-    secs = t_tokens * (full_tokens / tokens) + t_step
-    flop = 6.0 * full_tokens * (2 * ffn * d + d * ffn)
+        layer.step(ev, seed=1 + 1_000_003 * k, step=0)  # the step consumes its evidence as scratch
+    t_step = time.perf_counter() - t1
+    secs = t_products + t_step
+    flop = 6.0 * tokens * (2 * ffn * d + d * ffn)
     return {"value": round(flop / secs / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "cpu_model": cb.cpu_model(),
-            "sample": f"cfg4 SwiGLU d={d} ffn={ffn}, fp32: token-proportional work timed on {tokens} of "
-                      f"{full_tokens} tokens ({t_tokens * 1e3:.1f} ms per pass, {iters} passes) and scaled "
-                      f"to {full_tokens}; the three coordinate steps timed in full ({t_step * 1e3:.1f} ms, "
-                      f"token-independent); estimated step {secs:.2f} s on {threads} threads"}
+            "cpu_model": cb.cpu_model(), "seconds_per_step": round(secs, 3),
+            "sample": f"one whole cfg4 SwiGLU step (d={d}, ffn={ffn}, {tokens} tokens, fp32): forward, backward "
+                      f"products {t_products:.2f} s, the three coordinate steps {t_step:.2f} s, on {threads} "
+                      f"threads, after a warm-up pass of the products on {warm_tokens} tokens"}
 
 
 def main():
@@ -780,7 +935,9 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) activations and gradients, U{-127..127} int8 coordinates)",
         "config": {"workload": "cfg4 Llama-3-8B SwiGLU MLP fwd+bwd+coordinate step",
-                   "tokens": T, "d": d, "ffn": ffn, "layers": 3, "flop_per_step": flop},
+                   "tokens": T, "d": d, "ffn": ffn, "layers": 3, "flop_per_step": flop,
+                   "gate": "qste_amd.nn.swiglu (one fused kernel each way, values and gradients equal to "
+                           "F.silu(g) * u bit for bit); the step with torch's silu and mul is step_torch_gate_ms"},
         "frac_of_mfma_peak": round(flop / secs / MFMA_BF16_PEAK, 4),
     }
     if not args.no_extras:
@@ -798,7 +955,15 @@ def main():
                             "frac": round(dk["tflops"] * 1e12 / MFMA_BF16_PEAK, 4),
                             "traffic": None if traffic is None else int(traffic),
                             "launches": launches[dominant]}
+        # the same products inside the training step (the chip is power-limited
+        # there, so they run slower than back to back in isolation)
+        line["in_step"] = in_step_times(step, T, d, ffn)
+        if "backward_call" in line["in_step"]:
+            line["roofline"]["in_step_backward_call_frac"] = line["in_step"]["backward_call"]["frac_of_mfma_peak"]
+            line["roofline"]["isolated_backward_call_frac"] = kernels_t["backward_call"]["frac_of_mfma_peak"]
         line["kernels"] = kernels_t
+        line["device"] = device_report(device, T, d, ffn)
+        line["memory_bandwidth"] = memory_bandwidth(device)
         line["vendor_dense_bf16_gemm"] = vendor_dense(T, d, ffn, device)
         line["fp32_products"] = fp32_products(device)
         line["coordinate_step"] = step_bandwidth(ffn, d, device)
@@ -827,7 +992,7 @@ def main():
             line["configs"] = config_steps(device)
     line["cfg1"] = cfg1_lines(device, cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(d, ffn, args.cpu_tokens)
+        line["cpu_baseline"] = cpu_baseline(d, ffn, T)
     print(json.dumps(line), flush=True)
 
 

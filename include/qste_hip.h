@@ -219,6 +219,23 @@ size_t qste_coordinate_update_scalars_offset(int64_t rows, int64_t cols, int64_t
  * takes the multi-launch path (vector-aligned operands are needed too).
  * Both give the same results bit for bit.  No counterpart in the reference. */
 int qste_coordinate_update_one_launch(int64_t rows, int64_t cols, int64_t block_size);
+
+/* Measurement probes; no counterpart in the reference (bench.py and
+ * qste_amd.device_profile() use them).
+ * qste_stream_read: a plain streaming read of `bytes` (a multiple of 16, from
+ * a 16-byte aligned device pointer) by `groups` workgroups of 256 threads,
+ * each reading a contiguous share with eight 16-byte loads in flight per
+ * thread -- the time any kernel that reads those bytes once can approach.
+ * `sink` (groups * 256 words) is written only in an unlikely case.
+ * qste_clock_probe: one wave runs `spins` dependent integer steps and stores
+ * the shader-clock cycles (s_memtime) and 100 MHz real-time ticks
+ * (s_memrealtime) they took in out[0], out[1] (device int64[3]). */
+int qste_stream_read(const void* src, int64_t bytes, uint32_t* sink, int64_t groups, void* stream);
+int qste_clock_probe(int64_t* out, int64_t spins, void* stream);
+/* What the runtime reports for the current device, into host int64[4]:
+ * compute units, maximum shader clock (kHz), memory clock (kHz), LDS bytes
+ * per compute unit.  No counterpart in the reference. */
+int qste_device_info(int64_t* out);
 int qste_coordinate_update(const float* evidence, int8_t* coordinate, uint8_t* packed,
                            int8_t* moment_q, uint16_t* moment_scale, uint16_t* row_v,
                            uint16_t* col_v, int64_t rows, int64_t cols, double beta1,

@@ -38,6 +38,7 @@ __all__ = [
     "QSTEOptimizer",
     "Surface",
     "coerce_config",
+    "device_profile",
     "continuous_parameters",
     "convert",
     "export_packed",
@@ -59,3 +60,15 @@ def kernel_status() -> dict:
     from . import kernels
 
     return kernels.status()
+
+
+def device_profile(device=None) -> str:
+    """What this build runs on a device, as one line (reference
+    src/qste/__init__.py:105-120): device and architecture, compute units,
+    shader clock (reported maximum and measured now), HBM and LDS sizes, the
+    HIP library's version and the kernel each operator takes.  Without a GPU
+    the line says that qste_amd has no CPU path."""
+
+    from . import kernels
+
+    return kernels.profile(device)

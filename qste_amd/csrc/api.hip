@@ -23,6 +23,9 @@ size_t coordinate_update_workspace(int64_t, int64_t, int64_t);
 size_t coordinate_update_scalars_offset(int64_t, int64_t, int64_t);
 size_t coordinate_update_static_limit();
 int coordinate_update_one_launch(int64_t, int64_t, int64_t);
+int launch_stream_read(const void*, int64_t, uint32_t*, int64_t, hipStream_t);
+int launch_clock_probe(int64_t*, int64_t, hipStream_t);
+int device_info(int64_t*);
 int launch_coordinate_update_static(const float*, int8_t*, uint8_t*, int8_t*, uint16_t*, uint16_t*, uint16_t*,
                                     int64_t, int64_t, double, double, double, double, int64_t, int64_t, int64_t,
                                     const int64_t*, int64_t*, const uint8_t*, hipStream_t);
@@ -477,6 +480,19 @@ size_t qste_coordinate_update_scalars_offset(int64_t rows, int64_t cols, int64_t
 
 int qste_coordinate_update_one_launch(int64_t rows, int64_t cols, int64_t block_size) {
   return coordinate_update_one_launch(rows, cols, block_size);
+}
+
+int qste_stream_read(const void* src, int64_t bytes, uint32_t* sink, int64_t groups, void* stream) {
+  return launch_stream_read(src, bytes, sink, groups, as_stream(stream));
+}
+
+int qste_clock_probe(int64_t* out, int64_t spins, void* stream) {
+  return launch_clock_probe(out, spins, as_stream(stream));
+}
+
+int qste_device_info(int64_t* out) {
+  if (!out) return QSTE_E_NULL;
+  return device_info(out);
 }
 
 int qste_coordinate_update(const float* evidence, int8_t* coordinate, uint8_t* packed, int8_t* moment_q,

@@ -169,6 +169,75 @@ def status() -> dict:
     }
 
 
+def stream_read(src: Tensor, groups: int | None = None) -> None:
+    """A plain streaming read of ``src``'s bytes (measurement probe, no
+    counterpart in the reference): the floor for any kernel reading them once."""
+
+    device = _require_gpu(src)
+    if not src.is_contiguous() or src.numel() * src.element_size() % 16:
+        raise ValueError("stream_read needs a contiguous tensor of a multiple of 16 bytes")
+    props = torch.cuda.get_device_properties(device)
+    groups = int(groups or 4 * props.multi_processor_count)
+    sink = torch.empty(groups * 256, dtype=torch.int32, device=device)
+    lib = _lib.load()
+    _lib.check(lib.qste_stream_read(_ptr(src), src.numel() * src.element_size(), _ptr(sink), groups,
+                                    _stream(device)), "stream_read")
+
+
+def device_info(device=None) -> dict:
+    """What the runtime reports for ``device``: compute units, maximum shader
+    clock and memory clock (MHz), LDS bytes per compute unit."""
+
+    import ctypes
+
+    device = torch.device(device or "cuda")
+    out = (ctypes.c_int64 * 4)()
+    with torch.cuda.device(device):
+        _lib.check(_lib.load().qste_device_info(ctypes.cast(out, ctypes.c_void_p)), "device_info")
+    return {"cus": int(out[0]), "max_sclk_mhz": out[1] / 1000.0, "mclk_mhz": out[2] / 1000.0,
+            "lds_per_cu": int(out[3])}
+
+
+def measured_sclk_mhz(device=None, spins: int = 1 << 18) -> float:
+    """Shader clock one wave sees right now, in MHz: s_memtime cycles over
+    s_memrealtime (100 MHz) ticks across a dependent integer loop."""
+
+    device = torch.device(device or "cuda")
+    out = torch.zeros(3, dtype=torch.int64, device=device)
+    lib = _lib.load()
+    _lib.check(lib.qste_clock_probe(_ptr(out), int(spins), _stream(device)), "clock_probe")
+    cycles, ticks, _ = (int(v) for v in out.cpu().tolist())
+    return cycles / ticks * 100.0 if ticks > 0 else float("nan")
+
+
+def profile(device=None) -> str:
+    """One line: what this build runs on ``device`` (reference
+    ``kernels.profile(device).describe()``, src/qste/kernels/device.py:85-91).
+
+    Nothing is autotuned: the kernels are written for gfx950 and take their
+    grid sizes from the compute-unit count the runtime reports.  The line
+    names the device and architecture, that count, the shader clock (the
+    maximum the runtime reports and the one a wave measures now), HBM and LDS
+    sizes, the library version, and which kernel each operator takes."""
+
+    device = torch.device(device) if device is not None else torch.device(
+        "cuda" if torch.cuda.is_available() else "cpu")
+    version = _lib.load().qste_version() if native_available() else None
+    if device.type != "cuda":
+        return (f"{device} [no QSTE kernels: qste_amd runs on gfx950 GPUs only]  "
+                f"library={'libqste_hip v%d' % version if version is not None else 'not built'}")
+    props = torch.cuda.get_device_properties(device)
+    arch = getattr(props, "gcnArchName", "?").split(":")[0]
+    info = device_info(device)
+    now_mhz = measured_sclk_mhz(device)
+    return (f"{props.name} [{arch}]  cus={info['cus']}  "
+            f"sclk={info['max_sclk_mhz']:.0f}MHz max / {now_mhz:.0f}MHz measured  "
+            f"hbm={props.total_memory / 2**30:.0f}GiB  lds={info['lds_per_cu'] / 1024:.0f}KiB/CU  "
+            f"library=libqste_hip v{version}  "
+            "(products: bf16/fp16 MFMA 256x256 tiles, fp32 as three bf16 limbs; decode M<=16: biased-operand "
+            "MFMA; coordinate step: one launch for columns % 2048 == 0, else six)")
+
+
 # ---------------------------------------------------------------------------
 # operators (reference: src/qste/kernels/loader.py:247-368)
 # ---------------------------------------------------------------------------

@@ -53,6 +53,9 @@ SIGNATURES = {
     "qste_coordinate_update_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "qste_coordinate_update_scalars_offset": (_sz, [_i64, _i64, _i64]),
     "qste_coordinate_update_one_launch": (_int, [_i64, _i64, _i64]),
+    "qste_stream_read": (_int, [_vp, _i64, _vp, _i64, _vp]),
+    "qste_clock_probe": (_int, [_vp, _i64, _vp]),
+    "qste_device_info": (_int, [_vp]),
     "qste_coordinate_update_static_limit": (_sz, []),
     "qste_coordinate_update_static": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _dbl, _dbl,
                                              _dbl, _dbl, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
