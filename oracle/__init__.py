@@ -84,7 +84,7 @@ def lib():
         handle.qo_coordinate_update.restype = _i64
         handle.qo_coordinate_update.argtypes = [
             _f32p, _i8p, _u8p, _i8p, _u16p, _u16p, _u16p, _i64, _i64,
-            _dbl, _dbl, _dbl, _dbl, _i64, _i64, _i64, _vp, _vp, _vp,
+            _dbl, _dbl, _dbl, _dbl, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
         ]
         handle.qo_step_size.restype = ctypes.c_float
         handle.qo_step_size.argtypes = [ctypes.c_float, _dbl]
@@ -268,14 +268,17 @@ def step_size(moment_rms: float, coordinate_lr: float) -> np.float32:
 
 
 def coordinate_update(grad, state: dict, *, beta1, beta2, update_clip, coordinate_lr,
-                      block_size, seed, step, margins: bool = False, scalars=None):
+                      block_size, seed, step, margins: bool = False, scalars=None,
+                      scale_margin=None):
     """Run the spec step on numpy state in place; returns flips (and margins).
 
     ``state`` holds ``coordinate`` (int8 [R,C]), ``packed`` (uint8 [R,PB]),
     ``moment_q`` (int8 [R,C]), and ``moment_scale`` / ``row_v`` / ``col_v`` as
     float16 arrays (their bit patterns are updated through a uint16 view).
     ``scalars``, a float32 array of 4, receives sqrt(mean row statistic),
-    the clip divisor, the step size and the momentum RMS.
+    the clip divisor, the step size and the momentum RMS.  ``scale_margin``,
+    a float32 array of one value per block, receives each block's distance
+    in fp16 ulps of amax / 127 from the fp16 rounding midpoint.
     """
 
     g = np.array(grad, dtype=np.float32, order="C", copy=True)
@@ -286,6 +289,10 @@ def coordinate_update(grad, state: dict, *, beta1, beta2, update_clip, coordinat
     if scalars is not None and (scalars.dtype != np.float32 or scalars.size < 4
                                 or not scalars.flags["C_CONTIGUOUS"]):
         raise ValueError("scalars must be a contiguous float32 array of at least 4")
+    blocks = -(-rows * cols // int(block_size))
+    if scale_margin is not None and (scale_margin.dtype != np.float32 or scale_margin.size < blocks
+                                     or not scale_margin.flags["C_CONTIGUOUS"]):
+        raise ValueError(f"scale_margin must be a contiguous float32 array of at least {blocks}")
     tm = np.empty((rows, cols), dtype=np.float32) if margins else None
     mm = np.empty((rows, cols), dtype=np.float32) if margins else None
     flips = lib().qo_coordinate_update(
@@ -293,7 +300,7 @@ def coordinate_update(grad, state: dict, *, beta1, beta2, update_clip, coordinat
         state["moment_scale"].view(np.uint16), state["row_v"].view(np.uint16),
         state["col_v"].view(np.uint16), rows, cols, float(beta1), float(beta2),
         float(update_clip), float(coordinate_lr), int(block_size), _wrap64(seed),
-        _wrap64(step), _ptr(tm), _ptr(mm), _ptr(scalars),
+        _wrap64(step), _ptr(tm), _ptr(mm), _ptr(scalars), _ptr(scale_margin),
     )
     if margins:
         return int(flips), tm, mm

@@ -279,6 +279,11 @@ float qo_step_size(float moment_rms, double coordinate_lr) {
 /* move the decision.                                                        */
 /*   scalars_out[0..3] = sqrt(mean clamped row statistic), RMS-clip divisor, */
 /*                      step size (qo_step_size), momentum RMS.              */
+/*   scale_margin[b]  = the distance, in fp16 ulps, of block b's fp32 scale  */
+/*                      amax / 127 from the midpoint between its two fp16    */
+/*                      neighbours: the tie a one-ulp difference in amax can */
+/*                      cross, moving the stored scale (and so every q of    */
+/*                      the block) by one.                                   */
 /* ------------------------------------------------------------------------ */
 
 int64_t qo_coordinate_update(float* grad, int8_t* coord, uint8_t* packed, int8_t* moment_q,
@@ -286,7 +291,7 @@ int64_t qo_coordinate_update(float* grad, int8_t* coord, uint8_t* packed, int8_t
                              int64_t rows, int64_t cols, double beta1, double beta2,
                              double update_clip, double coordinate_lr, int64_t block_size,
                              int64_t seed, int64_t step, float* target_margin,
-                             float* moment_margin, float* scalars_out) {
+                             float* moment_margin, float* scalars_out, float* scale_margin) {
   const int64_t count = rows * cols;
   const int64_t blocks = (count + block_size - 1) / block_size;
   const int64_t padded = blocks * block_size;
@@ -402,6 +407,14 @@ int64_t qo_coordinate_update(float* grad, int8_t* coord, uint8_t* packed, int8_t
     float s_new = fmaxf(amax, (float)1e-6) / 127.0f;
     uint16_t h = qo_float_to_half(s_new);
     moment_scale[b] = h;
+    if (scale_margin) {
+      /* fp16 keeps 11 significant bits; below 2^-14 its spacing is 2^-24 */
+      int e;
+      frexpf(s_new, &e);
+      const double ulp = ldexp(1.0, (e - 11) < -24 ? -24 : (e - 11));
+      const double pos = (double)s_new / ulp - floor((double)s_new / ulp);
+      scale_margin[b] = (float)fabs(pos - 0.5);
+    }
     float decode = fmaxf(qo_half_to_float(h), (float)1e-12);
     for (int64_t j = 0; j < block_size; ++j) {
       int64_t i = b * block_size + j;

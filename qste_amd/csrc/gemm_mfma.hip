@@ -1371,8 +1371,14 @@ __global__ __launch_bounds__(256) void split_kernel(const float* __restrict__ x,
     float v = x[i];
     if (row_mul) v = v * row_mul[r];
     if (col_mul) v = v * col_mul[c];
-    const uint16_t hi = f32_to_bf16(v);
-    const float r1 = v - bf16_to_f32(hi);
+    uint16_t hi = f32_to_bf16(v);
+    const bool finite = __builtin_isfinite(v);
+    // a finite value that rounds past bf16's largest finite one keeps its
+    // top 16 bits instead (truncation: the residual is exact as well); an
+    // infinite or NaN value is carried by hi alone, its other limbs zero,
+    // so the products see the same inf or NaN the fp32 operand holds
+    if (finite && (hi & 0x7F80u) == 0x7F80u) hi = static_cast<uint16_t>(__float_as_uint(v) >> 16);
+    const float r1 = finite ? v - bf16_to_f32(hi) : 0.0f;
     const uint16_t mid = f32_to_bf16(r1);
     const float r2 = r1 - bf16_to_f32(mid);
     const uint16_t lo = f32_to_bf16(r2);
@@ -1415,97 +1421,141 @@ int launch_transpose_bits(const uint8_t*, uint8_t*, int64_t, int64_t, int64_t, i
 // fill 256-row tiles; below that the fp32 SIMT kernels are as fast)
 static bool f32_limbs_worth(int64_t m) { return m >= 128; }
 
+// The limbs of the dense operand (6 bytes per fp32 value) are held to this
+// many bytes of workspace: the forward and dX products run over chunks of
+// output rows whose limbs fit it, and an evidence product whose limbs do not
+// fit takes the fp32 SIMT kernels.
+constexpr size_t kLimbBudget = static_cast<size_t>(512) << 20;
+
+// Output rows per chunk of a product over k: all m when they fit the budget,
+// else a multiple of the 256-row tile (0 when not even one tile fits).
+static int64_t f32_chunk_rows(int64_t m, int64_t k) {
+  const int64_t fit = static_cast<int64_t>(kLimbBudget / (static_cast<size_t>(k) * 3 * 2));
+  return fit >= m ? m : fit / mfma::wide::BM * mfma::wide::BM;
+}
+
 static SplitK f32_forward_split(int64_t m, int64_t rows, int64_t cols) {
   return forward_split_plan(wide_grid(m, rows), static_cast<int>(3 * cols / mfma::wide::BK));
 }
 
-size_t f32_forward_workspace(int64_t m, int64_t rows, int64_t cols) {
-  if (m <= 0 || rows <= 0 || cols <= 0 || cols % 64 != 0 || !f32_limbs_worth(m)) return 0;
+static size_t f32_forward_partial(int64_t m, int64_t rows, int64_t cols) {
   const SplitK sp = f32_forward_split(m, rows, cols);
-  const size_t partial = sp.splits > 1 ? static_cast<size_t>(sp.splits) * wide_grid(m, rows) *
-                                             mfma::wide::BM * mfma::wide::BN * sizeof(float)
-                                       : 0;
-  return limbs::up256(static_cast<size_t>(m) * 3 * cols * 2) + limbs::up256(static_cast<size_t>(rows) * 3 * cols / 8) +
-         partial;
+  return sp.splits > 1 ? static_cast<size_t>(sp.splits) * wide_grid(m, rows) * mfma::wide::BM * mfma::wide::BN *
+                             sizeof(float)
+                       : 0;
 }
 
-// y [m, rows] fp32 = (x @ sign^T) * scale + bias through the limbs.  Returns
-// 1 when the call is not for this path (shape, or too little workspace).
+size_t f32_forward_workspace(int64_t m, int64_t rows, int64_t cols) {
+  if (m <= 0 || rows <= 0 || cols <= 0 || cols % 64 != 0 || !f32_limbs_worth(m)) return 0;
+  const int64_t mc = f32_chunk_rows(m, cols);
+  if (mc == 0) return 0;
+  // the split-K partials of a full chunk or of the last, shorter one
+  size_t partial = f32_forward_partial(mc, rows, cols);
+  if (m % mc) {
+    const size_t tail = f32_forward_partial(m % mc, rows, cols);
+    if (tail > partial) partial = tail;
+  }
+  return limbs::up256(static_cast<size_t>(mc) * 3 * cols * 2) +
+         limbs::up256(static_cast<size_t>(rows) * 3 * cols / 8) + partial;
+}
+
+// y [m, rows] fp32 = (x @ sign^T) * scale + bias through the limbs, over
+// chunks of f32_chunk_rows rows of x.  Returns 1 when the call is not for
+// this path (shape, or too little workspace).
 int mfma_f32_forward(const float* x, const uint8_t* packed, const float* scale, const float* bias, float* y,
                      int64_t m, int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes,
                      hipStream_t stream) {
   const size_t need = f32_forward_workspace(m, rows, cols);
   if (need == 0 || !workspace || workspace_bytes < need) return 1;
-  const int64_t k3 = 3 * cols, kb = cols / 8;
-  if (!fits32(m * k3 * 2) || !fits32(rows * k3 / 8)) return 1;
+  const int64_t k3 = 3 * cols, kb = cols / 8, mc = f32_chunk_rows(m, cols);
+  if (!fits32(mc * k3 * 2) || !fits32(rows * k3 / 8)) return 1;
   uint16_t* a = static_cast<uint16_t*>(workspace);
-  uint8_t* b = static_cast<uint8_t*>(workspace) + limbs::up256(static_cast<size_t>(m) * k3 * 2);
-  limbs::split_kernel<<<limbs::grid_for(m * cols), 256, 0, stream>>>(x, m, cols, nullptr, nullptr, a, k3, cols);
+  uint8_t* b = static_cast<uint8_t*>(workspace) + limbs::up256(static_cast<size_t>(mc) * k3 * 2);
+  float* partial = reinterpret_cast<float*>(b + limbs::up256(static_cast<size_t>(rows) * k3 / 8));
   limbs::repeat_kernel<<<limbs::grid_for(rows * kb), 256, 0, stream>>>(packed, rows, kb, kb, b, 3 * kb, kb);
-  mfma::Params p{};
-  p.a = a;
-  p.bits = b;
-  p.out = y;
-  p.M = m; p.N = rows; p.K = k3;
-  p.lda = k3; p.pb = 3 * kb;
-  p.a_rows = m; p.bit_rows = rows;
-  p.n_scale = scale; p.n_bias = bias;
-  const SplitK sp = f32_forward_split(m, rows, cols);
-  const int tiles = wide_grid(m, rows);
-  if (sp.splits > 1) {
-    float* partial = reinterpret_cast<float*>(b + limbs::up256(static_cast<size_t>(rows) * k3 / 8));
-    mfma::wide::forward_split_kernel<QSTE_BF16>
-        <<<tiles * sp.splits, mfma::wide::THREADS, 0, stream>>>(p, tiles, sp.ks_steps, partial);
-    int rc = static_cast<int>(hipGetLastError());
+  for (int64_t i0 = 0; i0 < m; i0 += mc) {
+    const int64_t mi = m - i0 < mc ? m - i0 : mc;
+    float* yi = y + i0 * rows;
+    limbs::split_kernel<<<limbs::grid_for(mi * cols), 256, 0, stream>>>(x + i0 * cols, mi, cols, nullptr, nullptr, a,
+                                                                        k3, cols);
+    mfma::Params p{};
+    p.a = a;
+    p.bits = b;
+    p.out = yi;
+    p.M = mi; p.N = rows; p.K = k3;
+    p.lda = k3; p.pb = 3 * kb;
+    p.a_rows = mi; p.bit_rows = rows;
+    p.n_scale = scale; p.n_bias = bias;
+    const SplitK sp = f32_forward_split(mi, rows, cols);
+    const int tiles = wide_grid(mi, rows);
+    if (sp.splits > 1) {
+      mfma::wide::forward_split_kernel<QSTE_BF16>
+          <<<tiles * sp.splits, mfma::wide::THREADS, 0, stream>>>(p, tiles, sp.ks_steps, partial);
+      int rc = static_cast<int>(hipGetLastError());
+      if (rc) return rc;
+      const dim3 grid(mfma::wide::BM / (mfma::wide::THREADS / kWave), static_cast<unsigned>(tiles));
+      mfma::wide::forward_combine_kernel<QSTE_F32>
+          <<<grid, mfma::wide::THREADS, 0, stream>>>(partial, tiles, sp.splits, scale, bias, yi, mi, rows);
+    } else {
+      mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD_F32, QSTE_BF16>
+          <<<tiles, mfma::wide::THREADS, 0, stream>>>(p);
+    }
+    const int rc = static_cast<int>(hipGetLastError());
     if (rc) return rc;
-    const dim3 grid(mfma::wide::BM / (mfma::wide::THREADS / kWave), static_cast<unsigned>(tiles));
-    mfma::wide::forward_combine_kernel<QSTE_F32>
-        <<<grid, mfma::wide::THREADS, 0, stream>>>(partial, tiles, sp.splits, scale, bias, y, m, rows);
-    return static_cast<int>(hipGetLastError());
   }
-  mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD_F32, QSTE_BF16>
-      <<<tiles, mfma::wide::THREADS, 0, stream>>>(p);
-  return static_cast<int>(hipGetLastError());
+  return 0;
 }
 
 size_t f32_dgrad_workspace(int64_t m, int64_t rows, int64_t cols) {
   if (m <= 0 || rows <= 0 || cols <= 0 || rows % 64 != 0 || !f32_limbs_worth(m)) return 0;
-  return limbs::up256(static_cast<size_t>(m) * 3 * rows * 2) + limbs::up256(static_cast<size_t>(cols) * 3 * rows / 8);
+  const int64_t mc = f32_chunk_rows(m, rows);
+  if (mc == 0) return 0;
+  return limbs::up256(static_cast<size_t>(mc) * 3 * rows * 2) +
+         limbs::up256(static_cast<size_t>(cols) * 3 * rows / 8);
 }
 
 // dx [m, cols] fp32 = dy @ (row_scale * sign) through the limbs: dy scaled
-// by the row scale along K, the signs transposed (bits along K).
+// by the row scale along K, the signs transposed (bits along K); over chunks
+// of f32_chunk_rows rows of dy.
 int mfma_f32_dgrad(const float* dy, const uint8_t* packed, const float* row_scale, float* dx, int64_t m,
                    int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   const size_t need = f32_dgrad_workspace(m, rows, cols);
   if (need == 0 || !workspace || workspace_bytes < need) return 1;
-  const int64_t k3 = 3 * rows, kb = rows / 8;
-  if (!fits32(m * k3 * 2) || !fits32(cols * k3 / 8)) return 1;
+  const int64_t k3 = 3 * rows, kb = rows / 8, mc = f32_chunk_rows(m, rows);
+  if (!fits32(mc * k3 * 2) || !fits32(cols * k3 / 8)) return 1;
   uint16_t* a = static_cast<uint16_t*>(workspace);
-  uint8_t* b = static_cast<uint8_t*>(workspace) + limbs::up256(static_cast<size_t>(m) * k3 * 2);
-  limbs::split_kernel<<<limbs::grid_for(m * rows), 256, 0, stream>>>(dy, m, rows, nullptr, row_scale, a, k3, rows);
+  uint8_t* b = static_cast<uint8_t*>(workspace) + limbs::up256(static_cast<size_t>(mc) * k3 * 2);
   // the transposed signs into plane 0 of each row of b (its pitch 3 * kb is
   // a multiple of 8 as rows % 64 == 0), then repeated into planes 1 and 2
   int rc = launch_transpose_bits(packed, b, rows, cols, (cols + 7) / 8, 3 * kb, stream);
   if (rc) return rc;
   limbs::repeat_kernel<<<limbs::grid_for(cols * kb), 256, 0, stream>>>(b, cols, kb, 3 * kb, b, 3 * kb, kb);
-  mfma::Params p{};
-  p.a = a;
-  p.bits = b;
-  p.out = dx;
-  p.M = m; p.N = cols; p.K = k3;
-  p.lda = k3; p.pb = 3 * kb;
-  p.a_rows = m; p.bit_rows = cols;
-  mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD_F32, QSTE_BF16>
-      <<<wide_grid(m, cols), mfma::wide::THREADS, 0, stream>>>(p);
-  return static_cast<int>(hipGetLastError());
+  for (int64_t i0 = 0; i0 < m; i0 += mc) {
+    const int64_t mi = m - i0 < mc ? m - i0 : mc;
+    limbs::split_kernel<<<limbs::grid_for(mi * rows), 256, 0, stream>>>(dy + i0 * rows, mi, rows, nullptr, row_scale,
+                                                                        a, k3, rows);
+    mfma::Params p{};
+    p.a = a;
+    p.bits = b;
+    p.out = dx + i0 * cols;
+    p.M = mi; p.N = cols; p.K = k3;
+    p.lda = k3; p.pb = 3 * kb;
+    p.a_rows = mi; p.bit_rows = cols;
+    mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K, mfma::EPI_FORWARD_F32, QSTE_BF16>
+        <<<wide_grid(mi, cols), mfma::wide::THREADS, 0, stream>>>(p);
+    if ((rc = static_cast<int>(hipGetLastError()))) return rc;
+  }
+  return 0;
 }
 
 size_t f32_evidence_workspace(int64_t samples, int64_t rows, int64_t cols) {
   if (samples <= 0 || rows <= 0 || cols <= 0 || rows % 64 != 0 || cols % 64 != 0 || !f32_limbs_worth(rows))
     return 0;
-  return limbs::up256(static_cast<size_t>(3 * samples) * rows * 2) +
-         limbs::up256(static_cast<size_t>(3 * samples) * (cols / 8));
+  // K is the samples here: the fused epilogue needs the whole sum in one
+  // pass, so a product whose limbs exceed the budget is not split up
+  const size_t a = static_cast<size_t>(3 * samples) * rows * 2;
+  if (a > kLimbBudget) return 0;
+  return limbs::up256(a) + limbs::up256(static_cast<size_t>(3 * samples) * (cols / 8));
 }
 
 // The evidence of fp32 dy through the limbs: dy scaled by the sample scale,

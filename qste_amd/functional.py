@@ -81,6 +81,9 @@ def remember_encoding(value: Tensor, payload: Tensor, aux: Tensor) -> None:
 # was.  An offer names the gradient tensor it belongs to (held, with its
 # version) and the aux it was summed against; a layer takes it only when
 # autograd hands it exactly that gradient, unchanged, and it saved that aux.
+# Offers live for one backward pass: one that no layer took (a gradient that
+# autograd summed with another use of the same output) is dropped when the
+# pass ends, so it holds no gradient past it.
 _AUX_ATTR = "_qste_input_aux"
 _offers: dict[int, tuple] = {}
 
@@ -214,6 +217,7 @@ class SwiGLUFn(Function):
         grad_gate, grad_up = grad_gate.view(gate.shape), grad_up.view(up.shape)
         _offer_offset_dot(grad_gate, aux_g, sums[0])
         _offer_offset_dot(grad_up, aux_u, sums[1])
+        torch.autograd.Variable._execution_engine.queue_callback(forget_offers)
         return grad_gate, grad_up, None
 
 

@@ -182,6 +182,45 @@ def _update_cases(fallback) -> dict:
     return out
 
 
+def _update_case_large(fallback) -> dict:
+    """A 1024 x 1024 surface, first step from fresh state then a second one
+    (block 256): reductions over 1024 columns, rows and 4096 blocks, the
+    length at which the fp32 reduction-order band would show.  The evidence
+    values are bf16-representable fp32 (they compress; the step's own
+    arithmetic is fp32 throughout)."""
+
+    out = {}
+    rows = cols = 1024
+    block, seed, step, lr = 256, 77, 1, 1.0
+    g = torch.Generator().manual_seed(4096)
+    coord = torch.randint(-127, 128, (rows, cols), generator=g, dtype=torch.int32).to(torch.int8)
+    blocks = (rows * cols + block - 1) // block
+    state = {
+        "coordinate": coord.clone(),
+        "packed": fallback.pack_coordinate(coord),
+        "moment_q": torch.zeros(rows, cols, dtype=torch.int8),
+        "moment_scale": torch.full((blocks,), 1 / 127, dtype=torch.float16),
+        "row_v": torch.zeros(rows, dtype=torch.float16),
+        "col_v": torch.zeros(cols, dtype=torch.float16),
+    }
+    for phase in range(2):
+        evidence = (torch.randn(rows, cols, generator=g) * 0.05).to(torch.bfloat16).float()
+        key = f"u1024x1024_p{phase}"
+        if phase == 0:  # the second step starts from the first one's outputs (not stored twice)
+            for k, v in state.items():
+                out[f"{key}__in_{k}"] = v.numpy().copy()
+        out[f"{key}__evidence"] = evidence.numpy().copy()
+        out[f"{key}__params"] = np.array([0.9, 0.99, 2.0, lr, block, seed, step + phase], dtype=np.float64)
+        flips = fallback.coordinate_update(
+            evidence.clone(), state["coordinate"], state["packed"], state["moment_q"], state["moment_scale"],
+            state["row_v"], state["col_v"], beta1=0.9, beta2=0.99, update_clip=2.0, coordinate_lr=lr,
+            block_size=block, seed=seed, step=step + phase)
+        for k, v in state.items():
+            out[f"{key}__out_{k}"] = v.numpy().copy()
+        out[f"{key}__flips"] = np.array(flips, dtype=np.int64)
+    return out
+
+
 def main(argv: list[str]) -> None:
     root = Path(argv[1] if len(argv) > 1 else "/root/reference")
     fallback, stream = _load_reference(root)
@@ -190,6 +229,7 @@ def main(argv: list[str]) -> None:
     np.savez_compressed(HERE / "pack_affine.npz", **_affine_cases(fallback))
     np.savez_compressed(HERE / "products.npz", **_product_cases(fallback))
     np.savez_compressed(HERE / "coordinate_update.npz", **_update_cases(fallback))
+    np.savez_compressed(HERE / "coordinate_update_1024.npz", **_update_case_large(fallback))
     for path in sorted(HERE.glob("*.npz")):
         print(f"{path.name}: {path.stat().st_size} bytes")
 

@@ -20,9 +20,12 @@ The workloads are bench.py's own (``relu_mlp``, ``GPT2Small``).
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
+
+import oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -137,9 +140,32 @@ def test_config2_relu_mlp():
     coords = qste.QSTEOptimizer(model)
     surfaces = qste.surfaces(model)
     before = [s.coordinate.clone() for s in surfaces]
+    # the signs the backward multiplies by (the optimizer moves the
+    # coordinates, and so the packed signs, inside the backward)
+    signs = {id(layer): layer.surface.packed_sign.cpu().numpy().copy() for layer in (model[0], model[2])}
     xq = x.clone().requires_grad_(True)
-    model(xq).backward(dy)
-    assert _rel(xq.grad, xr.grad) <= 1.5e-2
+    h = model[0](xq)
+    r = model[1](h)
+    r.retain_grad()
+    model[2](r).backward(dy)
+    assert _rel(xq.grad, xr.grad) <= 1.5e-2  # against fp32 autograd through dense weights
+    # each layer's input gradient against the operand-rounded float64 oracle
+    # (the row scale rounded to bf16 inside the contraction, as the MFMA
+    # operand holds it; the product rounded to bf16), on 512 sampled tokens:
+    # the second layer's on the upstream gradient, the first layer's on the
+    # ReLU's output gradient the block formed
+    tok = np.sort(np.random.default_rng(2).choice(8192, 512, replace=False))
+
+    def dgrad_oracle(layer, grad, columns):
+        scale = oracle.round_bf16(layer.scale.detach().float().cpu().numpy())
+        want = oracle.linear_dgrad(grad, signs[id(layer)], columns, scale)
+        return torch.from_numpy(want.astype(np.float32)).to(torch.bfloat16).double()
+
+    dy_s = np.ascontiguousarray(dy.float().cpu().numpy()[tok])
+    assert _rel(r.grad[tok].cpu(), dgrad_oracle(model[2], dy_s, 4096)) <= 1e-3
+    dh = torch.where(h > 0, r.grad, torch.zeros_like(r.grad))
+    dh_s = np.ascontiguousarray(dh.float().cpu().numpy()[tok])
+    assert _rel(xq.grad[tok].cpu(), dgrad_oracle(model[0], dh_s, 1024)) <= 1e-3
     flips = coords.step()
     assert flips > 0
     for s, b in zip(surfaces, before):

@@ -163,3 +163,99 @@ def test_config1_layer_backward():
     sign = oracle.signs_f64(pw, C)
     assert _rel(gs.cpu().numpy(), (e0 * sign).sum(1)) <= 2e-6
     assert _rel(db.cpu().numpy(), d.astype(np.float64).sum(0)) <= 1e-6
+
+
+def _nonfinite_agree(got, want):
+    """Same NaN positions, same infinities with the same signs."""
+
+    got = np.asarray(got, np.float64)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isposinf(got), np.isposinf(want))
+    assert np.array_equal(np.isneginf(got), np.isneginf(want))
+
+
+def test_special_values_keep_their_ieee_results():
+    """inf, NaN and values near fp32's largest through the limbs: the
+    forward and the input gradient give the infinities and NaNs an fp32
+    product gives (the float64 oracle on the same operands), and a finite
+    value too large for bf16's rounding (above 3.3961e38) stays finite."""
+
+    from qste_amd import kernels
+
+    m, rows, cols = 256, 512, 1024
+    x, packed, scale, bias = _problem(m, rows, cols, 11)
+    big = np.float32(3.40e38)
+    x[0, 5] = float("inf")                      # +-inf in every output of row 0
+    x[1, 7] = float("nan")                      # NaN everywhere in row 1
+    x[2, 3], x[2, 900] = float("inf"), -float("inf")  # NaN or +-inf by the two signs
+    x[3, 10] = float(big)                       # finite, rounds to inf in bf16
+    x[4, 20] = -float(big)
+    y = kernels.packed_linear_affine(x, packed, scale, bias, cols)
+    torch.cuda.synchronize()
+    xs, pk, sc, bi = x.cpu().numpy(), packed.cpu().numpy(), scale.cpu().numpy(), bias.cpu().numpy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = oracle.linear_fwd_f64(xs, pk, sc, bi, cols)
+    got = y.cpu().numpy()
+    _nonfinite_agree(got, want)
+    assert np.isfinite(got[3:]).all()
+    assert np.isinf(got[0]).all() and np.isnan(got[1]).all()
+    assert np.isnan(got[2]).any() and np.isinf(got[2]).any()
+    fin = slice(3, m)
+    assert _rel(got[fin], want[fin]) <= 2e-6
+    mag = np.abs(xs[fin].astype(np.float64)).sum(1)[:, None] * sc[None, :]
+    _bounded(got[fin], want[fin], mag)
+
+    # the input gradient: the same values in dy, along K = rows
+    g = torch.Generator(device=DEV).manual_seed(12)
+    dy = torch.randn(m, rows, generator=g, device=DEV)
+    dy[0, 5] = float("inf")
+    dy[1, 7] = float("nan")
+    dy[3, 10] = float(big)
+    one = torch.ones(rows, device=DEV)          # row scale 1 keeps the near-max value as it is
+    dx = kernels.packed_transpose(dy, packed, cols, row_scale=one)
+    torch.cuda.synchronize()
+    d = dy.cpu().numpy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = oracle.linear_dgrad_f64(d, pk, cols, one.cpu().numpy())
+    got = dx.cpu().numpy()
+    _nonfinite_agree(got, want)
+    assert np.isinf(got[0]).all() and np.isnan(got[1]).all() and np.isfinite(got[2:]).all()
+    assert _rel(got[2:], want[2:]) <= 2e-6
+
+
+def test_products_over_row_chunks():
+    """A dense operand whose limbs exceed the 512 MiB budget runs in chunks
+    of output rows (8192 x 14336 fp32 -> chunks of 6144 and 2048 rows): the
+    rows on both sides of the chunk boundary and the last rows against the
+    float64 oracle, forward and input gradient."""
+
+    from qste_amd import kernels
+
+    lib = kernels._lib.load()
+    m, k, n = 8192, 14336, 256
+    # the workspace holds one chunk's limbs, not the whole operand's
+    assert 0 < lib.qste_packed_linear_affine_workspace_bytes(m, n, k, 0) < m * k * 6
+    assert 0 < lib.qste_packed_transpose_workspace_bytes(m, k, n, 0) < m * k * 6
+    g = torch.Generator(device=DEV).manual_seed(13)
+    x = torch.randn(m, k, generator=g, device=DEV)
+    coord = torch.randint(-127, 128, (n, k), generator=g, device=DEV, dtype=torch.int32).to(torch.int8)
+    packed = kernels.pack_coordinate(coord)
+    scale = torch.rand(n, generator=g, device=DEV) * 0.02 + 0.005
+    bias = torch.randn(n, generator=g, device=DEV) * 0.1
+    sel = np.r_[0:8, 6140:6150, m - 8:m]
+    y = kernels.packed_linear_affine(x, packed, scale, bias, k)
+    torch.cuda.synchronize()
+    xs = x[torch.from_numpy(sel).to(DEV)].cpu().numpy()
+    pk, sc = packed.cpu().numpy(), scale.cpu().numpy()
+    want = oracle.linear_fwd_f64(xs, pk, sc, bias.cpu().numpy(), k)
+    assert _rel(y[torch.from_numpy(sel).to(DEV)].cpu().numpy(), want) <= 2e-6
+    del y
+
+    # input gradient: dy [m, k] against signs [k, n] (K = k rows of signs)
+    coord_t = torch.randint(-127, 128, (k, n), generator=g, device=DEV, dtype=torch.int32).to(torch.int8)
+    packed_t = kernels.pack_coordinate(coord_t)
+    row_scale = torch.rand(k, generator=g, device=DEV) * 0.02 + 0.005
+    dx = kernels.packed_transpose(x, packed_t, n, row_scale=row_scale)
+    torch.cuda.synchronize()
+    want = oracle.linear_dgrad_f64(xs, packed_t.cpu().numpy(), n, row_scale.cpu().numpy())
+    assert _rel(dx[torch.from_numpy(sel).to(DEV)].cpu().numpy(), want) <= 2e-6

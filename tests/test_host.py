@@ -112,6 +112,35 @@ def test_error_codes_and_workspace_queries_need_no_gpu():
                                       64, 1, 0, None, None, None, None, 0, None) == -3
 
 
+def test_fp32_limb_workspaces_are_capped_and_shared():
+    """The fp32 products' bf16 limbs (6 bytes per dense value) are held to
+    512 MiB: forward and input gradient in chunks of output rows, an
+    evidence whose limbs exceed it on the SIMT kernels (no limbs workspace).
+    The layer backward's limbs region serves its dX and evidence products in
+    turn, so it holds the larger of the two."""
+
+    from qste_amd.kernels import _lib
+
+    lib = _lib.load()
+    f32, budget = 0, 512 << 20
+    # config 4's down projection in fp32: 16384 x 14336 -> 4096
+    fwd = lib.qste_packed_linear_affine_workspace_bytes(16384, 4096, 14336, f32)
+    assert 0 < fwd <= budget + 4096 * 14336 * 3 // 8 + (64 << 20)
+    dgr = lib.qste_packed_transpose_workspace_bytes(16384, 14336, 4096, f32)
+    assert 0 < dgr <= budget + 4096 * 14336 * 3 // 8 + 4096
+    assert lib.qste_evidence_from_packed_workspace_bytes_dtype(16384, 14336, 4096, f32) == 0
+    assert lib.qste_evidence_from_packed_workspace_bytes_dtype(4096, 4096, 4096, f32) >= 3 * 4096 * 4096 * 2
+    # small products need no chunks: the whole operand's limbs
+    assert lib.qste_packed_linear_affine_workspace_bytes(256, 2048, 2048, f32) >= 256 * 2048 * 6
+    for t, r, c in ((256, 2048, 2048), (4096, 4096, 4096), (16384, 14336, 4096), (16384, 4096, 14336),
+                    (1024, 640, 1024), (8192, 14336, 64)):
+        extra = lib.qste_linear_backward_workspace_bytes_dtype(t, r, c, f32) - lib.qste_linear_backward_workspace_bytes(
+            t, r, c)
+        d = lib.qste_packed_transpose_workspace_bytes(t, r, c, f32)
+        e = lib.qste_evidence_from_packed_workspace_bytes_dtype(t, r, c, f32)
+        assert extra >= max(d, e), (t, r, c, extra, d, e)
+
+
 def test_operator_layer_refuses_cpu_tensors():
     from qste_amd import kernels
 
@@ -120,6 +149,19 @@ def test_operator_layer_refuses_cpu_tensors():
     with pytest.raises(RuntimeError, match="GPU"):
         kernels.packed_linear_affine(torch.zeros(2, 8), torch.zeros(3, 1, dtype=torch.uint8),
                                      torch.ones(3), None, 8)
+
+
+def test_device_profile_without_a_gpu():
+    """``qste_amd.device_profile`` on a host: one line that says the package
+    has no CPU path and names the library build (reference
+    src/qste/__init__.py:105-120 describes the selected kernel profile)."""
+
+    import qste_amd
+
+    line = qste_amd.device_profile("cpu")
+    assert "\n" not in line
+    assert "no QSTE kernels" in line and "gfx950" in line
+    assert re.search(r"library=libqste_hip v\d+", line), line
 
 
 # ---------------------------------------------------------------------------
@@ -769,3 +811,15 @@ def test_swiglu_hands_its_encoding_to_the_down_layer(fake, monkeypatch):
     assert sorted(fake.offset_dots) == [False, True, True]
     assert torch.allclose(y0, y1, rtol=1e-6, atol=1e-6)
     assert torch.allclose(g0, g1, rtol=1e-5, atol=1e-6)
+
+    # the gate layer's output also feeds the loss directly: autograd sums
+    # its two gradients into a new tensor, so the offer for it is not taken;
+    # the pass's end drops it (no gradient is held afterwards)
+    from qste_amd import functional
+
+    fake.offset_dots = []
+    xr = x.clone().requires_grad_(True)
+    a, b = gate(xr), up(xr)
+    (down(qste.nn.swiglu(a, b)).square().sum() + a.sum()).backward()
+    assert sorted(fake.offset_dots) == [False, False, True]
+    assert functional._offers == {}
