@@ -8,11 +8,14 @@ activations, seeded int8 coordinates U{-127..127}, row scales |N(0,1)|*0.01,
 upstream gradient N(0,1).  One step = forward of the three layers (with the
 1-bit activation encoding), backward (input gradient, evidence, scale
 gradient) and the coordinate step of all three surfaces, which runs inside
-backward as in the reference.  The SwiGLU gate between the layers is
-qste_amd.nn.swiglu, one fused kernel each way whose values and gradients
-equal torch's F.silu(g) * u bit for bit; the same step with torch's silu and
-mul is reported as ``step_torch_gate_ms``.  ``value`` = 6 * T * sum(R*C) /
-step time.
+backward as in the reference.  The MLP runs as qste_amd.nn.swiglu_mlp, one
+autograd node: its forward values, evidence and scale gradients equal the
+three layers with torch's F.silu(g) * u between them bit for bit; its
+backward forms the gate and up layers' input gradient as one product (one
+rounding, one launch, no separate sum).  The same step with the layers
+called one by one is reported as ``step_layer_by_layer_ms`` (the fused gate
+qste_amd.nn.swiglu between them) and ``step_torch_gate_ms`` (torch's silu
+and mul).  ``value`` = 6 * T * sum(R*C) / step time.
 
 Alongside, measured live with HIP events on the stream the kernels run on:
 each GEMM kind at the gate-layer shape (the dominant kernel is reported as
@@ -128,26 +131,36 @@ def make_layer(rows, cols, seed, device, scale_std=0.01):
 
 
 class SwiGLU:
-    """down(silu(gate(x)) * up(x)) over three binary layers.  ``fused``: the
-    gate is qste_amd.nn.swiglu (one kernel each way, same values and
-    gradients as torch's F.silu(.) * (.), and the down layer's activation
-    encoding made by that kernel); otherwise torch's silu and mul."""
+    """down(silu(gate(x)) * up(x)) over three binary layers, run as
+    ``mode`` says:
 
-    def __init__(self, d, ffn, device, fused=True):
+    * "node": qste_amd.nn.swiglu_mlp -- the MLP as one autograd node (the
+      gate and up layers' input gradients as one product);
+    * "gate": the layers one by one with qste_amd.nn.swiglu between them
+      (one kernel each way, the down layer's encoding made by that kernel);
+    * "torch": the layers one by one with torch's F.silu and mul.
+
+    All three compute the same forward values, evidence and scale
+    gradients; the input gradient is the same in "gate" and "torch" and
+    rounded once instead of three times in "node"."""
+
+    def __init__(self, d, ffn, device, mode="node"):
         import torch.nn as nn
 
         self.gate = make_layer(ffn, d, 11, device)
         self.up = make_layer(ffn, d, 21, device)
         self.down = make_layer(d, ffn, 31, device)
         self.modules = nn.ModuleList([self.gate, self.up, self.down])
-        self.fused = fused
+        self.mode = mode
 
     def __call__(self, x):
         import torch.nn.functional as F
 
         import qste_amd as qste
 
-        if self.fused:
+        if self.mode == "node":
+            return qste.nn.swiglu_mlp(x, self.gate, self.up, self.down)
+        if self.mode == "gate":
             return self.down(qste.nn.swiglu(self.gate(x), self.up(x)))
         return self.down(F.silu(self.gate(x)) * self.up(x))
 
@@ -308,42 +321,55 @@ class GPT2Small:
 
 
 def in_step_times(step, T, d, ffn, steps=3):
-    """Per-call time of the layers' forward and backward products inside the
-    training step: HIP events recorded on the current stream around every
-    ``packed_linear_affine`` and ``linear_backward`` call of ``steps`` steps
-    (events do not synchronize, so the step runs as it does untimed)."""
+    """Per-call time of the layers' products inside the training step: HIP
+    events recorded on the current stream around every operator call that
+    runs them, over ``steps`` steps (events do not synchronize, so the step
+    runs as it does untimed).  Kinds: "forward" (packed_linear_affine, one
+    product), "backward_call" (linear_backward with the input gradient: two
+    products), "evidence_call" (linear_backward without it: the evidence
+    alone), "dgrad_pair" (packed_transpose_pair: two products)."""
 
     import torch
 
     from qste_amd import kernels
 
     records = []
-    originals = (kernels.packed_linear_affine, kernels.linear_backward)
+    names = ("packed_linear_affine", "linear_backward", "packed_transpose_pair")
+    originals = {n: getattr(kernels, n) for n in names}
 
-    def wrap(kind, fn):
+    def kind_of(name, kwargs):
+        if name == "packed_linear_affine":
+            return "forward", 1
+        if name == "linear_backward":
+            return ("backward_call", 2) if kwargs.get("need_input", True) else ("evidence_call", 1)
+        return "dgrad_pair", 2
+
+    def wrap(name, fn):
         def timed(*args, **kwargs):
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
             out = fn(*args, **kwargs)
             b.record()
-            records.append((kind, args[0].shape[-1], a, b))
+            records.append((kind_of(name, kwargs), a, b))
             return out
         return timed
 
-    kernels.packed_linear_affine = wrap("forward", originals[0])
-    kernels.linear_backward = wrap("backward_call", originals[1])
+    for n in names:
+        setattr(kernels, n, wrap(n, originals[n]))
     try:
         for _ in range(steps):
             step()
         torch.cuda.synchronize()
     finally:
-        kernels.packed_linear_affine, kernels.linear_backward = originals
+        for n in names:
+            setattr(kernels, n, originals[n])
     flop = 2.0 * T * ffn * d  # one product at any of the three shapes
     out = {}
-    for kind, products in (("forward", 1), ("backward_call", 2)):
-        times = [a.elapsed_time(b) for k, _, a, b in records if k == kind]
+    for kind in ("forward", "backward_call", "evidence_call", "dgrad_pair"):
+        times = [a.elapsed_time(b) for (k, _), a, b in records if k == kind]
         if not times:
             continue
+        products = next(p for (k, p), _, _ in records if k == kind)
         ms = sum(times) / len(times)
         out[kind] = {"ms": round(ms, 4), "calls": len(times), "tflops": round(products * flop / ms / 1e9, 2),
                      "frac_of_mfma_peak": round(products * flop / (ms * 1e-3) / MFMA_BF16_PEAK, 4)}
@@ -936,8 +962,10 @@ def main():
         "data": "synthetic (seeded N(0,1) activations and gradients, U{-127..127} int8 coordinates)",
         "config": {"workload": "cfg4 Llama-3-8B SwiGLU MLP fwd+bwd+coordinate step",
                    "tokens": T, "d": d, "ffn": ffn, "layers": 3, "flop_per_step": flop,
-                   "gate": "qste_amd.nn.swiglu (one fused kernel each way, values and gradients equal to "
-                           "F.silu(g) * u bit for bit); the step with torch's silu and mul is step_torch_gate_ms"},
+                   "gate": "qste_amd.nn.swiglu_mlp: the MLP as one autograd node (forward values, evidence "
+                           "and scale gradients equal to the layers with F.silu(g) * u bit for bit; one product "
+                           "for the gate and up layers' input gradient); the layers one by one are "
+                           "step_layer_by_layer_ms (fused gate) and step_torch_gate_ms (torch's silu and mul)"},
         "frac_of_mfma_peak": round(flop / secs / MFMA_BF16_PEAK, 4),
     }
     if not args.no_extras:
@@ -958,9 +986,12 @@ def main():
         # the same products inside the training step (the chip is power-limited
         # there, so they run slower than back to back in isolation)
         line["in_step"] = in_step_times(step, T, d, ffn)
+        if "evidence_call" in line["in_step"] and dominant == "evidence":
+            # the roofline kernel inside the step: the node's evidence-only calls
+            line["roofline"]["in_step_frac"] = line["in_step"]["evidence_call"]["frac_of_mfma_peak"]
         if "backward_call" in line["in_step"]:
             line["roofline"]["in_step_backward_call_frac"] = line["in_step"]["backward_call"]["frac_of_mfma_peak"]
-            line["roofline"]["isolated_backward_call_frac"] = kernels_t["backward_call"]["frac_of_mfma_peak"]
+        line["roofline"]["isolated_backward_call_frac"] = kernels_t["backward_call"]["frac_of_mfma_peak"]
         line["kernels"] = kernels_t
         line["device"] = device_report(device, T, d, ffn)
         line["memory_bandwidth"] = memory_bandwidth(device)
@@ -969,16 +1000,18 @@ def main():
         line["coordinate_step"] = step_bandwidth(ffn, d, device)
         line["decode_gemv"] = decode_gemv(device)
         line["packed_activations"] = packed_activation_bandwidth(T, ffn, device)
-        # the same step with torch's silu and mul for the gate (what a model
+        # the same step with the layers called one by one: with the fused
+        # gate between them, and with torch's silu and mul (what a model
         # written F.silu(gate(x)) * up(x) runs)
-        mlp.fused = False
-        step()
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        for _ in range(3):
+        for mode, key in (("gate", "step_layer_by_layer_ms"), ("torch", "step_torch_gate_ms")):
+            mlp.mode = mode
             step()
-        torch.cuda.synchronize()
-        line["step_torch_gate_ms"] = round((time.perf_counter() - t1) / 3 * 1e3, 3)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            for _ in range(3):
+                step()
+            torch.cuda.synchronize()
+            line[key] = round((time.perf_counter() - t1) / 3 * 1e3, 3)
         # and with the SiLU retaining its int8 derivative (qste.packed_activations())
         packed_step()
         torch.cuda.synchronize()
@@ -987,7 +1020,7 @@ def main():
             packed_step()
         torch.cuda.synchronize()
         line["packed_activations"]["step_ms"] = round((time.perf_counter() - t1) / 3 * 1e3, 3)
-        mlp.fused = True
+        mlp.mode = "node"
         if not args.no_configs:
             line["configs"] = config_steps(device)
     line["cfg1"] = cfg1_lines(device, cpu=not args.no_cpu_baseline)

@@ -221,6 +221,94 @@ class SwiGLUFn(Function):
         return grad_gate, grad_up, None
 
 
+class SwiGLUMLPFn(Function):
+    """``down(swiglu(gate(x), up(x)))`` as one autograd node, bf16.
+
+    The values are those of the three QSTELinearFn nodes and SwiGLUFn
+    composed: the same products, the same gate arithmetic, the same
+    encodings (x's shared by gate and up; h's from the gate kernel), and the
+    same evidence and scale gradients bit for bit (the gate's backward sums
+    the offset corrections of the gate and up layers as those layers would,
+    ``swiglu_backward_sums``).  One thing differs: x's gradient is one
+    product over both layers (``packed_transpose_pair``), rounded once, where
+    autograd rounds each layer's input gradient and then their sum -- one
+    launch and one pass over [tokens, d] tensors fewer.
+
+    Evidence goes to each surface after every product that reads that
+    surface's signs (a delivery may step the surface, rewriting them), as in
+    QSTELinearFn: down first, then gate and up."""
+
+    @staticmethod
+    def forward(ctx, inputs, packed_g, scale_g, bias_g, packed_u, scale_u, bias_u, packed_d, scale_d, bias_d,
+                surfaces, grad_on: bool):
+        sg, su, sd = surfaces
+        d, ffn = sg.columns, sg.rows
+        flat = inputs.reshape(-1, d)
+        g = kernels.packed_linear_affine(flat, packed_g, scale_g, bias_g, d)
+        u = kernels.packed_linear_affine(flat, packed_u, scale_u, bias_u, d)
+        h, enc = kernels.swiglu_forward(g, u, encode=grad_on)
+        y = kernels.packed_linear_affine(h, packed_d, scale_d, bias_d, ffn)
+        if grad_on:
+            payload_x, aux_x = _encoding_of(inputs, flat, d)
+            aux_h = kernels.stacked_pair(enc[1], enc[2])
+            ctx.save_for_backward(payload_x, aux_x, g, u, enc[0], aux_h, packed_g, scale_g, packed_u, scale_u,
+                                  packed_d, scale_d)
+        ctx.surfaces = surfaces
+        ctx.input_shape = inputs.shape
+        ctx.bias_dtypes = tuple(None if b is None else b.dtype for b in (bias_g, bias_u, bias_d))
+        return y.reshape(*inputs.shape[:-1], d)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        forget_encodings()
+        (payload_x, aux_x, g, u, payload_h, aux_h, packed_g, scale_g, packed_u, scale_u, packed_d,
+         scale_d) = ctx.saved_tensors
+        sg, su, sd = ctx.surfaces
+        d, ffn = sg.columns, sg.rows
+        bg, bu, bd = ctx.bias_dtypes
+        dy = grad_output.reshape(-1, d)
+        # A surface's evidence may step it on delivery, rewriting its packed
+        # signs in place; every product that multiplies by a layer's signs
+        # runs before that layer's evidence is delivered, as in QSTELinearFn
+        # (whose one call forms the input gradient before the delivery).
+        dh, ev_d, gs_d, gb_d = kernels.linear_backward(
+            dy, payload_h, aux_h[0], aux_h[1], packed_d, scale_d.detach(), ffn, need_bias=bd is not None)
+        sd.consume_evidence(ev_d)
+        del ev_d
+        dg, du, sums = kernels.swiglu_backward_sums(dh, g, u, aux_x[0], aux_x[0])
+        del dh
+        _, ev_g, gs_g, gb_g = kernels.linear_backward(
+            dg, payload_x, aux_x[0], aux_x[1], packed_g, scale_g.detach(), d, need_bias=bg is not None,
+            need_input=False, offset_dot=sums[0])
+        _, ev_u, gs_u, gb_u = kernels.linear_backward(
+            du, payload_x, aux_x[0], aux_x[1], packed_u, scale_u.detach(), d, need_bias=bu is not None,
+            need_input=False, offset_dot=sums[1])
+        dx = None
+        if ctx.needs_input_grad[0]:
+            dx = kernels.packed_transpose_pair(dg, packed_g, scale_g.detach(), du, packed_u, scale_u.detach(), d)
+            dx = dx.reshape(ctx.input_shape)
+        sg.consume_evidence(ev_g)
+        su.consume_evidence(ev_u)
+
+        def cast(grad, dtype):
+            return None if grad is None or dtype is None else grad.to(dtype)
+
+        return (dx, None, gs_g.to(scale_g.dtype), cast(gb_g, bg), None, gs_u.to(scale_u.dtype), cast(gb_u, bu),
+                None, gs_d.to(scale_d.dtype), cast(gb_d, bd), None, None)
+
+
+def swiglu_mlp_fusable(inputs: Tensor, gate, up, down) -> bool:
+    """Whether ``SwiGLUMLPFn`` takes this MLP: bf16 input on the GPU, the
+    gate and up layers d -> ffn and the down layer ffn -> d, d and ffn
+    multiples of 64."""
+
+    sg, su, sd = gate.surface, up.surface, down.surface
+    d, ffn = sg.columns, sg.rows
+    return (inputs.is_cuda and inputs.dtype == torch.bfloat16 and inputs.dim() >= 1 and inputs.shape[-1] == d
+            and su.columns == d and su.rows == ffn and sd.columns == ffn and sd.rows == d
+            and d % 64 == 0 and ffn % 64 == 0 and inputs.numel() > 0)
+
+
 def swiglu(gate: Tensor, up: Tensor) -> Tensor:
     """The SwiGLU gate ``F.silu(gate) * up`` (same values and gradients), fused.
 

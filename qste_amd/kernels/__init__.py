@@ -775,6 +775,34 @@ def swiglu_backward_sums(grad: Tensor, gate: Tensor, up: Tensor, offset_gate: Te
     return dg, du, sums
 
 
+def packed_transpose_pair(grad_a: Tensor, packed_a: Tensor, scale_a: Tensor, grad_b: Tensor, packed_b: Tensor,
+                          scale_b: Tensor, columns: int) -> Tensor:
+    """``grad_a @ (scale_a * sign_a) + grad_b @ (scale_b * sign_b)`` in one
+    product (one fp32 accumulation, one rounding to the dtype): the input
+    gradient of two layers that read one input.  grad_a, grad_b [tokens,
+    rows] bf16 or fp16; packed_* [rows, columns/8]; scale_* fp32 [rows];
+    rows and columns multiples of 64.  No counterpart in the reference,
+    where autograd adds the two layers' input gradients."""
+
+    device = _require_gpu(grad_a, packed_a, scale_a, grad_b, packed_b, scale_b)
+    if grad_a.dim() != 2 or grad_a.shape != grad_b.shape or grad_a.dtype != grad_b.dtype:
+        raise ValueError("packed_transpose_pair expects two rank-2 gradients of one shape and dtype")
+    tokens, rows = grad_a.shape
+    pa, pb = _check_packed(packed_a, columns), _check_packed(packed_b, columns)
+    if pa.shape[0] != rows or pb.shape[0] != rows or scale_a.numel() != rows or scale_b.numel() != rows:
+        raise ValueError("packed_transpose_pair operands disagree on rows")
+    ga, gb = _aligned(grad_a), _aligned(grad_b)
+    sa, sb = _f32(scale_a), _f32(scale_b)
+    out = torch.empty(tokens, int(columns), dtype=grad_a.dtype, device=device)
+    lib = _lib.load()
+    work = _workspace(lib.qste_packed_transpose_pair_workspace_bytes(tokens, rows, int(columns)), device)
+    code = lib.qste_packed_transpose_pair(
+        _ptr(ga), _ptr(gb), _dtype_code(ga), _ptr(pa), _ptr(sa), _ptr(pb), _ptr(sb), _ptr(out), tokens, rows,
+        int(columns), _ptr(work), work.numel(), _stream(device))
+    _lib.check(code, "packed_transpose_pair")
+    return out
+
+
 def row_scale(log_scale: Tensor, lo: float, hi: float) -> tuple[Tensor, Tensor]:
     """``(clamp(exp(log_scale), lo, hi), exp(log_scale))`` in log_scale's
     dtype (fp32, fp16 or bf16), one launch (surface.py:84-85), rounded as

@@ -71,6 +71,31 @@ def _take_activation_input(value: Tensor) -> Tensor | None:
     return value if getattr(value, "_qste_activation_input", False) else None
 
 
+def swiglu_mlp(inputs: Tensor, gate, up, down) -> Tensor:
+    """``down(swiglu(gate(inputs), up(inputs)))`` for three converted layers
+    (QSTELinear: gate and up d -> ffn, down ffn -> d).
+
+    No counterpart in the reference.  Same forward values, evidence and
+    scale gradients as the three layers and the gate called one by one; for
+    bf16 inputs on the GPU with d and ffn multiples of 64 the whole MLP is
+    one autograd node whose input gradient is one product over the gate and
+    up layers, rounded once (``functional.SwiGLUMLPFn``).  Anything else is
+    the layer-by-layer composition."""
+
+    from .functional import SwiGLUMLPFn, _autocast, swiglu_mlp_fusable
+
+    x = _autocast(inputs)
+    if not swiglu_mlp_fusable(x, gate, up, down):
+        return down(swiglu(gate(inputs), up(inputs)))
+    surfaces = (gate.surface, up.surface, down.surface)
+    for s in surfaces:
+        s.note_forward()
+    y = SwiGLUMLPFn.apply(x, gate.surface.packed_sign, gate.surface.scale, gate.bias, up.surface.packed_sign,
+                          up.surface.scale, up.bias, down.surface.packed_sign, down.surface.scale, down.bias,
+                          surfaces, torch.is_grad_enabled())
+    return _mark_activation_input(y)
+
+
 # ---------------------------------------------------------------------------
 # One bit per element
 # ---------------------------------------------------------------------------
@@ -736,7 +761,7 @@ def packed_activations():
 __all__ = [
     "CELU", "Dropout", "ELU", "EXACT_REPLACEMENTS", "GELU", "Hardsigmoid", "Hardswish", "Hardtanh",
     "LeakyReLU", "Mish", "REPLACEMENTS", "ReLU", "ReLU6", "SELU", "SMOOTH_REPLACEMENTS", "SiLU",
-    "Sigmoid", "Softplus", "Tanh", "celu", "dropout", "elementwise", "elu", "gelu", "hardsigmoid", "swiglu",
+    "Sigmoid", "Softplus", "Tanh", "celu", "dropout", "elementwise", "elu", "gelu", "hardsigmoid", "swiglu", "swiglu_mlp",
     "hardswish", "hardtanh", "leaky_relu", "mish", "packed", "packed_activations", "relu",
     "relu6", "relu_square", "replace", "selu", "sigmoid", "silu", "softplus", "tanh",
 ]

@@ -297,6 +297,14 @@ class OracleKernels:
         self.swiglu_sums = getattr(self, "swiglu_sums", 0) + 1
         return dg, du, sums.float()
 
+    # the SwiGLU MLP node's summed input gradient of the gate and up layers
+    def packed_transpose_pair(self, grad_a, packed_a, scale_a, grad_b, packed_b, scale_b, columns):
+        dx = oracle.linear_dgrad(grad_a.float().numpy(), packed_a.numpy(), columns, scale_a.detach().float().numpy())
+        dx = dx + oracle.linear_dgrad(grad_b.float().numpy(), packed_b.numpy(), columns,
+                                      scale_b.detach().float().numpy())
+        self.pairs = getattr(self, "pairs", 0) + 1
+        return torch.from_numpy(dx).float().to(grad_a.dtype)
+
     # binary embedding (oracle/embedding.py)
     def packed_embedding(self, ids, packed, scale, columns):
         out = oe.lookup(ids.numpy(), packed.numpy(), scale.detach().float().numpy(), columns)
@@ -309,7 +317,7 @@ class OracleKernels:
 
 ACTIVATION_OPS = ("pack_bits", "unpack_bits", "masked_backward", "masked_activation",
                   "smooth_activation", "smooth_backward", "packed_embedding", "embedding_backward",
-                  "swiglu_forward", "swiglu_backward", "swiglu_backward_sums")
+                  "swiglu_forward", "swiglu_backward", "swiglu_backward_sums", "packed_transpose_pair")
 
 
 @pytest.fixture
@@ -823,3 +831,54 @@ def test_swiglu_hands_its_encoding_to_the_down_layer(fake, monkeypatch):
     (down(qste.nn.swiglu(a, b)).square().sum() + a.sum()).backward()
     assert sorted(fake.offset_dots) == [False, False, True]
     assert functional._offers == {}
+
+
+def test_swiglu_mlp_node_composes_the_layers(fake, monkeypatch):
+    """qste_amd.nn.swiglu_mlp as one node (its eligibility check relaxed to
+    CPU tensors so the oracle-backed operators run it): the same output as
+    the layers called one by one, each surface's evidence once (the same
+    evidence), the gate and up layers' input gradients from one two-layer
+    product, and the steps inside backward reading each layer's signs only
+    after every product that needs them."""
+
+    import qste_amd as qste
+    from qste_amd import functional
+
+    monkeypatch.setattr(functional, "swiglu_mlp_fusable",
+                        lambda x, g, u, d: x.dtype == torch.bfloat16 and x.shape[-1] % 64 == 0)
+
+    def layer(rows, cols, seed):
+        g = torch.Generator().manual_seed(seed)
+        coord = torch.randint(-127, 128, (rows, cols), generator=g, dtype=torch.int32).to(torch.int8)
+        return qste.QSTELinear(qste.Surface.from_state(coord, torch.full((rows,), -3.0)), None)
+
+    def run(node):
+        gate, up, down = layer(128, 64, 1), layer(128, 64, 2), layer(64, 128, 3)
+        # the steps run inside backward, rewriting each surface's signs as its
+        # evidence arrives: a product that read a layer's signs after that
+        # layer's delivery would see the stepped ones
+        coords = qste.QSTEOptimizer([gate.surface, up.surface, down.surface])
+        got = {}
+        for name, m in (("gate", gate), ("up", up), ("down", down)):
+            m.surface.route_evidence(lambda s, e, name=name: (got.__setitem__(name, e.clone()), coords._apply(s, e)))
+        x = torch.randn(10, 64, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).requires_grad_(True)
+        if node:
+            y = qste.nn.swiglu_mlp(x, gate, up, down)
+        else:
+            y = down(qste.nn.swiglu(gate(x), up(x)))
+        y.float().square().sum().backward()
+        return y.detach(), x.grad, got, [m.surface.log_scale.grad.clone() for m in (gate, up, down)]
+
+    y0, g0, e0, s0 = run(False)
+    fake.backward_calls = []
+    fake.swiglu_sums = 0
+    y1, g1, e1, s1 = run(True)
+    assert fake.pairs == 1 and fake.swiglu_sums == 1
+    # the down layer forms its input gradient; gate and up leave theirs to the pair product
+    assert fake.backward_calls == [True, False, False]
+    assert torch.equal(y0, y1)
+    assert torch.allclose(g0.float(), g1.float(), rtol=2e-2, atol=2e-2)
+    for name in ("gate", "up", "down"):
+        assert torch.allclose(e0[name], e1[name], rtol=1e-4, atol=1e-6), name
+    for a, b in zip(s0, s1):
+        assert torch.allclose(a, b, rtol=1e-4, atol=1e-6)
