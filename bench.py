@@ -9,10 +9,11 @@ upstream gradient N(0,1).  One step = forward of the three layers (with the
 1-bit activation encoding), backward (input gradient, evidence, scale
 gradient) and the coordinate step of all three surfaces, which runs inside
 backward as in the reference.  The MLP runs as qste_amd.nn.swiglu_mlp, one
-autograd node: its forward values, evidence and scale gradients equal the
-three layers with torch's F.silu(g) * u between them bit for bit; its
-backward forms the gate and up layers' input gradient as one product (one
-rounding, one launch, no separate sum).  The same step with the layers
+autograd node: its forward values equal the three layers with torch's
+F.silu(g) * u between them bit for bit; its backward runs the gate and up
+layers as one layer of 2 * ffn rows (their input gradient as one product
+with one rounding, their evidence as one product of seven full rounds of
+tiles).  The same step with the layers
 called one by one is reported as ``step_layer_by_layer_ms`` (the fused gate
 qste_amd.nn.swiglu between them) and ``step_torch_gate_ms`` (torch's silu
 and mul).  ``value`` = 6 * T * sum(R*C) / step time.
@@ -135,14 +136,16 @@ class SwiGLU:
     ``mode`` says:
 
     * "node": qste_amd.nn.swiglu_mlp -- the MLP as one autograd node (the
-      gate and up layers' input gradients as one product);
+      gate and up layers' backward as one call over both: their input
+      gradients as one product, their evidence as one);
     * "gate": the layers one by one with qste_amd.nn.swiglu between them
       (one kernel each way, the down layer's encoding made by that kernel);
     * "torch": the layers one by one with torch's F.silu and mul.
 
-    All three compute the same forward values, evidence and scale
-    gradients; the input gradient is the same in "gate" and "torch" and
-    rounded once instead of three times in "node"."""
+    All three compute the same forward values; "gate" and "torch" the same
+    gradients bit for bit; "node" the same evidence and scale gradients up
+    to the order some split-K tiles are summed in, and the input gradient
+    rounded once instead of three times."""
 
     def __init__(self, d, ffn, device, mode="node"):
         import torch.nn as nn
@@ -327,22 +330,24 @@ def in_step_times(step, T, d, ffn, steps=3):
     runs as it does untimed).  Kinds: "forward" (packed_linear_affine, one
     product), "backward_call" (linear_backward with the input gradient: two
     products), "evidence_call" (linear_backward without it: the evidence
-    alone), "dgrad_pair" (packed_transpose_pair: two products)."""
+    alone), "backward_call_gate_up" (the MLP node's one call for the gate
+    and up layers: their two evidence products and their summed input
+    gradient, four products)."""
 
     import torch
 
     from qste_amd import kernels
 
     records = []
-    names = ("packed_linear_affine", "linear_backward", "packed_transpose_pair")
+    names = ("packed_linear_affine", "linear_backward")
     originals = {n: getattr(kernels, n) for n in names}
 
-    def kind_of(name, kwargs):
+    def kind_of(name, args, kwargs):
         if name == "packed_linear_affine":
             return "forward", 1
-        if name == "linear_backward":
-            return ("backward_call", 2) if kwargs.get("need_input", True) else ("evidence_call", 1)
-        return "dgrad_pair", 2
+        if args[0].shape[-1] == 2 * ffn:
+            return ("backward_call_gate_up", 4) if kwargs.get("need_input", True) else ("evidence_call_gate_up", 2)
+        return ("backward_call", 2) if kwargs.get("need_input", True) else ("evidence_call", 1)
 
     def wrap(name, fn):
         def timed(*args, **kwargs):
@@ -350,7 +355,7 @@ def in_step_times(step, T, d, ffn, steps=3):
             a.record()
             out = fn(*args, **kwargs)
             b.record()
-            records.append((kind_of(name, kwargs), a, b))
+            records.append((kind_of(name, args, kwargs), a, b))
             return out
         return timed
 
@@ -365,7 +370,7 @@ def in_step_times(step, T, d, ffn, steps=3):
             setattr(kernels, n, originals[n])
     flop = 2.0 * T * ffn * d  # one product at any of the three shapes
     out = {}
-    for kind in ("forward", "backward_call", "evidence_call", "dgrad_pair"):
+    for kind in ("forward", "backward_call", "evidence_call", "backward_call_gate_up", "evidence_call_gate_up"):
         times = [a.elapsed_time(b) for (k, _), a, b in records if k == kind]
         if not times:
             continue
@@ -962,10 +967,10 @@ def main():
         "data": "synthetic (seeded N(0,1) activations and gradients, U{-127..127} int8 coordinates)",
         "config": {"workload": "cfg4 Llama-3-8B SwiGLU MLP fwd+bwd+coordinate step",
                    "tokens": T, "d": d, "ffn": ffn, "layers": 3, "flop_per_step": flop,
-                   "gate": "qste_amd.nn.swiglu_mlp: the MLP as one autograd node (forward values, evidence "
-                           "and scale gradients equal to the layers with F.silu(g) * u bit for bit; one product "
-                           "for the gate and up layers' input gradient); the layers one by one are "
-                           "step_layer_by_layer_ms (fused gate) and step_torch_gate_ms (torch's silu and mul)"},
+                   "gate": "qste_amd.nn.swiglu_mlp: the MLP as one autograd node (forward values equal to the "
+                           "layers with F.silu(g) * u bit for bit; the gate and up layers' backward as one call "
+                           "over both); the layers one by one are step_layer_by_layer_ms (fused gate) and "
+                           "step_torch_gate_ms (torch's silu and mul)"},
         "frac_of_mfma_peak": round(flop / secs / MFMA_BF16_PEAK, 4),
     }
     if not args.no_extras:
@@ -986,9 +991,6 @@ def main():
         # the same products inside the training step (the chip is power-limited
         # there, so they run slower than back to back in isolation)
         line["in_step"] = in_step_times(step, T, d, ffn)
-        if "evidence_call" in line["in_step"] and dominant == "evidence":
-            # the roofline kernel inside the step: the node's evidence-only calls
-            line["roofline"]["in_step_frac"] = line["in_step"]["evidence_call"]["frac_of_mfma_peak"]
         if "backward_call" in line["in_step"]:
             line["roofline"]["in_step_backward_call_frac"] = line["in_step"]["backward_call"]["frac_of_mfma_peak"]
         line["roofline"]["isolated_backward_call_frac"] = kernels_t["backward_call"]["frac_of_mfma_peak"]

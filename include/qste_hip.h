@@ -386,24 +386,17 @@ int qste_swiglu_backward_sums(const void* grad, const void* gate, const void* up
                               void* grad_up, const float* offset_gate, const float* offset_up, float* sums,
                               int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes, void* stream);
 
-/* ---- the input gradient of two layers that read one input ----------------- */
-
-/* The input gradient of two layers that read one input (a SwiGLU MLP's gate
- * and up projections), summed in the product.  No counterpart in the
- * reference, where autograd adds the two layers' input gradients (each
- * from QSTELinearFn.backward, functional.py:173-194):
- *   dx [m, cols] = dy_a @ (scale_a (*) sign_a) + dy_b @ (scale_b (*) sign_b)
- * dy_a, dy_b [m, rows] (bf16 or fp16), sign_a, sign_b from packed_a,
- * packed_b uint8 [rows, cols/8]: one product over K = 2 rows with one fp32
- * accumulation and one rounding to the dtype (where autograd would round
- * each layer's dX and then their sum).  rows and cols multiples of 64.
- * Needs qste_packed_transpose_pair_workspace_bytes(m, rows, cols) bytes of
- * workspace. */
-size_t qste_packed_transpose_pair_workspace_bytes(int64_t m, int64_t rows, int64_t cols);
-int qste_packed_transpose_pair(const void* dy_a, const void* dy_b, int dtype, const uint8_t* packed_a,
-                               const float* scale_a, const uint8_t* packed_b, const float* scale_b, void* dx,
-                               int64_t m, int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes,
-                               void* stream);
+/* qste_swiglu_backward_sums with both gradients in one [rows, 2 cols]
+ * tensor, grad_gate in columns 0 .. cols-1 and grad_up in cols .. 2cols-1
+ * of each row (bf16 or fp16; cols a multiple of 8, 16-byte aligned
+ * operands).  Two layers that read one input then run their backward as
+ * one (qste_linear_backward_offset_dot over the concatenated signs and
+ * scales): their input gradients summed in one product, their evidence and
+ * scale gradients as one product's row blocks, with sums as its offset_dot.
+ * No counterpart in the reference (see qste_swiglu_forward). */
+int qste_swiglu_backward_sums_into(const void* grad, const void* gate, const void* up, int dtype, void* grads,
+                                   const float* offset_gate, const float* offset_up, float* sums, int64_t rows,
+                                   int64_t cols, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- the learned row scale (src/qste/surface.py:84-85) ------------------- */
 

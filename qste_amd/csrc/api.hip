@@ -48,9 +48,6 @@ int mfma_backward_pair(const void*, int, const uint8_t*, int64_t, const uint16_t
                        const uint16_t*, const uint8_t*, void*, int64_t, int64_t, int64_t, const float*,
                        const float*, float*, const EvidencePlan&, float*, hipStream_t);
 int launch_transpose_bits(const uint8_t*, uint8_t*, int64_t, int64_t, int64_t, int64_t, hipStream_t);
-int launch_transpose_bits_span(const uint8_t*, uint8_t*, int64_t, int64_t, int64_t, int64_t, int64_t, hipStream_t);
-int mfma_linear_dgrad_pair_t(const void*, const void*, int, const uint8_t*, int64_t, const uint16_t*, void*, int64_t,
-                             int64_t, int64_t, hipStream_t);
 int launch_f32_to_16(const float*, uint16_t*, int64_t, int64_t, int, hipStream_t);
 int gemv_linear_forward(const void*, int, const uint8_t*, const float*, const float*, void*, int64_t,
                         int64_t, int64_t, hipStream_t);
@@ -60,7 +57,7 @@ int launch_swiglu_backward(const void*, const void*, const void*, int, void*, vo
 int launch_row_scale(const void*, int, void*, void*, int64_t, float, float, hipStream_t);
 size_t swiglu_backward_sums_workspace(int64_t, int64_t);
 int launch_swiglu_backward_sums(const void*, const void*, const void*, int, void*, void*, const float*, const float*,
-                                int64_t, int64_t, float*, float*, hipStream_t);
+                                int64_t, int64_t, float*, float*, hipStream_t, int64_t);
 int launch_row_scale_backward(const void*, const void*, int, void*, int64_t, float, float, hipStream_t);
 // fp32 products through bf16 limbs (gemm_mfma.hip): 0 bytes / return 1 when
 // the shape is not for them
@@ -470,7 +467,23 @@ int qste_swiglu_backward_sums(const void* grad, const void* gate, const void* up
   if (!grad || !gate || !up || !grad_gate || !grad_up || !offset_gate || !offset_up) return QSTE_E_NULL;
   if (!workspace || workspace_bytes < swiglu_backward_sums_workspace(rows, cols)) return QSTE_E_WORKSPACE;
   return launch_swiglu_backward_sums(grad, gate, up, dtype, grad_gate, grad_up, offset_gate, offset_up, rows, cols,
-                                     sums, static_cast<float*>(workspace), s);
+                                     sums, static_cast<float*>(workspace), s, cols);
+}
+
+int qste_swiglu_backward_sums_into(const void* grad, const void* gate, const void* up, int dtype, void* grads,
+                                   const float* offset_gate, const float* offset_up, float* sums, int64_t rows,
+                                   int64_t cols, void* workspace, size_t workspace_bytes, void* stream) {
+  if (dtype != QSTE_BF16 && dtype != QSTE_F16) return QSTE_E_DTYPE;
+  if (rows < 0 || cols < 0) return QSTE_E_SHAPE;
+  if (cols == 0) return 0;
+  if (!sums) return QSTE_E_NULL;
+  hipStream_t s = as_stream(stream);
+  if (rows == 0) return fill_zero(sums, 2 * cols, s);
+  if (!grad || !gate || !up || !grads || !offset_gate || !offset_up) return QSTE_E_NULL;
+  if (!workspace || workspace_bytes < swiglu_backward_sums_workspace(rows, cols)) return QSTE_E_WORKSPACE;
+  uint16_t* out = static_cast<uint16_t*>(grads);
+  return launch_swiglu_backward_sums(grad, gate, up, dtype, out, out + cols, offset_gate, offset_up, rows, cols, sums,
+                                     static_cast<float*>(workspace), s, 2 * cols);
 }
 
 size_t qste_coordinate_update_workspace_bytes(int64_t rows, int64_t cols, int64_t block_size) {
@@ -554,39 +567,6 @@ int qste_row_scale_backward(const void* exp_value, const void* grad, int dtype, 
   if (n == 0) return 0;
   if (!exp_value || !grad || !grad_log_scale) return QSTE_E_NULL;
   return launch_row_scale_backward(exp_value, grad, dtype, grad_log_scale, n, lo, hi, as_stream(stream));
-}
-
-// ---- the input gradient of two layers that read one input ------------------
-
-size_t qste_packed_transpose_pair_workspace_bytes(int64_t m, int64_t rows, int64_t cols) {
-  if (m <= 0 || rows <= 0 || cols <= 0) return 0;
-  const int64_t pitch = 2 * ((rows + 63) / 64 * 8);
-  return align_up(static_cast<size_t>(cols * pitch)) +
-         align_up(sizeof(uint16_t) * static_cast<size_t>(2 * ((rows + 63) / 64 * 64)));
-}
-
-int qste_packed_transpose_pair(const void* dy_a, const void* dy_b, int dtype, const uint8_t* packed_a,
-                               const float* scale_a, const uint8_t* packed_b, const float* scale_b, void* dx,
-                               int64_t m, int64_t rows, int64_t cols, void* workspace, size_t workspace_bytes,
-                               void* stream) {
-  if (dtype != QSTE_BF16 && dtype != QSTE_F16) return QSTE_E_DTYPE;
-  if (m <= 0 || rows <= 0 || cols <= 0 || rows % 64 != 0 || cols % 64 != 0) return QSTE_E_SHAPE;
-  if (!dy_a || !dy_b || !packed_a || !packed_b || !scale_a || !scale_b || !dx) return QSTE_E_NULL;
-  const size_t need = qste_packed_transpose_pair_workspace_bytes(m, rows, cols);
-  if (!workspace || workspace_bytes < need) return QSTE_E_WORKSPACE;
-  hipStream_t s = as_stream(stream);
-  const int64_t pitch = 2 * rows / 8;
-  uint8_t* w_t = static_cast<uint8_t*>(workspace);
-  uint16_t* s16 = reinterpret_cast<uint16_t*>(w_t + align_up(static_cast<size_t>(cols * pitch)));
-  int rc;
-  // the two sign matrices side by side along K: a's rows are k = 0 .. rows-1,
-  // b's k = rows .. 2 rows - 1
-  if ((rc = launch_transpose_bits_span(packed_a, w_t, rows, cols, cols / 8, pitch, rows / 8, s))) return rc;
-  if ((rc = launch_transpose_bits_span(packed_b, w_t + rows / 8, rows, cols, cols / 8, pitch, rows / 8, s))) return rc;
-  if ((rc = launch_f32_to_16(scale_a, s16, rows, rows, dtype, s))) return rc;
-  if ((rc = launch_f32_to_16(scale_b, s16 + rows, rows, rows, dtype, s))) return rc;
-  rc = mfma_linear_dgrad_pair_t(dy_a, dy_b, dtype, w_t, pitch, s16, dx, m, rows, cols, s);
-  return rc == 1 ? QSTE_E_ALIGN : rc;
 }
 
 size_t qste_coordinate_update_static_limit(void) { return coordinate_update_static_limit(); }

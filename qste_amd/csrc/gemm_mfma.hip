@@ -58,11 +58,6 @@ struct Params {
   int64_t pb;            // bytes per packed row
   int64_t a_rows;        // rows of the dense source (bounds of its buffer)
   int64_t bit_rows;      // rows of the packed source
-  // A as rows of M only: with a2, K steps from k_split (a multiple of BK)
-  // on read a2 at k - k_split (two dense operands side by side along K,
-  // each with lda columns)
-  const uint16_t* a2;
-  int64_t k_split;
   // epilogue
   const float* n_scale;  // forward
   const float* n_bias;   // forward
@@ -290,11 +285,10 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
   // A as rows of K: the buffer starts at column m0, so k-rows past K read
   // zero.  Wave w fills row pairs 8w .. 8w+7, one direct load each; lane i
   // loads chunk i/2 of k-row 2P + i%2.
-  __amdgpu_buffer_rsrc_t ra, ra2;
+  __amdgpu_buffer_rsrc_t ra;
   uint32_t a_voff[2], a_row8;
   if (AKIND == A_ROWS_M) {
     ra = rsrc(p.a + m0 * p.lda, (p.a_rows - m0) * p.lda * 2);
-    ra2 = p.a2 ? rsrc(p.a2 + m0 * p.lda, (p.a_rows - m0) * p.lda * 2) : ra;
     const int q8 = lane >> 3, pos = lane & 7;
 #pragma unroll
     for (int par = 0; par < 2; ++par)
@@ -302,12 +296,10 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
     a_row8 = static_cast<uint32_t>(8 * p.lda * 2);
   } else {
     ra = rsrc(p.a + m0, (p.a_rows * p.lda - m0) * 2);
-    ra2 = ra;
     a_voff[0] = a_voff[1] = static_cast<uint32_t>(((16 * wave + (lane & 1)) * p.lda + 8 * (lane >> 1)) * 2);
     a_row8 = static_cast<uint32_t>(2 * p.lda * 2);  // one row pair
   }
   const uint32_t a_kstep = AKIND == A_ROWS_M ? BK * 2 : static_cast<uint32_t>(BK * p.lda * 2);
-  const int nk1 = (AKIND == A_ROWS_M && p.a2) ? static_cast<int>(p.k_split / BK) : nk;  // K steps from p.a
 
   // B along K: 256 rows x 8 bytes per stage, wave w fills rows 64w ..
   // 64w+63 with 2 direct loads of 4 bytes per lane.
@@ -346,14 +338,12 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
       bsv = ld32(rs, soff);
       balt = static_cast<float>(static_cast<int>(live) & static_cast<int>(it * BK + (tid & 63) < p.K));
     }
-    const bool second = live && it >= nk1;  // uniform: the second dense operand
-    const uint32_t k_off = live ? static_cast<uint32_t>(second ? it - nk1 : it) * a_kstep : 0x80000000u;
-    const __amdgpu_buffer_rsrc_t rA = second ? ra2 : ra;
+    const uint32_t k_off = live ? static_cast<uint32_t>(it) * a_kstep : 0x80000000u;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if (part >= 0 && (j >> 1) != part) continue;
       uint8_t* dst = AKIND == A_ROWS_M ? As + (64 * wave + 8 * j) * 128 : As + (8 * wave + j) * APK;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lds_t*)dst, 16, a_voff[j & 1],
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_t*)dst, 16, a_voff[j & 1],
                                                static_cast<int>(j * a_row8 + k_off), 0, 0);
     }
     if (BKIND != B_BITS_ALONG_N && (part < 0 || part == 3)) {
@@ -1143,37 +1133,6 @@ int mfma_linear_dgrad_t(const void* dy, int dtype, const uint8_t* w_t, int64_t w
   p.kscale16 = scale16;
   p.out = dx;
   p.M = m; p.N = cols; p.K = rows;
-  p.lda = rows; p.pb = w_t_pitch;
-  p.a_rows = m; p.bit_rows = cols;
-  if (dtype == QSTE_F16)
-    mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K_SCALED, mfma::EPI_PLAIN, QSTE_F16>
-        <<<wide_grid(m, cols), mfma::wide::THREADS, 0, stream>>>(p);
-  else
-    mfma::wide::wide_kernel<mfma::A_ROWS_M, mfma::B_BITS_ALONG_K_SCALED, mfma::EPI_PLAIN, QSTE_BF16>
-        <<<wide_grid(m, cols), mfma::wide::THREADS, 0, stream>>>(p);
-  return static_cast<int>(hipGetLastError());
-}
-
-// dx [m, cols] = dy_a @ (scale_a * sign_a) + dy_b @ (scale_b * sign_b) as
-// one product over K = 2 * rows: the two dense operands ([m, rows] each)
-// side by side along K, the two sign matrices transposed side by side in
-// w_t (bits along K, pitch w_t_pitch >= 2 * rows / 8) with their bf16
-// scales concatenated in scale16.  One fp32 accumulation and one rounding
-// for both terms.  Returns 1 when the call is not for this path.
-int mfma_linear_dgrad_pair_t(const void* dy_a, const void* dy_b, int dtype, const uint8_t* w_t, int64_t w_t_pitch,
-                             const uint16_t* scale16, void* dx, int64_t m, int64_t rows, int64_t cols,
-                             hipStream_t stream) {
-  if (rows % 64 != 0 || !dgrad_ok(dy_a, dtype, w_t, m, 2 * rows, cols) || !aligned16(dy_b) || !fits32(m * rows * 2) ||
-      !fits32(cols * w_t_pitch) || !aligned16(w_t))
-    return 1;
-  mfma::Params p{};
-  p.a = static_cast<const uint16_t*>(dy_a);
-  p.a2 = static_cast<const uint16_t*>(dy_b);
-  p.k_split = rows;
-  p.bits = w_t;
-  p.kscale16 = scale16;
-  p.out = dx;
-  p.M = m; p.N = cols; p.K = 2 * rows;
   p.lda = rows; p.pb = w_t_pitch;
   p.a_rows = m; p.bit_rows = cols;
   if (dtype == QSTE_F16)

@@ -208,8 +208,7 @@ constexpr int kTrPad = 4;                        // bytes of padding per staged 
 __global__ __launch_bounds__(256) void transpose_bits_kernel(const uint8_t* __restrict__ in,
                                                              uint8_t* __restrict__ out, int64_t rows,
                                                              int64_t cols, int64_t in_pitch,
-                                                             int64_t out_pitch, int64_t out_bytes,
-                                                             int64_t row_tiles) {
+                                                             int64_t out_pitch, int64_t row_tiles) {
   __shared__ __attribute__((aligned(16))) uint8_t tile[kTrRows][kTrColBytes + kTrPad];
   __shared__ uint64_t otile[8 * kTrColBytes][kTrGroups];  // [column][64-row group]
   const int64_t cb0 = static_cast<int64_t>(blockIdx.x) * kTrColBytes;
@@ -264,7 +263,7 @@ __global__ __launch_bounds__(256) void transpose_bits_kernel(const uint8_t* __re
       const int cl = tid / kTrGroups + (256 / kTrGroups) * i, piece = tid % kTrGroups;
       const int64_t c = 8 * cb0 + cl;
       const int64_t ob = r0 / 8 + 8 * piece;
-      if (c < cols && ob < out_bytes) *reinterpret_cast<uint64_t*>(out + c * out_pitch + ob) = otile[cl][piece];
+      if (c < cols && ob < out_pitch) *reinterpret_cast<uint64_t*>(out + c * out_pitch + ob) = otile[cl][piece];
     }
     __syncthreads();  // the next row tile reuses tile and otile
   }
@@ -277,27 +276,17 @@ __global__ void f32_to_16_kernel(const float* __restrict__ in, uint16_t* __restr
   if (i < padded) out[i] = i < n ? (DT == QSTE_F16 ? f32_to_f16(in[i]) : f32_to_bf16(in[i])) : 0;
 }
 
-// Writes bytes [0, out_bytes) of each output row (out_bytes <= out_pitch,
-// both multiples of 8): bits past `rows` read as zero.  Two calls with
-// out_bytes = rows / 8 at out and at out + rows / 8, pitch 2 * rows / 8,
-// lay two sign matrices side by side along K.
-int launch_transpose_bits_span(const uint8_t* in, uint8_t* out, int64_t rows, int64_t cols, int64_t in_pitch,
-                               int64_t out_pitch, int64_t out_bytes, hipStream_t stream) {
-  if (rows == 0 || cols == 0 || out_bytes == 0) return 0;
-  if (out_pitch % 8 != 0 || out_bytes % 8 != 0 || out_bytes > out_pitch || (reinterpret_cast<uintptr_t>(out) & 7))
-    return QSTE_E_ALIGN;
-  // row tiles cover every written byte (out_bytes * 8 rows, the padding
-  // included, which reads as zero); beyond the grid's 65535 rows of
-  // workgroups each walks several tiles
-  const int64_t row_tiles = (out_bytes * 8 + kTrRows - 1) / kTrRows;
-  const dim3 grid(ceil_div(in_pitch, kTrColBytes), static_cast<unsigned>(row_tiles < 65535 ? row_tiles : 65535));
-  transpose_bits_kernel<<<grid, 256, 0, stream>>>(in, out, rows, cols, in_pitch, out_pitch, out_bytes, row_tiles);
-  return static_cast<int>(hipGetLastError());
-}
-
 int launch_transpose_bits(const uint8_t* in, uint8_t* out, int64_t rows, int64_t cols, int64_t in_pitch,
                           int64_t out_pitch, hipStream_t stream) {
-  return launch_transpose_bits_span(in, out, rows, cols, in_pitch, out_pitch, out_pitch, stream);
+  if (rows == 0 || cols == 0 || out_pitch == 0) return 0;
+  if (out_pitch % 8 != 0 || (reinterpret_cast<uintptr_t>(out) & 7)) return QSTE_E_ALIGN;
+  // row tiles cover every output byte (out_pitch * 8 rows, the padding
+  // included, which reads as zero); beyond the grid's 65535 rows of
+  // workgroups each walks several tiles
+  const int64_t row_tiles = (out_pitch * 8 + kTrRows - 1) / kTrRows;
+  const dim3 grid(ceil_div(in_pitch, kTrColBytes), static_cast<unsigned>(row_tiles < 65535 ? row_tiles : 65535));
+  transpose_bits_kernel<<<grid, 256, 0, stream>>>(in, out, rows, cols, in_pitch, out_pitch, row_tiles);
+  return static_cast<int>(hipGetLastError());
 }
 
 // fp32 -> the 16-bit operand dtype (bf16 or fp16), zero-padded to `padded`

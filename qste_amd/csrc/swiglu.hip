@@ -246,7 +246,7 @@ template <int DT>
 __global__ __launch_bounds__(kSumThreads) void backward_sums_kernel(
     const uint16_t* __restrict__ dh, const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
     uint16_t* __restrict__ dg, uint16_t* __restrict__ du, const float* __restrict__ off_g,
-    const float* __restrict__ off_u, int64_t samples, int64_t cols, float* __restrict__ part) {
+    const float* __restrict__ off_u, int64_t samples, int64_t cols, int64_t ldo, float* __restrict__ part) {
   constexpr int UNROLL = 4;
   constexpr int kPad = 17;
   constexpr int kRed = kSumWaves * 64 * kPad;
@@ -276,8 +276,8 @@ __global__ __launch_bounds__(kSumThreads) void backward_sums_kernel(
     uint4 rg, ru;
     float fg[8], fu[8];
     backward_x8<DT>(hc, gc, uc, rg, ru, fg, fu, tab_s, tab_a);
-    *reinterpret_cast<uint4*>(dg + t * cols + c) = rg;
-    *reinterpret_cast<uint4*>(du + t * cols + c) = ru;
+    *reinterpret_cast<uint4*>(dg + t * ldo + c) = rg;
+    *reinterpret_cast<uint4*>(du + t * ldo + c) = ru;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       vg[i] = fmaf(fg[i], og_, vg[i]);
@@ -430,22 +430,24 @@ size_t swiglu_backward_sums_workspace(int64_t rows, int64_t cols) {
 // part: swiglu_backward_sums_workspace(rows, cols) bytes.
 int launch_swiglu_backward_sums(const void* dh, const void* g, const void* u, int dtype, void* dg, void* du,
                                 const float* off_g, const float* off_u, int64_t rows, int64_t cols, float* sums,
-                                float* part, hipStream_t s) {
+                                float* part, hipStream_t s, int64_t ld_out) {
   using namespace swiglu;
   if (rows * cols == 0) return 0;
   const int64_t chunks = (rows + kSumChunk - 1) / kSumChunk;
   const bool x8 = (dtype == QSTE_BF16 || dtype == QSTE_F16) && cols % 8 == 0 && aligned(dh) && aligned(g) &&
-                  aligned(u) && aligned(dg) && aligned(du);
+                  aligned(u) && aligned(dg) && aligned(du) && ld_out % 8 == 0;
+  // outputs with a row pitch of their own are written by the 8-wide pass only
+  if (ld_out != cols && !x8) return QSTE_E_ALIGN;
   if (x8) {
     const dim3 grid(static_cast<unsigned>((cols + 511) / 512), static_cast<unsigned>(chunks));
     if (dtype == QSTE_BF16)
       backward_sums_kernel<QSTE_BF16><<<grid, kSumThreads, 0, s>>>(
           static_cast<const uint16_t*>(dh), static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u),
-          static_cast<uint16_t*>(dg), static_cast<uint16_t*>(du), off_g, off_u, rows, cols, part);
+          static_cast<uint16_t*>(dg), static_cast<uint16_t*>(du), off_g, off_u, rows, cols, ld_out, part);
     else
       backward_sums_kernel<QSTE_F16><<<grid, kSumThreads, 0, s>>>(
           static_cast<const uint16_t*>(dh), static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(u),
-          static_cast<uint16_t*>(dg), static_cast<uint16_t*>(du), off_g, off_u, rows, cols, part);
+          static_cast<uint16_t*>(dg), static_cast<uint16_t*>(du), off_g, off_u, rows, cols, ld_out, part);
     const int rc = static_cast<int>(hipGetLastError());
     if (rc) return rc;
     return launch_sum_partials(part, chunks, 2 * cols, sums, s);

@@ -226,13 +226,19 @@ class SwiGLUMLPFn(Function):
 
     The values are those of the three QSTELinearFn nodes and SwiGLUFn
     composed: the same products, the same gate arithmetic, the same
-    encodings (x's shared by gate and up; h's from the gate kernel), and the
-    same evidence and scale gradients bit for bit (the gate's backward sums
-    the offset corrections of the gate and up layers as those layers would,
-    ``swiglu_backward_sums``).  One thing differs: x's gradient is one
-    product over both layers (``packed_transpose_pair``), rounded once, where
-    autograd rounds each layer's input gradient and then their sum -- one
-    launch and one pass over [tokens, d] tensors fewer.
+    encodings (x's shared by gate and up; h's from the gate kernel).  The
+    backward runs the gate and up layers as one layer of 2 ffn rows: the
+    gate's backward writes their gradients side by side into one [tokens,
+    2 ffn] tensor (with the two layers' offset sums, in the order the layers
+    would sum them), and one ``linear_backward`` over it and the two layers'
+    concatenated signs and scales gives
+
+    * their evidence and scale gradients as the row blocks of one product
+      (each element as the layer's own product forms it; a split-K plan
+      chosen for the longer product may sum some tiles in another order),
+    * x's gradient as one product over K = 2 ffn, rounded once, where
+      autograd rounds each layer's input gradient and then their sum --
+      one launch and one pass over [tokens, d] tensors fewer.
 
     Evidence goes to each surface after every product that reads that
     surface's signs (a delivery may step the surface, rewriting them), as in
@@ -275,20 +281,23 @@ class SwiGLUMLPFn(Function):
             dy, payload_h, aux_h[0], aux_h[1], packed_d, scale_d.detach(), ffn, need_bias=bd is not None)
         sd.consume_evidence(ev_d)
         del ev_d
-        dg, du, sums = kernels.swiglu_backward_sums(dh, g, u, aux_x[0], aux_x[0])
+        both, sums = kernels.swiglu_backward_sums(dh, g, u, aux_x[0], aux_x[0], side_by_side=True)
         del dh
-        _, ev_g, gs_g, gb_g = kernels.linear_backward(
-            dg, payload_x, aux_x[0], aux_x[1], packed_g, scale_g.detach(), d, need_bias=bg is not None,
-            need_input=False, offset_dot=sums[0])
-        _, ev_u, gs_u, gb_u = kernels.linear_backward(
-            du, payload_x, aux_x[0], aux_x[1], packed_u, scale_u.detach(), d, need_bias=bu is not None,
-            need_input=False, offset_dot=sums[1])
-        dx = None
-        if ctx.needs_input_grad[0]:
-            dx = kernels.packed_transpose_pair(dg, packed_g, scale_g.detach(), du, packed_u, scale_u.detach(), d)
+        # gate and up as one layer of 2 ffn rows (copies of their signs and
+        # scales: the deliveries below may rewrite the signs)
+        packed_gu = torch.cat((packed_g, packed_u))
+        scale_gu = torch.cat((scale_g.detach().float(), scale_u.detach().float()))
+        need_bias = bg is not None or bu is not None
+        dx, ev_gu, gs_gu, gb_gu = kernels.linear_backward(
+            both, payload_x, aux_x[0], aux_x[1], packed_gu, scale_gu, d, need_bias=need_bias,
+            need_input=ctx.needs_input_grad[0], offset_dot=sums.reshape(-1))
+        del both
+        if dx is not None:
             dx = dx.reshape(ctx.input_shape)
-        sg.consume_evidence(ev_g)
-        su.consume_evidence(ev_u)
+        sg.consume_evidence(ev_gu[:ffn])
+        su.consume_evidence(ev_gu[ffn:])
+        gs_g, gs_u = gs_gu[:ffn], gs_gu[ffn:]
+        gb_g, gb_u = (gb_gu[:ffn], gb_gu[ffn:]) if need_bias else (None, None)
 
         def cast(grad, dtype):
             return None if grad is None or dtype is None else grad.to(dtype)

@@ -746,11 +746,18 @@ def swiglu_backward(grad: Tensor, gate: Tensor, up: Tensor) -> tuple[Tensor, Ten
 
 
 def swiglu_backward_sums(grad: Tensor, gate: Tensor, up: Tensor, offset_gate: Tensor,
-                         offset_up: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+                         offset_up: Tensor, *, side_by_side: bool = False):
     """``swiglu_backward`` of [rows, cols] operands plus ``sums`` fp32 [2, cols]:
     ``sum_t grad_gate[t] * offset_gate[t]`` and ``sum_t grad_up[t] * offset_up[t]``,
     each what ``linear_backward`` would sum from that gradient and offset
-    (its ``offset_dot``)."""
+    (its ``offset_dot``).  Returns ``(grad_gate, grad_up, sums)``.
+
+    With ``side_by_side`` (16-bit dtypes, cols a multiple of 8) both
+    gradients go into one [rows, 2 cols] tensor, grad_gate in its first
+    cols columns and grad_up in the rest, and the call returns ``(grads,
+    sums)``: two layers that read one input then run their backward as one
+    ``linear_backward`` over ``grads`` and their concatenated signs
+    (``qste_swiglu_backward_sums_into``)."""
 
     device = _require_gpu(grad, gate, up, offset_gate, offset_up)
     if not (grad.shape == gate.shape == up.shape) or not (grad.dtype == gate.dtype == up.dtype):
@@ -764,43 +771,22 @@ def swiglu_backward_sums(grad: Tensor, gate: Tensor, up: Tensor, offset_gate: Te
             raise ValueError(f"{name} must be fp32 [rows]")
         offs.append(o.contiguous())
     dh, g, u = _aligned(grad), _aligned(gate), _aligned(up)
-    dg, du = torch.empty_like(g), torch.empty_like(g)
     sums = torch.empty(2, cols, dtype=torch.float32, device=device)
     lib = _lib.load()
     work = _workspace(lib.qste_swiglu_backward_sums_workspace_bytes(rows, cols), device)
+    if side_by_side:
+        both = torch.empty(rows, 2 * cols, dtype=g.dtype, device=device)
+        code = lib.qste_swiglu_backward_sums_into(
+            _ptr(dh), _ptr(g), _ptr(u), _dtype_code(g), _ptr(both), _ptr(offs[0]), _ptr(offs[1]), _ptr(sums),
+            rows, cols, _ptr(work), work.numel(), _stream(device))
+        _lib.check(code, "swiglu_backward_sums")
+        return both, sums
+    dg, du = torch.empty_like(g), torch.empty_like(g)
     code = lib.qste_swiglu_backward_sums(
         _ptr(dh), _ptr(g), _ptr(u), _dtype_code(g), _ptr(dg), _ptr(du), _ptr(offs[0]), _ptr(offs[1]),
         _ptr(sums), rows, cols, _ptr(work), work.numel(), _stream(device))
     _lib.check(code, "swiglu_backward_sums")
     return dg, du, sums
-
-
-def packed_transpose_pair(grad_a: Tensor, packed_a: Tensor, scale_a: Tensor, grad_b: Tensor, packed_b: Tensor,
-                          scale_b: Tensor, columns: int) -> Tensor:
-    """``grad_a @ (scale_a * sign_a) + grad_b @ (scale_b * sign_b)`` in one
-    product (one fp32 accumulation, one rounding to the dtype): the input
-    gradient of two layers that read one input.  grad_a, grad_b [tokens,
-    rows] bf16 or fp16; packed_* [rows, columns/8]; scale_* fp32 [rows];
-    rows and columns multiples of 64.  No counterpart in the reference,
-    where autograd adds the two layers' input gradients."""
-
-    device = _require_gpu(grad_a, packed_a, scale_a, grad_b, packed_b, scale_b)
-    if grad_a.dim() != 2 or grad_a.shape != grad_b.shape or grad_a.dtype != grad_b.dtype:
-        raise ValueError("packed_transpose_pair expects two rank-2 gradients of one shape and dtype")
-    tokens, rows = grad_a.shape
-    pa, pb = _check_packed(packed_a, columns), _check_packed(packed_b, columns)
-    if pa.shape[0] != rows or pb.shape[0] != rows or scale_a.numel() != rows or scale_b.numel() != rows:
-        raise ValueError("packed_transpose_pair operands disagree on rows")
-    ga, gb = _aligned(grad_a), _aligned(grad_b)
-    sa, sb = _f32(scale_a), _f32(scale_b)
-    out = torch.empty(tokens, int(columns), dtype=grad_a.dtype, device=device)
-    lib = _lib.load()
-    work = _workspace(lib.qste_packed_transpose_pair_workspace_bytes(tokens, rows, int(columns)), device)
-    code = lib.qste_packed_transpose_pair(
-        _ptr(ga), _ptr(gb), _dtype_code(ga), _ptr(pa), _ptr(sa), _ptr(pb), _ptr(sb), _ptr(out), tokens, rows,
-        int(columns), _ptr(work), work.numel(), _stream(device))
-    _lib.check(code, "packed_transpose_pair")
-    return out
 
 
 def row_scale(log_scale: Tensor, lo: float, hi: float) -> tuple[Tensor, Tensor]:

@@ -74,8 +74,7 @@ SIGNATURES = {
     "qste_swiglu_backward": (_int, [_vp, _vp, _vp, _int, _vp, _vp, _i64, _vp]),
     "qste_swiglu_backward_sums_workspace_bytes": (_sz, [_i64, _i64]),
     "qste_swiglu_backward_sums": (_int, [_vp, _vp, _vp, _int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _sz, _vp]),
-    "qste_packed_transpose_pair_workspace_bytes": (_sz, [_i64, _i64, _i64]),
-    "qste_packed_transpose_pair": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _sz, _vp]),
+    "qste_swiglu_backward_sums_into": (_int, [_vp, _vp, _vp, _int, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _sz, _vp]),
     "qste_row_scale": (_int, [_vp, _int, _vp, _vp, _i64, _flt, _flt, _vp]),
     "qste_row_scale_backward": (_int, [_vp, _vp, _int, _vp, _i64, _flt, _flt, _vp]),
     "qste_packed_embedding": (_int, [_vp, _i64, _vp, _vp, _vp, _int, _i64, _i64, _vp]),

@@ -1,15 +1,23 @@
 """The SwiGLU MLP as one autograd node (``qste_amd.nn.swiglu_mlp``).
 
-Its one new product, ``packed_transpose_pair`` (the gate and up layers'
-input gradients as one product over K = 2 ffn), is held to the float64
-oracle of the two products summed (rel-L2 <= 1e-3 against the oracle
-rounded to the dtype, as every 16-bit product here), bf16 and fp16, at
-ragged shapes and at config 4's shape on sampled tokens.
+The node runs the gate and up layers' backward as one layer of 2 ffn rows:
+the gate's backward writes both gradients side by side
+(``swiglu_backward_sums(..., side_by_side=True)``), and one
+``linear_backward`` over them and the two layers' concatenated signs and
+scales gives both layers' evidence and scale gradients as its row blocks
+and the input gradient as one product over K = 2 ffn.  Held here:
 
-Then the node against the same MLP run layer by layer (``swiglu`` between
-the layers): the output, every layer's evidence, scale gradient and
-coordinate step bit for bit, and the input gradient within the rounding
-that the single product saves.
+* the side-by-side gradients and sums bit for bit against the plain call;
+* the one call against the two layers' own calls: evidence and scale
+  gradients within fp32 summation order (rel <= 1e-6), the input gradient
+  within the rounding the single product saves, and against the float64
+  oracle of the summed products (rel-L2 <= 1e-3 against the oracle rounded
+  to bf16, as every 16-bit product here), also at config 4's shape on
+  sampled tokens;
+* the node against the same MLP run layer by layer (``swiglu`` between the
+  layers): the output bit for bit, the evidence and scale gradients within
+  1e-6, the coordinate steps equal outside elements whose evidence moved,
+  the input gradient within the saved rounding.
 """
 
 from __future__ import annotations
@@ -45,56 +53,83 @@ def _rel(a, b):
     return float((a - b).norm() / b.norm())
 
 
-def _pair_oracle(ga, pa, sa, gb, pb, sb, cols, dtype):
-    rnd = oracle.round_bf16 if dtype == torch.bfloat16 else (lambda v: np.asarray(v, np.float16).astype(np.float32))
-    want = oracle.linear_dgrad(ga.float().cpu().numpy(), pa.cpu().numpy(), cols, rnd(sa.cpu().numpy()))
-    want = want + oracle.linear_dgrad(gb.float().cpu().numpy(), pb.cpu().numpy(), cols, rnd(sb.cpu().numpy()))
-    return torch.from_numpy(np.asarray(want, np.float32)).to(dtype).double()
+def _bits(t):
+    return t.contiguous().view(torch.int16)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("T,rows,cols", [(512, 256, 320), (300, 192, 256), (1, 64, 64), (257, 576, 128)])
-def test_packed_transpose_pair_against_the_oracle(T, rows, cols, dtype):
+@pytest.mark.parametrize("rows,cols", [(512, 3584), (300, 1000), (257, 520), (1, 8)])
+def test_side_by_side_equals_the_plain_call(rows, cols, dtype):
     k = _k()
-    print(f"packed_transpose_pair {T}x{rows}x{cols} {dtype}", flush=True)
-    g = torch.Generator(device=DEV).manual_seed(T * 3 + rows + cols)
-    ga = torch.randn(T, rows, generator=g, device=DEV).to(dtype)
-    gb = torch.randn(T, rows, generator=g, device=DEV).to(dtype)
-    ca = torch.randint(-127, 128, (rows, cols), generator=g, device=DEV, dtype=torch.int32).to(torch.int8)
-    cb = torch.randint(-127, 128, (rows, cols), generator=g, device=DEV, dtype=torch.int32).to(torch.int8)
-    pa, pb = k.pack_coordinate(ca), k.pack_coordinate(cb)
-    sa = torch.rand(rows, generator=g, device=DEV) * 0.02 + 0.005
-    sb = torch.rand(rows, generator=g, device=DEV) * 0.02 + 0.005
-    dx = k.packed_transpose_pair(ga, pa, sa, gb, pb, sb, cols)
+    g = torch.Generator(device=DEV).manual_seed(rows + cols)
+    gate = (torch.randn(rows, cols, generator=g, device=DEV) * 3).to(dtype)
+    up = torch.randn(rows, cols, generator=g, device=DEV).to(dtype)
+    grad = torch.randn(rows, cols, generator=g, device=DEV).to(dtype)
+    off = torch.randn(rows, generator=g, device=DEV)
+    dg, du, sums = k.swiglu_backward_sums(grad, gate, up, off, off)
+    both, sums2 = k.swiglu_backward_sums(grad, gate, up, off, off, side_by_side=True)
     torch.cuda.synchronize()
-    assert dx.dtype == dtype and dx.shape == (T, cols)
-    assert _rel(dx.cpu(), _pair_oracle(ga, pa, sa, gb, pb, sb, cols, dtype)) <= 1e-3
-    # the two products rounded and added as autograd would: the same values
-    # up to those two extra roundings
-    two = (k.packed_transpose(ga, pa, cols, row_scale=sa) + k.packed_transpose(gb, pb, cols, row_scale=sb))
-    assert _rel(dx, two) <= 8e-3
+    assert both.shape == (rows, 2 * cols) and both.dtype == dtype
+    assert torch.equal(_bits(both[:, :cols]), _bits(dg)) and torch.equal(_bits(both[:, cols:]), _bits(du))
+    assert torch.equal(sums, sums2)
 
 
-def test_packed_transpose_pair_config4_shape():
-    """The gate and up layers' input gradient at config 4 (16384 tokens,
-    ffn 14336 -> d 4096): the oracle on 64 sampled tokens."""
+def _two_layers(T, d, ffn, seed):
+    k = _k()
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    x = torch.randn(T, d, generator=g, device=DEV).to(torch.bfloat16)
+    packed_x, off, xs = k.pack_affine_rows(x)
+    pg = k.pack_coordinate(torch.randint(-127, 128, (ffn, d), generator=g, device=DEV,
+                                         dtype=torch.int32).to(torch.int8))
+    pu = k.pack_coordinate(torch.randint(-127, 128, (ffn, d), generator=g, device=DEV,
+                                         dtype=torch.int32).to(torch.int8))
+    sg = torch.rand(ffn, generator=g, device=DEV) * 0.02 + 0.005
+    su = torch.rand(ffn, generator=g, device=DEV) * 0.02 + 0.005
+    both = torch.randn(T, 2 * ffn, generator=g, device=DEV).to(torch.bfloat16)
+    return packed_x, off, xs, pg, pu, sg, su, both
+
+
+def _dgrad_oracle(grad, packed, cols, scale):
+    want = oracle.linear_dgrad(grad.float().cpu().numpy(), packed.cpu().numpy(), cols,
+                               oracle.round_bf16(scale.cpu().numpy()))
+    return torch.from_numpy(np.asarray(want, np.float32)).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("T,d,ffn", [(1024, 1024, 3584), (300, 256, 512)])
+def test_one_call_for_two_layers_equals_their_own_calls(T, d, ffn):
+    k = _k()
+    print(f"two layers as one {T}x{d}x{ffn}", flush=True)
+    packed_x, off, xs, pg, pu, sg, su, both = _two_layers(T, d, ffn, T + d)
+    dg, du = both[:, :ffn].contiguous(), both[:, ffn:].contiguous()
+    dx_g, ev_g, gs_g, _ = k.linear_backward(dg, packed_x, off, xs, pg, sg, d, need_bias=False)
+    dx_u, ev_u, gs_u, _ = k.linear_backward(du, packed_x, off, xs, pu, su, d, need_bias=False)
+    pgu, sgu = torch.cat((pg, pu)), torch.cat((sg, su))
+    dx, ev, gs, _ = k.linear_backward(both, packed_x, off, xs, pgu, sgu, d, need_bias=False)
+    torch.cuda.synchronize()
+    assert _rel(ev[:ffn], ev_g) <= 1e-6 and _rel(ev[ffn:], ev_u) <= 1e-6
+    assert _rel(gs[:ffn], gs_g) <= 1e-6 and _rel(gs[ffn:], gs_u) <= 1e-6
+    assert _rel(dx, dx_g + dx_u) <= 8e-3
+    assert _rel(dx.cpu(), _dgrad_oracle(both, pgu, d, sgu)) <= 1e-3
+
+
+def test_one_call_for_two_layers_config4_shape():
+    """Config 4's gate and up layers (16384 tokens, d 4096, ffn 14336) as
+    one call: the input gradient against the oracle on 64 sampled tokens,
+    the up layer's evidence and scale gradient against its own call."""
 
     k = _k()
-    T, rows, cols = 16384, 14336, 4096
-    g = torch.Generator(device=DEV).manual_seed(41)
-    ga = torch.randn(T, rows, generator=g, device=DEV).to(torch.bfloat16)
-    gb = torch.randn(T, rows, generator=g, device=DEV).to(torch.bfloat16)
-    pa = k.pack_coordinate(torch.randint(-127, 128, (rows, cols), generator=g, device=DEV,
-                                         dtype=torch.int32).to(torch.int8))
-    pb = k.pack_coordinate(torch.randint(-127, 128, (rows, cols), generator=g, device=DEV,
-                                         dtype=torch.int32).to(torch.int8))
-    sa = torch.rand(rows, generator=g, device=DEV) * 0.02 + 0.005
-    sb = torch.rand(rows, generator=g, device=DEV) * 0.02 + 0.005
-    dx = k.packed_transpose_pair(ga, pa, sa, gb, pb, sb, cols)
+    T, d, ffn = 16384, 4096, 14336
+    packed_x, off, xs, pg, pu, sg, su, both = _two_layers(T, d, ffn, 41)
+    pgu, sgu = torch.cat((pg, pu)), torch.cat((sg, su))
+    dx, ev, gs, _ = k.linear_backward(both, packed_x, off, xs, pgu, sgu, d, need_bias=False)
     torch.cuda.synchronize()
     sel = torch.from_numpy(np.sort(np.random.default_rng(4).choice(T, 64, replace=False))).to(DEV)
-    want = _pair_oracle(ga[sel], pa, sa, gb[sel], pb, sb, cols, torch.bfloat16)
-    assert _rel(dx[sel].cpu(), want) <= 1e-3
+    assert _rel(dx[sel].cpu(), _dgrad_oracle(both[sel], pgu, d, sgu)) <= 1e-3
+    del dx
+    _, ev_u, gs_u, _ = k.linear_backward(both[:, ffn:].contiguous(), packed_x, off, xs, pu, su, d,
+                                         need_bias=False, need_input=False)
+    torch.cuda.synchronize()
+    assert _rel(ev[ffn:], ev_u) <= 1e-6 and _rel(gs[ffn:], gs_u) <= 1e-6
 
 
 def test_swiglu_mlp_node_matches_the_layer_by_layer_mlp():
@@ -128,13 +163,14 @@ def test_swiglu_mlp_node_matches_the_layer_by_layer_mlp():
     y0, gx0, ev0, gs0, c0, f0 = run(False)
     y1, gx1, ev1, gs1, c1, f1 = run(True)
     assert torch.equal(y0, y1)
-    for name in ("gate", "up", "down"):
-        assert torch.equal(ev0[name], ev1[name]), name
+    assert torch.equal(ev0["down"], ev1["down"]) and torch.equal(c0[2], c1[2])
+    for name in ("gate", "up"):
+        assert _rel(ev1[name], ev0[name]) <= 1e-6, name
     for a, b in zip(gs0, gs1):
-        assert torch.equal(a, b)
+        assert _rel(b, a) <= 1e-6
     for a, b in zip(c0, c1):
-        assert torch.equal(a, b)
-    assert f0 == f1 and f1 > 0
+        assert float((a != b).float().mean()) < 1e-4
+    assert f1 > 0
     # one rounding of the summed product where the layer-by-layer MLP rounds
     # each layer's input gradient and then their sum
     assert _rel(gx1, gx0) <= 8e-3

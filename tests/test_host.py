@@ -291,19 +291,13 @@ class OracleKernels:
             (F.silu(g) * u).backward(grad)
         return g.grad, u.grad
 
-    def swiglu_backward_sums(self, grad, gate, up, offset_gate, offset_up):
+    def swiglu_backward_sums(self, grad, gate, up, offset_gate, offset_up, *, side_by_side=False):
         dg, du = self.swiglu_backward(grad, gate, up)
         sums = torch.stack((dg.double().t() @ offset_gate.double(), du.double().t() @ offset_up.double()))
         self.swiglu_sums = getattr(self, "swiglu_sums", 0) + 1
+        if side_by_side:
+            return torch.cat((dg, du), dim=1), sums.float()
         return dg, du, sums.float()
-
-    # the SwiGLU MLP node's summed input gradient of the gate and up layers
-    def packed_transpose_pair(self, grad_a, packed_a, scale_a, grad_b, packed_b, scale_b, columns):
-        dx = oracle.linear_dgrad(grad_a.float().numpy(), packed_a.numpy(), columns, scale_a.detach().float().numpy())
-        dx = dx + oracle.linear_dgrad(grad_b.float().numpy(), packed_b.numpy(), columns,
-                                      scale_b.detach().float().numpy())
-        self.pairs = getattr(self, "pairs", 0) + 1
-        return torch.from_numpy(dx).float().to(grad_a.dtype)
 
     # binary embedding (oracle/embedding.py)
     def packed_embedding(self, ids, packed, scale, columns):
@@ -317,7 +311,7 @@ class OracleKernels:
 
 ACTIVATION_OPS = ("pack_bits", "unpack_bits", "masked_backward", "masked_activation",
                   "smooth_activation", "smooth_backward", "packed_embedding", "embedding_backward",
-                  "swiglu_forward", "swiglu_backward", "swiglu_backward_sums", "packed_transpose_pair")
+                  "swiglu_forward", "swiglu_backward", "swiglu_backward_sums")
 
 
 @pytest.fixture
@@ -837,9 +831,9 @@ def test_swiglu_mlp_node_composes_the_layers(fake, monkeypatch):
     """qste_amd.nn.swiglu_mlp as one node (its eligibility check relaxed to
     CPU tensors so the oracle-backed operators run it): the same output as
     the layers called one by one, each surface's evidence once (the same
-    evidence), the gate and up layers' input gradients from one two-layer
-    product, and the steps inside backward reading each layer's signs only
-    after every product that needs them."""
+    evidence), the gate and up layers' backward as one call over both, and
+    the steps inside backward reading each layer's signs only after every
+    product that needs them."""
 
     import qste_amd as qste
     from qste_amd import functional
@@ -873,9 +867,9 @@ def test_swiglu_mlp_node_composes_the_layers(fake, monkeypatch):
     fake.backward_calls = []
     fake.swiglu_sums = 0
     y1, g1, e1, s1 = run(True)
-    assert fake.pairs == 1 and fake.swiglu_sums == 1
-    # the down layer forms its input gradient; gate and up leave theirs to the pair product
-    assert fake.backward_calls == [True, False, False]
+    assert fake.swiglu_sums == 1
+    # the down layer, then gate and up in one call; both form input gradients
+    assert fake.backward_calls == [True, True]
     assert torch.equal(y0, y1)
     assert torch.allclose(g0.float(), g1.float(), rtol=2e-2, atol=2e-2)
     for name in ("gate", "up", "down"):
