@@ -29,6 +29,8 @@ namespace qste {
 namespace swiglu {
 
 constexpr int kThreads = 256;
+constexpr int64_t kEncodeGroups = 1024;  // workgroups of the tabled encoding forward (4 per CU on 256 CUs)
+constexpr int64_t kTabRows = 4;          // rows per workgroup from which the table pays for itself
 
 __device__ __forceinline__ float silu_value(float x) { return x / (1.0f + expf(-x)); }
 
@@ -86,36 +88,87 @@ __global__ __launch_bounds__(kThreads) void forward_bf16x8_kernel(const uint4* _
     h[q] = forward_chunk(g[q], u[q]);
 }
 
-// bf16 rows of `stride` 8-value chunks (stride <= CH * kThreads), a
-// workgroup per row: h is written and its row encoded from the registers.
-template <int CH>
+// The forward's table of the rounded silu covers the bf16 gates whose
+// magnitude lies in [2^-12, 2^8) (both signs: 2 x 20 binades of 128
+// values), wider than the common tables' [2^-12, 2^4): a gate of magnitude
+// 16 .. 255 is unusual but not rare enough for the computed path, which
+// runs the whole wave through the exponential and the division.
+constexpr uint32_t kFwdExps = 20;
+constexpr uint32_t kFwdHalf = kFwdExps * 128;
+constexpr int kFwdEntries = 2 * kFwdHalf;
+
+__device__ __forceinline__ uint32_t fwd_tab_bits(uint32_t j) {
+  const uint32_t neg = j >= kFwdHalf ? 1u : 0u;
+  return (neg << 15) | ((kTab16ExpLo << 7) + (j - neg * kFwdHalf));
+}
+
+// The rounded silu of bf16 gate bits `bits` (value x): from the table when
+// tabulated, else computed the same way the table was filled.
+__device__ __forceinline__ float silu_rounded_bf16(uint32_t bits, float x, const uint16_t* tab_a) {
+  const uint32_t off = (bits & 0x7FFFu) - (kTab16ExpLo << 7);  // wraps above the range when below it
+  return off < kFwdHalf ? bf16_to_f32(tab_a[off + ((bits >> 15) ? kFwdHalf : 0u)])
+                        : Elem<QSTE_BF16>::round(silu_value(x));
+}
+
+// forward_chunk with the rounded silu looked up
+__device__ __forceinline__ uint4 forward_chunk_tab(const uint4& gc, const uint4& uc, const uint16_t* tab_a) {
+  uint32_t out[4];
+  const uint32_t gw[4] = {gc.x, gc.y, gc.z, gc.w}, uw[4] = {uc.x, uc.y, uc.z, uc.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float g0 = __uint_as_float(gw[j] << 16), g1 = __uint_as_float(gw[j] & 0xFFFF0000u);
+    const float u0 = __uint_as_float(uw[j] << 16), u1 = __uint_as_float(uw[j] & 0xFFFF0000u);
+    const float a0 = silu_rounded_bf16(gw[j] & 0xFFFFu, g0, tab_a);
+    const float a1 = silu_rounded_bf16(gw[j] >> 16, g1, tab_a);
+    out[j] = f32x2_to_bf16x2(a0 * u0, a1 * u1);
+  }
+  return make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+// bf16 rows of `stride` 8-value chunks (stride <= CH * kThreads); workgroup
+// b takes rows b, b + gridDim.x, ...: h is written and its row encoded from
+// the registers.  With TAB the rounded silu of tabulated gates comes from an
+// LDS table the workgroup fills once for all its rows (the exponential and
+// the correctly rounded division per entry, not per element); without, for
+// grids of about one row per workgroup, every element computes it.
+template <int CH, bool TAB>
 __global__ __launch_bounds__(kThreads) void forward_encode_kernel(const uint16_t* __restrict__ g,
                                                                   const uint16_t* __restrict__ u,
                                                                   uint16_t* __restrict__ h,
                                                                   uint8_t* __restrict__ packed,
                                                                   float* __restrict__ offset,
-                                                                  float* __restrict__ scale, int64_t cols,
-                                                                  int64_t stride) {
+                                                                  float* __restrict__ scale, int64_t rows,
+                                                                  int64_t cols, int64_t stride) {
   __shared__ double red[kThreads / kWave];
-  const int64_t row = blockIdx.x;
-  const uint4* gr = reinterpret_cast<const uint4*>(g + row * cols);
-  const uint4* ur = reinterpret_cast<const uint4*>(u + row * cols);
-  uint4* hr = reinterpret_cast<uint4*>(h + row * cols);
+  __shared__ uint16_t tab_a[TAB ? kFwdEntries : 1];
+  if (TAB) {
+    for (int j = threadIdx.x; j < kFwdEntries; j += kThreads) {
+      const float x = __uint_as_float(fwd_tab_bits(static_cast<uint32_t>(j)) << 16);
+      tab_a[j] = f32_to_bf16(silu_value(x));
+    }
+    __syncthreads();
+  }
   const int t = threadIdx.x;
-  uint4 gv[CH], uv[CH], v[CH];
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const uint4* gr = reinterpret_cast<const uint4*>(g + row * cols);
+    const uint4* ur = reinterpret_cast<const uint4*>(u + row * cols);
+    uint4* hr = reinterpret_cast<uint4*>(h + row * cols);
+    uint4 gv[CH], uv[CH], v[CH];
 #pragma unroll
-  for (int k = 0; k < CH; ++k) {
-    const int64_t q = t + static_cast<int64_t>(k) * kThreads;
-    gv[k] = q < stride ? gr[q] : make_uint4(0, 0, 0, 0);
-    uv[k] = q < stride ? ur[q] : make_uint4(0, 0, 0, 0);
-  }
+    for (int k = 0; k < CH; ++k) {
+      const int64_t q = t + static_cast<int64_t>(k) * kThreads;
+      gv[k] = q < stride ? gr[q] : make_uint4(0, 0, 0, 0);
+      uv[k] = q < stride ? ur[q] : make_uint4(0, 0, 0, 0);
+    }
 #pragma unroll
-  for (int k = 0; k < CH; ++k) {
-    const int64_t q = t + static_cast<int64_t>(k) * kThreads;
-    v[k] = q < stride ? forward_chunk(gv[k], uv[k]) : make_uint4(0, 0, 0, 0);
-    if (q < stride) hr[q] = v[k];
+    for (int k = 0; k < CH; ++k) {
+      const int64_t q = t + static_cast<int64_t>(k) * kThreads;
+      v[k] = q >= stride ? make_uint4(0, 0, 0, 0)
+                         : TAB ? forward_chunk_tab(gv[k], uv[k], tab_a) : forward_chunk(gv[k], uv[k]);
+      if (q < stride) hr[q] = v[k];
+    }
+    encode_row_chunks<kThreads, CH>(v, packed + row * stride, offset + row, scale + row, cols, stride, red);
   }
-  encode_row_chunks<kThreads, CH>(v, packed + row * stride, offset + row, scale + row, cols, stride, red);
 }
 
 template <int DT>
@@ -349,14 +402,25 @@ int launch_swiglu_forward(const void* g, const void* u, int dtype, void* h, uint
   const int64_t stride = cols / 8;
   const bool vec = dtype == QSTE_BF16 && cols % 8 == 0 && aligned(g) && aligned(u) && aligned(h);
   if (packed && vec && stride <= 8 * kThreads) {
-    if (stride <= 2 * kThreads)
-      forward_encode_kernel<2><<<rows, kThreads, 0, s>>>(static_cast<const uint16_t*>(g),
-                                                         static_cast<const uint16_t*>(u), static_cast<uint16_t*>(h),
-                                                         packed, offset, scale, cols, stride);
+    // with at least kTabRows rows per workgroup of kEncodeGroups, each fills
+    // the table once for its rows; fewer rows take a workgroup per row
+    const bool tab = rows >= kTabRows * kEncodeGroups;
+    const unsigned grid = static_cast<unsigned>(tab ? kEncodeGroups : rows);
+    const auto* gp = static_cast<const uint16_t*>(g);
+    const auto* upp = static_cast<const uint16_t*>(u);
+    auto* hp = static_cast<uint16_t*>(h);
+    if (stride <= 2 * kThreads && tab)
+      forward_encode_kernel<2, true>
+          <<<grid, kThreads, 0, s>>>(gp, upp, hp, packed, offset, scale, rows, cols, stride);
+    else if (stride <= 2 * kThreads)
+      forward_encode_kernel<2, false>
+          <<<grid, kThreads, 0, s>>>(gp, upp, hp, packed, offset, scale, rows, cols, stride);
+    else if (tab)
+      forward_encode_kernel<8, true>
+          <<<grid, kThreads, 0, s>>>(gp, upp, hp, packed, offset, scale, rows, cols, stride);
     else
-      forward_encode_kernel<8><<<rows, kThreads, 0, s>>>(static_cast<const uint16_t*>(g),
-                                                         static_cast<const uint16_t*>(u), static_cast<uint16_t*>(h),
-                                                         packed, offset, scale, cols, stride);
+      forward_encode_kernel<8, false>
+          <<<grid, kThreads, 0, s>>>(gp, upp, hp, packed, offset, scale, rows, cols, stride);
     return static_cast<int>(hipGetLastError());
   }
   if (vec) {

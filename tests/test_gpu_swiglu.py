@@ -215,6 +215,43 @@ def _same_or_both_nan(a, b):
     return bool(((_bits(a) == _bits(b)) | nan).all())
 
 
+@pytest.mark.parametrize("rows,cols", [(4096, 1024), (4096, 14336)])
+def test_tabled_forward_every_bf16_gate(rows, cols):
+    """From 4096 rows on, the encoding forward takes the rounded silu of
+    gates with magnitude in [2^-12, 2^8) from a table each workgroup fills
+    once for several rows.  Every one of the 65536 bf16 gate values, spread
+    over the rows in a seeded random order (so that waves mix tabulated gates
+    with zeros, subnormals, tiny and huge magnitudes, infinities and NaNs):
+    the output bit for bit against torch's F.silu(g) * u, and the encoding
+    byte for byte against pack_affine_rows on that output (the even rows keep
+    only gates below 2^100 in magnitude, so that their statistics are finite
+    too)."""
+
+    from qste_amd import kernels
+
+    print(f"tabled swiglu forward {rows}x{cols}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(rows + cols)
+    order = torch.randperm(rows * cols, generator=g, device=DEV) % 65536
+    gate = (order - 32768).to(torch.int16).view(torch.bfloat16).reshape(rows, cols)
+    # the even rows without their infinities, NaNs and magnitudes from 2^100
+    # on (whose products can overflow), so that their statistics are finite
+    # and compared exactly
+    even = gate[0::2]
+    even[~(even.float().abs() < 2.0**100)] = 0.5
+    up = torch.randn(rows, cols, generator=g, device=DEV).bfloat16()
+    want = F.silu(gate) * up
+    out, (packed, offset, scale) = kernels.swiglu_forward(gate, up, encode=True)
+    torch.cuda.synchronize()
+    assert _same_or_both_nan(out, want)
+    p2, o2, s2 = kernels.pack_affine_rows(out)
+    assert torch.equal(packed, p2)
+    # rows holding a NaN or an infinity have NaN statistics, whose payload
+    # depends on the order the sums met them in
+    for a, b in ((offset, o2), (scale, s2)):
+        assert bool(((a.view(torch.int32) == b.view(torch.int32)) | (torch.isnan(a) & torch.isnan(b))).all())
+    assert bool(torch.isfinite(offset[0::2]).all())
+
+
 def test_backward_sums_every_bf16_gate():
     """Every one of the 65536 bf16 gate values (in and out of the range the
     kernel's sigmoid/silu tables hold: zeros, subnormals, tiny and huge
