@@ -229,8 +229,8 @@ def cfg1_lines(device, cpu: bool):
         secs = (time.perf_counter() - t0) / iters
         out.update({"cpu_ms_per_step": round(secs * 1e3, 3), "cpu_tflops": round(flop / secs / 1e12, 4),
                     "cpu_threads": threads, "cpu_model": cb.cpu_model(), "cpu_iterations": iters,
-                    "cpu_kind": "port of the reference's cpu.cpp (LUT expansion + torch fp32 GEMM, "
-                                "OpenMP encoding and 4-pass step)"})
+                    "cpu_kind": "port of the reference's cpu.cpp (tile sign expansion + torch fp32 GEMM, "
+                                "OpenMP encoding and 4-phase step)"})
     return out
 
 
@@ -854,8 +854,8 @@ def memory_bandwidth(device, pair_bytes=256 << 20, pairs=3):
 
 def cpu_baseline(d, ffn, tokens=16384, warm_tokens=512):
     """Config 4 on this host's cores with the port of the reference's CPU
-    backend (oracle/cpu_baseline.py): LUT tile expansion + torch's fp32 GEMMs,
-    OpenMP encodings and four-pass coordinate steps.
+    backend (oracle/cpu_baseline.py): packed signs expanded one tile at a time
+    + torch's fp32 GEMMs, OpenMP encodings and four-phase coordinate steps.
 
     One whole training step at the full token count: the three forwards with
     their encodings, the SwiGLU, every backward product (each layer's input

@@ -4,15 +4,16 @@ Used only by ``bench.py``'s ``cpu_baseline`` leg (and its CPU test).  It runs
 what the reference's native CPU backend (``src/qste/kernels/cpu.cpp``) runs,
 multi-threaded on the host:
 
-* forward / input gradient / evidence: packed signs expanded one tile of rows
-  at a time through a byte -> eight floats table (``cpu_port.c``
-  ``cp_expand``; cpu.cpp:59-87, 103-125) and each tile handed to torch's
+* forward / input gradient / evidence: packed signs expanded to +-1 floats
+  one tile of rows at a time (``cpu_port.c`` ``cp_expand``; cpu.cpp expands
+  through a byte table, cpu.cpp:59-87, 103-125) and each tile handed to torch's
   fp32 CPU GEMM (``torch.mm`` / ``addmm_`` are the reference's ``at::mm`` /
   ``addmm_``, cpu.cpp:342-456), the row scale folded into the expanded tile
   for the input gradient (cpu.cpp:402) and the per-sample scale into the
   gradient tile for the evidence (cpu.cpp:444-447);
-* activation encoding, row inner product and the four-pass coordinate step:
-  ``cpu_port.c`` with OpenMP (cpu.cpp:143-203, 460-496, 578-808);
+* activation encoding, row inner product and the coordinate step's four
+  dependent phases: ``cpu_port.c`` with OpenMP (cpu.cpp:143-203, 460-496,
+  578-808);
 * the layer's backward composition of ``functional.py:173-194``.
 
 Everything is fp32, as the reference's CPU kernels are fp32-only

@@ -3,7 +3,7 @@ oracle/cpu_port.c) checked against the oracle, so the timed baseline computes
 what the reference's CPU path computes and not something cheaper.
 
 Its products must equal the float64 oracle within fp32 GEMM error, its
-activation bits must equal the oracle's, and its four-pass step (cpu.cpp's
+activation bits must equal the oracle's, and its four-phase step (cpu.cpp's
 numerics: +1e-12 after the mean, fp32 sums, one division for the step size)
 must keep the step's invariants and land on the specification's integers
 almost everywhere.
