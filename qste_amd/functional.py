@@ -226,7 +226,10 @@ class SwiGLUMLPFn(Function):
 
     The values are those of the three QSTELinearFn nodes and SwiGLUFn
     composed: the same products, the same gate arithmetic, the same
-    encodings (x's shared by gate and up; h's from the gate kernel).  The
+    encodings (x's shared by gate and up; h's from the gate kernel), and
+    the row scales of the three surfaces from their log-scales with the
+    kernels of ``surface.row_scale`` (inputs are the log-scales, so their
+    gradients leave this node as RowScaleFn's would).  The
     backward runs the gate and up layers as one layer of 2 ffn rows: the
     gate's backward writes their gradients side by side into one [tokens,
     2 ffn] tensor (with the two layers' offset sums, in the order the layers
@@ -245,20 +248,26 @@ class SwiGLUMLPFn(Function):
     QSTELinearFn: down first, then gate and up."""
 
     @staticmethod
-    def forward(ctx, inputs, packed_g, scale_g, bias_g, packed_u, scale_u, bias_u, packed_d, scale_d, bias_d,
+    def forward(ctx, inputs, packed_g, log_g, bias_g, packed_u, log_u, bias_u, packed_d, log_d, bias_d,
                 surfaces, grad_on: bool):
         sg, su, sd = surfaces
         d, ffn = sg.columns, sg.rows
         flat = inputs.reshape(-1, d)
+        # each layer's row scale (the kernel of surface.row_scale) right
+        # before the product that needs it, so the first product is queued
+        # after one small launch rather than three
+        scale_g, e_g = kernels.row_scale(log_g, sg.cfg.scale_min, sg.cfg.scale_max)
         g = kernels.packed_linear_affine(flat, packed_g, scale_g, bias_g, d)
+        scale_u, e_u = kernels.row_scale(log_u, su.cfg.scale_min, su.cfg.scale_max)
         u = kernels.packed_linear_affine(flat, packed_u, scale_u, bias_u, d)
         h, enc = kernels.swiglu_forward(g, u, encode=grad_on)
+        scale_d, e_d = kernels.row_scale(log_d, sd.cfg.scale_min, sd.cfg.scale_max)
         y = kernels.packed_linear_affine(h, packed_d, scale_d, bias_d, ffn)
         if grad_on:
             payload_x, aux_x = _encoding_of(inputs, flat, d)
             aux_h = kernels.stacked_pair(enc[1], enc[2])
             ctx.save_for_backward(payload_x, aux_x, g, u, enc[0], aux_h, packed_g, scale_g, packed_u, scale_u,
-                                  packed_d, scale_d)
+                                  packed_d, scale_d, e_g, e_u, e_d)
         ctx.surfaces = surfaces
         ctx.input_shape = inputs.shape
         ctx.bias_dtypes = tuple(None if b is None else b.dtype for b in (bias_g, bias_u, bias_d))
@@ -268,7 +277,7 @@ class SwiGLUMLPFn(Function):
     def backward(ctx, grad_output):
         forget_encodings()
         (payload_x, aux_x, g, u, payload_h, aux_h, packed_g, scale_g, packed_u, scale_u, packed_d,
-         scale_d) = ctx.saved_tensors
+         scale_d, e_g, e_u, e_d) = ctx.saved_tensors
         sg, su, sd = ctx.surfaces
         d, ffn = sg.columns, sg.rows
         bg, bu, bd = ctx.bias_dtypes
@@ -302,8 +311,16 @@ class SwiGLUMLPFn(Function):
         def cast(grad, dtype):
             return None if grad is None or dtype is None else grad.to(dtype)
 
-        return (dx, None, gs_g.to(scale_g.dtype), cast(gb_g, bg), None, gs_u.to(scale_u.dtype), cast(gb_u, bu),
-                None, gs_d.to(scale_d.dtype), cast(gb_d, bd), None, None)
+        def through_scale(gs, e, surface):
+            # the scale's gradient carried to the log-scale, as RowScaleFn does
+            return kernels.row_scale_backward(e, gs.to(e.dtype), surface.cfg.scale_min, surface.cfg.scale_max)
+
+        return (dx, None, through_scale(gs_g, e_g, sg), cast(gb_g, bg), None, through_scale(gs_u, e_u, su),
+                cast(gb_u, bu), None, through_scale(gs_d, e_d, sd), cast(gb_d, bd), None, None)
+
+
+# log-scale dtypes the row-scale kernels take (surface.row_scale)
+_SCALE_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
 
 
 def swiglu_mlp_fusable(inputs: Tensor, gate, up, down) -> bool:
@@ -315,7 +332,8 @@ def swiglu_mlp_fusable(inputs: Tensor, gate, up, down) -> bool:
     d, ffn = sg.columns, sg.rows
     return (inputs.is_cuda and inputs.dtype == torch.bfloat16 and inputs.dim() >= 1 and inputs.shape[-1] == d
             and su.columns == d and su.rows == ffn and sd.columns == ffn and sd.rows == d
-            and d % 64 == 0 and ffn % 64 == 0 and inputs.numel() > 0)
+            and d % 64 == 0 and ffn % 64 == 0 and inputs.numel() > 0
+            and all(s.log_scale.is_cuda and s.log_scale.dtype in _SCALE_DTYPES for s in (sg, su, sd)))
 
 
 def swiglu(gate: Tensor, up: Tensor) -> Tensor:

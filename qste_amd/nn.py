@@ -90,8 +90,8 @@ def swiglu_mlp(inputs: Tensor, gate, up, down) -> Tensor:
     surfaces = (gate.surface, up.surface, down.surface)
     for s in surfaces:
         s.note_forward()
-    y = SwiGLUMLPFn.apply(x, gate.surface.packed_sign, gate.surface.scale, gate.bias, up.surface.packed_sign,
-                          up.surface.scale, up.bias, down.surface.packed_sign, down.surface.scale, down.bias,
+    y = SwiGLUMLPFn.apply(x, gate.surface.packed_sign, gate.surface.log_scale, gate.bias, up.surface.packed_sign,
+                          up.surface.log_scale, up.bias, down.surface.packed_sign, down.surface.log_scale, down.bias,
                           surfaces, torch.is_grad_enabled())
     return _mark_activation_input(y)
 

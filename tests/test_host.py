@@ -272,6 +272,13 @@ class OracleKernels:
 
 
     # the SwiGLU gate: torch's own chain on the CPU, encoding by the oracle
+    def row_scale(self, log_scale, lo, hi):
+        e = log_scale.detach().exp()
+        return e.clamp(lo, hi), e
+
+    def row_scale_backward(self, e, grad, lo, hi):
+        return torch.where((e >= lo) & (e <= hi), grad.to(e.dtype), torch.zeros_like(e)) * e
+
     def swiglu_forward(self, gate, up, *, encode=False):
         import torch.nn.functional as F
 
@@ -321,7 +328,8 @@ def fake(monkeypatch):
 
     ok = OracleKernels()
     for name in ("pack_coordinate", "unpack_rows", "pack_affine_rows", "packed_linear_affine",
-                 "packed_row_inner", "linear_backward", "coordinate_update") + ACTIVATION_OPS:
+                 "packed_row_inner", "linear_backward", "coordinate_update", "row_scale",
+                 "row_scale_backward") + ACTIVATION_OPS:
         monkeypatch.setattr(kernels, name, getattr(ok, name))
     monkeypatch.setattr(surface, "_on_gpu", lambda fn, t, *a, **k: fn(t, *a, **k))
     return ok
