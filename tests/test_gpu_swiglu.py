@@ -215,7 +215,7 @@ def _same_or_both_nan(a, b):
     return bool(((_bits(a) == _bits(b)) | nan).all())
 
 
-@pytest.mark.parametrize("rows,cols", [(4096, 1024), (4096, 14336)])
+@pytest.mark.parametrize("rows,cols", [(4096, 1024), (4100, 520), (4096, 14336)])
 def test_tabled_forward_every_bf16_gate(rows, cols):
     """From 4096 rows on, the encoding forward takes the rounded silu of
     gates with magnitude in [2^-12, 2^8) from a table each workgroup fills
