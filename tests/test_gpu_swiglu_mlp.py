@@ -17,7 +17,9 @@ and the input gradient as one product over K = 2 ffn.  Held here:
 * the node against the same MLP run layer by layer (``swiglu`` between the
   layers): the output bit for bit, the evidence and scale gradients within
   1e-6, the coordinate steps equal outside elements whose evidence moved,
-  the input gradient within the saved rounding.
+  the input gradient within the saved rounding; also with biases on all
+  three layers and a batched [2, 96, d] input (the bias gradients within
+  1e-6), and with an input that takes no gradient.
 """
 
 from __future__ import annotations
@@ -174,3 +176,79 @@ def test_swiglu_mlp_node_matches_the_layer_by_layer_mlp():
     # one rounding of the summed product where the layer-by-layer MLP rounds
     # each layer's input gradient and then their sum
     assert _rel(gx1, gx0) <= 8e-3
+
+
+def _biased_layer(rows, cols, seed, dev):
+    import qste_amd as qste
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    coord = torch.randint(-127, 128, (rows, cols), generator=g, device=dev, dtype=torch.int32).to(torch.int8)
+    scale = torch.randn(rows, generator=g, device=dev).abs_().mul_(0.02).clamp_min_(1e-6)
+    bias = torch.randn(rows, generator=g, device=dev) * 0.1
+    return qste.QSTELinear(qste.Surface.from_state(coord, scale.log()), bias)
+
+
+def _node_against_layers(x_shape, needs_input):
+    """The node and the layers called one by one (with the fused gate) on
+    fresh copies of the same three biased layers, each with an optimizer
+    stepping inside backward; returns both runs' output, input gradient,
+    delivered evidence, log-scale and bias gradients and coordinates."""
+
+    import qste_amd as qste
+
+    d, ffn = x_shape[-1], 1024
+    dev = torch.device(DEV)
+
+    def run(node):
+        gate, up, down = (_biased_layer(ffn, d, 1, dev), _biased_layer(ffn, d, 2, dev),
+                          _biased_layer(d, ffn, 3, dev))
+        surfaces = [gate.surface, up.surface, down.surface]
+        coords = qste.QSTEOptimizer(surfaces)
+        seen = {}
+        apply = coords._apply
+        for name, s in zip(("gate", "up", "down"), surfaces):
+            s.route_evidence(lambda srf, e, name=name: (seen.__setitem__(name, e.detach().clone()), apply(srf, e)))
+        g = torch.Generator(device=dev).manual_seed(9)
+        x = torch.randn(*x_shape, generator=g, device=dev).to(torch.bfloat16).requires_grad_(needs_input)
+        dy = torch.randn(*x_shape, generator=g, device=dev).to(torch.bfloat16)
+        y = qste.nn.swiglu_mlp(x, gate, up, down) if node else down(qste.nn.swiglu(gate(x), up(x)))
+        y.backward(dy)
+        torch.cuda.synchronize()
+        layers = (gate, up, down)
+        return (y.detach(), x.grad, seen, [m.surface.log_scale.grad.clone() for m in layers],
+                [m.bias.grad.clone() for m in layers], [s.coordinate.clone() for s in surfaces])
+
+    return run(False), run(True)
+
+
+def test_swiglu_mlp_node_with_biases_and_batched_input():
+    """Biases on all three layers and a [2, 96, d] input: the output bit for
+    bit, the bias gradients (the gate and up layers' as the two halves of
+    one call's column sums) equal to the layers' own, the evidence and
+    log-scale gradients within 1e-6, the input gradient within the rounding
+    the single product saves, its shape the input's."""
+
+    a, b = _node_against_layers((2, 96, 512), True)
+    assert b[0].shape == (2, 96, 512) and torch.equal(a[0], b[0])
+    assert b[1].shape == (2, 96, 512) and _rel(b[1], a[1]) <= 8e-3
+    for name in ("gate", "up", "down"):
+        assert _rel(b[2][name], a[2][name]) <= 1e-6, name
+    for ga, gb in zip(a[3], b[3]):
+        assert _rel(gb, ga) <= 1e-6
+    for ga, gb in zip(a[4], b[4]):
+        assert gb.dtype == ga.dtype == torch.float32 and _rel(gb, ga) <= 1e-6
+    for ca, cb in zip(a[5], b[5]):
+        assert float((ca != cb).float().mean()) < 1e-4
+
+
+def test_swiglu_mlp_node_without_input_gradient():
+    """An input that takes no gradient: no input-gradient product in the
+    node's backward, the same evidence and scale gradients as the layers'."""
+
+    a, b = _node_against_layers((192, 512), False)
+    assert a[1] is None and b[1] is None
+    assert torch.equal(a[0], b[0])
+    for name in ("gate", "up", "down"):
+        assert _rel(b[2][name], a[2][name]) <= 1e-6, name
+    for ga, gb in zip(a[3] + a[4], b[3] + b[4]):
+        assert _rel(gb, ga) <= 1e-6
