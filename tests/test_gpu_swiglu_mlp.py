@@ -19,7 +19,9 @@ and the input gradient as one product over K = 2 ffn.  Held here:
   1e-6, the coordinate steps equal outside elements whose evidence moved,
   the input gradient within the saved rounding; also with biases on all
   three layers and a batched [2, 96, d] input (the bias gradients within
-  1e-6), and with an input that takes no gradient.
+  1e-6), and with an input that takes no gradient;
+* inputs the node does not take (fp16, an ffn that is not a multiple of 64)
+  running the layers one by one, bit for bit.
 """
 
 from __future__ import annotations
@@ -252,3 +254,31 @@ def test_swiglu_mlp_node_without_input_gradient():
         assert _rel(b[2][name], a[2][name]) <= 1e-6, name
     for ga, gb in zip(a[3] + a[4], b[3] + b[4]):
         assert _rel(gb, ga) <= 1e-6
+
+
+@pytest.mark.parametrize("dtype,ffn", [(torch.float16, 1024), (torch.bfloat16, 1000)])
+def test_swiglu_mlp_outside_the_node_is_the_layers(dtype, ffn):
+    """Inputs the node does not take (fp16; an ffn that is not a multiple of
+    64) run the layers one by one: output and every gradient bit for bit
+    those of down(swiglu(gate(x), up(x)))."""
+
+    import qste_amd as qste
+    from qste_amd import functional
+
+    dev = torch.device(DEV)
+    d = 512
+
+    def run(composed):
+        gate, up, down = (_biased_layer(ffn, d, 1, dev), _biased_layer(ffn, d, 2, dev),
+                          _biased_layer(d, ffn, 3, dev))
+        g = torch.Generator(device=dev).manual_seed(4)
+        x = torch.randn(128, d, generator=g, device=dev).to(dtype).requires_grad_(True)
+        assert not functional.swiglu_mlp_fusable(x, gate, up, down)
+        y = down(qste.nn.swiglu(gate(x), up(x))) if composed else qste.nn.swiglu_mlp(x, gate, up, down)
+        y.float().square().sum().backward()
+        torch.cuda.synchronize()
+        layers = (gate, up, down)
+        return [y.detach(), x.grad] + [m.surface.log_scale.grad for m in layers] + [m.bias.grad for m in layers]
+
+    for a, b in zip(run(True), run(False)):
+        assert a.dtype == b.dtype and torch.equal(a, b)
