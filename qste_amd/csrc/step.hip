@@ -1244,6 +1244,22 @@ __global__ void sync_clear_kernel(unsigned* sync) {
   for (int i = threadIdx.x; i < kSyncWords; i += blockDim.x) sync[i] = 0u;
 }
 
+// Wave priority `x mod 4` (s_setprio takes an immediate).  A SIMD holds four
+// waves of this kernel: waves w and w + 4 of two workgroups.  The hardware
+// breaks priority ties by age, and with ties everywhere the oldest wave of a
+// SIMD streamed its rows ~40% faster than the youngest, so every pass ended
+// on a tail of young waves.  The passes rotate each wave's priority per
+// batch of rows, offset by its rank among the four, so that waves at the
+// same batch hold distinct priorities and each leads a quarter of the time.
+__device__ __forceinline__ void rotate_priority(int x) {
+  switch (x & 3) {
+    case 0: __builtin_amdgcn_s_setprio(0); break;
+    case 1: __builtin_amdgcn_s_setprio(1); break;
+    case 2: __builtin_amdgcn_s_setprio(2); break;
+    default: __builtin_amdgcn_s_setprio(3); break;
+  }
+}
+
 typedef __attribute__((address_space(3))) void lds_t;
 
 // Buffer resource over `bytes` bytes at `base` (loads past the end read 0).
@@ -1294,6 +1310,9 @@ __global__ __launch_bounds__(kThreads, kPerCU) void fused_step_kernel(const floa
   const uint32_t voff = static_cast<uint32_t>(col * 4);
   float4* st = stage + wave * kWave + lane;  // LDS row j of this lane: st[j * kThreads]
   const int nb = (nrows + kBatch - 1) / kBatch;
+  // rank among the SIMD's four waves: the grid holds two workgroups per CU,
+  // and its first half takes one slot on every CU, the second half the other
+  const int prank = __builtin_amdgcn_readfirstlane((wave >> 2) + 2 * (b >= static_cast<int>(gridDim.x >> 1)));
 
   for (int t = threadIdx.x; t < nrows; t += kThreads) rowv_prev[t] = f16_to_f32(row_v[r0 + t]);
 
@@ -1348,6 +1367,7 @@ __global__ __launch_bounds__(kThreads, kPerCU) void fused_step_kernel(const floa
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) load(need_tag, u < nrows ? row_at(u, fwd) : -1, cur[u]);
     for (int k = 0; k < nb; ++k) {
+      rotate_priority(k + prank);
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const int pos = (k + 1) * kBatch + u;
@@ -1365,6 +1385,7 @@ __global__ __launch_bounds__(kThreads, kPerCU) void fused_step_kernel(const floa
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) cur[u] = nxt[u];
     }
+    __builtin_amdgcn_s_setprio(0);
   };
   using E_ = std::integral_constant<int, kNeedE>;
   using EQ_ = std::integral_constant<int, kNeedE | kNeedQ>;
@@ -1391,6 +1412,7 @@ __global__ __launch_bounds__(kThreads, kPerCU) void fused_step_kernel(const floa
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) load(E_{}, u < nm ? nL + u : -1, cur[u]);
     for (int k = 0; k < nbm; ++k) {
+      rotate_priority(k + prank);
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const int pos = (k + 1) * kBatch + u;
@@ -1403,6 +1425,7 @@ __global__ __launch_bounds__(kThreads, kPerCU) void fused_step_kernel(const floa
       for (int u = 0; u < kBatch; ++u) cur[u] = nxt[u];
     }
   }
+  __builtin_amdgcn_s_setprio(0);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the direct loads have landed in LDS
   for (int j = 0; j < nL; ++j) {
     RowIn in;
