@@ -25,7 +25,10 @@ Semantics that fix the integer trajectory and so follow the reference:
 
 Flip counts are written by the kernel into one preallocated device slot per
 surface and read back once per ``step()``, so backward never waits on the
-host and nothing is allocated per application.  Evidence all-reduce across
+host and nothing is allocated per application.  That read polls an event
+behind a copy into pinned host memory rather than blocking in the copy: a
+blocking read returned ~70 us after the device had finished, and the
+caller's next launches (the next forward) waited with it.  Evidence all-reduce across
 ranks is not part of this single-GPU build: with a multi-rank process group
 pass ``gradient_reducer`` explicitly (``False`` to opt out), or construction
 fails rather than letting ranks silently drift apart.
@@ -34,6 +37,7 @@ fails rather than letting ranks silently drift apart.
 from __future__ import annotations
 
 import math
+import time
 from dataclasses import dataclass, field
 from typing import Callable, Iterable, Mapping
 
@@ -86,6 +90,21 @@ def _no_reducer_check(requested):
     return None
 
 
+def _read_count(total: Tensor, host: Tensor | None) -> int:
+    """``int(total)``.  A GPU total is copied into ``host`` (pinned int64)
+    behind an event on the current stream, which is polled; the poll yields
+    the interpreter lock between queries."""
+
+    if not total.is_cuda or host is None:
+        return int(total.item())
+    host.copy_(total, non_blocking=True)
+    done = torch.cuda.Event()
+    done.record(torch.cuda.current_stream(total.device))
+    while not done.query():
+        time.sleep(0)
+    return int(host.item())
+
+
 class QSTEOptimizer:
     """Steps int8 coordinates from the evidence backward produces.
 
@@ -114,6 +133,7 @@ class QSTEOptimizer:
         self.step_number = 0
         self.deferred = False
         self._slots: dict[int, _Slot] = {}
+        self._host_count: Tensor | None = None  # pinned int64 for step()'s flip total
         for position, surface in enumerate(found):
             self._slots[id(surface)] = _Slot(
                 surface=surface,
@@ -205,7 +225,12 @@ class QSTEOptimizer:
                 self._apply(slot.surface, pending)
             slot.surface.log_scale.data.clamp_(lo, hi)
         counts = [slot.flips for slot in self._slots.values() if slot.applied]
-        flips = int(torch.stack(counts).sum().item()) if counts else 0
+        flips = 0
+        if counts:
+            total = torch.stack(counts).sum()
+            if total.is_cuda and self._host_count is None:
+                self._host_count = torch.empty((), dtype=torch.int64, pin_memory=True)
+            flips = _read_count(total, self._host_count)
         for slot in self._slots.values():
             slot.applied = False
         self.step_number += 1
