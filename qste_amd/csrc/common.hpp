@@ -212,4 +212,20 @@ __device__ __forceinline__ float div_by(float x, float d, float r) {
 
 inline int ceil_div(int64_t a, int64_t b) { return static_cast<int>((a + b - 1) / b); }
 
+// Wave priority `x mod 4` (s_setprio takes an immediate).  The hardware
+// breaks ties between waves of equal priority by age, so in a kernel whose
+// workgroups each own a fixed share of a stream, the waves a SIMD received
+// first finish first and the pass ends on a tail of the youngest.  Rotating
+// each wave's priority as it moves through its share, offset by its rank
+// among the SIMD's waves, gives waves at the same point distinct
+// priorities, each leading in turn.
+__device__ __forceinline__ void rotate_priority(int x) {
+  switch (x & 3) {
+    case 0: __builtin_amdgcn_s_setprio(0); break;
+    case 1: __builtin_amdgcn_s_setprio(1); break;
+    case 2: __builtin_amdgcn_s_setprio(2); break;
+    default: __builtin_amdgcn_s_setprio(3); break;
+  }
+}
+
 }  // namespace qste

@@ -1244,21 +1244,11 @@ __global__ void sync_clear_kernel(unsigned* sync) {
   for (int i = threadIdx.x; i < kSyncWords; i += blockDim.x) sync[i] = 0u;
 }
 
-// Wave priority `x mod 4` (s_setprio takes an immediate).  A SIMD holds four
-// waves of this kernel: waves w and w + 4 of two workgroups.  The hardware
-// breaks priority ties by age, and with ties everywhere the oldest wave of a
-// SIMD streamed its rows ~40% faster than the youngest, so every pass ended
-// on a tail of young waves.  The passes rotate each wave's priority per
-// batch of rows, offset by its rank among the four, so that waves at the
-// same batch hold distinct priorities and each leads a quarter of the time.
-__device__ __forceinline__ void rotate_priority(int x) {
-  switch (x & 3) {
-    case 0: __builtin_amdgcn_s_setprio(0); break;
-    case 1: __builtin_amdgcn_s_setprio(1); break;
-    case 2: __builtin_amdgcn_s_setprio(2); break;
-    default: __builtin_amdgcn_s_setprio(3); break;
-  }
-}
+// A SIMD holds four waves of this kernel: waves w and w + 4 of two
+// workgroups.  With priority ties everywhere the oldest of them streamed its
+// rows ~40% faster than the youngest, so every pass ended on a tail of young
+// waves; the passes rotate each wave's priority per batch of rows
+// (rotate_priority), offset by its rank among the four.
 
 typedef __attribute__((address_space(3))) void lds_t;
 
