@@ -16,9 +16,10 @@ with one rounding, their evidence as one product of seven full rounds of
 tiles).  The same step with the layers
 called one by one is reported as ``step_layer_by_layer_ms`` (the fused gate
 qste_amd.nn.swiglu between them) and ``step_torch_gate_ms`` (torch's silu
-and mul), and the node's step once the optimizer is past step 64 (settled
-second moments, the clip idle: the coordinate step's momentum formed in its
-U^2 pass) as ``step_past_64_ms``.  ``value`` = 6 * T * sum(R*C) / step time
+and mul), and the node's step once the optimizer is past step 64 (where the
+coordinate step forms the momentum speculatively in its U^2 pass, which
+saves a pass over the evidence for surfaces whose clip is idle and costs
+one where it still engages) as ``step_past_64_ms``.  ``value`` = 6 * T * sum(R*C) / step time
 of the steps timed from a fresh optimizer.
 
 Alongside, measured live with HIP events on the stream the kernels run on:
@@ -1028,10 +1029,10 @@ def main():
         mlp.mode = "node"
         # The headline times the optimizer's steps W .. W+K-1 from a fresh
         # state, where the clip engages and the coordinate step forms the
-        # momentum in a pass of its own.  A long run is past step 64 with
-        # settled second moments: there the U^2 pass forms the momentum too,
-        # and while the clip stays idle one pass over the evidence is saved.
-        # The same step timed there (the steps in between untimed):
+        # momentum in a pass of its own.  Past step 64 the U^2 pass forms
+        # the momentum too, which saves a pass over the evidence wherever
+        # the clip is idle.  The same step timed there (the steps in
+        # between untimed):
         while coords.step_number < 64:
             step()
         torch.cuda.synchronize()
