@@ -725,9 +725,8 @@ __device__ __forceinline__ void wide_tile(const Params& p, int pid, uint8_t* A0,
         const int64_t gcol = n0 + WNC * wn + 8 * chunk;
         if (grow < p.M) {
           if (vec_ok && gcol + 8 <= p.N) {
-            // streaming (nontemporal) stores: every CU writes its 128 KiB
-            // tile at about the same moment, and a plain store burst held
-            // the epilogue ~9.5 us per tile at the forward's shape
+            // streaming (nontemporal) stores: nothing in this launch reads
+            // the outputs again (0.3-3% faster per launch than plain stores)
             const u32x4 w = {v.x, v.y, v.z, v.w};
             __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(y + grow * p.N + gcol));
           } else {

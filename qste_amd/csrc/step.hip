@@ -1244,12 +1244,6 @@ __global__ void sync_clear_kernel(unsigned* sync) {
   for (int i = threadIdx.x; i < kSyncWords; i += blockDim.x) sync[i] = 0u;
 }
 
-// A SIMD holds four waves of this kernel: waves w and w + 4 of two
-// workgroups.  With priority ties everywhere the oldest of them streamed its
-// rows ~40% faster than the youngest, so every pass ended on a tail of young
-// waves; the passes rotate each wave's priority per batch of rows
-// (rotate_priority), offset by its rank among the four.
-
 typedef __attribute__((address_space(3))) void lds_t;
 
 // Buffer resource over `bytes` bytes at `base` (loads past the end read 0).
@@ -1300,8 +1294,13 @@ __global__ __launch_bounds__(kThreads, kPerCU) void fused_step_kernel(const floa
   const uint32_t voff = static_cast<uint32_t>(col * 4);
   float4* st = stage + wave * kWave + lane;  // LDS row j of this lane: st[j * kThreads]
   const int nb = (nrows + kBatch - 1) / kBatch;
-  // rank among the SIMD's four waves: the grid holds two workgroups per CU,
-  // and its first half takes one slot on every CU, the second half the other
+  // A SIMD holds four waves of this kernel: waves w and w + 4 of two
+  // workgroups.  With priority ties everywhere the oldest of them streamed
+  // its rows ~40% faster than the youngest, so every pass ended on a tail of
+  // young waves; the passes rotate each wave's priority per batch of rows
+  // (rotate_priority), offset by its rank among the four.  The grid holds
+  // two workgroups per CU, its first half taking one slot on every CU and
+  // the second half the other.
   const int prank = __builtin_amdgcn_readfirstlane((wave >> 2) + 2 * (b >= static_cast<int>(gridDim.x >> 1)));
 
   for (int t = threadIdx.x; t < nrows; t += kThreads) rowv_prev[t] = f16_to_f32(row_v[r0 + t]);

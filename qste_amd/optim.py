@@ -28,10 +28,12 @@ surface and read back once per ``step()``, so backward never waits on the
 host and nothing is allocated per application.  That read polls an event
 behind a copy into pinned host memory rather than blocking in the copy: a
 blocking read returned ~70 us after the device had finished, and the
-caller's next launches (the next forward) waited with it.  Evidence all-reduce across
-ranks is not part of this single-GPU build: with a multi-rank process group
-pass ``gradient_reducer`` explicitly (``False`` to opt out), or construction
-fails rather than letting ranks silently drift apart.
+caller's next launches (the next forward) waited with it.
+
+Evidence all-reduce across ranks is not part of this single-GPU build: with
+a multi-rank process group pass ``gradient_reducer`` explicitly (``False``
+to opt out), or construction fails rather than letting ranks silently drift
+apart.
 """
 
 from __future__ import annotations
