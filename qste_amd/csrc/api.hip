@@ -41,6 +41,8 @@ int mfma_linear_dgrad_t(const void*, int, const uint8_t*, int64_t, const uint16_
                         int64_t, hipStream_t);
 int mfma_evidence(const void*, int, const uint8_t*, const float*, float*, int64_t, int64_t, int64_t,
                   const float*, const float*, const uint8_t*, float*, const EvidencePlan*, float*, hipStream_t);
+int mfma_evidence_t(const void*, int, const uint8_t*, int64_t, const uint16_t*, float*, int64_t, int64_t, int64_t,
+                    const float*, const float*, const uint8_t*, float*, const EvidencePlan*, float*, hipStream_t);
 int64_t mfma_evidence_tiles(int64_t cols);
 bool mfma_pair_ok(const void*, int, int64_t, int64_t, int64_t);
 EvidencePlan mfma_evidence_plan(int64_t, int64_t, int64_t, bool);
@@ -394,6 +396,16 @@ int linear_backward_impl(const void* dy, int dtype, const uint8_t* packed_x, con
           if (rc) return rc;
         }
         dgrad_done = true;
+        // the evidence from a transposed copy of x's signs (bits along K,
+        // bf16 scales), as the pair reads them
+        uint8_t* x_t = reinterpret_cast<uint8_t*>(base + l.x_t);
+        uint16_t* xs16 = reinterpret_cast<uint16_t*>(base + l.xs16);
+        if ((rc = launch_transpose_bits(packed_x, x_t, samples, cols, pb, l.x_t_pitch, s))) return rc;
+        if ((rc = launch_f32_to_16(x_scale, xs16, samples, (samples + 63) / 64 * 64, dtype, s))) return rc;
+        rc = mfma_evidence_t(dy, dtype, x_t, l.x_t_pitch, xs16, evidence, samples, rows, cols, v, scale, packed_w,
+                             gs_part, &plan, partial, s);
+        if (rc == 0) return launch_sum_partials(gs_part, mfma_evidence_tiles(cols), rows, grad_scale, s);
+        if (rc != 1) return rc;
         int64_t tiles = 0;
         if ((rc = evidence_dispatch(dy, dtype, packed_x, x_scale, evidence, samples, rows, cols, v, scale,
                                     packed_w, gs_part, &plan, partial, &tiles, s)))
